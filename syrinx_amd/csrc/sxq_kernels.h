@@ -1,0 +1,33 @@
+// sxq_kernels.h -- launchers shared between the library's translation units.
+#pragma once
+#include "sxq_common.h"
+
+namespace sxq {
+
+// Activation quantization (QMatMul's first step): x [m, k] -> Q8_K / Q8_0 blocks.
+// canon = Candle's block bytes; otherwise the device layout (ActQ8K / ActQ8_0).
+hipError_t launch_quantize_act(int vdt, bool canon, const float* x, int64_t ldx, int m, int k, void* out,
+                               hipStream_t s);
+// Weight quantization (QTensor::quantize): x [nblocks * bs] -> canonical blocks.
+hipError_t launch_from_float(int dt, const float* x, int64_t nblocks, void* out, hipStream_t s);
+// Dequantization (QTensor::dequantize) of canonical blocks.
+hipError_t launch_to_float(int dt, const void* blocks, int64_t nelem, float* y, hipStream_t s);
+// Canonical <-> device weight layout.
+hipError_t launch_repack(int dt, const void* canon, int64_t nblocks, void* hdr, void* qs, bool to_device,
+                         hipStream_t s);
+hipError_t launch_fill_normal(float* y, int64_t n, uint64_t seed, float mean, float stdv, hipStream_t s);
+
+// A quantized weight in the device layout.
+struct QWeight {
+    int dtype = 0;
+    int64_t n = 0, k = 0, nb = 0;
+    const uint8_t* hdr = nullptr;  // Q4_K: 16 B per block; Q8_0/Q4_0: f16 d per block
+    const uint8_t* qs = nullptr;   // Q4_K: 128 B; Q8_0: 32 B; Q4_0: 16 B per block
+};
+
+// Decode GEMV, m in 1..16: y[m, n] (row stride ldy) = act[m] . W^T (+ bias).
+// act is the device activation layout [m][nb] (ActQ8K for Q4_K, ActQ8_0 otherwise).
+hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
+                       hipStream_t s);
+
+}  // namespace sxq

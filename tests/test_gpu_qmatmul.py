@@ -1,0 +1,212 @@
+"""GPU parity of the quantized path against the CPU oracle (Candle's generic CPU path).
+
+Bar: bit-exact.  Weight and activation blocks are byte-identical, dequantized weights
+bit-identical, and QMatMul outputs bit-identical to Candle's generic vec-dot order,
+for every row count (decode GEMV) -- integer and float steps replay Candle's order.
+"""
+import threading
+
+import numpy as np
+import pytest
+import torch
+
+from syrinx_amd import GgmlDType, QMatMul, QTensor, SxqError
+from syrinx_amd.quantized import qmatmul_host
+
+pytestmark = pytest.mark.gpu
+
+G = GgmlDType
+
+
+@pytest.fixture(scope="module")
+def cuda():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU (torch.cuda.is_available() is False)")
+    return torch.device("cuda:0")
+
+
+def _weights(n, k, seed, std=0.02):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k)) * std).astype(np.float32)
+    # edge rows: a zero row, a row of ties, a row with f16-subnormal scales, a large row
+    if n >= 4:
+        w[0] = 0.0
+        w[1, :] = 0.5
+        w[1, ::2] = -0.5
+        w[2] *= 1e-4
+        w[3] *= 1e4
+    return w
+
+
+def _acts(m, k, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if m >= 3:
+        x[1] = 0.0             # all-zero activation row -> d = 0 blocks
+        x[2, :64] = 3.0        # ties at the maximum magnitude
+        x[2, 64:128] = -3.0
+    return x
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _eq_bits(got, want):
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    assert got.shape == want.shape
+    same = (_bits(got) == _bits(want)) | ((got == 0) & (want == 0))  # +0 == -0
+    if not same.all():
+        i = np.argwhere(~same)[:5]
+        raise AssertionError(f"{(~same).sum()} of {same.size} differ; first {i.tolist()}: "
+                             f"got {got[tuple(i[0])]!r} want {want[tuple(i[0])]!r}")
+
+
+# ------------------------------------------------------------------ quantize / dequantize
+@pytest.mark.parametrize("dt,k", [(G.Q8_0, 896), (G.Q4_0, 896), (G.Q4K, 2560), (G.Q8_0, 4864), (G.Q8K, 2560)])
+def test_quantize_rows_bytes_match_oracle(cuda, ora, dt, k):
+    w = _weights(48, k, 1)
+    qt = QTensor.quantize(torch.from_numpy(w).to(cuda), dt)
+    got = qt.data().cpu().numpy().reshape(48, -1)
+    want = ora.quantize(int(dt), w)
+    np.testing.assert_array_equal(got, want)
+    assert qt.storage_size_in_bytes() == want.size
+
+
+@pytest.mark.parametrize("dt,k", [(G.Q8_0, 896), (G.Q4_0, 896), (G.Q4K, 2560), (G.Q8K, 512)])
+def test_dequantize_bit_exact(cuda, ora, dt, k):
+    w = _weights(32, k, 2)
+    blocks = ora.quantize(int(dt), w)
+    qt = QTensor.from_blocks(blocks, (32, k), dt, device=cuda)
+    _eq_bits(qt.dequantize().cpu().numpy(), ora.dequantize(int(dt), blocks, k))
+
+
+def test_dequantize_q4k_arbitrary_bytes(cuda, ora):
+    # random scale/min/nibble bytes (finite f16 d, dmin): exercises every 6-bit packing path
+    rng = np.random.default_rng(3)
+    blk = rng.integers(0, 256, size=(64, 144), dtype=np.uint8)
+    d = (rng.standard_normal((64, 2)) * 0.01).astype(np.float16)
+    blk[:, :4] = d.view(np.uint8).reshape(64, 4)
+    qt = QTensor.from_blocks(blk, (64, 256), G.Q4K, device=cuda)
+    _eq_bits(qt.dequantize().cpu().numpy(), ora.dequantize(ora.Q4K, blk, 256))
+
+
+@pytest.mark.parametrize("vdt,k", [(G.Q8_0, 896), (G.Q8_0, 4864), (G.Q8K, 2560), (G.Q8K, 9728)])
+def test_activation_blocks_bit_exact(cuda, ora, vdt, k):
+    import ctypes
+    from syrinx_amd._lib import check, lib
+    x = _acts(5, k, 4)
+    xt = torch.from_numpy(x).to(cuda)
+    nbytes = 5 * (k // vdt.block_size()) * vdt.type_size()
+    out = torch.zeros(nbytes, dtype=torch.uint8, device=cuda)
+    check(lib().sxq_act_quantize(0, int(vdt), ctypes.c_void_p(xt.data_ptr()), 5, k, ctypes.c_void_p(out.data_ptr()),
+                                 torch.cuda.current_stream().cuda_stream))
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(5, -1), ora.quantize(int(vdt), x))
+
+
+# ------------------------------------------------------------------ QMatMul forward
+CASES = [
+    (G.Q8_0, 4864, 896, 1),    # BASELINE config 1 (Qwen2-0.5B MLP up-proj)
+    (G.Q8_0, 896, 4864, 1),    # down-proj
+    (G.Q8_0, 128, 896, 3),     # k/v proj, ragged rows
+    (G.Q4_0, 896, 896, 2),     # the dtype the reference ships
+    (G.Q4_0, 6564, 896, 1),    # CV2 head shape
+    (G.Q4K, 6144, 2560, 1),    # Qwen3-4B fused wqkv
+    (G.Q4K, 2560, 9728, 1),    # w2
+    (G.Q4K, 2560, 4096, 16),   # wo, skinny batch of 16
+    (G.Q4K, 1003, 2560, 5),    # n not a multiple of the 8-row group
+    (G.Q4K, 9728, 2560, 17),   # two 16-row slabs
+    (G.Q8_0, 2560, 9728, 4),   # Q8_0 at the Qwen3-4B shape
+]
+
+
+@pytest.mark.parametrize("dt,n,k,m", CASES)
+def test_qmatmul_bit_exact_vs_oracle(cuda, ora, dt, n, k, m):
+    w = _weights(n, k, 10 + n % 7)
+    x = _acts(m, k, 20 + m)
+    blocks = ora.quantize(int(dt), w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), dt, device=cuda))
+    y = qmm.forward(torch.from_numpy(x).to(cuda))
+    torch.cuda.synchronize()
+    _eq_bits(y.cpu().numpy(), ora.matmul(int(dt), x, blocks))
+
+
+def test_bias_batch_shape_and_host_pointers(cuda, ora):
+    n, k = 896, 896
+    w = _weights(n, k, 5)
+    b = (np.random.default_rng(6).standard_normal(n) * 0.02).astype(np.float32)
+    x = _acts(6, k, 7).reshape(2, 3, k)
+    blocks = ora.quantize(ora.Q8_0, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q8_0, device=cuda))
+    y = qmm.forward(torch.from_numpy(x).to(cuda), bias=torch.from_numpy(b).to(cuda)).cpu().numpy()
+    assert y.shape == (2, 3, n)
+    want = (ora.matmul(ora.Q8_0, x.reshape(6, k), blocks) + b[None, :]).astype(np.float32)  # f32 bias add
+    _eq_bits(y.reshape(6, n), want)
+    _eq_bits(qmatmul_host(qmm, x, b).reshape(6, n), want)
+
+
+def test_export_and_dequantize_round_trip(cuda, ora):
+    w = _weights(300, 2560, 8)
+    blocks = ora.quantize(ora.Q4K, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (300, 2560), G.Q4K, device=cuda))
+    np.testing.assert_array_equal(qmm.export_blocks().cpu().numpy(), blocks.ravel())
+    _eq_bits(qmm.dequantize().cpu().numpy(), ora.dequantize(ora.Q4K, blocks, 2560))
+    assert qmm.storage_size_in_bytes() == blocks.size
+
+
+def test_forward_error_behaviour(cuda):
+    qmm = QMatMul.from_qtensor(QTensor.quantize(torch.randn(64, 512, device=cuda) * 0.02, G.Q8_0))
+    with pytest.raises(SxqError) as e:
+        qmm.forward(torch.randn(2, 256, device=cuda))
+    assert "incompatible with [64, 512]" in str(e.value)
+    with pytest.raises(SxqError) as e:
+        qmm.forward(torch.randn(512, device=cuda))
+    assert "only one dimension" in str(e.value)
+    with pytest.raises(SxqError) as e:
+        qmm.forward(torch.randn(512, 4, device=cuda).t())
+    assert "not contiguous" in str(e.value)
+    with pytest.raises(SxqError):
+        qmm.forward(torch.randn(2, 512, device=cuda, dtype=torch.float16))
+    y = qmm.forward(torch.zeros(0, 512, device=cuda))
+    assert y.shape == (0, 64)
+
+
+def test_concurrent_forward_on_one_handle(cuda, ora):
+    # tests/real_lm_hammer.rs:48-83 shares one model across threads; forward is re-entrant.
+    n, k = 2048, 2560
+    w = _weights(n, k, 9)
+    blocks = ora.quantize(ora.Q4K, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    xs = [_acts(1 + i % 3, k, 30 + i) for i in range(6)]
+    want = [ora.matmul(ora.Q4K, x, blocks) for x in xs]
+    out = [None] * len(xs)
+
+    def run(i):
+        s = torch.cuda.Stream(device=cuda)
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                y = qmm.forward(torch.from_numpy(xs[i]).to(cuda))
+            s.synchronize()
+            out[i] = y.cpu().numpy()
+
+    th = [threading.Thread(target=run, args=(i,)) for i in range(len(xs))]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    for o, wnt in zip(out, want):
+        _eq_bits(o, wnt)
+
+
+def test_full_size_tied_head_q4k(cuda, ora):
+    # The Qwen3-4B tied LM head [155776 x 2560] at full size, bit-exact on every row.
+    n, k = 155776, 2560
+    g = torch.Generator(device=cuda).manual_seed(11)
+    w = torch.randn(n, k, device=cuda, generator=g) * 0.02
+    qt = QTensor.quantize(w, G.Q4K)
+    del w
+    qmm = QMatMul.from_qtensor(qt)
+    x = _acts(1, k, 12)
+    y = qmm.forward(torch.from_numpy(x).to(cuda)).cpu().numpy()
+    blocks = qt.data().cpu().numpy().reshape(n, -1)
+    _eq_bits(y, ora.matmul(ora.Q4K, x, blocks))
