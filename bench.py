@@ -1,0 +1,193 @@
+"""Decode benchmark of the quantized-linear hot path on one MI355X.
+
+Workload (the headline metric's configuration): batch-1 greedy decode of a
+Qwen3-4B-shaped Fish s2-pro slow AR -- 36 layers, dim 2560, 32/8 heads x 128,
+SwiGLU 9728, tied 155776-row head, every projection Q4_K -- with an f32 KV cache
+prefilled to 1024 positions (N(0,1)), generating `--steps` tokens (default 256).
+Weights are random N(0, 0.02) quantized with Candle's from_float (synthetic data).
+
+A step is one decode token (embedding -> 36 layers -> head -> argmax fed back on the
+device), replayed as a captured HIP graph.  `value` is tokens per second over the
+timed steps.  `roofline` is the Q4_K GEMV family (every projection of a token,
+launched back to back over 2.27 GB of weights) timed with HIP events on the stream
+the kernels run on: algorithmic bytes (weight blocks + activations + outputs) per
+launch over the average launch duration, against 8 TB/s.  `cpu_baseline` times the
+oracle (the CPU restatement of Candle's quantized matmul) on one layer's projections
+plus the head, on this host's cores, and scales it to one token's GEMV work.
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtype q4k|q8_0]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--dtype", default="q4k", choices=["q4k", "q8_0"])
+    ap.add_argument("--kv", type=int, default=1024)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--gemv-iters", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    return ap.parse_args()
+
+
+def gemv_roofline(lm, torch, iters):
+    """Average duration of the GEMV launches of one token (all 36 layers + head)."""
+    dev = lm.device
+    from syrinx_amd._lib import check, lib
+    import ctypes
+    s = torch.cuda.current_stream(dev)
+    n_launch = 4 * lm.cfg.n_layers + 1
+    layer_b, head_b = lm.weight_bytes()
+    # algorithmic bytes per token of GEMV: weight blocks + f32 outputs + activation blocks
+    c = lm.cfg
+    qkv_n = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
+    outs = 4 * (qkv_n + c.dim + 2 * c.intermediate + c.dim) * c.n_layers + 4 * c.vocab
+    act_blk = 292 if c.weight_dtype == 12 else 34
+    bs = 256 if c.weight_dtype == 12 else 32
+    acts = act_blk * ((2 * c.dim + c.n_heads * c.head_dim + c.intermediate) // bs * c.n_layers + c.dim // bs)
+    algo = layer_b + head_b + outs + acts
+    for _ in range(2):
+        check(lib().sxq_lm_gemv_pass(lm._h, 1, 1, ctypes.c_void_p(s.cuda_stream)))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(iters):
+        check(lib().sxq_lm_gemv_pass(lm._h, 1, 1, ctypes.c_void_p(s.cuda_stream)))
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    avg_us = ms * 1000.0 / n_launch
+    achieved = algo / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_gemv_q4k" if c.weight_dtype == 12 else "k_gemv_q80",
+            "bytes_per_token": algo, "launches_per_token": n_launch, "avg_launch_us": round(avg_us, 3),
+            "gemv_us_per_token": round(ms * 1000.0, 2)}
+
+
+def cpu_baseline(lm, torch):
+    """Oracle (CPU port of Candle's quantized matmul) on one layer + the head, all cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle  # the checker / CPU baseline
+    from syrinx_amd import GgmlDType, QTensor
+    c = lm.cfg
+    dt = GgmlDType(c.weight_dtype)
+    dev = lm.device
+    rng = np.random.default_rng(0)
+    qkv_n = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
+    shapes = [(qkv_n, c.dim), (c.dim, c.n_heads * c.head_dim), (2 * c.intermediate, c.dim), (c.dim, c.intermediate)]
+    blocks = []
+    g = torch.Generator(device=dev).manual_seed(1)
+    for n, k in shapes + [(c.vocab, c.dim)]:
+        w = torch.randn(n, k, device=dev, generator=g) * 0.02
+        blocks.append((k, QTensor.quantize(w, dt).data().cpu().numpy().reshape(n, -1)))
+        del w
+    xs = {k: rng.standard_normal((1, k)).astype(np.float32) for k, _ in blocks}
+    threads = os.cpu_count() or 1
+    t_layer = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for k, b in blocks[:4]:
+            oracle.matmul(int(dt), xs[k], b, threads=threads)
+        t_layer.append(time.perf_counter() - t0)
+    t0 = time.perf_counter()
+    k, b = blocks[4]
+    oracle.matmul(int(dt), xs[k], b, threads=threads)
+    t_head = time.perf_counter() - t0
+    per_token = c.n_layers * min(t_layer) + t_head
+    return {"value": round(1.0 / per_token, 3), "unit": "tok/s (GEMV share of a token)", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle k_quants::matmul (generic vec-dot, {threads} threads) over layer-0's four "
+                      f"projections x3 and the head once; token = {c.n_layers} x layer + head "
+                      f"= {per_token * 1000:.0f} ms"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
+              "output rows, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from syrinx_amd import GgmlDType
+    from syrinx_amd import decoder as D
+
+    dev = torch.device("cuda:0")
+    dt = GgmlDType.Q4K if args.dtype == "q4k" else GgmlDType.Q8_0
+    max_seq = args.kv + args.steps + args.warmup + 8
+    cfg = D.fish_s2_slow_ar_config(n_layers=36, max_seq=max_seq, max_batch=args.batch, dtype=dt)
+    t0 = time.time()
+    lm = D.SlowAr(cfg, device=dev)
+    lm.init_random(seed=0, std=0.02)
+    lm.kv_fill_random([args.kv] * args.batch, seed=1)
+    print(f"[bench] model ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    rng_frame = torch.zeros((args.batch, 1 + cfg.n_codebooks), dtype=torch.int32)
+    rng_frame[:, 0] = 151700
+    rng_frame[:, 1:] = torch.arange(cfg.n_codebooks, dtype=torch.int32) * 37 % 4096
+    lm.step(ids=rng_frame, graph=True)  # captures the graph
+    for _ in range(args.warmup):
+        lm.step(n=args.batch, graph=True, want_logits=False)
+    torch.cuda.synchronize()
+    lm.set_lengths([args.kv] * args.batch)
+    lm.step(ids=rng_frame, graph=True, want_logits=False)
+    lm.set_lengths([args.kv] * args.batch)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_host0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(args.steps):
+        lm.step(n=args.batch, graph=True, want_logits=False)
+    e1.record(s)
+    torch.cuda.synchronize()
+    t_host = time.perf_counter() - t_host0
+    ms = e0.elapsed_time(e1)
+    ms_per_step = ms / args.steps
+    tok_s = args.batch * args.steps / (ms / 1000.0)
+    print(f"[bench] {args.steps} steps in {ms:.1f} ms ({ms_per_step * 1000:.1f} us/token, host {t_host * 1000:.1f} ms)",
+          file=sys.stderr, flush=True)
+    roof = gemv_roofline(lm, torch, args.gemv_iters)
+    print(f"[bench] GEMV: {roof['gemv_us_per_token']} us/token, {roof['achieved']} GB/s", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else cpu_baseline(lm, torch)
+    out = {
+        "metric": "decode tok/s Qwen3-4B-shape Q4_K bs=1; quant-GEMV HBM GB/s as % of peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": ("q4k-weight x q8k-activation int dot, f32" if dt == GgmlDType.Q4K
+                  else "q8_0-weight x q8_0-activation int dot, f32"),
+        "data": "synthetic (random N(0,0.02) weights quantized by from_float; KV N(0,1))",
+        "config": {"workload": f"Fish s2-pro slow AR (Qwen3-4B shape) greedy decode, {args.dtype.upper()} "
+                               f"projections, batch {args.batch}, f32 KV prefilled to {args.kv}, "
+                               f"{args.steps} tokens",
+                   "n_layers": 36, "dim": 2560, "heads": "32/8x128", "intermediate": 9728, "vocab": 155776,
+                   "kv_len": args.kv, "batch": args.batch, "graph": True},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

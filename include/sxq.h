@@ -122,6 +122,130 @@ sxq_status sxq_qmm_destroy(sxq_qmm *qmm);
 sxq_status sxq_fill_normal(int device, float *out, int64_t n, uint64_t seed, float mean, float std_dev,
                            void *stream);
 
+/* ---- Decoder step: the callers of QMatMul in one autoregressive LM token ------------
+ *
+ * One decode step of a Qwen2/Qwen3-style LM for up to 16 independent streams, all on
+ * the device: embedding -> n_layers x [RMSNorm -> fused QKV projection (+bias) ->
+ * QK-RMSNorm -> RoPE -> KV append -> GQA attention -> O projection + residual ->
+ * RMSNorm -> gate|up projection -> SiLU*mul -> down projection + residual] -> final
+ * RMSNorm -> head projection (+bias) -> logits and greedy argmax.  Every projection is
+ * the library's QMatMul GEMV over the same weight dtype.  It replaces, per token:
+ *   Fish s2 slow AR:  SlowAr::slow_step / slow_step_batch (crates/syrinx-fish/src/s2/slow_ar.rs:259-271,456-499),
+ *                     run_layers (:166-202), head (:207-246), embed (:101-161);
+ *   CosyVoice2 LM:    Qwen2Lm::forward_logits_cached (crates/syrinx-lm/src/cv2/mod.rs:261-286),
+ *                     attn_cached (crates/syrinx-lm/src/cv2/attention.rs:46-78);
+ * with the per-token loops of crates/syrinx-fish/src/common/dualar.rs:188-219 and
+ * crates/syrinx-lm/src/cv2/generate.rs:150-161 keeping their host-side sampling.
+ * Streams may hold different cache lengths (ragged batches) and need no left padding.
+ */
+typedef struct sxq_lm sxq_lm;
+
+typedef struct {
+    int32_t n_layers;
+    int32_t dim;              /* hidden size */
+    int32_t n_heads;          /* query heads */
+    int32_t n_kv_heads;       /* key/value heads (GQA) */
+    int32_t head_dim;         /* <= 256, multiple of 4 */
+    int32_t intermediate;     /* SwiGLU width */
+    int32_t vocab;            /* head output rows */
+    int32_t embed_rows;       /* rows of a dense embedding table (0 = vocab); unused when tied */
+    int32_t max_seq;          /* KV capacity per stream (positions) */
+    int32_t max_batch;        /* streams per step, 1..16 */
+    int32_t weight_dtype;     /* SXQ_Q4K, SXQ_Q8_0 or SXQ_Q4_0 for every projection */
+    float norm_eps;           /* RMSNorm eps (also QK-RMSNorm) */
+    float rope_theta;         /* RoPE base */
+    int32_t rope_interleaved; /* 1: rotate pairs (2i, 2i+1) (Fish); 0: (i, i + hd/2) (Qwen2) */
+    int32_t qk_norm;          /* per-head RMSNorm of q and k before RoPE (Qwen3) */
+    int32_t qkv_bias;         /* biases on q, k, v (Qwen2) */
+    int32_t head_bias;        /* bias on the head (CosyVoice2 llm_decoder) */
+    int32_t tied_embedding;   /* token embedding = dequantized row of the head weight (Fish) */
+    int32_t n_codebooks;      /* Fish MCF: codebook rows summed on semantic positions; 0 = none */
+    int32_t codebook_size;
+    int32_t semantic_begin;   /* semantic token id range (inclusive) for the MCF scale */
+    int32_t semantic_end;
+} sxq_lm_config;
+
+/* Projection slots for sxq_lm_set_linear (layer-local unless noted). */
+enum {
+    SXQ_LM_WQKV = 0, /* fused [q; k; v] rows (Fish wqkv, crates/syrinx-fish/src/s2/load.rs:271-312) */
+    SXQ_LM_WQ = 1,   /* separate q/k/v (Qwen2 q_proj/k_proj/v_proj) fused on upload */
+    SXQ_LM_WK = 2,
+    SXQ_LM_WV = 3,
+    SXQ_LM_WO = 4,
+    SXQ_LM_W1 = 5,   /* gate */
+    SXQ_LM_W3 = 6,   /* up */
+    SXQ_LM_W2 = 7,   /* down */
+    SXQ_LM_HEAD = 8  /* model-level: output head (tied embedding table for Fish) */
+};
+/* Vector slots for sxq_lm_set_vector. */
+enum {
+    SXQ_LM_ATTN_NORM = 0,
+    SXQ_LM_FFN_NORM = 1,
+    SXQ_LM_Q_NORM = 2,
+    SXQ_LM_K_NORM = 3,
+    SXQ_LM_BQ = 4,
+    SXQ_LM_BK = 5,
+    SXQ_LM_BV = 6,
+    SXQ_LM_FINAL_NORM = 7,     /* model-level */
+    SXQ_LM_HEAD_BIAS = 8,      /* model-level */
+    SXQ_LM_EMBED = 9,          /* model-level dense table [embed_rows, dim] */
+    SXQ_LM_CODEBOOK_EMBED = 10 /* model-level [n_codebooks * codebook_size, dim] */
+};
+
+/* sxq_lm_step flags */
+#define SXQ_LM_GRAPH 1u /* replay the step as a captured HIP graph (captured on first use per batch size) */
+
+sxq_status sxq_lm_create(int device, const sxq_lm_config *cfg, sxq_lm **out);
+/* Copy a QMatMul's weight into a projection slot (shape and dtype must match). */
+sxq_status sxq_lm_set_linear(sxq_lm *lm, int layer, int which, const sxq_qmm *w);
+/* Copy an f32 vector (norm weight, bias, embedding table) into a slot. */
+sxq_status sxq_lm_set_vector(sxq_lm *lm, int layer, int which, const float *data, int64_t n, int src_is_device);
+/* Synthetic weights: every projection N(0, std) quantized with from_float, norm weights
+ * 1, biases / tables N(0, std).  For benchmarks; no reference counterpart. */
+sxq_status sxq_lm_init_random(sxq_lm *lm, uint64_t seed, float std_dev);
+/* Fill the whole KV cache with N(0, 1) and set the first n_streams lengths (a
+ * prefilled cache for decode benchmarks). */
+sxq_status sxq_lm_kv_fill_random(sxq_lm *lm, const int32_t *lengths, int n_streams, uint64_t seed);
+/* Set / read the cached lengths (= next positions) of the first n_streams streams
+ * (KvCache::len, crates/syrinx-fish/src/s2/nn.rs:237-240).  Setting 0 resets a stream
+ * (SlowAr::reset, slow_ar.rs:79-81). */
+sxq_status sxq_lm_set_lengths(sxq_lm *lm, const int32_t *lengths, int n_streams);
+sxq_status sxq_lm_get_lengths(const sxq_lm *lm, int32_t *lengths, int n_streams);
+/* One decode step for streams 0..n_streams-1 (device pointers, enqueued on `stream`):
+ *   ids      int32 [n_streams, 1 + n_codebooks] token ids (Fish frame: semantic id then
+ *            codes), or NULL to reuse the previous step's argmax (codes kept);
+ *   embeds   f32 [n_streams, dim] input embeddings instead of ids (CosyVoice2 passes
+ *            embeddings to forward_logits_cached), or NULL;
+ *   logits   f32 [n_streams, vocab] output, or NULL;  next_ids int32 [n_streams], or NULL.
+ * Each stream's token is placed at its current length, which then advances by one. */
+sxq_status sxq_lm_step(sxq_lm *lm, int n_streams, const int32_t *ids, const float *embeds, float *logits,
+                       int32_t *next_ids, unsigned flags, void *stream);
+/* Enqueue only the projection GEMVs of one step (every layer's fused QKV, O, gate|up
+ * and down, plus the head if with_head) on the step's current activations: the
+ * GEMV share of a token, for bandwidth measurement.  No reference counterpart. */
+sxq_status sxq_lm_gemv_pass(sxq_lm *lm, int n_streams, int with_head, void *stream);
+/* Read cached post-RoPE keys and values [count, head_dim] (device) for tests. */
+sxq_status sxq_lm_read_kv(const sxq_lm *lm, int layer, int stream_idx, int kv_head, int pos0, int count, float *k_out,
+                          float *v_out, void *stream);
+/* Copy a step buffer of the first n streams (device) for tests: 0 = residual stream
+ * after the last layer [n, dim], 1 = logits [n, vocab], 2 = last layer's q|k|v
+ * projection [n, qkv], 3 = last layer's gate|up [n, 2*intermediate], 4 = last layer's
+ * post-RoPE queries [n, n_heads*head_dim].  No reference counterpart. */
+sxq_status sxq_lm_read_state(const sxq_lm *lm, int which, int n_streams, float *out, void *stream);
+/* Test instrumentation (no reference counterpart): with a trace buffer set, every
+ * step also records its f32 intermediates, for n_streams streams, in this order:
+ * embedding output [n, dim]; per layer hn_attn [n, dim], qkv [n, qkv], post-RoPE q
+ * [n, n_heads*head_dim], attention context [n, n_heads*head_dim], h after the O
+ * residual [n, dim], hn_ffn [n, dim], gate|up [n, 2*intermediate], silu*mul [n,
+ * intermediate], h after the down residual [n, dim]; then the final hn [n, dim].
+ * sxq_lm_trace_floats gives the size for n streams; the buffer must hold the size
+ * for max_batch.  NULL turns tracing off. */
+sxq_status sxq_lm_trace_floats(const sxq_lm *lm, int n_streams, size_t *floats);
+sxq_status sxq_lm_set_trace(sxq_lm *lm, float *trace, size_t capacity_floats);
+/* Bytes of quantized projection weights read by one step (layers + head). */
+sxq_status sxq_lm_weight_bytes(const sxq_lm *lm, size_t *layer_bytes, size_t *head_bytes);
+sxq_status sxq_lm_destroy(sxq_lm *lm);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,8 @@ def lib() -> ctypes.CDLL:
         L.ora_softmax.argtypes = [P, I64]
         L.ora_silu.restype = ctypes.c_float
         L.ora_silu.argtypes = [ctypes.c_float]
+        L.ora_silu_mul.restype = None
+        L.ora_silu_mul.argtypes = [P, P, I64, P]
         L.ora_attend_one.restype = None
         L.ora_attend_one.argtypes = [P, P, P, I64, I64, P]
         _lib = L
@@ -144,6 +146,42 @@ def matmul(dtype: int, x: np.ndarray, w_blocks: np.ndarray, threads: int = 0) ->
     return y
 
 
+def quant_margin(vdt: int, x: np.ndarray) -> float:
+    """How close activation quantization of x comes to a decision boundary.
+
+    Returns the smallest distance (in quantization steps) of any scaled value
+    |x * iscale| from a rounding tie (k + 0.5), and, for Q8_K, of the two largest
+    magnitudes of a block from each other (which one is "max" sets the sign of the
+    scale).  Two f32 inputs that differ by a relative 1e-6 can only quantize
+    differently where this margin is below ~1e-4."""
+    x = np.asarray(x, np.float32).reshape(-1)
+    bs = BLOCK[vdt]
+    b = x.reshape(-1, bs)
+    a = np.abs(b)
+    if vdt == Q8K:
+        idx = a.argmax(axis=1)
+        mx = b[np.arange(len(b)), idx]
+        ok = a.max(axis=1) > 0
+        if not ok.any():
+            return 1.0
+        iscale = (np.float32(-128.0) / mx[ok]).astype(np.float32)
+        v = (iscale[:, None] * b[ok]).astype(np.float32)
+        top2 = np.sort(a[ok], axis=1)[:, -2:]
+        tie = float((128.0 * (top2[:, 1] - top2[:, 0]) / top2[:, 1]).min())
+    else:
+        amax = a.max(axis=1)
+        d = (amax / np.float32(127.0)).astype(np.float32)
+        ok = d != 0
+        if not ok.any():
+            return 1.0
+        inv = (np.float32(1.0) / d[ok]).astype(np.float32)
+        v = (b[ok] * inv[:, None]).astype(np.float32)
+        tie = 1.0
+    av = np.abs(v.astype(np.float64))
+    frac = av - np.floor(av)
+    return float(min(np.abs(frac - 0.5).min(), tie))
+
+
 def dot_f64(dtype: int, w_row: np.ndarray, x: np.ndarray) -> float:
     w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
     x = np.ascontiguousarray(x, dtype=np.float32)
@@ -206,6 +244,14 @@ def silu(x: np.ndarray) -> np.ndarray:
     L = lib()
     x = np.asarray(x, dtype=np.float32)
     return np.array([L.ora_silu(float(v)) for v in x.ravel()], np.float32).reshape(x.shape)
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    out = np.empty_like(g)
+    lib().ora_silu_mul(_p(g), _p(u), g.size, _p(out))
+    return out
 
 
 def attend_one(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray) -> np.ndarray:

@@ -638,6 +638,10 @@ void ora_softmax(float *x, int64_t n) {
 /* candle's unary silu: v / (1 + exp(-v)). */
 float ora_silu(float v) { return v / (1.0f + expf(-v)); }
 
+void ora_silu_mul(const float *g, const float *u, int64_t n, float *out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = ora_silu(g[i]) * u[i];
+}
+
 /* crates/syrinx-fish/src/s2/nn.rs:340-351 (and cv2/attention.rs:67-75) for one
  * decode query: scores = (q . k_j) * f32(1/sqrt(hd)), softmax, sum_j p_j v_j. */
 void ora_attend_one(const float *q, const float *kc, const float *vc, int64_t L, int64_t hd,

@@ -98,6 +98,8 @@ void ora_rope_half(float *x, int64_t n_heads, int64_t head_dim, const float *cos
                    const float *sin_row);
 void ora_softmax(float *x, int64_t n);
 float ora_silu(float x);
+/* out[i] = silu(g[i]) * u[i] (candle_nn::ops::silu then Tensor::mul). */
+void ora_silu_mul(const float *g, const float *u, int64_t n, float *out);
 /* One query row of GQA decode attention for one q head over L cached positions.
  * k_cache/v_cache: [L, head_dim] for this head's kv head. */
 void ora_attend_one(const float *q, const float *k_cache, const float *v_cache, int64_t L,

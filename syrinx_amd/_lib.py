@@ -55,6 +55,21 @@ _SIGS = {
     "sxq_qmm_export": (_I, [_P, _P, _P]),
     "sxq_qmm_destroy": (_I, [_P]),
     "sxq_fill_normal": (_I, [_I, _P, _I64, _U64, _F, _F, _P]),
+    "sxq_lm_create": (_I, [_I, _P, _P]),
+    "sxq_lm_set_linear": (_I, [_P, _I, _I, _P]),
+    "sxq_lm_set_vector": (_I, [_P, _I, _I, _P, _I64, _I]),
+    "sxq_lm_init_random": (_I, [_P, _U64, _F]),
+    "sxq_lm_kv_fill_random": (_I, [_P, _P, _I, _U64]),
+    "sxq_lm_set_lengths": (_I, [_P, _P, _I]),
+    "sxq_lm_get_lengths": (_I, [_P, _P, _I]),
+    "sxq_lm_step": (_I, [_P, _I, _P, _P, _P, _P, _U, _P]),
+    "sxq_lm_read_kv": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "sxq_lm_gemv_pass": (_I, [_P, _I, _I, _P]),
+    "sxq_lm_read_state": (_I, [_P, _I, _I, _P, _P]),
+    "sxq_lm_trace_floats": (_I, [_P, _I, _P]),
+    "sxq_lm_set_trace": (_I, [_P, _P, _SZ]),
+    "sxq_lm_weight_bytes": (_I, [_P, _P, _P]),
+    "sxq_lm_destroy": (_I, [_P]),
 }
 
 

@@ -8,11 +8,13 @@
 #include <string>
 
 #include "../../include/sxq.h"
+#include "sxq_abi.h"
 #include "sxq_kernels.h"
 
 using namespace sxq;
 
-namespace {
+namespace sxq {
+namespace abi {
 
 thread_local std::string g_last_error;
 
@@ -30,25 +32,12 @@ sxq_status hip_fail(hipError_t e, const char* what) {
     return fail(e == hipErrorOutOfMemory ? SXQ_ERR_OOM : SXQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
-#define HIP_TRY(expr, what)                          \
-    do {                                             \
-        hipError_t e_ = (expr);                      \
-        if (e_ != hipSuccess) return hip_fail(e_, what); \
-    } while (0)
+}  // namespace abi
+}  // namespace sxq
 
-// Makes `dev` current for the scope and restores the caller's device afterwards.
-struct DeviceGuard {
-    int prev = -1;
-    hipError_t err = hipSuccess;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) err = hipSetDevice(dev);
-    }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
+using namespace sxq::abi;
+
+namespace {
 
 bool quant_weight_dtype(int dt) { return dt == kQ4_0 || dt == kQ8_0 || dt == kQ4K; }
 bool block_dtype(int dt) { return dt == kQ4_0 || dt == kQ8_0 || dt == kQ4K || dt == kQ8K; }
@@ -75,13 +64,6 @@ std::string shape_str(const int64_t* s, int nd) {
 }
 
 }  // namespace
-
-struct sxq_qmm {
-    int device = 0;
-    QWeight w;
-    void* mem = nullptr;  // one allocation: hdr region then qs region
-    size_t storage = 0;   // canonical byte count (storage_size_in_bytes)
-};
 
 extern "C" {
 
@@ -315,7 +297,7 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
     if (e == hipSuccess) e = launch_quantize_act(vdt, false, dx, k, (int)m, (int)k, act, s);
     for (int64_t r0 = 0; r0 < m && e == hipSuccess; r0 += 16) {
         const int mm = (int)(m - r0 < 16 ? m - r0 : 16);
-        e = launch_gemv(q->w, (const uint8_t*)act + (size_t)r0 * nbv * act_block_bytes(vdt), mm, dy + r0 * n, n, dbias, s);
+        e = launch_gemv(q->w, (const uint8_t*)act + (size_t)r0 * nbv * act_block_bytes(vdt), mm, dy + r0 * n, n, dbias, nullptr, 0, s);
     }
     if (host && e == hipSuccess) e = hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, s);
     hipError_t ef = hipFreeAsync(ws, s);

@@ -1,0 +1,30 @@
+// sxq_decoder.h -- launchers of the decoder-step glue kernels (sxq_decoder.hip).
+#pragma once
+#include "sxq_kernels.h"
+
+namespace sxq {
+
+hipError_t launch_rmsnorm_quant(int vdt, const float* h, int rows, int dim, const float* w, float eps, uint8_t* act,
+                                float* normed, hipStream_t s);
+hipError_t launch_qk_rope_append(const float* qkv, int B, int qkv_n, int nh, int nkv, int hd, const float* qn,
+                                 const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
+                                 const int* len, float* qout, float* kc, float* vc, int64_t kv_stream_stride,
+                                 int max_seq, hipStream_t s);
+// Attention splits: at most kMaxSplits partials per head are merged, so a stream holds
+// at most kMaxSplits * kAttnSplit positions.
+constexpr int kAttnSplit = 32;
+constexpr int kMaxSplits = 512;
+size_t attn_partial_lds(int nh, int nkv, int hd, int P);
+hipError_t launch_attention(int vdt, const float* q, const float* kc, const float* vc, const int* len, int B, int nh,
+                            int nkv, int hd, int max_seq, int64_t kv_stream_stride, int P, int max_splits,
+                            float* part, uint8_t* act, float* ctx_out, hipStream_t s);
+hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s);
+hipError_t launch_embed_quant_table(const int* ids, int ids_per, int B, const QWeight& w, int dim, const float* cb,
+                                    int n_cb, int cb_size, int sem_begin, int sem_end, float* h, hipStream_t s);
+hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
+                              hipStream_t s);
+hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, hipStream_t s);
+hipError_t launch_advance(int* len, int B, hipStream_t s);
+hipError_t launch_fill_value(float* y, int64_t n, float v, hipStream_t s);
+
+}  // namespace sxq

@@ -1,0 +1,504 @@
+// sxq_decoder.hip -- the per-token glue between the quantized projections of one
+// decoder step, on the device: RMSNorm (+ activation quantization), QK-RMSNorm + RoPE
+// + KV-cache append, split-K GQA decode attention (+ activation quantization of the
+// context), SiLU*mul (+ quantization), embeddings, argmax and length bookkeeping.
+//
+// Reference (what each kernel restates, f32 throughout as on the reference CPU path):
+//   RMSNorm            crates/syrinx-fish/src/s2/nn.rs:100-106, crates/syrinx-lm/src/cv2/mod.rs:181-186
+//   QK-RMSNorm         crates/syrinx-fish/src/s2/nn.rs:325-331
+//   RoPE interleaved   crates/syrinx-fish/src/s2/nn.rs:154-166 (tables :117-141)
+//   RoPE rotate-half   crates/syrinx-lm/src/cv2/attention.rs:82-88 (tables :108-119)
+//   KV append          crates/syrinx-fish/src/s2/nn.rs:244-254, crates/syrinx-lm/src/cv2/mod.rs:147-157
+//   decode attention   crates/syrinx-fish/src/s2/nn.rs:340-352, crates/syrinx-lm/src/cv2/attention.rs:67-76
+//   SwiGLU             crates/syrinx-fish/src/s2/nn.rs:452-457, crates/syrinx-lm/src/cv2/mod.rs:222-228
+//   MCF embedding      crates/syrinx-fish/src/s2/slow_ar.rs:101-161
+// The quantization kernels feed the next projection exactly what QMatMul::forward would
+// compute from the same f32 input (the wave quantizers of sxq_quant_dev.h).
+#include "sxq_decoder.h"
+#include "sxq_quant_dev.h"
+
+namespace sxq {
+
+SXQ_DEV float wave_sum_f32(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Quantize chunk c of a row of `dim` elements (elements c*256 .. c*256+255, whose
+// values start at `vals`) into the device activation layout `act_row` (row of blocks).
+template <int VDT>
+SXQ_DEV void quantize_chunk(const float* vals, int c, int dim, int lane, uint8_t* act_row) {
+    const int e0 = c * 256 + 4 * lane;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e0 < dim) v = make_float4(vals[4 * lane], vals[4 * lane + 1], vals[4 * lane + 2], vals[4 * lane + 3]);
+    if (VDT == kQ8K) {
+        wave_quantize_q8k<false>(v, lane, act_row + (size_t)c * sizeof(ActQ8K));
+    } else {
+        const int nb = dim / 32;
+        wave_quantize_q8_0<false>(v, lane, c * 8 + (lane >> 3) < nb, act_row + (size_t)c * 8 * sizeof(ActQ8_0));
+    }
+}
+
+// ---------------------------------------------------------------------------- RMSNorm
+// y = (x / sqrt(sum(x*x) * inv_n + eps)) * w  over each row; then quantized.  The sum
+// is a tree here and sequential in Candle's CPU loop: results agree to rounding.
+// grid (rows, ceil(dim/256)): every workgroup reduces the whole row (an L2-resident
+// read) and then normalises and quantizes only its own 256-element chunk.
+template <int VDT>
+__global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ h, int dim, const float* __restrict__ w,
+                                                       float inv_n, float eps, uint8_t* __restrict__ act,
+                                                       float* __restrict__ normed) {
+    __shared__ float xs[256];
+    __shared__ float red[4];
+    const int row = blockIdx.x, c = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float* x = h + (int64_t)row * dim;
+    float ss = 0.0f;
+    for (int i = 4 * threadIdx.x; i < dim; i += 1024) {  // dim is a multiple of 32
+        const float4 v = *(const float4*)(x + i);
+        ss += v.x * v.x;
+        ss += v.y * v.y;
+        ss += v.z * v.z;
+        ss += v.w * v.w;
+    }
+    ss = wave_sum_f32(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float var = ss * inv_n + 0.0f;
+    const float den = sqrtf(var * 1.0f + eps);
+    const int e = c * 256 + threadIdx.x;
+    float v = 0.0f;
+    if (e < dim) {
+        v = (x[e] / den) * w[e];
+        if (normed) normed[(int64_t)row * dim + e] = v;
+    }
+    xs[threadIdx.x] = v;
+    __syncthreads();
+    if (wave == 0) {
+        const int nb = VDT == kQ8K ? dim / 256 : dim / 32;
+        uint8_t* arow = act + (int64_t)row * nb * act_block_bytes(VDT);
+        quantize_chunk<VDT>(xs, c, dim, lane, arow);
+    }
+}
+
+// ---------------------------------------------------- QK-RMSNorm + RoPE + KV-cache append
+// grid (B, n_heads + 2 * n_kv), one wave per head of the fused qkv row
+// [q (nh*hd) | k (nkv*hd) | v (nkv*hd)].  Lane i owns rotation pairs i, i+64, ...
+__global__ __launch_bounds__(64) void k_qk_rope_append(const float* __restrict__ qkv, int qkv_n, int nh, int nkv,
+                                                       int hd, const float* __restrict__ qn,
+                                                       const float* __restrict__ kn, float eps, float inv_hd,
+                                                       int interleaved, const float* __restrict__ cos_t,
+                                                       const float* __restrict__ sin_t, const int* __restrict__ len,
+                                                       float* __restrict__ qout, float* __restrict__ kc,
+                                                       float* __restrict__ vc, int64_t kv_stream_stride,
+                                                       int max_seq) {
+    const int s = blockIdx.x, hid = blockIdx.y, lane = threadIdx.x;
+    const int pos = len[s];
+    const float* src = qkv + (int64_t)s * qkv_n + (int64_t)hid * hd;
+    const int half = hd / 2;
+    const bool is_q = hid < nh, is_k = !is_q && hid < nh + nkv;
+    if (!is_q && !is_k) {  // V: stored as projected
+        const int g = hid - nh - nkv;
+        float* dst = vc + (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + pos) * hd;
+        for (int d = lane; d < hd; d += 64) dst[d] = src[d];
+        return;
+    }
+    const float* nw = is_q ? qn : kn;
+    // pairs: interleaved (2i, 2i+1) or rotate-half (i, i + hd/2)
+    constexpr int MAXP = 2;  // hd <= 256
+    float a[MAXP], b[MAXP];
+    int ia[MAXP], ib[MAXP];
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < MAXP; ++t) {
+        const int i = lane + 64 * t;
+        ia[t] = interleaved ? 2 * i : i;
+        ib[t] = interleaved ? 2 * i + 1 : i + half;
+        a[t] = b[t] = 0.0f;
+        if (i < half) {
+            a[t] = src[ia[t]];
+            b[t] = src[ib[t]];
+            ss += a[t] * a[t] + b[t] * b[t];
+        }
+    }
+    if (nw) {
+        ss = wave_sum_f32(ss);
+        const float den = sqrtf((ss * inv_hd + 0.0f) * 1.0f + eps);
+#pragma unroll
+        for (int t = 0; t < MAXP; ++t) {
+            if (lane + 64 * t < half) {
+                a[t] = (a[t] / den) * nw[ia[t]];
+                b[t] = (b[t] / den) * nw[ib[t]];
+            }
+        }
+    }
+    float* dst;
+    if (is_q) {
+        dst = qout + ((int64_t)s * nh + hid) * hd;
+    } else {
+        const int g = hid - nh;
+        dst = kc + (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + pos) * hd;
+    }
+#pragma unroll
+    for (int t = 0; t < MAXP; ++t) {
+        const int i = lane + 64 * t;
+        if (i < half) {
+            const float c = cos_t[(int64_t)pos * half + i], sn = sin_t[(int64_t)pos * half + i];
+            dst[ia[t]] = a[t] * c - b[t] * sn;
+            dst[ib[t]] = b[t] * c + a[t] * sn;
+        }
+    }
+}
+
+// ------------------------------------------------------------- split-K decode attention
+// grid (B, n_kv, max_splits), 256 threads.  Each workgroup takes P consecutive cached
+// positions of one KV head for all G = nh/nkv query heads sharing it (GQA without
+// materialising repeat_kv), and writes per-head partials {m, l, acc[hd]}:
+//   m = max_j s_j, l = sum_j exp(s_j - m), acc = sum_j exp(s_j - m) v_j,
+// with s_j = (q . k_j) * scale.  The K and V tiles are fetched together up front.
+// k_attn_combine_quant merges the splits.
+__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ kc,
+                                                      const float* __restrict__ vc, const int* __restrict__ len,
+                                                      int nh, int nkv, int hd, int max_seq,
+                                                      int64_t kv_stream_stride, int P, float scale,
+                                                      float* __restrict__ part, int max_splits) {
+    extern __shared__ float smem[];
+    const int s = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+    const int L = len[s] + 1;  // the token appended this step is attended too
+    const int p0 = sp * P;
+    if (p0 >= L) return;
+    const int np = min(P, L - p0);
+    const int G = nh / nkv, hdp = hd + 4;
+    float* qs = smem;               // [G][hd]
+    float* kt = qs + G * hd;        // [P][hd + 4]
+    float* vt = kt + P * hdp;       // [P][hd + 4]
+    float* sc = vt + P * hdp;       // [G][P]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t off = (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + p0) * hd;
+    const float* kb = kc + off;
+    const float* vb = vc + off;
+    const int hd4 = hd / 4, n4 = np * hd4;
+    for (int i = tid; i < G * hd; i += 256) qs[i] = q[((int64_t)s * nh + g * G) * hd + i];
+    for (int i = tid; i < n4; i += 256) {
+        const int p = i / hd4, d4 = i - p * hd4;
+        const float4 kv = *(const float4*)(kb + (int64_t)p * hd + 4 * d4);
+        const float4 vv = *(const float4*)(vb + (int64_t)p * hd + 4 * d4);
+        *(float4*)(kt + p * hdp + 4 * d4) = kv;
+        *(float4*)(vt + p * hdp + 4 * d4) = vv;
+    }
+    __syncthreads();
+    // scores: a lane pair per (head, position), each lane half of the head dim
+    for (int base = 0; base < 2 * G * P; base += 256) {
+        const int i = base + tid;
+        const int pair = i >> 1, half = i & 1;
+        const int h = pair / P, p = pair - h * P;
+        float acc = 0.0f;
+        if (i < 2 * G * P && p < np) {
+            const float* qh = qs + h * hd + half * (hd / 2);
+            const float* kr = kt + p * hdp + half * (hd / 2);
+            for (int d = 0; d < hd / 2; d += 4) {
+                const float4 kv = *(const float4*)(kr + d);
+                const float4 qv = *(const float4*)(qh + d);
+                acc += qv.x * kv.x;
+                acc += qv.y * kv.y;
+                acc += qv.z * kv.z;
+                acc += qv.w * kv.w;
+            }
+        }
+        acc += __shfl_xor(acc, 1, 64);
+        if (i < 2 * G * P && half == 0 && p < np) sc[h * P + p] = acc * scale + 0.0f;
+    }
+    __syncthreads();
+    float* pm = part + (((int64_t)s * nh + g * G) * max_splits + sp) * (2 + hd);
+    const int64_t head_stride = (int64_t)max_splits * (2 + hd);
+    for (int h = wave; h < G; h += 4) {
+        float mx = -INFINITY;
+        for (int p = lane; p < np; p += 64) mx = fmaxf(mx, sc[h * P + p]);
+        mx = wave_max_f32(mx);
+        float l = 0.0f;
+        for (int p = lane; p < np; p += 64) {
+            const float e = expf(sc[h * P + p] - mx);
+            sc[h * P + p] = e;
+            l += e;
+        }
+        l = wave_sum_f32(l);
+        if (lane == 0) {
+            pm[h * head_stride] = mx;
+            pm[h * head_stride + 1] = l;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < G * hd; i += 256) {
+        const int h = i / hd, d = i - h * hd;
+        const float* e = sc + h * P;
+        float acc = 0.0f;
+        for (int p = 0; p < np; ++p) acc += e[p] * vt[p * hdp + d];
+        pm[h * head_stride + 2 + d] = acc;
+    }
+}
+
+// grid (B, ceil(nh*hd/256)), 256 threads: merge the splits of the heads covering
+// context elements [c*256, c*256 + 256), then quantize that chunk for the O projection:
+//   ctx = sum_i exp(m_i - M) acc_i / sum_i exp(m_i - M) l_i,  M = max_i m_i.
+template <int VDT>
+__global__ __launch_bounds__(256) void k_attn_combine_quant(const float* __restrict__ part, const int* __restrict__ len,
+                                                            int nh, int hd, int P, int max_splits,
+                                                            uint8_t* __restrict__ act, float* __restrict__ ctx_out) {
+    __shared__ float xs[256];
+    __shared__ float wts[8][kMaxSplits];
+    __shared__ float lsum[8];
+    const int s = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int dim = nh * hd;
+    const int L = len[s] + 1;
+    const int nsp = (L + P - 1) / P;
+    const int h0 = (c * 256) / hd;
+    const int nhc = min((256 + hd - 1) / hd, nh - h0);  // heads touching this chunk (<= 8)
+    // per-head split weights exp(m_i - M) and the normaliser, one wave per head
+    for (int hh = wave; hh < nhc; hh += 4) {
+        const float* ph = part + ((int64_t)s * nh + h0 + hh) * max_splits * (2 + hd);
+        float M = -INFINITY;
+        for (int i = lane; i < nsp; i += 64) M = fmaxf(M, ph[i * (2 + hd)]);
+        M = wave_max_f32(M);
+        float Ls = 0.0f;
+        for (int i = lane; i < nsp; i += 64) {
+            const float w = expf(ph[i * (2 + hd)] - M);
+            wts[hh][i] = w;
+            Ls += ph[i * (2 + hd) + 1] * w;
+        }
+        Ls = wave_sum_f32(Ls);
+        if (lane == 0) lsum[hh] = Ls;
+    }
+    __syncthreads();
+    const int e = c * 256 + tid;
+    float v = 0.0f;
+    if (e < dim) {
+        const int h = e / hd, d = e - h * hd, hh = h - h0;
+        const float* ph = part + ((int64_t)s * nh + h) * max_splits * (2 + hd) + 2 + d;
+        float acc = 0.0f;
+        for (int i = 0; i < nsp; ++i) acc += ph[i * (2 + hd)] * wts[hh][i];
+        v = acc / lsum[hh];
+        if (ctx_out) ctx_out[(int64_t)s * dim + e] = v;
+    }
+    xs[tid] = v;
+    __syncthreads();
+    if (tid < 64) {
+        const int nb = VDT == kQ8K ? dim / 256 : dim / 32;
+        uint8_t* arow = act + (int64_t)s * nb * act_block_bytes(VDT);
+        quantize_chunk<VDT>(xs, c, dim, tid, arow);
+    }
+}
+
+// ------------------------------------------------------------------------ SwiGLU glue
+// gu row = [gate (I) | up (I)]; a = silu(g) * u with silu(g) = g / (1 + exp(-g)).
+template <int VDT>
+__global__ __launch_bounds__(64) void k_silu_mul_quant(const float* __restrict__ gu, int I, uint8_t* __restrict__ act,
+                                                       float* __restrict__ act_f32) {
+    const int s = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+    const float* g = gu + (int64_t)s * 2 * I;
+    const float* u = g + I;
+    const int e0 = c * 256 + 4 * lane;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    if (e0 < I) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float gv = g[e0 + r];
+            a[r] = (gv / (1.0f + expf(-gv))) * u[e0 + r];
+            if (act_f32) act_f32[(int64_t)s * I + e0 + r] = a[r];
+        }
+    }
+    const float4 v = make_float4(a[0], a[1], a[2], a[3]);
+    const int nb = VDT == kQ8K ? I / 256 : I / 32;
+    uint8_t* arow = act + (int64_t)s * nb * act_block_bytes(VDT);
+    if (VDT == kQ8K) wave_quantize_q8k<false>(v, lane, arow + (size_t)c * sizeof(ActQ8K));
+    else wave_quantize_q8_0<false>(v, lane, c * 8 + (lane >> 3) < nb, arow + (size_t)c * 8 * sizeof(ActQ8_0));
+}
+
+// ------------------------------------------------------------------------ embeddings
+// Element e of row `r` of a quantized weight in the device layout, exactly to_float.
+SXQ_DEV float weight_elem(const QWeight& w, int64_t r, int e) {
+    if (w.dtype == kQ4K) {
+        const int b = e >> 8, i = e & 255;
+        const int64_t blk = r * w.nb + b;
+        const uint8_t* hb = w.hdr + blk * 16;
+        const int c = i >> 6, hi = (i >> 5) & 1, l32 = i & 31;
+        const int j = 2 * c + hi;
+        int sc, m;
+        const uint8_t* q = hb + 4;
+        if (j < 4) {
+            sc = q[j] & 63;
+            m = q[j + 4] & 63;
+        } else {
+            sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+            m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+        }
+        const float d = f16_bits_to_f32((uint16_t)(hb[0] | (hb[1] << 8)));
+        const float dmin = f16_bits_to_f32((uint16_t)(hb[2] | (hb[3] << 8)));
+        const int l = l32 & 7, t = l32 >> 3;
+        const uint8_t byte = w.qs[blk * 128 + 4 * (4 * l + c) + t];
+        const int qv = hi ? (byte >> 4) : (byte & 0xF);
+        return (d * (float)sc) * (float)qv - dmin * (float)m;
+    }
+    const int b = e >> 5, i = e & 31;
+    const int64_t blk = r * w.nb + b;
+    const float d = f16_bits_to_f32((uint16_t)(w.hdr[2 * blk] | (w.hdr[2 * blk + 1] << 8)));
+    if (w.dtype == kQ8_0) return (float)(int8_t)w.qs[blk * 32 + i] * d;
+    const uint8_t byte = w.qs[blk * 16 + (i & 15)];
+    return (float)((i < 16 ? (byte & 0xF) : (byte >> 4)) - 8) * d;
+}
+
+// Fish MCF (slow_ar.rs:101-161) over the tied, quantized table:
+//   x = (E[tok] + sum_i C[code_i + i*cb]) * 1/sqrt(n_cb + 1)   on semantic positions,
+//   x = E[tok] + 0 * (...)                                      otherwise.
+// Without codebooks (n_cb = 0) this is the plain gather E[tok].  Ids outside the table
+// (token >= rows, code >= cb_size, negatives) read nothing: their rows count as zero.
+__global__ __launch_bounds__(256) void k_embed_quant_table(const int* __restrict__ ids, int ids_per, QWeight w, int dim,
+                                                           const float* __restrict__ cb, int n_cb, int cb_size,
+                                                           int sem_begin, int sem_end, float inv_scale,
+                                                           float* __restrict__ h) {
+    const int s = blockIdx.x;
+    const int* fr = ids + (int64_t)s * ids_per;
+    const int tok = fr[0];
+    const bool tok_ok = tok >= 0 && (int64_t)tok < w.n;
+    const bool sem = tok >= sem_begin && tok <= sem_end;
+    for (int e = threadIdx.x; e < dim; e += 256) {
+        float x = tok_ok ? weight_elem(w, tok, e) : 0.0f;
+        if (n_cb > 0) {
+            float vq = 0.0f;
+            for (int i = 0; i < n_cb; ++i) {
+                const int code = fr[1 + i];
+                const float v = (code >= 0 && code < cb_size) ? cb[((int64_t)code + (int64_t)i * cb_size) * dim + e] : 0.0f;
+                vq = i == 0 ? v : vq + v;
+            }
+            x = (x + vq * (sem ? 1.0f : 0.0f)) * (sem ? inv_scale : 1.0f);
+        }
+        h[(int64_t)s * dim + e] = x;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_embed_dense(const int* __restrict__ ids, int ids_per,
+                                                     const float* __restrict__ table, int rows, int dim,
+                                                     float* __restrict__ h) {
+    const int s = blockIdx.x;
+    const int tok = ids[(int64_t)s * ids_per];
+    const bool ok = tok >= 0 && tok < rows;
+    for (int e = threadIdx.x; e < dim; e += 256) h[(int64_t)s * dim + e] = ok ? table[(int64_t)tok * dim + e] : 0.0f;
+}
+
+// ------------------------------------------------------------------------ argmax / length
+// First index of the largest logit (NaN never wins); written to ids[s * ids_per].
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ logits, int vocab, int* __restrict__ ids,
+                                                 int ids_per, int* __restrict__ out_ids) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* x = logits + (int64_t)s * vocab;
+    float best = -INFINITY;
+    int idx = 0x7FFFFFFF;
+    for (int i = tid; i < vocab; i += 1024) {
+        const float v = x[i];
+        if (v > best) { best = v; idx = i; }  // per-thread indices rise: first max kept
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
+    }
+    if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
+        if (idx == 0x7FFFFFFF) idx = 0;
+        ids[(int64_t)s * ids_per] = idx;
+        if (out_ids) out_ids[s] = idx;
+    }
+}
+
+__global__ void k_advance(int* __restrict__ len, int B) {
+    const int s = threadIdx.x;
+    if (s < B) len[s] += 1;
+}
+
+__global__ void k_fill_value(float* __restrict__ y, int64_t n, float v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = v;
+}
+
+// ------------------------------------------------------------------------ launchers
+hipError_t launch_rmsnorm_quant(int vdt, const float* h, int rows, int dim, const float* w, float eps, uint8_t* act,
+                                float* normed, hipStream_t s) {
+    const float inv_n = (float)(1.0 / (double)dim);
+    const dim3 grid(rows, (dim + 255) / 256);
+    if (vdt == kQ8K) hipLaunchKernelGGL((k_rmsnorm_quant<kQ8K>), grid, dim3(256), 0, s, h, dim, w, inv_n, eps, act, normed);
+    else hipLaunchKernelGGL((k_rmsnorm_quant<kQ8_0>), grid, dim3(256), 0, s, h, dim, w, inv_n, eps, act, normed);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_rope_append(const float* qkv, int B, int qkv_n, int nh, int nkv, int hd, const float* qn,
+                                 const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
+                                 const int* len, float* qout, float* kc, float* vc, int64_t kv_stream_stride,
+                                 int max_seq, hipStream_t s) {
+    const float inv_hd = (float)(1.0 / (double)hd);
+    hipLaunchKernelGGL(k_qk_rope_append, dim3(B, nh + 2 * nkv), dim3(64), 0, s, qkv, qkv_n, nh, nkv, hd, qn, kn, eps,
+                       inv_hd, interleaved, cos_t, sin_t, len, qout, kc, vc, kv_stream_stride, max_seq);
+    return hipGetLastError();
+}
+
+size_t attn_partial_lds(int nh, int nkv, int hd, int P) {
+    const int G = nh / nkv;
+    return sizeof(float) * ((size_t)G * hd + 2 * (size_t)P * (hd + 4) + (size_t)G * P);
+}
+
+hipError_t launch_attention(int vdt, const float* q, const float* kc, const float* vc, const int* len, int B, int nh,
+                            int nkv, int hd, int max_seq, int64_t kv_stream_stride, int P, int max_splits,
+                            float* part, uint8_t* act, float* ctx_out, hipStream_t s) {
+    const float scale = (float)(1.0 / sqrt((double)hd));
+    hipLaunchKernelGGL(k_attn_partial, dim3(B, nkv, max_splits), dim3(256), attn_partial_lds(nh, nkv, hd, P), s, q, kc,
+                       vc, len, nh, nkv, hd, max_seq, kv_stream_stride, P, scale, part, max_splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int chunks = (nh * hd + 255) / 256;
+    if (vdt == kQ8K) hipLaunchKernelGGL((k_attn_combine_quant<kQ8K>), dim3(B, chunks), dim3(256), 0, s, part, len, nh, hd, P, max_splits, act, ctx_out);
+    else hipLaunchKernelGGL((k_attn_combine_quant<kQ8_0>), dim3(B, chunks), dim3(256), 0, s, part, len, nh, hd, P, max_splits, act, ctx_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s) {
+    const dim3 grid(B, (I + 255) / 256);
+    if (vdt == kQ8K) hipLaunchKernelGGL((k_silu_mul_quant<kQ8K>), grid, dim3(64), 0, s, gu, I, act, act_f32);
+    else hipLaunchKernelGGL((k_silu_mul_quant<kQ8_0>), grid, dim3(64), 0, s, gu, I, act, act_f32);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_quant_table(const int* ids, int ids_per, int B, const QWeight& w, int dim, const float* cb,
+                                    int n_cb, int cb_size, int sem_begin, int sem_end, float* h, hipStream_t s) {
+    const float inv_scale = 1.0f / sqrtf((float)n_cb + 1.0f);
+    hipLaunchKernelGGL(k_embed_quant_table, dim3(B), dim3(256), 0, s, ids, ids_per, w, dim, cb, n_cb, cb_size, sem_begin,
+                       sem_end, inv_scale, h);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(k_embed_dense, dim3(B), dim3(256), 0, s, ids, ids_per, table, rows, dim, h);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(B), dim3(1024), 0, s, logits, vocab, ids, ids_per, out_ids);
+    return hipGetLastError();
+}
+
+hipError_t launch_advance(int* len, int B, hipStream_t s) {
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, len, B);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_value(float* y, int64_t n, float v, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_value, dim3((n + 255) / 256), dim3(256), 0, s, y, n, v);
+    return hipGetLastError();
+}
+
+}  // namespace sxq

@@ -15,6 +15,8 @@
 // Q4_0 lane l takes block b0 + l and the group folds the eight block terms in order.
 // Activations are copied from their quantized device layout into LDS once per
 // workgroup (in K chunks when m * K does not fit).
+#include <stdlib.h>
+
 #include "sxq_kernels.h"
 
 namespace sxq {
@@ -39,8 +41,8 @@ SXQ_DEV void stage_act(uint4* lds, const uint8_t* __restrict__ act, int m, int n
 template <int MMAX, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void k_gemv_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
                                                          int n, int nb, const uint8_t* __restrict__ act, int m,
-                                                         int cbmax, float* __restrict__ y, int64_t ldy,
-                                                         const float* __restrict__ bias) {
+                                                         int cbmax, float* y, int64_t ldy,
+                                                         const float* __restrict__ bias, const float* res, int64_t ldr) {
     extern __shared__ uint4 lds[];
     const ActQ8K* la = (const ActQ8K*)lds;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -109,6 +111,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_q4k(const uint4* __restrict
             float v = sumf[r] + tot;
             if (active && l == 0) {
                 if (bias) v = v + bias[row];
+                if (res) v = res[(int64_t)r * ldr + row] + v;  // residual: `r + a`
                 y[(int64_t)r * ldy + row] = v;
             }
         }
@@ -119,8 +122,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_q4k(const uint4* __restrict
 template <int MMAX, int WAVES, bool Q4>
 __global__ __launch_bounds__(64 * WAVES) void k_gemv_q80(const uint16_t* __restrict__ dw16, const uint4* __restrict__ qs,
                                                          int n, int nb, const uint8_t* __restrict__ act, int m,
-                                                         int cbmax, float* __restrict__ y, int64_t ldy,
-                                                         const float* __restrict__ bias) {
+                                                         int cbmax, float* y, int64_t ldy,
+                                                         const float* __restrict__ bias, const float* res, int64_t ldr) {
     extern __shared__ uint4 lds[];
     const ActQ8_0* la = (const ActQ8_0*)lds;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -189,14 +192,271 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_q80(const uint16_t* __restr
         if (r < m && active && l == 0) {
             float v = sumf[r];
             if (bias) v = v + bias[row];
+            if (res) v = res[(int64_t)r * ldr + row] + v;  // residual: `r + a`
             y[(int64_t)r * ldy + row] = v;
         }
     }
 }
 
+// ---------------------------------------------------------------------------------
+// Task-split GEMV (m = 1..4).  A 256-thread workgroup owns R consecutive rows; their
+// R*nb (row, block) tasks are dealt round-robin to 32 eight-lane groups (Q4_K), 128
+// lane pairs (Q8_0) or 256 lanes (Q4_0), at most TMAX tasks each.  Every group first
+// issues the weight loads of all its tasks (clamped, unconditional), then the
+// activation loads into LDS, so a wave has up to 2*TMAX 16-byte loads in flight and
+// the compute that follows is branch-free.  Each task leaves Candle's per-block float
+// product(s) in LDS: Q4_K the eight lane terms (d_w*d_a)*(f32)aux32[l] and the min term
+// (dmin_w*d_a)*(f32)sumi; Q8_0/Q4_0 the term ((f32)isum*d_w)*d_a.  The epilogue folds
+// them in block order per (row, lane) -- the only order-dependent part -- so results
+// stay bit-identical to Candle's generic vec-dot.
+constexpr int kTmax = 8;
+
+// Activation staging in two halves so the caller can put its weight loads between
+// them: act_fetch issues a thread's first kActPer 16-byte loads (clamped, so all are
+// unconditional and in flight together); act_store writes them to LDS and copies any
+// remainder (only when m * nb blocks exceed 256 * kActPer uint4).
+constexpr int kActPer = 4;
+SXQ_DEV void act_fetch(uint4 (&v)[kActPer], const uint8_t* __restrict__ act, int total_u4) {
+#pragma unroll
+    for (int k = 0; k < kActPer; ++k) v[k] = ((const uint4*)act)[min(k * 256 + (int)threadIdx.x, total_u4 - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
+}
+SXQ_DEV void act_store(const uint4 (&v)[kActPer], uint4* lds, const uint8_t* __restrict__ act, int total_u4) {
+    // clamped like the loads: out-of-range threads rewrite the last element with its own value
+#pragma unroll
+    for (int k = 0; k < kActPer; ++k) lds[min(k * 256 + (int)threadIdx.x, total_u4 - 1)] = v[k];
+    for (int i = kActPer * 256 + threadIdx.x; i < total_u4; i += 256) lds[i] = ((const uint4*)act)[i];
+}
+
+template <int MMAX>
+__global__ __launch_bounds__(256) void k_gemv2_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, int n,
+                                                   int nb, const uint8_t* __restrict__ act, int m, int R, float* y,
+                                                   int64_t ldy, const float* __restrict__ bias, const float* res,
+                                                   int64_t ldr) {
+    extern __shared__ uint4 lds[];
+    const ActQ8K* la = (const ActQ8K*)lds;
+    float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8K) / 16));  // [task][m][9]
+    const int row0 = blockIdx.x * R;
+    const int rows = min(R, n - row0);
+    const int tasks = rows * nb;
+    const int lane = threadIdx.x & 63, l = lane & 7, grp = threadIdx.x >> 3;
+    const uint4* hb = hdr + (int64_t)row0 * nb;
+    const uint4* qb = qs + (int64_t)row0 * nb * 8 + l;
+    const int act_u4 = m * nb * (int)(sizeof(ActQ8K) / 16);
+    uint4 av[kActPer];
+    act_fetch(av, act, act_u4);
+    uint4 q[kTmax], h[kTmax];
+#pragma unroll
+    for (int u = 0; u < kTmax; ++u) {
+        const int t = min(u * 32 + grp, tasks - 1);
+        q[u] = qb[(int64_t)t * 8];
+        h[u] = hb[t];
+    }
+    act_store(av, lds, act, act_u4);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kTmax; ++u) {
+        const int t_raw = u * 32 + grp;
+        if (u * 32 >= tasks) break;  // uniform: no group has a task in this round
+        const int t = min(t_raw, tasks - 1);
+        const int b = t % nb;
+        const uint32_t sc_lo = h[u].y & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (h[u].w & 0x0F0F0F0Fu) | (((h[u].y >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = h[u].z & 0x3F3F3F3Fu;
+        const uint32_t mn_hi = ((h[u].w >> 4) & 0x0F0F0F0Fu) | (((h[u].z >> 6) & 0x03030303u) << 4);
+        const int ml = (int)(((l < 4 ? mn_lo : mn_hi) >> (8 * (l & 3))) & 0xFF);
+        const uint32_t w4[8] = {q[u].x & 0x0F0F0F0Fu, (q[u].x >> 4) & 0x0F0F0F0Fu, q[u].y & 0x0F0F0F0Fu,
+                                (q[u].y >> 4) & 0x0F0F0F0Fu, q[u].z & 0x0F0F0F0Fu, (q[u].z >> 4) & 0x0F0F0F0Fu,
+                                q[u].w & 0x0F0F0F0Fu, (q[u].w >> 4) & 0x0F0F0F0Fu};
+        int sc[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sc[j] = (int)((sc_lo >> (8 * j)) & 0xFF);
+            sc[4 + j] = (int)((sc_hi >> (8 * j)) & 0xFF);
+        }
+        const float dw = h2f(h[u].x & 0xFFFF), dminw = h2f(h[u].x >> 16);
+        const bool valid = t_raw < tasks;
+#pragma unroll
+        for (int r = 0; r < MMAX; ++r) {
+            if (r < m) {
+                const ActQ8K& a = la[r * nb + b];
+                const uint4 A0 = ((const uint4*)a.qs)[2 * l];
+                const uint4 A1 = ((const uint4*)a.qs)[2 * l + 1];
+                const int Aj[8] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w,
+                                   (int)A1.x, (int)A1.y, (int)A1.z, (int)A1.w};
+                int aux = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) aux += __mul24(__builtin_amdgcn_sdot4((int)w4[j], Aj[j], 0, false), sc[j]);
+                const int sumi = sum8_i32(__mul24(ml, a.bs2[l]));
+                const float ad = a.d;
+                const float pl = (dw * ad) * (float)aux;
+                const float pm = (dminw * ad) * (float)sumi;
+                if (valid) {
+                    float* p = pr + ((size_t)t * m + r) * 9;
+                    p[l] = pl;
+                    if (l == 0) p[8] = pm;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // epilogue: thread (row r, lane class l) folds its chain in block order
+    const int r = threadIdx.x >> 3;
+    const bool act_row = r < rows;
+    for (int rr = 0; rr < m; ++rr) {
+        float sl = 0.0f, sf = 0.0f;
+        if (act_row) {
+            const float* p = pr + ((size_t)r * nb * m + rr) * 9;
+            for (int b = 0; b < nb; ++b) sl += p[(size_t)b * m * 9 + l];
+            if (l == 0)
+                for (int b = 0; b < nb; ++b) sf -= p[(size_t)b * m * 9 + 8];
+        }
+        float tot = -0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tot += __shfl(sl, (lane & ~7) + j, 64);
+        if (act_row && l == 0) {
+            const int row = row0 + r;
+            float v = sf + tot;
+            if (bias) v = v + bias[row];
+            if (res) v = res[(int64_t)rr * ldr + row] + v;
+            y[(int64_t)rr * ldy + row] = v;
+        }
+    }
+}
+
+template <int MMAX, bool Q4>
+__global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ dw16, const uint4* __restrict__ qs,
+                                                   int n, int nb, const uint8_t* __restrict__ act, int m, int R,
+                                                   float* y, int64_t ldy, const float* __restrict__ bias,
+                                                   const float* res, int64_t ldr) {
+    extern __shared__ uint4 lds[];
+    const ActQ8_0* la = (const ActQ8_0*)lds;
+    float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8_0) / 16));  // [task][m]
+    const int row0 = blockIdx.x * R;
+    const int rows = min(R, n - row0);
+    const int tasks = rows * nb;
+    // Q8_0: a lane pair per task (16 bytes each); Q4_0: one lane per task.
+    constexpr int LPT = Q4 ? 1 : 2, TPI = 256 / LPT, QU4 = Q4 ? 1 : 2;
+    const int half = Q4 ? 0 : (threadIdx.x & 1);
+    const int slot = threadIdx.x / LPT;
+    const int64_t base = (int64_t)row0 * nb;
+    const int act_u4 = m * nb * (int)(sizeof(ActQ8_0) / 16);
+    uint4 av[kActPer];
+    act_fetch(av, act, act_u4);
+    uint4 w[kTmax];
+    float dw[kTmax];
+#pragma unroll
+    for (int u = 0; u < kTmax; ++u) {
+        const int t = min(u * TPI + slot, tasks - 1);
+        w[u] = qs[(base + t) * QU4 + half];
+        dw[u] = h2f(dw16[base + t]);
+    }
+    act_store(av, lds, act, act_u4);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kTmax; ++u) {
+        if (u * TPI >= tasks) break;
+        const int t_raw = u * TPI + slot;
+        const bool valid = t_raw < tasks;
+        const int t = min(t_raw, tasks - 1);
+        const int b = t % nb;
+#pragma unroll
+        for (int r = 0; r < MMAX; ++r) {
+            if (r < m) {
+                const ActQ8_0& a = la[r * nb + b];
+                int isum;
+                if (Q4) {
+                    const uint4 A0 = ((const uint4*)a.qs)[0], A1 = ((const uint4*)a.qs)[1];
+                    const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+                    const int Alo[4] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w};
+                    const int Ahi[4] = {(int)A1.x, (int)A1.y, (int)A1.z, (int)A1.w};
+                    isum = -8 * a.asum;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        isum = __builtin_amdgcn_sdot4((int)(wd[k] & 0x0F0F0F0Fu), Alo[k], isum, false);
+                        isum = __builtin_amdgcn_sdot4((int)((wd[k] >> 4) & 0x0F0F0F0Fu), Ahi[k], isum, false);
+                    }
+                } else {
+                    const uint4 A = ((const uint4*)a.qs)[half];
+                    int s = __builtin_amdgcn_sdot4((int)w[u].x, (int)A.x, 0, false);
+                    s = __builtin_amdgcn_sdot4((int)w[u].y, (int)A.y, s, false);
+                    s = __builtin_amdgcn_sdot4((int)w[u].z, (int)A.z, s, false);
+                    s = __builtin_amdgcn_sdot4((int)w[u].w, (int)A.w, s, false);
+                    isum = s + dpp_xor1(s);
+                }
+                const float tv = ((float)isum * dw[u]) * a.d;
+                if (valid && half == 0) pr[(size_t)t * m + r] = tv;
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < rows * m; i += 256) {
+        const int r = i / m, rr = i - r * m;
+        const float* p = pr + (size_t)r * nb * m + rr;
+        float sumf = 0.0f;
+        for (int b = 0; b < nb; ++b) sumf += p[(size_t)b * m];
+        const int row = row0 + r;
+        if (bias) sumf = sumf + bias[row];
+        if (res) sumf = res[(int64_t)rr * ldr + row] + sumf;
+        y[(int64_t)rr * ldy + row] = sumf;
+    }
+}
+
+// Rows per workgroup: the largest power of two <= 32 that keeps each lane group at
+// <= kTmax tasks, leaves >= SXQ_GEMV_MIN_WG workgroups (default 640) and fits LDS.
+// Rows per workgroup: spread the rows over about SXQ_GEMV_WG (default 1024 = four
+// resident 256-thread workgroups on each of the 256 CUs) workgroups, so the whole grid
+// runs in one wave of workgroups with no tail; capped so every lane group holds at
+// most kTmax tasks, the epilogue has a thread per (row, lane class), and LDS fits.
+int gemv2_rows(int n, int nb, int m, int dtype) {
+    static const int target_wg = [] {
+        const char* e = getenv("SXQ_GEMV_WG");
+        return e ? atoi(e) : 1024;
+    }();
+    const size_t ab = act_block_bytes(vec_dot_type(dtype));
+    const size_t per_task = dtype == kQ4K ? 36 : 4;
+    const int slots = dtype == kQ4K ? 32 : (dtype == kQ8_0 ? 128 : 256);
+    int R = (n + target_wg - 1) / target_wg;
+    R = min(R, 32);
+    R = min(R, max(1, slots * kTmax / nb));
+    while (R > 1 && (size_t)m * nb * ab + (size_t)R * nb * m * per_task > 60 * 1024) --R;
+    return max(R, 1);
+}
+
+size_t gemv2_lds(int nb, int m, int R, int dtype) {
+    const size_t ab = act_block_bytes(vec_dot_type(dtype));
+    const size_t per_task = dtype == kQ4K ? 36 : 4;
+    return (size_t)m * nb * ab + (size_t)R * nb * m * per_task;
+}
+
+// Whether the task-split kernel covers this shape (one row's tasks within kTmax rounds).
+bool gemv2_fits(int nb, int m, int dtype) {
+    const int slots = dtype == kQ4K ? 32 : (dtype == kQ8_0 ? 128 : 256);
+    return nb <= slots * kTmax && gemv2_lds(nb, m, 1, dtype) <= 60 * 1024;
+}
+
+template <int MMAX>
+static hipError_t gemv2_dispatch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
+                                 const float* res, int64_t ldr, hipStream_t s) {
+    const int n = (int)w.n, nb = (int)w.nb;
+    const int R = gemv2_rows(n, nb, m, w.dtype);
+    const size_t lds = gemv2_lds(nb, m, R, w.dtype);
+    const dim3 grid((n + R - 1) / R), block(256);
+    const uint8_t* a = (const uint8_t*)act;
+    if (w.dtype == kQ4K)
+        hipLaunchKernelGGL((k_gemv2_q4k<MMAX>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr);
+    else if (w.dtype == kQ8_0)
+        hipLaunchKernelGGL((k_gemv2_q80<MMAX, false>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr);
+    else if (w.dtype == kQ4_0)
+        hipLaunchKernelGGL((k_gemv2_q80<MMAX, true>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 template <int MMAX>
 static hipError_t gemv_dispatch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
-                                hipStream_t s) {
+                                const float* res, int64_t ldr, hipStream_t s) {
     const int n = (int)w.n, nb = (int)w.nb;
     const int groups = (n + 7) / 8;
     // Four waves per workgroup once there are enough rows to fill the chip that way.
@@ -210,14 +470,14 @@ static hipError_t gemv_dispatch(const QWeight& w, const void* act, int m, float*
     const size_t lds = ab * (size_t)m * (size_t)cbmax;
     const uint8_t* a = (const uint8_t*)act;
     if (w.dtype == kQ4K) {
-        if (wide) hipLaunchKernelGGL((k_gemv_q4k<MMAX, 4>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias);
-        else hipLaunchKernelGGL((k_gemv_q4k<MMAX, 1>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias);
+        if (wide) hipLaunchKernelGGL((k_gemv_q4k<MMAX, 4>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias, res, ldr);
+        else hipLaunchKernelGGL((k_gemv_q4k<MMAX, 1>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias, res, ldr);
     } else if (w.dtype == kQ8_0) {
-        if (wide) hipLaunchKernelGGL((k_gemv_q80<MMAX, 4, false>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias);
-        else hipLaunchKernelGGL((k_gemv_q80<MMAX, 1, false>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias);
+        if (wide) hipLaunchKernelGGL((k_gemv_q80<MMAX, 4, false>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias, res, ldr);
+        else hipLaunchKernelGGL((k_gemv_q80<MMAX, 1, false>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias, res, ldr);
     } else if (w.dtype == kQ4_0) {
-        if (wide) hipLaunchKernelGGL((k_gemv_q80<MMAX, 4, true>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias);
-        else hipLaunchKernelGGL((k_gemv_q80<MMAX, 1, true>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias);
+        if (wide) hipLaunchKernelGGL((k_gemv_q80<MMAX, 4, true>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias, res, ldr);
+        else hipLaunchKernelGGL((k_gemv_q80<MMAX, 1, true>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, cbmax, y, ldy, bias, res, ldr);
     } else {
         return hipErrorInvalidValue;
     }
@@ -225,13 +485,21 @@ static hipError_t gemv_dispatch(const QWeight& w, const void* act, int m, float*
 }
 
 hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
-                       hipStream_t s) {
+                       const float* res, int64_t ldr, hipStream_t s) {
     if (m <= 0 || w.n <= 0) return hipSuccess;
-    if (m == 1) return gemv_dispatch<1>(w, act, m, y, ldy, bias, s);
-    if (m == 2) return gemv_dispatch<2>(w, act, m, y, ldy, bias, s);
-    if (m <= 4) return gemv_dispatch<4>(w, act, m, y, ldy, bias, s);
-    if (m <= 8) return gemv_dispatch<8>(w, act, m, y, ldy, bias, s);
-    if (m <= 16) return gemv_dispatch<16>(w, act, m, y, ldy, bias, s);
+    static const bool v1 = getenv("SXQ_GEMV_V1") != nullptr;
+    if (!v1) {
+        const int nb = (int)w.nb;
+        const bool fits = gemv2_fits(nb, m, w.dtype);
+        if (fits && m == 1) return gemv2_dispatch<1>(w, act, m, y, ldy, bias, res, ldr, s);
+        if (fits && m == 2) return gemv2_dispatch<2>(w, act, m, y, ldy, bias, res, ldr, s);
+        if (fits && m <= 4) return gemv2_dispatch<4>(w, act, m, y, ldy, bias, res, ldr, s);
+    }
+    if (m == 1) return gemv_dispatch<1>(w, act, m, y, ldy, bias, res, ldr, s);
+    if (m == 2) return gemv_dispatch<2>(w, act, m, y, ldy, bias, res, ldr, s);
+    if (m <= 4) return gemv_dispatch<4>(w, act, m, y, ldy, bias, res, ldr, s);
+    if (m <= 8) return gemv_dispatch<8>(w, act, m, y, ldy, bias, res, ldr, s);
+    if (m <= 16) return gemv_dispatch<16>(w, act, m, y, ldy, bias, res, ldr, s);
     return hipErrorInvalidValue;
 }
 

@@ -25,9 +25,19 @@ struct QWeight {
     const uint8_t* qs = nullptr;   // Q4_K: 128 B; Q8_0: 32 B; Q4_0: 16 B per block
 };
 
-// Decode GEMV, m in 1..16: y[m, n] (row stride ldy) = act[m] . W^T (+ bias).
-// act is the device activation layout [m][nb] (ActQ8K for Q4_K, ActQ8_0 otherwise).
+// Decode GEMV, m in 1..16: y[m, n] (row stride ldy) = act[m] . W^T (+ bias) and, if
+// `res` is given, y = res + that (res may alias y: each element is read then written
+// by one lane).  act is the device activation layout [m][nb] (ActQ8K for Q4_K,
+// ActQ8_0 otherwise).
 hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
-                       hipStream_t s);
+                       const float* res, int64_t ldr, hipStream_t s);
 
 }  // namespace sxq
+
+// The QMatMul handle behind the C-ABI's opaque sxq_qmm.
+struct sxq_qmm {
+    int device = 0;
+    sxq::QWeight w;
+    void* mem = nullptr;  // one allocation: hdr region, then qs region
+    size_t storage = 0;   // canonical byte count (storage_size_in_bytes)
+};

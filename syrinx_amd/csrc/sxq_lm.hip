@@ -1,0 +1,627 @@
+// sxq_lm.hip -- the decoder-step engine behind sxq_lm_* (include/sxq.h).
+//
+// One object holds a model's projections in the GEMV device layout (q|k|v and
+// gate|up fused row-wise, which leaves every output row's vec-dot unchanged), its
+// norm weights, RoPE tables, a preallocated per-stream KV cache and the step's
+// activation buffers.  A step is a fixed kernel sequence over fixed buffers, so it is
+// captured once per batch size as a HIP graph and replayed per token; the only
+// per-token host work is copying ids in and logits out.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "sxq_abi.h"
+#include "sxq_decoder.h"
+
+using namespace sxq;
+using namespace sxq::abi;
+
+namespace {
+
+
+struct DevWeight {
+    void* mem = nullptr;
+    size_t hdr_pad = 0;
+    QWeight w;
+};
+
+struct LmLayer {
+    DevWeight wqkv, wo, w13, w2;
+    float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *bqkv = nullptr;
+};
+
+struct GraphKey {
+    int n;
+    bool embeds;
+    bool trace;
+    bool operator<(const GraphKey& o) const {
+        if (n != o.n) return n < o.n;
+        if (embeds != o.embeds) return embeds < o.embeds;
+        return trace < o.trace;
+    }
+};
+
+}  // namespace
+
+struct sxq_lm {
+    int device = 0;
+    sxq_lm_config c{};
+    int vdt = 0;            // activation (vec-dot) block type
+    int qkv_n = 0, ctx = 0, ids_per = 1, max_splits = 0;
+    int64_t kv_stream_stride = 0, kv_layer_stride = 0;
+    std::vector<LmLayer> layers;
+    DevWeight head;
+    float *head_bias = nullptr, *final_norm = nullptr, *embed = nullptr, *cb_embed = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    float *kc = nullptr, *vc = nullptr;
+    int* d_len = nullptr;
+    std::vector<int> h_len;
+    float *h = nullptr, *qkv = nullptr, *qbuf = nullptr, *part = nullptr, *gu = nullptr, *logits = nullptr;
+    uint8_t *act_a = nullptr, *act_o = nullptr, *act_d = nullptr;
+    int *d_ids = nullptr, *d_next = nullptr;
+    float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
+    hipStream_t cap = nullptr;
+    std::map<GraphKey, hipGraphExec_t> graphs;
+    std::vector<void*> allocs;
+    std::mutex mu;
+};
+
+namespace {
+
+hipError_t dalloc(sxq_lm* lm, void** p, size_t bytes) {
+    hipError_t e = hipMalloc(p, bytes ? bytes : 1);
+    if (e == hipSuccess) lm->allocs.push_back(*p);
+    return e;
+}
+
+hipError_t alloc_weight(sxq_lm* lm, DevWeight& d, int dtype, int64_t n, int64_t k) {
+    const int64_t nb = k / block_size(dtype), nblk = n * nb;
+    const size_t hb = (size_t)nblk * weight_hdr_bytes(dtype);
+    d.hdr_pad = (hb + 255) & ~(size_t)255;
+    const size_t qb = (size_t)nblk * weight_qs_bytes(dtype);
+    hipError_t e = dalloc(lm, &d.mem, d.hdr_pad + qb);
+    if (e != hipSuccess) return e;
+    d.w.dtype = dtype;
+    d.w.n = n;
+    d.w.k = k;
+    d.w.nb = nb;
+    d.w.hdr = (const uint8_t*)d.mem;
+    d.w.qs = (const uint8_t*)d.mem + d.hdr_pad;
+    return hipSuccess;
+}
+
+// Copy rows [0, src.n) of a device-layout weight into rows [r0, r0 + src.n) of dst.
+hipError_t copy_rows(DevWeight& dst, const QWeight& src, int64_t r0, hipStream_t s) {
+    const size_t hb = weight_hdr_bytes(dst.w.dtype), qb = weight_qs_bytes(dst.w.dtype);
+    const size_t rows_blk = (size_t)src.n * (size_t)src.nb;
+    hipError_t e = hipMemcpyAsync((uint8_t*)dst.w.hdr + (size_t)r0 * dst.w.nb * hb, src.hdr, rows_blk * hb,
+                                  hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return e;
+    return hipMemcpyAsync((uint8_t*)dst.w.qs + (size_t)r0 * dst.w.nb * qb, src.qs, rows_blk * qb,
+                          hipMemcpyDeviceToDevice, s);
+}
+
+// Fill rows [r0, r0 + n) of dst with from_float(N(0, std)) in row chunks.
+hipError_t random_rows(DevWeight& dst, int64_t r0, int64_t n, uint64_t seed, float stdv, float* tmp_f32,
+                       uint8_t* tmp_blk, int64_t tmp_elems, hipStream_t s) {
+    const int64_t k = dst.w.k, nb = dst.w.nb;
+    const int64_t chunk = tmp_elems / k;
+    for (int64_t a = 0; a < n; a += chunk) {
+        const int64_t rows = n - a < chunk ? n - a : chunk;
+        hipError_t e = launch_fill_normal(tmp_f32, rows * k, seed * 1000003ull + (uint64_t)a, 0.0f, stdv, s);
+        if (e == hipSuccess) e = launch_from_float(dst.w.dtype, tmp_f32, rows * nb, tmp_blk, s);
+        QWeight part = dst.w;
+        const size_t hb = weight_hdr_bytes(dst.w.dtype), qb = weight_qs_bytes(dst.w.dtype);
+        part.hdr = dst.w.hdr + (size_t)(r0 + a) * nb * hb;
+        part.qs = dst.w.qs + (size_t)(r0 + a) * nb * qb;
+        if (e == hipSuccess) e = launch_repack(dst.w.dtype, tmp_blk, rows * nb, (void*)part.hdr, (void*)part.qs, true, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Per-layer trace segments (each [n, size] f32): hn_attn, qkv, q, ctx, h_mid, hn_ffn,
+// gu, act, h_out; preceded by the embedding output and followed by hn_final.
+size_t trace_layer_floats(const sxq_lm* lm, int n) {
+    const sxq_lm_config& c = lm->c;
+    return (size_t)n * (4 * (size_t)c.dim + lm->qkv_n + 2 * (size_t)lm->ctx + 3 * (size_t)c.intermediate);
+}
+size_t trace_floats(const sxq_lm* lm, int n) {
+    return 2 * (size_t)n * lm->c.dim + (size_t)lm->c.n_layers * trace_layer_floats(lm, n);
+}
+
+hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
+    const sxq_lm_config& c = lm->c;
+    hipError_t e = hipSuccess;
+#define STEP(x)                      \
+    do {                             \
+        e = (x);                     \
+        if (e != hipSuccess) return e; \
+    } while (0)
+    float* tr = lm->trace;
+    auto record = [&](const float* src, size_t floats) -> hipError_t {
+        hipError_t r = hipMemcpyAsync(tr, src, floats * sizeof(float), hipMemcpyDeviceToDevice, s);
+        tr += floats;
+        return r;
+    };
+    auto slot = [&](size_t floats) {
+        float* p = tr;
+        tr += floats;
+        return p;
+    };
+    if (!from_embeds) {
+        if (c.tied_embedding)
+            STEP(launch_embed_quant_table(lm->d_ids, lm->ids_per, n, lm->head.w, c.dim, lm->cb_embed, c.n_codebooks,
+                                          c.codebook_size, c.semantic_begin, c.semantic_end, lm->h, s));
+        else
+            STEP(launch_embed_dense(lm->d_ids, lm->ids_per, n, lm->embed, c.embed_rows > 0 ? c.embed_rows : c.vocab, c.dim,
+                                    lm->h, s));
+    }
+    if (tr) STEP(record(lm->h, (size_t)n * c.dim));
+    const int I = c.intermediate;
+    const size_t nd = (size_t)n * c.dim;
+    for (int l = 0; l < c.n_layers; ++l) {
+        LmLayer& L = lm->layers[l];
+        float* kc = lm->kc + (int64_t)l * lm->kv_layer_stride;
+        float* vc = lm->vc + (int64_t)l * lm->kv_layer_stride;
+        STEP(launch_rmsnorm_quant(lm->vdt, lm->h, n, c.dim, L.attn_norm, c.norm_eps, lm->act_a, tr ? slot(nd) : nullptr, s));
+        STEP(launch_gemv(L.wqkv.w, lm->act_a, n, lm->qkv, lm->qkv_n, L.bqkv, nullptr, 0, s));
+        if (tr) STEP(record(lm->qkv, (size_t)n * lm->qkv_n));
+        STEP(launch_qk_rope_append(lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim,
+                                   c.qk_norm ? L.q_norm : nullptr, c.qk_norm ? L.k_norm : nullptr, c.norm_eps,
+                                   c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len, lm->qbuf, kc, vc,
+                                   lm->kv_stream_stride, c.max_seq, s));
+        if (tr) STEP(record(lm->qbuf, (size_t)n * lm->ctx));
+        STEP(launch_attention(lm->vdt, lm->qbuf, kc, vc, lm->d_len, n, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
+                              lm->kv_stream_stride, kAttnSplit, lm->max_splits, lm->part, lm->act_o,
+                              tr ? slot((size_t)n * lm->ctx) : nullptr, s));
+        STEP(launch_gemv(L.wo.w, lm->act_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+        if (tr) STEP(record(lm->h, nd));
+        STEP(launch_rmsnorm_quant(lm->vdt, lm->h, n, c.dim, L.ffn_norm, c.norm_eps, lm->act_a, tr ? slot(nd) : nullptr, s));
+        STEP(launch_gemv(L.w13.w, lm->act_a, n, lm->gu, 2 * I, nullptr, nullptr, 0, s));
+        if (tr) STEP(record(lm->gu, (size_t)n * 2 * I));
+        STEP(launch_silu_mul_quant(lm->vdt, lm->gu, n, I, lm->act_d, tr ? slot((size_t)n * I) : nullptr, s));
+        STEP(launch_gemv(L.w2.w, lm->act_d, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+        if (tr) STEP(record(lm->h, nd));
+    }
+    STEP(launch_rmsnorm_quant(lm->vdt, lm->h, n, c.dim, lm->final_norm, c.norm_eps, lm->act_a, tr ? slot(nd) : nullptr, s));
+    STEP(launch_gemv(lm->head.w, lm->act_a, n, lm->logits, c.vocab, c.head_bias ? lm->head_bias : nullptr, nullptr, 0, s));
+    STEP(launch_argmax(lm->logits, n, c.vocab, lm->d_ids, lm->ids_per, lm->d_next, s));
+    STEP(launch_advance(lm->d_len, n, s));
+#undef STEP
+    return hipSuccess;
+}
+
+void destroy_lm(sxq_lm* lm) {
+    for (auto& kv : lm->graphs) (void)hipGraphExecDestroy(kv.second);
+    if (lm->cap) (void)hipStreamDestroy(lm->cap);
+    for (void* p : lm->allocs) (void)hipFree(p);
+    delete lm;
+}
+
+sxq_status check_config(const sxq_lm_config* c) {
+    if (!c) return fail(SXQ_ERR_INVALID, "lm_create: null config");
+    if (c->n_layers <= 0 || c->dim <= 0 || c->n_heads <= 0 || c->n_kv_heads <= 0 || c->head_dim <= 0 ||
+        c->intermediate <= 0 || c->vocab <= 0 || c->max_seq <= 0)
+        return fail(SXQ_ERR_INVALID, "lm_create: every size in the config must be positive");
+    if (c->max_batch < 1 || c->max_batch > 16) return fail(SXQ_ERR_INVALID, "lm_create: max_batch must be 1..16");
+    if (c->n_heads % c->n_kv_heads) return fail(SXQ_ERR_SHAPE, "lm_create: n_heads %% n_kv_heads != 0");
+    if (c->head_dim > 256 || c->head_dim < 32 || c->head_dim % 8)
+        return fail(SXQ_ERR_SHAPE, "lm_create: head_dim must be a multiple of 8 in [32, 256]");
+    if (c->max_seq > kMaxSplits * kAttnSplit)
+        return fail(SXQ_ERR_INVALID, "lm_create: max_seq %d exceeds %d positions", c->max_seq, kMaxSplits * kAttnSplit);
+    const int dt = c->weight_dtype;
+    if (dt != kQ4K && dt != kQ8_0 && dt != kQ4_0) return fail(SXQ_ERR_DTYPE, "lm_create: weight dtype %d not supported", dt);
+    const int bs = block_size(dt);
+    if (c->dim % bs || (c->n_heads * c->head_dim) % bs || c->intermediate % bs)
+        return fail(SXQ_ERR_BLOCK_ALIGN,
+                    "lm_create: dim %d, n_heads*head_dim %d and intermediate %d must be multiples of the block size %d",
+                    c->dim, c->n_heads * c->head_dim, c->intermediate, bs);
+    if (c->n_codebooks < 0 || (c->n_codebooks > 0 && (c->codebook_size <= 0 || !c->tied_embedding)))
+        return fail(SXQ_ERR_INVALID, "lm_create: codebooks need codebook_size > 0 and a tied embedding");
+    return SXQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
+    if (!out) return fail(SXQ_ERR_INVALID, "lm_create: null output handle");
+    *out = nullptr;
+    sxq_status st = check_config(cfg);
+    if (st != SXQ_OK) return st;
+    DeviceGuard g(device);
+    HIP_TRY(g.err, "hipSetDevice");
+    sxq_lm* lm = new sxq_lm();
+    lm->device = device;
+    lm->c = *cfg;
+    const sxq_lm_config& c = lm->c;
+    const int dt = c.weight_dtype;
+    lm->vdt = vec_dot_type(dt);
+    lm->ctx = c.n_heads * c.head_dim;
+    lm->qkv_n = lm->ctx + 2 * c.n_kv_heads * c.head_dim;
+    lm->ids_per = 1 + c.n_codebooks;
+    lm->max_splits = (c.max_seq + kAttnSplit - 1) / kAttnSplit;
+    lm->kv_stream_stride = (int64_t)c.n_kv_heads * c.max_seq * c.head_dim;
+    lm->kv_layer_stride = lm->kv_stream_stride * c.max_batch;
+    const int MB = c.max_batch, I = c.intermediate, hd = c.head_dim;
+    hipError_t e = hipSuccess;
+    auto A = [&](void** p, size_t bytes) {
+        if (e == hipSuccess) e = dalloc(lm, p, bytes);
+    };
+    lm->layers.resize(c.n_layers);
+    for (auto& L : lm->layers) {
+        if (e == hipSuccess) e = alloc_weight(lm, L.wqkv, dt, lm->qkv_n, c.dim);
+        if (e == hipSuccess) e = alloc_weight(lm, L.wo, dt, c.dim, lm->ctx);
+        if (e == hipSuccess) e = alloc_weight(lm, L.w13, dt, 2 * (int64_t)I, c.dim);
+        if (e == hipSuccess) e = alloc_weight(lm, L.w2, dt, c.dim, I);
+        A((void**)&L.attn_norm, sizeof(float) * c.dim);
+        A((void**)&L.ffn_norm, sizeof(float) * c.dim);
+        A((void**)&L.q_norm, sizeof(float) * hd);
+        A((void**)&L.k_norm, sizeof(float) * hd);
+        A((void**)&L.bqkv, sizeof(float) * lm->qkv_n);
+    }
+    if (e == hipSuccess) e = alloc_weight(lm, lm->head, dt, c.vocab, c.dim);
+    A((void**)&lm->head_bias, sizeof(float) * c.vocab);
+    A((void**)&lm->final_norm, sizeof(float) * c.dim);
+    if (!c.tied_embedding) A((void**)&lm->embed, sizeof(float) * (size_t)(c.embed_rows > 0 ? c.embed_rows : c.vocab) * c.dim);
+    if (c.n_codebooks > 0) A((void**)&lm->cb_embed, sizeof(float) * (size_t)c.n_codebooks * c.codebook_size * c.dim);
+    A((void**)&lm->rope_cos, sizeof(float) * (size_t)c.max_seq * (hd / 2));
+    A((void**)&lm->rope_sin, sizeof(float) * (size_t)c.max_seq * (hd / 2));
+    A((void**)&lm->kc, sizeof(float) * (size_t)lm->kv_layer_stride * c.n_layers);
+    A((void**)&lm->vc, sizeof(float) * (size_t)lm->kv_layer_stride * c.n_layers);
+    A((void**)&lm->d_len, sizeof(int) * MB);
+    A((void**)&lm->h, sizeof(float) * (size_t)MB * c.dim);
+    A((void**)&lm->qkv, sizeof(float) * (size_t)MB * lm->qkv_n);
+    A((void**)&lm->qbuf, sizeof(float) * (size_t)MB * lm->ctx);
+    A((void**)&lm->part, sizeof(float) * (size_t)MB * c.n_heads * lm->max_splits * (2 + hd));
+    A((void**)&lm->gu, sizeof(float) * (size_t)MB * 2 * I);
+    A((void**)&lm->logits, sizeof(float) * (size_t)MB * c.vocab);
+    const size_t ab = act_block_bytes(lm->vdt), bs = block_size(lm->vdt);
+    A((void**)&lm->act_a, ab * MB * (c.dim / bs));
+    A((void**)&lm->act_o, ab * MB * (lm->ctx / bs));
+    A((void**)&lm->act_d, ab * MB * (I / bs));
+    A((void**)&lm->d_ids, sizeof(int) * MB * lm->ids_per);
+    A((void**)&lm->d_next, sizeof(int) * MB);
+    if (e != hipSuccess) {
+        destroy_lm(lm);
+        return hip_fail(e, "lm_create: allocation");
+    }
+    // RoPE tables, computed on the host with the reference's f32 formula:
+    // inv_freq[i] = 1 / base^(2i/hd), angle = t * inv_freq[i] (s2/nn.rs:125-135, cv2/attention.rs:110-118).
+    {
+        const int half = hd / 2;
+        std::vector<float> cs((size_t)c.max_seq * half), sn((size_t)c.max_seq * half);
+        for (int i = 0; i < half; ++i) {
+            const float inv = 1.0f / powf(c.rope_theta, 2.0f * (float)i / (float)hd);
+            for (int t = 0; t < c.max_seq; ++t) {
+                const float a = (float)t * inv;
+                cs[(size_t)t * half + i] = cosf(a);
+                sn[(size_t)t * half + i] = sinf(a);
+            }
+        }
+        e = hipMemcpy(lm->rope_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(lm->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice);
+    }
+    // defaults: norm weights 1, biases 0, lengths 0, ids 0
+    for (auto& L : lm->layers) {
+        if (e == hipSuccess) e = launch_fill_value(L.attn_norm, c.dim, 1.0f, nullptr);
+        if (e == hipSuccess) e = launch_fill_value(L.ffn_norm, c.dim, 1.0f, nullptr);
+        if (e == hipSuccess) e = launch_fill_value(L.q_norm, hd, 1.0f, nullptr);
+        if (e == hipSuccess) e = launch_fill_value(L.k_norm, hd, 1.0f, nullptr);
+        if (e == hipSuccess) e = launch_fill_value(L.bqkv, lm->qkv_n, 0.0f, nullptr);
+    }
+    if (e == hipSuccess) e = launch_fill_value(lm->final_norm, c.dim, 1.0f, nullptr);
+    if (e == hipSuccess) e = launch_fill_value(lm->head_bias, c.vocab, 0.0f, nullptr);
+    if (e == hipSuccess) e = hipMemset(lm->d_len, 0, sizeof(int) * MB);
+    if (e == hipSuccess) e = hipMemset(lm->d_ids, 0, sizeof(int) * MB * lm->ids_per);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&lm->cap, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        destroy_lm(lm);
+        return hip_fail(e, "lm_create: initialisation");
+    }
+    lm->h_len.assign(MB, 0);
+    *out = lm;
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_destroy(sxq_lm* lm) {
+    if (!lm) return SXQ_OK;
+    DeviceGuard g(lm->device);
+    (void)hipDeviceSynchronize();
+    destroy_lm(lm);
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_set_linear(sxq_lm* lm, int layer, int which, const sxq_qmm* q) {
+    if (!lm || !q) return fail(SXQ_ERR_INVALID, "lm_set_linear: null handle");
+    const sxq_lm_config& c = lm->c;
+    if (q->w.dtype != c.weight_dtype)
+        return fail(SXQ_ERR_DTYPE, "lm_set_linear: weight dtype %d, the model uses %d", q->w.dtype, c.weight_dtype);
+    if (which != SXQ_LM_HEAD && (layer < 0 || layer >= c.n_layers))
+        return fail(SXQ_ERR_INVALID, "lm_set_linear: layer %d out of range", layer);
+    const int hd = c.head_dim;
+    DevWeight* dst = nullptr;
+    int64_t r0 = 0, rows = 0, k = 0;
+    switch (which) {
+    case SXQ_LM_WQKV: dst = &lm->layers[layer].wqkv; rows = lm->qkv_n; k = c.dim; break;
+    case SXQ_LM_WQ: dst = &lm->layers[layer].wqkv; rows = lm->ctx; k = c.dim; break;
+    case SXQ_LM_WK: dst = &lm->layers[layer].wqkv; r0 = lm->ctx; rows = (int64_t)c.n_kv_heads * hd; k = c.dim; break;
+    case SXQ_LM_WV:
+        dst = &lm->layers[layer].wqkv;
+        r0 = lm->ctx + (int64_t)c.n_kv_heads * hd;
+        rows = (int64_t)c.n_kv_heads * hd;
+        k = c.dim;
+        break;
+    case SXQ_LM_WO: dst = &lm->layers[layer].wo; rows = c.dim; k = lm->ctx; break;
+    case SXQ_LM_W1: dst = &lm->layers[layer].w13; rows = c.intermediate; k = c.dim; break;
+    case SXQ_LM_W3: dst = &lm->layers[layer].w13; r0 = c.intermediate; rows = c.intermediate; k = c.dim; break;
+    case SXQ_LM_W2: dst = &lm->layers[layer].w2; rows = c.dim; k = c.intermediate; break;
+    case SXQ_LM_HEAD: dst = &lm->head; rows = c.vocab; k = c.dim; break;
+    default: return fail(SXQ_ERR_INVALID, "lm_set_linear: unknown slot %d", which);
+    }
+    if (q->w.n != rows || q->w.k != k)
+        return fail(SXQ_ERR_SHAPE, "lm_set_linear: slot %d expects [%lld, %lld], got [%lld, %lld]", which,
+                    (long long)rows, (long long)k, (long long)q->w.n, (long long)q->w.k);
+    std::lock_guard<std::mutex> lock(lm->mu);
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    HIP_TRY(copy_rows(*dst, q->w, r0, nullptr), "lm_set_linear: copy");
+    HIP_TRY(hipDeviceSynchronize(), "lm_set_linear");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_set_vector(sxq_lm* lm, int layer, int which, const float* data, int64_t n, int src_is_device) {
+    if (!lm || !data) return fail(SXQ_ERR_INVALID, "lm_set_vector: null pointer");
+    const sxq_lm_config& c = lm->c;
+    const bool per_layer = which <= SXQ_LM_BV;
+    if (per_layer && (layer < 0 || layer >= c.n_layers)) return fail(SXQ_ERR_INVALID, "lm_set_vector: layer out of range");
+    const int hd = c.head_dim;
+    float* dst = nullptr;
+    int64_t want = 0;
+    switch (which) {
+    case SXQ_LM_ATTN_NORM: dst = lm->layers[layer].attn_norm; want = c.dim; break;
+    case SXQ_LM_FFN_NORM: dst = lm->layers[layer].ffn_norm; want = c.dim; break;
+    case SXQ_LM_Q_NORM: dst = lm->layers[layer].q_norm; want = hd; break;
+    case SXQ_LM_K_NORM: dst = lm->layers[layer].k_norm; want = hd; break;
+    case SXQ_LM_BQ: dst = lm->layers[layer].bqkv; want = lm->ctx; break;
+    case SXQ_LM_BK: dst = lm->layers[layer].bqkv + lm->ctx; want = (int64_t)c.n_kv_heads * hd; break;
+    case SXQ_LM_BV: dst = lm->layers[layer].bqkv + lm->ctx + (int64_t)c.n_kv_heads * hd; want = (int64_t)c.n_kv_heads * hd; break;
+    case SXQ_LM_FINAL_NORM: dst = lm->final_norm; want = c.dim; break;
+    case SXQ_LM_HEAD_BIAS: dst = lm->head_bias; want = c.vocab; break;
+    case SXQ_LM_EMBED:
+        if (!lm->embed) return fail(SXQ_ERR_INVALID, "lm_set_vector: this model has a tied embedding");
+        dst = lm->embed;
+        want = (int64_t)(c.embed_rows > 0 ? c.embed_rows : c.vocab) * c.dim;
+        break;
+    case SXQ_LM_CODEBOOK_EMBED:
+        if (!lm->cb_embed) return fail(SXQ_ERR_INVALID, "lm_set_vector: this model has no codebooks");
+        dst = lm->cb_embed;
+        want = (int64_t)c.n_codebooks * c.codebook_size * c.dim;
+        break;
+    default: return fail(SXQ_ERR_INVALID, "lm_set_vector: unknown slot %d", which);
+    }
+    if (n != want) return fail(SXQ_ERR_SHAPE, "lm_set_vector: slot %d expects %lld values, got %lld", which, (long long)want, (long long)n);
+    std::lock_guard<std::mutex> lock(lm->mu);
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    HIP_TRY(hipMemcpy(dst, data, sizeof(float) * n, src_is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
+            "lm_set_vector: copy");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_init_random(sxq_lm* lm, uint64_t seed, float stdv) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_init_random: null handle");
+    std::lock_guard<std::mutex> lock(lm->mu);
+    const sxq_lm_config& c = lm->c;
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    const int64_t tmp_elems = (int64_t)64 << 20;  // 256 MB of f32 staging
+    float* tmp = nullptr;
+    uint8_t* blk = nullptr;
+    HIP_TRY(hipMalloc(&tmp, sizeof(float) * tmp_elems), "lm_init_random: staging");
+    hipError_t e = hipMalloc(&blk, (size_t)tmp_elems * 2);  // >= bytes of any block encoding of tmp_elems
+    uint64_t sd = seed * 0x9E3779B97F4A7C15ull + 1;
+    auto W = [&](DevWeight& d, int64_t r0, int64_t n) {
+        if (e == hipSuccess) e = random_rows(d, r0, n, sd++, stdv, tmp, blk, tmp_elems, nullptr);
+    };
+    auto V = [&](float* p, int64_t n, float mean, float sdv) {
+        if (e == hipSuccess) e = sdv > 0 ? launch_fill_normal(p, n, sd++, mean, sdv, nullptr) : launch_fill_value(p, n, mean, nullptr);
+    };
+    for (auto& L : lm->layers) {
+        W(L.wqkv, 0, lm->qkv_n);
+        W(L.wo, 0, c.dim);
+        W(L.w13, 0, c.intermediate);
+        W(L.w13, c.intermediate, c.intermediate);
+        W(L.w2, 0, c.dim);
+        V(L.attn_norm, c.dim, 1.0f, 0.0f);
+        V(L.ffn_norm, c.dim, 1.0f, 0.0f);
+        V(L.q_norm, c.head_dim, 1.0f, 0.0f);
+        V(L.k_norm, c.head_dim, 1.0f, 0.0f);
+        V(L.bqkv, lm->qkv_n, 0.0f, c.qkv_bias ? stdv : 0.0f);
+    }
+    W(lm->head, 0, c.vocab);
+    V(lm->final_norm, c.dim, 1.0f, 0.0f);
+    V(lm->head_bias, c.vocab, 0.0f, c.head_bias ? stdv : 0.0f);
+    if (lm->embed) V(lm->embed, (int64_t)(c.embed_rows > 0 ? c.embed_rows : c.vocab) * c.dim, 0.0f, stdv);
+    if (lm->cb_embed) V(lm->cb_embed, (int64_t)c.n_codebooks * c.codebook_size * c.dim, 0.0f, stdv);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    (void)hipFree(tmp);
+    if (blk) (void)hipFree(blk);
+    if (e != hipSuccess) return hip_fail(e, "lm_init_random");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_set_lengths(sxq_lm* lm, const int32_t* lengths, int n) {
+    if (!lm || !lengths) return fail(SXQ_ERR_INVALID, "lm_set_lengths: null pointer");
+    if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_set_lengths: %d streams (max %d)", n, lm->c.max_batch);
+    for (int s = 0; s < n; ++s)
+        if (lengths[s] < 0 || lengths[s] > lm->c.max_seq)
+            return fail(SXQ_ERR_INVALID, "lm_set_lengths: length %d outside [0, %d]", lengths[s], lm->c.max_seq);
+    std::lock_guard<std::mutex> lock(lm->mu);
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    HIP_TRY(hipDeviceSynchronize(), "lm_set_lengths");
+    for (int s = 0; s < n; ++s) lm->h_len[s] = lengths[s];
+    HIP_TRY(hipMemcpy(lm->d_len, lm->h_len.data(), sizeof(int) * lm->c.max_batch, hipMemcpyHostToDevice), "lm_set_lengths");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_get_lengths(const sxq_lm* lm, int32_t* lengths, int n) {
+    if (!lm || !lengths) return fail(SXQ_ERR_INVALID, "lm_get_lengths: null pointer");
+    if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_get_lengths: bad stream count");
+    for (int s = 0; s < n; ++s) lengths[s] = lm->h_len[s];
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_kv_fill_random(sxq_lm* lm, const int32_t* lengths, int n, uint64_t seed) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_kv_fill_random: null handle");
+    {
+        std::lock_guard<std::mutex> lock(lm->mu);
+        DeviceGuard g(lm->device);
+        HIP_TRY(g.err, "hipSetDevice");
+        const int64_t total = lm->kv_layer_stride * lm->c.n_layers;
+        HIP_TRY(launch_fill_normal(lm->kc, total, seed * 2 + 11, 0.0f, 1.0f, nullptr), "lm_kv_fill_random");
+        HIP_TRY(launch_fill_normal(lm->vc, total, seed * 2 + 12, 0.0f, 1.0f, nullptr), "lm_kv_fill_random");
+        HIP_TRY(hipDeviceSynchronize(), "lm_kv_fill_random");
+    }
+    return lengths ? sxq_lm_set_lengths(lm, lengths, n) : SXQ_OK;
+}
+
+sxq_status sxq_lm_step(sxq_lm* lm, int n, const int32_t* ids, const float* embeds, float* logits, int32_t* next_ids,
+                       unsigned flags, void* stream) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_step: null handle");
+    if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_step: %d streams (max %d)", n, lm->c.max_batch);
+    if (flags & ~SXQ_LM_GRAPH) return fail(SXQ_ERR_INVALID, "lm_step: unknown flags 0x%x", flags);
+    std::lock_guard<std::mutex> lock(lm->mu);
+    for (int s = 0; s < n; ++s)
+        if (lm->h_len[s] >= lm->c.max_seq)
+            return fail(SXQ_ERR_INVALID, "lm_step: stream %d KV cache is full (%d positions)", s, lm->c.max_seq);
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    hipStream_t st = (hipStream_t)stream;
+    const bool emb = embeds != nullptr;
+    if (ids) HIP_TRY(hipMemcpyAsync(lm->d_ids, ids, sizeof(int) * n * lm->ids_per, hipMemcpyDeviceToDevice, st), "lm_step: ids");
+    if (emb) HIP_TRY(hipMemcpyAsync(lm->h, embeds, sizeof(float) * n * lm->c.dim, hipMemcpyDeviceToDevice, st), "lm_step: embeds");
+    if (flags & SXQ_LM_GRAPH) {
+        const GraphKey key{n, emb, lm->trace != nullptr};
+        auto it = lm->graphs.find(key);
+        if (it == lm->graphs.end()) {
+            // Capture on the library's own stream (the legacy default stream cannot capture).
+            hipGraph_t graph = nullptr;
+            hipGraphExec_t exec = nullptr;
+            HIP_TRY(hipStreamSynchronize(st), "lm_step: sync before capture");
+            HIP_TRY(hipStreamBeginCapture(lm->cap, hipStreamCaptureModeThreadLocal), "lm_step: begin capture");
+            hipError_t e = enqueue_step(lm, n, emb, lm->cap);
+            hipError_t e2 = hipStreamEndCapture(lm->cap, &graph);
+            if (e == hipSuccess) e = e2;
+            if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            if (graph) (void)hipGraphDestroy(graph);
+            if (e != hipSuccess) return hip_fail(e, "lm_step: graph capture");
+            it = lm->graphs.emplace(key, exec).first;
+        }
+        HIP_TRY(hipGraphLaunch(it->second, st), "lm_step: graph launch");
+    } else {
+        HIP_TRY(enqueue_step(lm, n, emb, st), "lm_step");
+    }
+    for (int s = 0; s < n; ++s) lm->h_len[s] += 1;
+    if (logits)
+        HIP_TRY(hipMemcpyAsync(logits, lm->logits, sizeof(float) * n * lm->c.vocab, hipMemcpyDeviceToDevice, st), "lm_step: logits");
+    if (next_ids) HIP_TRY(hipMemcpyAsync(next_ids, lm->d_next, sizeof(int) * n, hipMemcpyDeviceToDevice, st), "lm_step: next ids");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_gemv_pass(sxq_lm* lm, int n, int with_head, void* stream) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_gemv_pass: null handle");
+    if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_gemv_pass: %d streams", n);
+    std::lock_guard<std::mutex> lock(lm->mu);
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    hipStream_t s = (hipStream_t)stream;
+    const sxq_lm_config& c = lm->c;
+    const int I = c.intermediate;
+    for (int l = 0; l < c.n_layers; ++l) {
+        LmLayer& L = lm->layers[l];
+        HIP_TRY(launch_gemv(L.wqkv.w, lm->act_a, n, lm->qkv, lm->qkv_n, L.bqkv, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv(L.wo.w, lm->act_o, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv(L.w13.w, lm->act_a, n, lm->gu, 2 * I, nullptr, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv(L.w2.w, lm->act_d, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
+    }
+    if (with_head)
+        HIP_TRY(launch_gemv(lm->head.w, lm->act_a, n, lm->logits, c.vocab, nullptr, nullptr, 0, s), "lm_gemv_pass");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_read_kv(const sxq_lm* lm, int layer, int s, int g, int pos0, int count, float* k_out, float* v_out,
+                          void* stream) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_read_kv: null handle");
+    const sxq_lm_config& c = lm->c;
+    if (layer < 0 || layer >= c.n_layers || s < 0 || s >= c.max_batch || g < 0 || g >= c.n_kv_heads || pos0 < 0 ||
+        count < 0 || pos0 + count > c.max_seq)
+        return fail(SXQ_ERR_INVALID, "lm_read_kv: out of range");
+    DeviceGuard gd(lm->device);
+    HIP_TRY(gd.err, "hipSetDevice");
+    const int64_t off = (int64_t)layer * lm->kv_layer_stride + (int64_t)s * lm->kv_stream_stride +
+                        ((int64_t)g * c.max_seq + pos0) * c.head_dim;
+    const size_t bytes = sizeof(float) * (size_t)count * c.head_dim;
+    hipStream_t st = (hipStream_t)stream;
+    if (k_out) HIP_TRY(hipMemcpyAsync(k_out, lm->kc + off, bytes, hipMemcpyDeviceToDevice, st), "lm_read_kv");
+    if (v_out) HIP_TRY(hipMemcpyAsync(v_out, lm->vc + off, bytes, hipMemcpyDeviceToDevice, st), "lm_read_kv");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_trace_floats(const sxq_lm* lm, int n, size_t* floats) {
+    if (!lm || !floats) return fail(SXQ_ERR_INVALID, "lm_trace_floats: null pointer");
+    if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_trace_floats: bad stream count");
+    *floats = trace_floats(lm, n);
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_set_trace(sxq_lm* lm, float* trace, size_t capacity_floats) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_set_trace: null handle");
+    if (trace && capacity_floats < trace_floats(lm, lm->c.max_batch))
+        return fail(SXQ_ERR_SHAPE, "lm_set_trace: %zu floats given, %zu needed", capacity_floats,
+                    trace_floats(lm, lm->c.max_batch));
+    std::lock_guard<std::mutex> lock(lm->mu);
+    lm->trace = trace;
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_read_state(const sxq_lm* lm, int which, int n, float* out, void* stream) {
+    if (!lm || !out) return fail(SXQ_ERR_INVALID, "lm_read_state: null pointer");
+    if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_read_state: bad stream count");
+    const float* src = nullptr;
+    size_t per = 0;
+    switch (which) {
+    case 0: src = lm->h; per = lm->c.dim; break;
+    case 1: src = lm->logits; per = lm->c.vocab; break;
+    case 2: src = lm->qkv; per = lm->qkv_n; break;
+    case 3: src = lm->gu; per = 2 * (size_t)lm->c.intermediate; break;
+    case 4: src = lm->qbuf; per = lm->ctx; break;
+    default: return fail(SXQ_ERR_INVALID, "lm_read_state: unknown buffer %d", which);
+    }
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    HIP_TRY(hipMemcpyAsync(out, src, sizeof(float) * per * n, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+            "lm_read_state");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_weight_bytes(const sxq_lm* lm, size_t* layer_bytes, size_t* head_bytes) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_weight_bytes: null handle");
+    const int dt = lm->c.weight_dtype;
+    auto canon = [&](const QWeight& w) { return (size_t)w.n * (size_t)w.nb * (size_t)type_size(dt); };
+    size_t lb = 0;
+    for (const auto& L : lm->layers) lb += canon(L.wqkv.w) + canon(L.wo.w) + canon(L.w13.w) + canon(L.w2.w);
+    if (layer_bytes) *layer_bytes = lb;
+    if (head_bytes) *head_bytes = canon(lm->head.w);
+    return SXQ_OK;
+}
+
+}  // extern "C"

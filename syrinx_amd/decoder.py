@@ -1,0 +1,258 @@
+"""Host mirror of the decode-step callers of QMatMul, over libsxq's sxq_lm_* C-ABI.
+
+``DecoderLM`` is one Qwen2/Qwen3-style decoder whose every projection is a libsxq
+QMatMul and whose whole token step (embedding, layers, head, argmax) runs on the GPU,
+optionally as a replayed HIP graph.  Two presets mirror the reference's models:
+
+* ``fish_s2_slow_ar_config`` -- the Fish s2-pro slow AR (Qwen3-4B shape), whose
+  ``slow_step(frame, pos)`` is crates/syrinx-fish/src/s2/slow_ar.rs:259-271 and whose
+  batched form ``slow_step_batch`` is :456-499;
+* ``cosyvoice2_lm_config`` -- the CosyVoice2 Qwen2-0.5B LM, whose
+  ``forward_logits_cached(embeds, cache)`` is crates/syrinx-lm/src/cv2/mod.rs:283-286.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, fields
+
+import torch
+
+from ._lib import check, lib
+from .quantized import GgmlDType, QMatMul
+
+LM_GRAPH = 1
+WQKV, WQ, WK, WV, WO, W1, W3, W2, HEAD = range(9)
+ATTN_NORM, FFN_NORM, Q_NORM, K_NORM, BQ, BK, BV, FINAL_NORM, HEAD_BIAS, EMBED, CODEBOOK_EMBED = range(11)
+
+
+class LmConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", ctypes.c_int32), ("dim", ctypes.c_int32), ("n_heads", ctypes.c_int32),
+        ("n_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("intermediate", ctypes.c_int32),
+        ("vocab", ctypes.c_int32), ("embed_rows", ctypes.c_int32), ("max_seq", ctypes.c_int32),
+        ("max_batch", ctypes.c_int32), ("weight_dtype", ctypes.c_int32), ("norm_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float), ("rope_interleaved", ctypes.c_int32), ("qk_norm", ctypes.c_int32),
+        ("qkv_bias", ctypes.c_int32), ("head_bias", ctypes.c_int32), ("tied_embedding", ctypes.c_int32),
+        ("n_codebooks", ctypes.c_int32), ("codebook_size", ctypes.c_int32), ("semantic_begin", ctypes.c_int32),
+        ("semantic_end", ctypes.c_int32),
+    ]
+
+
+@dataclass
+class DecoderConfig:
+    n_layers: int
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    intermediate: int
+    vocab: int
+    max_seq: int
+    max_batch: int = 1
+    weight_dtype: int = int(GgmlDType.Q4K)
+    norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    rope_interleaved: int = 1
+    qk_norm: int = 1
+    qkv_bias: int = 0
+    head_bias: int = 0
+    tied_embedding: int = 1
+    embed_rows: int = 0
+    n_codebooks: int = 0
+    codebook_size: int = 0
+    semantic_begin: int = 0
+    semantic_end: int = -1
+
+    def to_c(self) -> LmConfig:
+        c = LmConfig()
+        for f in fields(self):
+            setattr(c, f.name, getattr(self, f.name))
+        return c
+
+
+def fish_s2_slow_ar_config(n_layers=36, max_seq=1280, max_batch=1, dtype=GgmlDType.Q4K, n_codebooks=10,
+                           **kw) -> DecoderConfig:
+    """Qwen3-4B slow AR of Fish s2-pro (crates/syrinx-fish/src/common/config.rs:194-251):
+    36 layers, dim 2560, 32/8 heads of 128, SwiGLU 9728, eps 1e-6, RoPE base 1e6
+    interleaved, QK-RMSNorm, no qkv/o bias, head tied to the 155776-row embedding, MCF
+    over 10 codebooks of 4096 (semantic ids 151678..155773)."""
+    base = dict(n_layers=n_layers, dim=2560, n_heads=32, n_kv_heads=8, head_dim=128, intermediate=9728,
+                vocab=155776, max_seq=max_seq, max_batch=max_batch, weight_dtype=int(dtype), norm_eps=1e-6,
+                rope_theta=1e6, rope_interleaved=1, qk_norm=1, qkv_bias=0, head_bias=0, tied_embedding=1,
+                n_codebooks=n_codebooks, codebook_size=4096 if n_codebooks else 0, semantic_begin=151678,
+                semantic_end=155773)
+    base.update(kw)
+    return DecoderConfig(**base)
+
+
+def cosyvoice2_lm_config(n_layers=24, max_seq=1024, max_batch=1, dtype=GgmlDType.Q8_0, **kw) -> DecoderConfig:
+    """CosyVoice2 Qwen2-0.5B LM (crates/syrinx-lm/src/cv2/mod.rs:36-56): 24 layers, hidden
+    896, 14/2 heads of 64, SwiGLU 4864, eps 1e-6, RoPE theta 1e6 rotate-half, q/k/v
+    biases, llm_decoder head [6564 x 896] with bias, speech embedding table."""
+    base = dict(n_layers=n_layers, dim=896, n_heads=14, n_kv_heads=2, head_dim=64, intermediate=4864,
+                vocab=6564, max_seq=max_seq, max_batch=max_batch, weight_dtype=int(dtype), norm_eps=1e-6,
+                rope_theta=1e6, rope_interleaved=0, qk_norm=0, qkv_bias=1, head_bias=1, tied_embedding=0,
+                embed_rows=6564 + 3)
+    base.update(kw)
+    return DecoderConfig(**base)
+
+
+class DecoderLM:
+    """A decode-step engine (sxq_lm) on one GPU."""
+
+    def __init__(self, cfg: DecoderConfig, device="cuda:0"):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self._h = ctypes.c_void_p()
+        self._c = cfg.to_c()
+        check(lib().sxq_lm_create(self._dev(), ctypes.byref(self._c), ctypes.byref(self._h)))
+        self.ids_per = 1 + cfg.n_codebooks
+
+    def _dev(self) -> int:
+        return self.device.index if self.device.index is not None else torch.cuda.current_device()
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                lib().sxq_lm_destroy(h)
+            except Exception:
+                pass
+            self._h = None
+
+    # -- weights ----------------------------------------------------------------------
+    def set_linear(self, layer: int, which: int, qmm: QMatMul) -> None:
+        check(lib().sxq_lm_set_linear(self._h, layer, which, ctypes.c_void_p(qmm.handle())))
+
+    def set_vector(self, layer: int, which: int, data: torch.Tensor) -> None:
+        t = data.detach().to(device=self.device, dtype=torch.float32).contiguous()
+        torch.cuda.current_stream(self.device).synchronize()
+        check(lib().sxq_lm_set_vector(self._h, layer, which, ctypes.c_void_p(t.data_ptr()), t.numel(), 1))
+
+    def init_random(self, seed: int = 0, std: float = 0.02) -> None:
+        check(lib().sxq_lm_init_random(self._h, seed, std))
+
+    def kv_fill_random(self, lengths, seed: int = 0) -> None:
+        arr = (ctypes.c_int32 * len(lengths))(*lengths)
+        check(lib().sxq_lm_kv_fill_random(self._h, arr, len(lengths), seed))
+
+    def set_lengths(self, lengths) -> None:
+        arr = (ctypes.c_int32 * len(lengths))(*lengths)
+        check(lib().sxq_lm_set_lengths(self._h, arr, len(lengths)))
+
+    def lengths(self, n=None):
+        n = n or self.cfg.max_batch
+        arr = (ctypes.c_int32 * n)()
+        check(lib().sxq_lm_get_lengths(self._h, arr, n))
+        return list(arr)
+
+    def reset(self, n=None) -> None:
+        """SlowAr::reset (slow_ar.rs:79-81): empty caches."""
+        self.set_lengths([0] * (n or self.cfg.max_batch))
+
+    def weight_bytes(self):
+        lb, hb = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib().sxq_lm_weight_bytes(self._h, ctypes.byref(lb), ctypes.byref(hb)))
+        return int(lb.value), int(hb.value)
+
+    # -- step ---------------------------------------------------------------------------
+    def step(self, ids: torch.Tensor = None, embeds: torch.Tensor = None, n: int = None, graph: bool = False,
+             want_logits: bool = True):
+        """One token for n streams.  ids int32 [n, 1 + n_codebooks] (or [n]) or embeds
+        f32 [n, dim]; None for both reuses the previous argmax.  Returns (logits, next_ids)."""
+        if ids is not None:
+            ids = ids.to(device=self.device, dtype=torch.int32).reshape(-1, self.ids_per).contiguous()
+            n = ids.shape[0]
+        if embeds is not None:
+            embeds = embeds.to(device=self.device, dtype=torch.float32).reshape(-1, self.cfg.dim).contiguous()
+            n = embeds.shape[0]
+        if n is None:
+            raise ValueError("step: give ids, embeds or n")
+        logits = torch.empty((n, self.cfg.vocab), dtype=torch.float32, device=self.device) if want_logits else None
+        nxt = torch.empty((n,), dtype=torch.int32, device=self.device)
+        P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+        check(lib().sxq_lm_step(self._h, n, P(ids), P(embeds), P(logits), P(nxt), LM_GRAPH if graph else 0,
+                                torch.cuda.current_stream(self.device).cuda_stream))
+        return logits, nxt
+
+    TRACE_SEGMENTS = ("hn_attn", "qkv", "q", "ctx", "h_mid", "hn_ffn", "gu", "act", "h_out")
+
+    def enable_trace(self, on: bool = True) -> None:
+        """Record every f32 intermediate of each following step (tests)."""
+        if not on:
+            check(lib().sxq_lm_set_trace(self._h, None, 0))
+            self._trace = None
+            return
+        sz = ctypes.c_size_t()
+        check(lib().sxq_lm_trace_floats(self._h, self.cfg.max_batch, ctypes.byref(sz)))
+        self._trace = torch.zeros(int(sz.value), dtype=torch.float32, device=self.device)
+        check(lib().sxq_lm_set_trace(self._h, ctypes.c_void_p(self._trace.data_ptr()), int(sz.value)))
+
+    def trace(self, n: int) -> dict:
+        """The last traced step of n streams: {'embed': [n, dim], 'final_hn': [n, dim],
+        'layers': [{segment: [n, size]} per layer]} as numpy arrays."""
+        c = self.cfg
+        t = self._trace.cpu().numpy()
+        qkv_n = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
+        ctx = c.n_heads * c.head_dim
+        sizes = dict(hn_attn=c.dim, qkv=qkv_n, q=ctx, ctx=ctx, h_mid=c.dim, hn_ffn=c.dim, gu=2 * c.intermediate,
+                     act=c.intermediate, h_out=c.dim)
+        off = 0
+
+        def take(size):
+            nonlocal off
+            a = t[off: off + n * size].reshape(n, size)
+            off += n * size
+            return a
+
+        out = {"embed": take(c.dim), "layers": []}
+        for _ in range(c.n_layers):
+            out["layers"].append({seg: take(sizes[seg]) for seg in self.TRACE_SEGMENTS})
+        out["final_hn"] = take(c.dim)
+        return out
+
+    def read_state(self, which: int, n: int = 1) -> torch.Tensor:
+        """A step buffer (tests): 0 residual after the last layer, 1 logits, 2 last qkv,
+        3 last gate|up, 4 last post-RoPE queries."""
+        c = self.cfg
+        per = {0: c.dim, 1: c.vocab, 2: (c.n_heads + 2 * c.n_kv_heads) * c.head_dim, 3: 2 * c.intermediate,
+               4: c.n_heads * c.head_dim}[which]
+        out = torch.empty((n, per), dtype=torch.float32, device=self.device)
+        check(lib().sxq_lm_read_state(self._h, which, n, ctypes.c_void_p(out.data_ptr()),
+                                      torch.cuda.current_stream(self.device).cuda_stream))
+        return out
+
+    def read_kv(self, layer: int, stream: int, kv_head: int, pos0: int, count: int):
+        hd = self.cfg.head_dim
+        k = torch.empty((count, hd), dtype=torch.float32, device=self.device)
+        v = torch.empty_like(k)
+        check(lib().sxq_lm_read_kv(self._h, layer, stream, kv_head, pos0, count, ctypes.c_void_p(k.data_ptr()),
+                                   ctypes.c_void_p(v.data_ptr()), torch.cuda.current_stream(self.device).cuda_stream))
+        return k, v
+
+
+class SlowAr(DecoderLM):
+    """Fish s2 slow AR decode (crates/syrinx-fish/src/s2/slow_ar.rs)."""
+
+    def slow_step(self, frame, pos: int = None, graph: bool = True):
+        """frame: [1 + num_codebooks] ids of the previous frame; pos must equal the cache
+        length (slow_ar.rs:259-271).  Returns (semantic_logits [vocab], next argmax id)."""
+        if pos is not None and pos != self.lengths(1)[0]:
+            raise ValueError(f"slow_step pos {pos} must equal the current cache length {self.lengths(1)[0]}")
+        ids = torch.as_tensor(frame, dtype=torch.int32).reshape(1, -1)
+        logits, nxt = self.step(ids=ids, graph=graph)
+        return logits[0], nxt[0]
+
+    def slow_step_batch(self, frames, graph: bool = True):
+        """frames: [n, 1 + num_codebooks]; ragged cache lengths need no left padding."""
+        return self.step(ids=torch.as_tensor(frames, dtype=torch.int32), graph=graph)
+
+
+class Qwen2Lm(DecoderLM):
+    """CosyVoice2 LM cached decode (crates/syrinx-lm/src/cv2/mod.rs:255-286)."""
+
+    def forward_logits_cached(self, embeds: torch.Tensor, graph: bool = True):
+        """embeds [b, 1, 896] -> logits [b, 1, 6564] for one new position per stream."""
+        b = embeds.shape[0]
+        logits, _ = self.step(embeds=embeds.reshape(b, -1), graph=graph)
+        return logits.reshape(b, 1, -1)
