@@ -235,31 +235,35 @@ __global__ __launch_bounds__(256) void k_gemv2_q4k(const uint4* __restrict__ hdr
                                                    int64_t ldr) {
     extern __shared__ uint4 lds[];
     const ActQ8K* la = (const ActQ8K*)lds;
-    float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8K) / 16));  // [task][m][9]
     const int row0 = blockIdx.x * R;
     const int rows = min(R, n - row0);
     const int tasks = rows * nb;
+    const int TS = (tasks + 31) & ~31;  // product slots: whole rounds of 32 tasks
+    float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8K) / 16));  // [m][TS][9]
     const int lane = threadIdx.x & 63, l = lane & 7, grp = threadIdx.x >> 3;
-    const uint4* hb = hdr + (int64_t)row0 * nb;
-    const uint4* qb = qs + (int64_t)row0 * nb * 8 + l;
+    const uint32_t blk0 = (uint32_t)row0 * (uint32_t)nb;
+    const char* qbase = (const char*)qs + (l << 4);
+    const char* hbase = (const char*)hdr;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8K) / 16);
     uint4 av[kActPer];
     act_fetch(av, act, act_u4);
     uint4 q[kTmax], h[kTmax];
 #pragma unroll
     for (int u = 0; u < kTmax; ++u) {
-        const int t = min(u * 32 + grp, tasks - 1);
-        q[u] = qb[(int64_t)t * 8];
-        h[u] = hb[t];
+        const uint32_t blk = blk0 + (uint32_t)min(u * 32 + grp, tasks - 1);
+        q[u] = *(const uint4*)(qbase + (blk << 7));
+        h[u] = *(const uint4*)(hbase + (blk << 4));
     }
     act_store(av, lds, act, act_u4);
     __syncthreads();
+    // Block index of task u*32 + grp: grp mod nb, stepped by 32 mod nb each round.
+    // Tasks past the end (last round) compute on clamped loads into their own spare
+    // slots, which the epilogue never reads.
+    const uint32_t step = 32u % (uint32_t)nb;
+    uint32_t b = (uint32_t)grp % (uint32_t)nb;
 #pragma unroll
     for (int u = 0; u < kTmax; ++u) {
-        const int t_raw = u * 32 + grp;
         if (u * 32 >= tasks) break;  // uniform: no group has a task in this round
-        const int t = min(t_raw, tasks - 1);
-        const int b = t % nb;
         const uint32_t sc_lo = h[u].y & 0x3F3F3F3Fu;
         const uint32_t sc_hi = (h[u].w & 0x0F0F0F0Fu) | (((h[u].y >> 6) & 0x03030303u) << 4);
         const uint32_t mn_lo = h[u].z & 0x3F3F3F3Fu;
@@ -275,11 +279,10 @@ __global__ __launch_bounds__(256) void k_gemv2_q4k(const uint4* __restrict__ hdr
             sc[4 + j] = (int)((sc_hi >> (8 * j)) & 0xFF);
         }
         const float dw = h2f(h[u].x & 0xFFFF), dminw = h2f(h[u].x >> 16);
-        const bool valid = t_raw < tasks;
 #pragma unroll
         for (int r = 0; r < MMAX; ++r) {
             if (r < m) {
-                const ActQ8K& a = la[r * nb + b];
+                const ActQ8K& a = la[r * nb + (int)b];
                 const uint4 A0 = ((const uint4*)a.qs)[2 * l];
                 const uint4 A1 = ((const uint4*)a.qs)[2 * l + 1];
                 const int Aj[8] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w,
@@ -289,15 +292,13 @@ __global__ __launch_bounds__(256) void k_gemv2_q4k(const uint4* __restrict__ hdr
                 for (int j = 0; j < 8; ++j) aux += __mul24(__builtin_amdgcn_sdot4((int)w4[j], Aj[j], 0, false), sc[j]);
                 const int sumi = sum8_i32(__mul24(ml, a.bs2[l]));
                 const float ad = a.d;
-                const float pl = (dw * ad) * (float)aux;
-                const float pm = (dminw * ad) * (float)sumi;
-                if (valid) {
-                    float* p = pr + ((size_t)t * m + r) * 9;
-                    p[l] = pl;
-                    if (l == 0) p[8] = pm;
-                }
+                float* p = pr + (r * TS + u * 32 + grp) * 9;
+                p[l] = (dw * ad) * (float)aux;
+                p[8] = (dminw * ad) * (float)sumi;  // same value from all eight lanes
             }
         }
+        b += step;
+        b = min(b, b - (uint32_t)nb);  // unsigned: subtracts nb only when b >= nb
     }
     __syncthreads();
     // epilogue: thread (row r, lane class l) folds its chain in block order
@@ -306,10 +307,10 @@ __global__ __launch_bounds__(256) void k_gemv2_q4k(const uint4* __restrict__ hdr
     for (int rr = 0; rr < m; ++rr) {
         float sl = 0.0f, sf = 0.0f;
         if (act_row) {
-            const float* p = pr + ((size_t)r * nb * m + rr) * 9;
-            for (int b = 0; b < nb; ++b) sl += p[(size_t)b * m * 9 + l];
+            const float* p = pr + (rr * TS + r * nb) * 9;
+            for (int b = 0; b < nb; ++b) sl += p[b * 9 + l];
             if (l == 0)
-                for (int b = 0; b < nb; ++b) sf -= p[(size_t)b * m * 9 + 8];
+                for (int b = 0; b < nb; ++b) sf -= p[b * 9 + 8];
         }
         float tot = -0.0f;
 #pragma unroll
@@ -331,12 +332,13 @@ __global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ 
                                                    const float* res, int64_t ldr) {
     extern __shared__ uint4 lds[];
     const ActQ8_0* la = (const ActQ8_0*)lds;
-    float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8_0) / 16));  // [task][m]
     const int row0 = blockIdx.x * R;
     const int rows = min(R, n - row0);
     const int tasks = rows * nb;
     // Q8_0: a lane pair per task (16 bytes each); Q4_0: one lane per task.
     constexpr int LPT = Q4 ? 1 : 2, TPI = 256 / LPT, QU4 = Q4 ? 1 : 2;
+    const int TS = (tasks + TPI - 1) / TPI * TPI;  // product slots: whole rounds
+    float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8_0) / 16));  // [m][TS]
     const int half = Q4 ? 0 : (threadIdx.x & 1);
     const int slot = threadIdx.x / LPT;
     const int64_t base = (int64_t)row0 * nb;
@@ -353,17 +355,17 @@ __global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ 
     }
     act_store(av, lds, act, act_u4);
     __syncthreads();
+    // Block index of task u*TPI + slot, stepped by TPI mod nb each round; tasks past the
+    // end write spare slots that the epilogue never reads.
+    const uint32_t step = (uint32_t)TPI % (uint32_t)nb;
+    uint32_t b = (uint32_t)slot % (uint32_t)nb;
 #pragma unroll
     for (int u = 0; u < kTmax; ++u) {
         if (u * TPI >= tasks) break;
-        const int t_raw = u * TPI + slot;
-        const bool valid = t_raw < tasks;
-        const int t = min(t_raw, tasks - 1);
-        const int b = t % nb;
 #pragma unroll
         for (int r = 0; r < MMAX; ++r) {
             if (r < m) {
-                const ActQ8_0& a = la[r * nb + b];
+                const ActQ8_0& a = la[r * nb + (int)b];
                 int isum;
                 if (Q4) {
                     const uint4 A0 = ((const uint4*)a.qs)[0], A1 = ((const uint4*)a.qs)[1];
@@ -384,17 +386,19 @@ __global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ 
                     s = __builtin_amdgcn_sdot4((int)w[u].w, (int)A.w, s, false);
                     isum = s + dpp_xor1(s);
                 }
-                const float tv = ((float)isum * dw[u]) * a.d;
-                if (valid && half == 0) pr[(size_t)t * m + r] = tv;
+                // Q8_0: both lanes of the pair hold the full isum and write the same value
+                pr[r * TS + u * TPI + slot] = ((float)isum * dw[u]) * a.d;
             }
         }
+        b += step;
+        b = min(b, b - (uint32_t)nb);  // unsigned: subtracts nb only when b >= nb
     }
     __syncthreads();
     for (int i = threadIdx.x; i < rows * m; i += 256) {
         const int r = i / m, rr = i - r * m;
-        const float* p = pr + (size_t)r * nb * m + rr;
+        const float* p = pr + rr * TS + r * nb;
         float sumf = 0.0f;
-        for (int b = 0; b < nb; ++b) sumf += p[(size_t)b * m];
+        for (int b = 0; b < nb; ++b) sumf += p[b];
         const int row = row0 + r;
         if (bias) sumf = sumf + bias[row];
         if (res) sumf = res[(int64_t)rr * ldr + row] + sumf;
@@ -402,8 +406,8 @@ __global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ 
     }
 }
 
-// Rows per workgroup: the largest power of two <= 32 that keeps each lane group at
-// <= kTmax tasks, leaves >= SXQ_GEMV_MIN_WG workgroups (default 640) and fits LDS.
+size_t gemv2_lds(int nb, int m, int R, int dtype);
+
 // Rows per workgroup: spread the rows over about SXQ_GEMV_WG (default 1024 = four
 // resident 256-thread workgroups on each of the 256 CUs) workgroups, so the whole grid
 // runs in one wave of workgroups with no tail; capped so every lane group holds at
@@ -413,20 +417,20 @@ int gemv2_rows(int n, int nb, int m, int dtype) {
         const char* e = getenv("SXQ_GEMV_WG");
         return e ? atoi(e) : 1024;
     }();
-    const size_t ab = act_block_bytes(vec_dot_type(dtype));
-    const size_t per_task = dtype == kQ4K ? 36 : 4;
     const int slots = dtype == kQ4K ? 32 : (dtype == kQ8_0 ? 128 : 256);
     int R = (n + target_wg - 1) / target_wg;
     R = min(R, 32);
     R = min(R, max(1, slots * kTmax / nb));
-    while (R > 1 && (size_t)m * nb * ab + (size_t)R * nb * m * per_task > 60 * 1024) --R;
+    while (R > 1 && gemv2_lds(nb, m, R, dtype) > 60 * 1024) --R;
     return max(R, 1);
 }
 
 size_t gemv2_lds(int nb, int m, int R, int dtype) {
     const size_t ab = act_block_bytes(vec_dot_type(dtype));
     const size_t per_task = dtype == kQ4K ? 36 : 4;
-    return (size_t)m * nb * ab + (size_t)R * nb * m * per_task;
+    const int tpi = dtype == kQ4K ? 32 : (dtype == kQ8_0 ? 128 : 256);  // tasks per round
+    const size_t slots = ((size_t)R * nb + tpi - 1) / tpi * tpi;
+    return (size_t)m * nb * ab + slots * m * per_task;
 }
 
 // Whether the task-split kernel covers this shape (one row's tasks within kTmax rounds).

@@ -117,6 +117,12 @@ CASES = [
     (G.Q4K, 1003, 2560, 5),    # n not a multiple of the 8-row group
     (G.Q4K, 9728, 2560, 17),   # two 16-row slabs
     (G.Q8_0, 2560, 9728, 4),   # Q8_0 at the Qwen3-4B shape
+    # >= 16384 rows: the row-streaming Q4_K kernel; 16389 leaves a partial last row set
+    (G.Q4K, 16389, 1024, 1),
+    (G.Q4K, 16389, 1024, 2),
+    (G.Q4K, 16389, 512, 3),
+    (G.Q4K, 16384, 9728, 4),   # nb = 38: each wave's rounds span several row sets
+    (G.Q4K, 19456, 2560, 1),   # Qwen3-4B fused w1|w3
 ]
 
 
@@ -143,6 +149,18 @@ def test_bias_batch_shape_and_host_pointers(cuda, ora):
     want = (ora.matmul(ora.Q8_0, x.reshape(6, k), blocks) + b[None, :]).astype(np.float32)  # f32 bias add
     _eq_bits(y.reshape(6, n), want)
     _eq_bits(qmatmul_host(qmm, x, b).reshape(6, n), want)
+
+
+def test_bias_on_tall_q4k(cuda, ora):
+    # bias epilogue of the row-streaming kernel, rows not a multiple of 8
+    n, k = 16395, 512
+    w = _weights(n, k, 31)
+    b = (np.random.default_rng(32).standard_normal(n) * 0.02).astype(np.float32)
+    x = _acts(2, k, 33)
+    blocks = ora.quantize(ora.Q4K, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    y = qmm.forward(torch.from_numpy(x).to(cuda), bias=torch.from_numpy(b).to(cuda)).cpu().numpy()
+    _eq_bits(y, (ora.matmul(ora.Q4K, x, blocks) + b[None, :]).astype(np.float32))
 
 
 def test_export_and_dequantize_round_trip(cuda, ora):
