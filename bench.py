@@ -15,7 +15,13 @@ launch over the average launch duration, against 8 TB/s.  `cpu_baseline` times t
 oracle (the CPU restatement of Candle's quantized matmul) on one layer's projections
 plus the head, on this host's cores, and scales it to one token's GEMV work.
 
+`roofline.traffic` is the HBM bytes per GEMV launch that rocprofv3's FETCH_SIZE and
+WRITE_SIZE counters report for the same GEMV pass (read from the committed summary
+under profiles/, whose header gives the commands and the copy-kernel scale factor).
+
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtype q4k|q8_0]
+       python bench.py --mode gemv [--gemv-iters N]   (GEMV pass only, for counter runs)
+       python bench.py --mode copy                     (plain 1 GiB device copy, the counter scale)
 """
 from __future__ import annotations
 
@@ -41,7 +47,25 @@ def parse():
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--gemv-iters", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--mode", default="decode", choices=["decode", "gemv", "copy"],
+                    help="decode: the benchmark; gemv: only the per-token GEMV pass (for counter runs); "
+                         "copy: a plain device copy of known size (the counter scale)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv2_q4k_qwen3_4b_decode_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed counter summary (None if absent)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def gemv_roofline(lm, torch, iters):
@@ -72,15 +96,31 @@ def gemv_roofline(lm, torch, iters):
     ms = e0.elapsed_time(e1) / iters
     avg_us = ms * 1000.0 / n_launch
     achieved = algo / (ms * 1e-3) / 1e9
+    traffic = measured_traffic() if c.weight_dtype == 12 else None
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemv_q4k" if c.weight_dtype == 12 else "k_gemv_q80",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None if traffic is None else round(traffic),
+            "algorithmic_bytes_per_launch": round(algo / n_launch),
+            "kernel": "k_gemv2_q4k" if c.weight_dtype == 12 else "k_gemv2_q80",
             "bytes_per_token": algo, "launches_per_token": n_launch, "avg_launch_us": round(avg_us, 3),
             "gemv_us_per_token": round(ms * 1000.0, 2)}
 
 
-def cpu_baseline(lm, torch):
-    """Oracle (CPU port of Candle's quantized matmul) on one layer + the head, all cores."""
+def cpu_threads():
+    """The host cores this process may use, capped at 16 (one GPU's share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline(lm, torch, budget_s=12.0):
+    """Oracle (CPU port of Candle's quantized matmul) on whole tokens' GEMV work.
+
+    One token = the four projections 36 times (layer 0's weights stand in for every
+    layer: 57 MB per layer, far beyond the host caches) + the head; tokens are run until
+    `budget_s` seconds have passed (at least one)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle  # the checker / CPU baseline
@@ -98,32 +138,45 @@ def cpu_baseline(lm, torch):
         blocks.append((k, QTensor.quantize(w, dt).data().cpu().numpy().reshape(n, -1)))
         del w
     xs = {k: rng.standard_normal((1, k)).astype(np.float32) for k, _ in blocks}
-    threads = os.cpu_count() or 1
-    t_layer = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        for k, b in blocks[:4]:
-            oracle.matmul(int(dt), xs[k], b, threads=threads)
-        t_layer.append(time.perf_counter() - t0)
+    threads = cpu_threads()
+    tokens = 0
     t0 = time.perf_counter()
-    k, b = blocks[4]
-    oracle.matmul(int(dt), xs[k], b, threads=threads)
-    t_head = time.perf_counter() - t0
-    per_token = c.n_layers * min(t_layer) + t_head
-    return {"value": round(1.0 / per_token, 3), "unit": "tok/s (GEMV share of a token)", "cores": threads,
+    while tokens == 0 or time.perf_counter() - t0 < budget_s:
+        for _ in range(c.n_layers):
+            for k, b in blocks[:4]:
+                oracle.matmul(int(dt), xs[k], b, threads=threads)
+        k, b = blocks[4]
+        oracle.matmul(int(dt), xs[k], b, threads=threads)
+        tokens += 1
+    total = time.perf_counter() - t0
+    return {"value": round(tokens / total, 3), "unit": "tok/s (GEMV share of a token)", "cores": threads,
             "kind": "port",
-            "sample": f"oracle k_quants::matmul (generic vec-dot, {threads} threads) over layer-0's four "
-                      f"projections x3 and the head once; token = {c.n_layers} x layer + head "
-                      f"= {per_token * 1000:.0f} ms"}
+            "sample": f"{tokens} tokens of GEMV work ({c.n_layers} x layer-0's four projections + the head, "
+                      f"batch 1) through the oracle's k_quants::matmul (generic vec-dot, {threads} threads) "
+                      f"in {total:.1f} s"}
+
+
+def copy_calibration(torch, iters=8):
+    """A plain device-to-device copy of 1 GiB: its counters give the FETCH/WRITE scale."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "copy", "bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": iters}))
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard by "
-              "output rows, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the GEMVs would shard "
+              "by output rows, one shard per GPU)", file=sys.stderr)
         sys.exit(2)
     import torch
+    if args.mode == "copy":
+        copy_calibration(torch)
+        return
     from syrinx_amd import GgmlDType
     from syrinx_amd import decoder as D
 
@@ -136,6 +189,10 @@ def main():
     lm.init_random(seed=0, std=0.02)
     lm.kv_fill_random([args.kv] * args.batch, seed=1)
     print(f"[bench] model ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    if args.mode == "gemv":
+        roof = gemv_roofline(lm, torch, args.gemv_iters)
+        print(json.dumps({"mode": "gemv", "passes": args.gemv_iters + 2, "roofline": roof}))
+        return
     rng_frame = torch.zeros((args.batch, 1 + cfg.n_codebooks), dtype=torch.int32)
     rng_frame[:, 0] = 151700
     rng_frame[:, 1:] = torch.arange(cfg.n_codebooks, dtype=torch.int32) * 37 % 4096
