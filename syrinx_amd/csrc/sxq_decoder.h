@@ -23,8 +23,12 @@ hipError_t launch_embed_quant_table(const int* ids, int ids_per, int B, const QW
                                     int n_cb, int cb_size, int sem_begin, int sem_end, float* h, hipStream_t s);
 hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
                               hipStream_t s);
-hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, hipStream_t s);
-hipError_t launch_advance(int* len, int B, hipStream_t s);
+// Greedy argmax per stream; with `len` also advances each stream's cached length.
+// pval/pidx: [B * kArgmaxSlices] partials; counter: [B], zero before the first call
+// (each call leaves it zero again).
+constexpr int kArgmaxSlices = 64;
+hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, int* len,
+                         float* pval, int* pidx, unsigned* counter, hipStream_t s);
 hipError_t launch_fill_value(float* y, int64_t n, float v, hipStream_t s);
 
 }  // namespace sxq

@@ -42,44 +42,43 @@ SXQ_DEV void quantize_chunk(const float* vals, int c, int dim, int lane, uint8_t
 
 // ---------------------------------------------------------------------------- RMSNorm
 // y = (x / sqrt(sum(x*x) * inv_n + eps)) * w  over each row; then quantized.  The sum
-// is a tree here and sequential in Candle's CPU loop: results agree to rounding.
-// grid (rows, ceil(dim/256)): every workgroup reduces the whole row (an L2-resident
-// read) and then normalises and quantizes only its own 256-element chunk.
+// is a fixed-order tree here (rmsnorm_sumsq_1024) and sequential in Candle's CPU loop:
+// results agree to rounding.  grid (rows, ceil(dim/256)), 1024 threads: every
+// workgroup reduces the whole row (an L2-resident read) and then its first wave
+// normalises and quantizes the workgroup's own 256-element chunk.
 template <int VDT>
-__global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ h, int dim, const float* __restrict__ w,
-                                                       float inv_n, float eps, uint8_t* __restrict__ act,
-                                                       float* __restrict__ normed) {
-    __shared__ float xs[256];
-    __shared__ float red[4];
+__global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float* __restrict__ h, int dim, const float* __restrict__ w,
+                                                        float inv_n, float eps, uint8_t* __restrict__ act,
+                                                        float* __restrict__ normed) {
+    __shared__ float red[16];
     const int row = blockIdx.x, c = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float* x = h + (int64_t)row * dim;
     float ss = 0.0f;
-    for (int i = 4 * threadIdx.x; i < dim; i += 1024) {  // dim is a multiple of 32
-        const float4 v = *(const float4*)(x + i);
+    for (int i = threadIdx.x; i < dim / 4; i += 1024) {  // dim is a multiple of 32
+        const float4 v = ((const float4*)x)[i];
         ss += v.x * v.x;
         ss += v.y * v.y;
         ss += v.z * v.z;
         ss += v.w * v.w;
     }
-    ss = wave_sum_f32(ss);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    ss = rmsnorm_sumsq_1024(ss, red);
     const float var = ss * inv_n + 0.0f;
     const float den = sqrtf(var * 1.0f + eps);
-    const int e = c * 256 + threadIdx.x;
-    float v = 0.0f;
-    if (e < dim) {
-        v = (x[e] / den) * w[e];
-        if (normed) normed[(int64_t)row * dim + e] = v;
+    if (wave != 0) return;
+    const int e0 = c * 256 + 4 * lane;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e0 < dim) {
+        const float4 xv = *(const float4*)(x + e0), wv = *(const float4*)(w + e0);
+        v.x = (xv.x / den) * wv.x;
+        v.y = (xv.y / den) * wv.y;
+        v.z = (xv.z / den) * wv.z;
+        v.w = (xv.w / den) * wv.w;
+        if (normed) *(float4*)(normed + (int64_t)row * dim + e0) = v;
     }
-    xs[threadIdx.x] = v;
-    __syncthreads();
-    if (wave == 0) {
-        const int nb = VDT == kQ8K ? dim / 256 : dim / 32;
-        uint8_t* arow = act + (int64_t)row * nb * act_block_bytes(VDT);
-        quantize_chunk<VDT>(xs, c, dim, lane, arow);
-    }
+    const int nb = VDT == kQ8K ? dim / 256 : dim / 32;
+    uint8_t* arow = act + (int64_t)row * nb * act_block_bytes(VDT);
+    if (VDT == kQ8K) wave_quantize_q8k<false>(v, lane, arow + (size_t)c * sizeof(ActQ8K));
+    else wave_quantize_q8_0<false>(v, lane, c * 8 + (lane >> 3) < nb, arow + (size_t)c * 8 * sizeof(ActQ8_0));
 }
 
 // ---------------------------------------------------- QK-RMSNorm + RoPE + KV-cache append
@@ -361,7 +360,8 @@ __global__ __launch_bounds__(256) void k_embed_quant_table(const int* __restrict
     const int tok = fr[0];
     const bool tok_ok = tok >= 0 && (int64_t)tok < w.n;
     const bool sem = tok >= sem_begin && tok <= sem_end;
-    for (int e = threadIdx.x; e < dim; e += 256) {
+    const int e = blockIdx.y * 256 + threadIdx.x;  // grid (B, ceil(dim / 256))
+    if (e < dim) {
         float x = tok_ok ? weight_elem(w, tok, e) : 0.0f;
         if (n_cb > 0) {
             float vq = 0.0f;
@@ -382,42 +382,62 @@ __global__ __launch_bounds__(256) void k_embed_dense(const int* __restrict__ ids
     const int s = blockIdx.x;
     const int tok = ids[(int64_t)s * ids_per];
     const bool ok = tok >= 0 && tok < rows;
-    for (int e = threadIdx.x; e < dim; e += 256) h[(int64_t)s * dim + e] = ok ? table[(int64_t)tok * dim + e] : 0.0f;
+    const int e = blockIdx.y * 256 + threadIdx.x;  // grid (B, ceil(dim / 256))
+    if (e < dim) h[(int64_t)s * dim + e] = ok ? table[(int64_t)tok * dim + e] : 0.0f;
 }
 
 // ------------------------------------------------------------------------ argmax / length
 // First index of the largest logit (NaN never wins); written to ids[s * ids_per].
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ logits, int vocab, int* __restrict__ ids,
-                                                 int ids_per, int* __restrict__ out_ids) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// grid (B, kArgmaxSlices): workgroup b reduces slice b of the row and publishes
+// (value, index); the last workgroup of a stream to finish (a per-stream counter) folds
+// the partials in slice order -- so ties keep the first index -- writes the id, bumps
+// the stream's cached length (the step is complete) and resets the counter for the
+// next step.
+SXQ_DEV void argmax_merge(float& best, int& idx, float ov, int oi) {
+    if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
+}
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits, int vocab, int* __restrict__ ids,
+                                                int ids_per, int* __restrict__ out_ids, int* __restrict__ len,
+                                                float* __restrict__ pval, int* __restrict__ pidx,
+                                                unsigned* __restrict__ counter) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    __shared__ bool last;
+    const int s = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slice = (vocab + kArgmaxSlices - 1) / kArgmaxSlices;
+    const int lo = b * slice, hi = min(vocab, lo + slice);
     const float* x = logits + (int64_t)s * vocab;
     float best = -INFINITY;
     int idx = 0x7FFFFFFF;
-    for (int i = tid; i < vocab; i += 1024) {
+    for (int i = lo + tid; i < hi; i += 256) {
         const float v = x[i];
         if (v > best) { best = v; idx = i; }  // per-thread indices rise: first max kept
     }
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(idx, o, 64);
-        if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
-    }
+    for (int o = 32; o >= 1; o >>= 1) argmax_merge(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
     if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 16; ++w)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
-        if (idx == 0x7FFFFFFF) idx = 0;
-        ids[(int64_t)s * ids_per] = idx;
-        if (out_ids) out_ids[s] = idx;
+        for (int w = 1; w < 4; ++w) argmax_merge(best, idx, bv[w], bi[w]);
+        pval[s * kArgmaxSlices + b] = best;
+        pidx[s * kArgmaxSlices + b] = idx;
+        __threadfence();  // publish the partial before counting it
+        last = atomicAdd(&counter[s], 1u) == kArgmaxSlices - 1;
     }
-}
-
-__global__ void k_advance(int* __restrict__ len, int B) {
-    const int s = threadIdx.x;
-    if (s < B) len[s] += 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();  // see every other workgroup's partial
+    if (wave == 0) {
+        best = __builtin_nontemporal_load(&pval[s * kArgmaxSlices + lane]);
+        idx = __builtin_nontemporal_load(&pidx[s * kArgmaxSlices + lane]);
+        for (int o = 32; o >= 1; o >>= 1) argmax_merge(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
+        if (lane == 0) {
+            if (idx == 0x7FFFFFFF) idx = 0;
+            ids[(int64_t)s * ids_per] = idx;
+            if (out_ids) out_ids[s] = idx;
+            if (len) len[s] += 1;
+            counter[s] = 0u;
+        }
+    }
 }
 
 __global__ void k_fill_value(float* __restrict__ y, int64_t n, float v) {
@@ -430,8 +450,8 @@ hipError_t launch_rmsnorm_quant(int vdt, const float* h, int rows, int dim, cons
                                 float* normed, hipStream_t s) {
     const float inv_n = (float)(1.0 / (double)dim);
     const dim3 grid(rows, (dim + 255) / 256);
-    if (vdt == kQ8K) hipLaunchKernelGGL((k_rmsnorm_quant<kQ8K>), grid, dim3(256), 0, s, h, dim, w, inv_n, eps, act, normed);
-    else hipLaunchKernelGGL((k_rmsnorm_quant<kQ8_0>), grid, dim3(256), 0, s, h, dim, w, inv_n, eps, act, normed);
+    if (vdt == kQ8K) hipLaunchKernelGGL((k_rmsnorm_quant<kQ8K>), grid, dim3(1024), 0, s, h, dim, w, inv_n, eps, act, normed);
+    else hipLaunchKernelGGL((k_rmsnorm_quant<kQ8_0>), grid, dim3(1024), 0, s, h, dim, w, inv_n, eps, act, normed);
     return hipGetLastError();
 }
 
@@ -474,24 +494,21 @@ hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t
 hipError_t launch_embed_quant_table(const int* ids, int ids_per, int B, const QWeight& w, int dim, const float* cb,
                                     int n_cb, int cb_size, int sem_begin, int sem_end, float* h, hipStream_t s) {
     const float inv_scale = 1.0f / sqrtf((float)n_cb + 1.0f);
-    hipLaunchKernelGGL(k_embed_quant_table, dim3(B), dim3(256), 0, s, ids, ids_per, w, dim, cb, n_cb, cb_size, sem_begin,
-                       sem_end, inv_scale, h);
+    hipLaunchKernelGGL(k_embed_quant_table, dim3(B, (dim + 255) / 256), dim3(256), 0, s, ids, ids_per, w, dim, cb, n_cb,
+                       cb_size, sem_begin, sem_end, inv_scale, h);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
                               hipStream_t s) {
-    hipLaunchKernelGGL(k_embed_dense, dim3(B), dim3(256), 0, s, ids, ids_per, table, rows, dim, h);
+    hipLaunchKernelGGL(k_embed_dense, dim3(B, (dim + 255) / 256), dim3(256), 0, s, ids, ids_per, table, rows, dim, h);
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3(B), dim3(1024), 0, s, logits, vocab, ids, ids_per, out_ids);
-    return hipGetLastError();
-}
-
-hipError_t launch_advance(int* len, int B, hipStream_t s) {
-    hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, len, B);
+hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, int* len,
+                         float* pval, int* pidx, unsigned* counter, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(B, kArgmaxSlices), dim3(256), 0, s, logits, vocab, ids, ids_per, out_ids, len,
+                       pval, pidx, counter);
     return hipGetLastError();
 }
 

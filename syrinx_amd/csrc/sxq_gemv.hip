@@ -17,7 +17,9 @@
 // workgroup (in K chunks when m * K does not fit).
 #include <stdlib.h>
 
+#include "sxq_decoder.h"
 #include "sxq_kernels.h"
+#include "sxq_quant_dev.h"
 
 namespace sxq {
 
@@ -212,58 +214,117 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_q80(const uint16_t* __restr
 constexpr int kTmax = 8;
 
 // Activation staging in two halves so the caller can put its weight loads between
-// them: act_fetch issues a thread's first kActPer 16-byte loads (clamped, so all are
+// them: act_fetch issues a thread's first 16-byte loads (clamped, so all are
 // unconditional and in flight together); act_store writes them to LDS and copies any
-// remainder (only when m * nb blocks exceed 256 * kActPer uint4).
-constexpr int kActPer = 4;
-SXQ_DEV void act_fetch(uint4 (&v)[kActPer], const uint8_t* __restrict__ act, int total_u4) {
+// remainder (only when m * nb blocks exceed 1024 uint4 = 16 KB).
+template <int NT>
+struct Stage {
+    static constexpr int kPer = 1024 / NT;
+};
+template <int NT>
+SXQ_DEV void act_fetch(uint4 (&v)[Stage<NT>::kPer], const uint8_t* __restrict__ act, int total_u4) {
 #pragma unroll
-    for (int k = 0; k < kActPer; ++k) v[k] = ((const uint4*)act)[min(k * 256 + (int)threadIdx.x, total_u4 - 1)];
+    for (int k = 0; k < Stage<NT>::kPer; ++k) v[k] = ((const uint4*)act)[min(k * NT + (int)threadIdx.x, total_u4 - 1)];
     __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
 }
-SXQ_DEV void act_store(const uint4 (&v)[kActPer], uint4* lds, const uint8_t* __restrict__ act, int total_u4) {
+template <int NT>
+SXQ_DEV void act_store(const uint4 (&v)[Stage<NT>::kPer], uint4* lds, const uint8_t* __restrict__ act, int total_u4) {
     // clamped like the loads: out-of-range threads rewrite the last element with its own value
 #pragma unroll
-    for (int k = 0; k < kActPer; ++k) lds[min(k * 256 + (int)threadIdx.x, total_u4 - 1)] = v[k];
-    for (int i = kActPer * 256 + threadIdx.x; i < total_u4; i += 256) lds[i] = ((const uint4*)act)[i];
+    for (int k = 0; k < Stage<NT>::kPer; ++k) lds[min(k * NT + (int)threadIdx.x, total_u4 - 1)] = v[k];
+    for (int i = Stage<NT>::kPer * NT + threadIdx.x; i < total_u4; i += NT) lds[i] = ((const uint4*)act)[i];
 }
 
-template <int MMAX>
-__global__ __launch_bounds__(256) void k_gemv2_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, int n,
-                                                   int nb, const uint8_t* __restrict__ act, int m, int R, float* y,
-                                                   int64_t ldy, const float* __restrict__ bias, const float* res,
-                                                   int64_t ldr) {
+// RMSNorm + activation quantization as the prologue of a 1024-thread GEMV (one row of
+// dim <= 4096): thread t holds float4 t of the row and of the norm weight, i.e. lane
+// t%64's share of 256-element chunk t/64, so wave w normalises and quantizes chunk w
+// straight from registers into the LDS activation blocks.  The row's sum of squares is
+// rmsnorm_sumsq_1024 -- the same function and order as k_rmsnorm_quant -- so both paths
+// produce the same bits.
+SXQ_DEV void norm_fetch(float4& xv, float4& wv, const NormIn& ni, int dim) {
+    const int i = min((int)threadIdx.x, dim / 4 - 1);  // clamped: every load in bounds
+    xv = ((const float4*)ni.x)[i];
+    wv = ((const float4*)ni.w)[i];
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
+}
+template <int VDT>
+SXQ_DEV void norm_quant_store(const float4& xv, const float4& wv, const NormIn& ni, int dim, uint8_t* lds_act,
+                              float* red) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool mine = tid < dim / 4;
+    float ss = 0.0f;
+    if (mine) {
+        ss += xv.x * xv.x;
+        ss += xv.y * xv.y;
+        ss += xv.z * xv.z;
+        ss += xv.w * xv.w;
+    }
+    ss = rmsnorm_sumsq_1024(ss, red);
+    const float var = ss * (float)(1.0 / (double)dim) + 0.0f;
+    const float den = sqrtf(var * 1.0f + ni.eps);
+    const int nchunks = (dim + 255) / 256;
+    if (wave >= nchunks) return;  // uniform per wave
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (mine) {
+        v.x = (xv.x / den) * wv.x;
+        v.y = (xv.y / den) * wv.y;
+        v.z = (xv.z / den) * wv.z;
+        v.w = (xv.w / den) * wv.w;
+        if (ni.normed && blockIdx.x == 0) ((float4*)ni.normed)[tid] = v;
+    }
+    if (VDT == kQ8K) {
+        wave_quantize_q8k<false>(v, lane, lds_act + (size_t)wave * sizeof(ActQ8K));
+    } else {
+        wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < dim / 32, lds_act + (size_t)wave * 8 * sizeof(ActQ8_0));
+    }
+}
+
+// Q4_K task-split GEMV, NT threads (256 or 1024) per workgroup: NT/8 eight-lane groups.
+template <int MMAX, bool NORM, int NT>
+__global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, int n,
+                                                  int nb, const uint8_t* __restrict__ act, int m, int R, float* y,
+                                                  int64_t ldy, const float* __restrict__ bias, const float* res,
+                                                  int64_t ldr, NormIn ni) {
+    static_assert(!NORM || (NT == 1024 && MMAX == 1), "the fused RMSNorm prologue is for one row, 1024 threads");
+    constexpr int SLOTS = NT / 8;  // eight-lane groups = tasks per round
     extern __shared__ uint4 lds[];
     const ActQ8K* la = (const ActQ8K*)lds;
     const int row0 = blockIdx.x * R;
     const int rows = min(R, n - row0);
     const int tasks = rows * nb;
-    const int TS = (tasks + 31) & ~31;  // product slots: whole rounds of 32 tasks
+    const int TS = (tasks + SLOTS - 1) / SLOTS * SLOTS;  // product slots: whole rounds
     float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8K) / 16));  // [m][TS][9]
     const int lane = threadIdx.x & 63, l = lane & 7, grp = threadIdx.x >> 3;
     const uint32_t blk0 = (uint32_t)row0 * (uint32_t)nb;
     const char* qbase = (const char*)qs + (l << 4);
     const char* hbase = (const char*)hdr;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8K) / 16);
-    uint4 av[kActPer];
-    act_fetch(av, act, act_u4);
+    uint4 av[Stage<NT>::kPer];
+    float4 xv, wv;
+    if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 256);
+    else act_fetch<NT>(av, act, act_u4);
     uint4 q[kTmax], h[kTmax];
 #pragma unroll
     for (int u = 0; u < kTmax; ++u) {
-        const uint32_t blk = blk0 + (uint32_t)min(u * 32 + grp, tasks - 1);
+        const uint32_t blk = blk0 + (uint32_t)min(u * SLOTS + grp, tasks - 1);
         q[u] = *(const uint4*)(qbase + (blk << 7));
         h[u] = *(const uint4*)(hbase + (blk << 4));
     }
-    act_store(av, lds, act, act_u4);
+    if constexpr (NORM) {
+        __shared__ float red[16];
+        norm_quant_store<kQ8K>(xv, wv, ni, nb * 256, (uint8_t*)lds, red);
+    } else {
+        act_store<NT>(av, lds, act, act_u4);
+    }
     __syncthreads();
-    // Block index of task u*32 + grp: grp mod nb, stepped by 32 mod nb each round.
+    // Block index of task u*SLOTS + grp: grp mod nb, stepped by SLOTS mod nb each round.
     // Tasks past the end (last round) compute on clamped loads into their own spare
     // slots, which the epilogue never reads.
-    const uint32_t step = 32u % (uint32_t)nb;
+    const uint32_t step = (uint32_t)SLOTS % (uint32_t)nb;
     uint32_t b = (uint32_t)grp % (uint32_t)nb;
 #pragma unroll
     for (int u = 0; u < kTmax; ++u) {
-        if (u * 32 >= tasks) break;  // uniform: no group has a task in this round
+        if (u * SLOTS >= tasks) break;  // uniform: no group has a task in this round
         const uint32_t sc_lo = h[u].y & 0x3F3F3F3Fu;
         const uint32_t sc_hi = (h[u].w & 0x0F0F0F0Fu) | (((h[u].y >> 6) & 0x03030303u) << 4);
         const uint32_t mn_lo = h[u].z & 0x3F3F3F3Fu;
@@ -292,7 +353,7 @@ __global__ __launch_bounds__(256) void k_gemv2_q4k(const uint4* __restrict__ hdr
                 for (int j = 0; j < 8; ++j) aux += __mul24(__builtin_amdgcn_sdot4((int)w4[j], Aj[j], 0, false), sc[j]);
                 const int sumi = sum8_i32(__mul24(ml, a.bs2[l]));
                 const float ad = a.d;
-                float* p = pr + (r * TS + u * 32 + grp) * 9;
+                float* p = pr + (r * TS + u * SLOTS + grp) * 9;
                 p[l] = (dw * ad) * (float)aux;
                 p[8] = (dminw * ad) * (float)sumi;  // same value from all eight lanes
             }
@@ -325,26 +386,30 @@ __global__ __launch_bounds__(256) void k_gemv2_q4k(const uint4* __restrict__ hdr
     }
 }
 
-template <int MMAX, bool Q4>
-__global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ dw16, const uint4* __restrict__ qs,
-                                                   int n, int nb, const uint8_t* __restrict__ act, int m, int R,
-                                                   float* y, int64_t ldy, const float* __restrict__ bias,
-                                                   const float* res, int64_t ldr) {
+// Q8_0 / Q4_0 task-split GEMV: a lane pair per Q8_0 task (16 bytes each), one lane per
+// Q4_0 task; NT threads per workgroup.
+template <int MMAX, bool Q4, bool NORM, int NT>
+__global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ dw16, const uint4* __restrict__ qs,
+                                                  int n, int nb, const uint8_t* __restrict__ act, int m, int R,
+                                                  float* y, int64_t ldy, const float* __restrict__ bias,
+                                                  const float* res, int64_t ldr, NormIn ni) {
+    static_assert(!NORM || (NT == 1024 && MMAX == 1), "the fused RMSNorm prologue is for one row, 1024 threads");
     extern __shared__ uint4 lds[];
     const ActQ8_0* la = (const ActQ8_0*)lds;
     const int row0 = blockIdx.x * R;
     const int rows = min(R, n - row0);
     const int tasks = rows * nb;
-    // Q8_0: a lane pair per task (16 bytes each); Q4_0: one lane per task.
-    constexpr int LPT = Q4 ? 1 : 2, TPI = 256 / LPT, QU4 = Q4 ? 1 : 2;
+    constexpr int LPT = Q4 ? 1 : 2, TPI = NT / LPT, QU4 = Q4 ? 1 : 2;
     const int TS = (tasks + TPI - 1) / TPI * TPI;  // product slots: whole rounds
     float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8_0) / 16));  // [m][TS]
     const int half = Q4 ? 0 : (threadIdx.x & 1);
     const int slot = threadIdx.x / LPT;
     const int64_t base = (int64_t)row0 * nb;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8_0) / 16);
-    uint4 av[kActPer];
-    act_fetch(av, act, act_u4);
+    uint4 av[Stage<NT>::kPer];
+    float4 xv, wv;
+    if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 32);
+    else act_fetch<NT>(av, act, act_u4);
     uint4 w[kTmax];
     float dw[kTmax];
 #pragma unroll
@@ -353,7 +418,12 @@ __global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ 
         w[u] = qs[(base + t) * QU4 + half];
         dw[u] = h2f(dw16[base + t]);
     }
-    act_store(av, lds, act, act_u4);
+    if constexpr (NORM) {
+        __shared__ float red[16];
+        norm_quant_store<kQ8_0>(xv, wv, ni, nb * 32, (uint8_t*)lds, red);
+    } else {
+        act_store<NT>(av, lds, act, act_u4);
+    }
     __syncthreads();
     // Block index of task u*TPI + slot, stepped by TPI mod nb each round; tasks past the
     // end write spare slots that the epilogue never reads.
@@ -394,7 +464,7 @@ __global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ 
         b = min(b, b - (uint32_t)nb);  // unsigned: subtracts nb only when b >= nb
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < rows * m; i += 256) {
+    for (int i = threadIdx.x; i < rows * m; i += NT) {
         const int r = i / m, rr = i - r * m;
         const float* p = pr + rr * TS + r * nb;
         float sumf = 0.0f;
@@ -406,56 +476,81 @@ __global__ __launch_bounds__(256) void k_gemv2_q80(const uint16_t* __restrict__ 
     }
 }
 
-size_t gemv2_lds(int nb, int m, int R, int dtype);
+// Task-split sizing for NT threads per workgroup.  Rows per workgroup R: spread the
+// rows over one full wave of workgroups -- 256 (one 1024-thread workgroup per CU) or
+// 1024 (four 256-thread workgroups per CU), overridable with SXQ_GEMV_WG -- capped so
+// every lane group holds at most kTmax tasks, the epilogue has a thread per (row, lane
+// class), and LDS fits in 60 KB.
+static int tasks_per_round(int dtype, int nt) { return dtype == kQ4K ? nt / 8 : (dtype == kQ8_0 ? nt / 2 : nt); }
 
-// Rows per workgroup: spread the rows over about SXQ_GEMV_WG (default 1024 = four
-// resident 256-thread workgroups on each of the 256 CUs) workgroups, so the whole grid
-// runs in one wave of workgroups with no tail; capped so every lane group holds at
-// most kTmax tasks, the epilogue has a thread per (row, lane class), and LDS fits.
-int gemv2_rows(int n, int nb, int m, int dtype) {
-    static const int target_wg = [] {
-        const char* e = getenv("SXQ_GEMV_WG");
-        return e ? atoi(e) : 1024;
-    }();
-    const int slots = dtype == kQ4K ? 32 : (dtype == kQ8_0 ? 128 : 256);
-    int R = (n + target_wg - 1) / target_wg;
-    R = min(R, 32);
-    R = min(R, max(1, slots * kTmax / nb));
-    while (R > 1 && gemv2_lds(nb, m, R, dtype) > 60 * 1024) --R;
-    return max(R, 1);
-}
-
-size_t gemv2_lds(int nb, int m, int R, int dtype) {
+size_t gemv2_lds(int nb, int m, int R, int dtype, int nt) {
     const size_t ab = act_block_bytes(vec_dot_type(dtype));
     const size_t per_task = dtype == kQ4K ? 36 : 4;
-    const int tpi = dtype == kQ4K ? 32 : (dtype == kQ8_0 ? 128 : 256);  // tasks per round
+    const int tpi = tasks_per_round(dtype, nt);
     const size_t slots = ((size_t)R * nb + tpi - 1) / tpi * tpi;
     return (size_t)m * nb * ab + slots * m * per_task;
 }
 
-// Whether the task-split kernel covers this shape (one row's tasks within kTmax rounds).
-bool gemv2_fits(int nb, int m, int dtype) {
-    const int slots = dtype == kQ4K ? 32 : (dtype == kQ8_0 ? 128 : 256);
-    return nb <= slots * kTmax && gemv2_lds(nb, m, 1, dtype) <= 60 * 1024;
+int gemv2_rows(int n, int nb, int m, int dtype, int nt) {
+    static const int env_wg = [] {
+        const char* e = getenv("SXQ_GEMV_WG");
+        return e ? atoi(e) : 0;
+    }();
+    const int target_wg = env_wg > 0 ? env_wg : (nt == 1024 ? 256 : 1024);
+    int R = (n + target_wg - 1) / target_wg;
+    R = min(R, nt / 8);
+    R = min(R, max(1, tasks_per_round(dtype, nt) * kTmax / nb));
+    while (R > 1 && gemv2_lds(nb, m, R, dtype, nt) > 60 * 1024) --R;
+    return max(R, 1);
+}
+
+// Whether the task-split kernel with NT threads covers this shape: one row's tasks
+// within kTmax rounds and LDS within 60 KB; for NT = 1024 also no more workgroups than
+// the one-per-CU target (otherwise the 256-thread kernel is the better fit).
+bool gemv2_fits(int n, int nb, int m, int dtype, int nt) {
+    if (nb > tasks_per_round(dtype, nt) * kTmax || gemv2_lds(nb, m, 1, dtype, nt) > 60 * 1024) return false;
+    if (nt == 256) return true;
+    const int R = gemv2_rows(n, nb, m, dtype, nt);
+    return (n + R - 1) / R <= 256;
+}
+
+// Threads per workgroup.  Plain launches use 256 (measured at least as fast as 1024 at
+// every decode shape, and faster for w1|w3); SXQ_GEMV_NT=1024 selects the larger one
+// where it fits.  The fused RMSNorm prologue always runs with 1024 threads, so the row
+// is normalised and quantized once per CU rather than four times.
+static int gemv2_nt(int n, int nb, int m, int dtype) {
+    static const int env_nt = [] {
+        const char* e = getenv("SXQ_GEMV_NT");
+        return e ? atoi(e) : 256;
+    }();
+    return env_nt == 1024 && gemv2_fits(n, nb, m, dtype, 1024) ? 1024 : 256;
+}
+
+template <int MMAX, bool NORM, int NT>
+static hipError_t gemv2_launch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
+                               const float* res, int64_t ldr, hipStream_t s, const NormIn& ni) {
+    const int n = (int)w.n, nb = (int)w.nb;
+    const int R = gemv2_rows(n, nb, m, w.dtype, NT);
+    const size_t lds = gemv2_lds(nb, m, R, w.dtype, NT);
+    const dim3 grid((n + R - 1) / R), block(NT);
+    const uint8_t* a = (const uint8_t*)act;
+    if (w.dtype == kQ4K)
+        hipLaunchKernelGGL((k_gemv2_q4k<MMAX, NORM, NT>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+    else if (w.dtype == kQ8_0)
+        hipLaunchKernelGGL((k_gemv2_q80<MMAX, false, NORM, NT>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+    else if (w.dtype == kQ4_0)
+        hipLaunchKernelGGL((k_gemv2_q80<MMAX, true, NORM, NT>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
 }
 
 template <int MMAX>
 static hipError_t gemv2_dispatch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                                  const float* res, int64_t ldr, hipStream_t s) {
-    const int n = (int)w.n, nb = (int)w.nb;
-    const int R = gemv2_rows(n, nb, m, w.dtype);
-    const size_t lds = gemv2_lds(nb, m, R, w.dtype);
-    const dim3 grid((n + R - 1) / R), block(256);
-    const uint8_t* a = (const uint8_t*)act;
-    if (w.dtype == kQ4K)
-        hipLaunchKernelGGL((k_gemv2_q4k<MMAX>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr);
-    else if (w.dtype == kQ8_0)
-        hipLaunchKernelGGL((k_gemv2_q80<MMAX, false>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr);
-    else if (w.dtype == kQ4_0)
-        hipLaunchKernelGGL((k_gemv2_q80<MMAX, true>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr);
-    else
-        return hipErrorInvalidValue;
-    return hipGetLastError();
+    if (gemv2_nt((int)w.n, (int)w.nb, m, w.dtype) == 1024)
+        return gemv2_launch<MMAX, false, 1024>(w, act, m, y, ldy, bias, res, ldr, s, NormIn());
+    return gemv2_launch<MMAX, false, 256>(w, act, m, y, ldy, bias, res, ldr, s, NormIn());
 }
 
 template <int MMAX>
@@ -494,7 +589,7 @@ hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64
     static const bool v1 = getenv("SXQ_GEMV_V1") != nullptr;
     if (!v1) {
         const int nb = (int)w.nb;
-        const bool fits = gemv2_fits(nb, m, w.dtype);
+        const bool fits = gemv2_fits((int)w.n, nb, m, w.dtype, 256);
         if (fits && m == 1) return gemv2_dispatch<1>(w, act, m, y, ldy, bias, res, ldr, s);
         if (fits && m == 2) return gemv2_dispatch<2>(w, act, m, y, ldy, bias, res, ldr, s);
         if (fits && m <= 4) return gemv2_dispatch<4>(w, act, m, y, ldy, bias, res, ldr, s);
@@ -505,6 +600,18 @@ hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64
     if (m <= 8) return gemv_dispatch<8>(w, act, m, y, ldy, bias, res, ldr, s);
     if (m <= 16) return gemv_dispatch<16>(w, act, m, y, ldy, bias, res, ldr, s);
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,
+                               int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s) {
+    if (m <= 0 || w.n <= 0) return hipSuccess;
+    static const bool v1 = getenv("SXQ_GEMV_V1") != nullptr;
+    const int k = (int)w.k;
+    if (!v1 && m == 1 && k <= kNormMaxDim && gemv2_fits((int)w.n, (int)w.nb, 1, w.dtype, 1024))
+        return gemv2_launch<1, true, 1024>(w, nullptr, 1, y, ldy, bias, res, ldr, s, ni);
+    hipError_t e = launch_rmsnorm_quant(vec_dot_type(w.dtype), ni.x, m, k, ni.w, ni.eps, act_scratch, ni.normed, s);
+    if (e != hipSuccess) return e;
+    return launch_gemv(w, act_scratch, m, y, ldy, bias, res, ldr, s);
 }
 
 }  // namespace sxq

@@ -32,6 +32,21 @@ struct QWeight {
 hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                        const float* res, int64_t ldr, hipStream_t s);
 
+// RMSNorm of f32 rows x [m, k] (crates/syrinx-fish/src/s2/nn.rs:100-106), the result
+// quantized and multiplied: y = quant(rmsnorm(x) * w_norm) . W^T (+ bias, + res).
+// For one row of at most kNormMaxDim elements the norm runs in the GEMV's own
+// prologue; otherwise a separate RMSNorm kernel fills `act_scratch` [m][nb] first.
+// Both give the same bits.  `normed` (optional) receives the f32 normalised rows.
+constexpr int kNormMaxDim = 4096;
+struct NormIn {
+    const float* x = nullptr;     // rows to normalise, row stride k
+    const float* w = nullptr;     // norm weight [k]
+    float eps = 0.0f;
+    float* normed = nullptr;      // optional f32 copy of the normalised rows [m, k]
+};
+hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,
+                               int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s);
+
 }  // namespace sxq
 
 // The QMatMul handle behind the C-ABI's opaque sxq_qmm.

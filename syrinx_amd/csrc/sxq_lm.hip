@@ -63,6 +63,9 @@ struct sxq_lm {
     float *h = nullptr, *qkv = nullptr, *qbuf = nullptr, *part = nullptr, *gu = nullptr, *logits = nullptr;
     uint8_t *act_a = nullptr, *act_o = nullptr, *act_d = nullptr;
     int *d_ids = nullptr, *d_next = nullptr;
+    float* am_val = nullptr;        // argmax partials [max_batch * kArgmaxSlices]
+    int* am_idx = nullptr;
+    unsigned* am_count = nullptr;   // per-stream arrival counters (zero between steps)
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
     hipStream_t cap = nullptr;
     std::map<GraphKey, hipGraphExec_t> graphs;
@@ -164,12 +167,20 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
     if (tr) STEP(record(lm->h, (size_t)n * c.dim));
     const int I = c.intermediate;
     const size_t nd = (size_t)n * c.dim;
+    auto norm_in = [&](const float* x, const float* w, float* normed) {
+        NormIn ni;
+        ni.x = x;
+        ni.w = w;
+        ni.eps = c.norm_eps;
+        ni.normed = normed;
+        return ni;
+    };
     for (int l = 0; l < c.n_layers; ++l) {
         LmLayer& L = lm->layers[l];
         float* kc = lm->kc + (int64_t)l * lm->kv_layer_stride;
         float* vc = lm->vc + (int64_t)l * lm->kv_layer_stride;
-        STEP(launch_rmsnorm_quant(lm->vdt, lm->h, n, c.dim, L.attn_norm, c.norm_eps, lm->act_a, tr ? slot(nd) : nullptr, s));
-        STEP(launch_gemv(L.wqkv.w, lm->act_a, n, lm->qkv, lm->qkv_n, L.bqkv, nullptr, 0, s));
+        STEP(launch_gemv_rmsnorm(L.wqkv.w, norm_in(lm->h, L.attn_norm, tr ? slot(nd) : nullptr), n, lm->act_a, lm->qkv,
+                                 lm->qkv_n, L.bqkv, nullptr, 0, s));
         if (tr) STEP(record(lm->qkv, (size_t)n * lm->qkv_n));
         STEP(launch_qk_rope_append(lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim,
                                    c.qk_norm ? L.q_norm : nullptr, c.qk_norm ? L.k_norm : nullptr, c.norm_eps,
@@ -181,17 +192,17 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                               tr ? slot((size_t)n * lm->ctx) : nullptr, s));
         STEP(launch_gemv(L.wo.w, lm->act_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
         if (tr) STEP(record(lm->h, nd));
-        STEP(launch_rmsnorm_quant(lm->vdt, lm->h, n, c.dim, L.ffn_norm, c.norm_eps, lm->act_a, tr ? slot(nd) : nullptr, s));
-        STEP(launch_gemv(L.w13.w, lm->act_a, n, lm->gu, 2 * I, nullptr, nullptr, 0, s));
+        STEP(launch_gemv_rmsnorm(L.w13.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), n, lm->act_a, lm->gu,
+                                 2 * I, nullptr, nullptr, 0, s));
         if (tr) STEP(record(lm->gu, (size_t)n * 2 * I));
         STEP(launch_silu_mul_quant(lm->vdt, lm->gu, n, I, lm->act_d, tr ? slot((size_t)n * I) : nullptr, s));
         STEP(launch_gemv(L.w2.w, lm->act_d, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
         if (tr) STEP(record(lm->h, nd));
     }
-    STEP(launch_rmsnorm_quant(lm->vdt, lm->h, n, c.dim, lm->final_norm, c.norm_eps, lm->act_a, tr ? slot(nd) : nullptr, s));
-    STEP(launch_gemv(lm->head.w, lm->act_a, n, lm->logits, c.vocab, c.head_bias ? lm->head_bias : nullptr, nullptr, 0, s));
-    STEP(launch_argmax(lm->logits, n, c.vocab, lm->d_ids, lm->ids_per, lm->d_next, s));
-    STEP(launch_advance(lm->d_len, n, s));
+    STEP(launch_gemv_rmsnorm(lm->head.w, norm_in(lm->h, lm->final_norm, tr ? slot(nd) : nullptr), n, lm->act_a,
+                             lm->logits, c.vocab, c.head_bias ? lm->head_bias : nullptr, nullptr, 0, s));
+    STEP(launch_argmax(lm->logits, n, c.vocab, lm->d_ids, lm->ids_per, lm->d_next, lm->d_len, lm->am_val, lm->am_idx,
+                       lm->am_count, s));
 #undef STEP
     return hipSuccess;
 }
@@ -288,6 +299,9 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->act_d, ab * MB * (I / bs));
     A((void**)&lm->d_ids, sizeof(int) * MB * lm->ids_per);
     A((void**)&lm->d_next, sizeof(int) * MB);
+    A((void**)&lm->am_val, sizeof(float) * MB * kArgmaxSlices);
+    A((void**)&lm->am_idx, sizeof(int) * MB * kArgmaxSlices);
+    A((void**)&lm->am_count, sizeof(unsigned) * MB);
     if (e != hipSuccess) {
         destroy_lm(lm);
         return hip_fail(e, "lm_create: allocation");
@@ -320,6 +334,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     if (e == hipSuccess) e = launch_fill_value(lm->head_bias, c.vocab, 0.0f, nullptr);
     if (e == hipSuccess) e = hipMemset(lm->d_len, 0, sizeof(int) * MB);
     if (e == hipSuccess) e = hipMemset(lm->d_ids, 0, sizeof(int) * MB * lm->ids_per);
+    if (e == hipSuccess) e = hipMemset(lm->am_count, 0, sizeof(unsigned) * MB);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&lm->cap, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {

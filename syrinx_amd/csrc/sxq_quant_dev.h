@@ -22,57 +22,137 @@ SXQ_DEV int wave_min_i32(int v) {
     return v;
 }
 
-// Quantize 256 consecutive activations (lane i holds elements 4i..4i+3 in v) to one
-// Q8_K block: k_quants.rs BlockQ8K::from_float.  Writes either the device layout
-// (ActQ8K, class-major qs) or the canonical BlockQ8K.
+// Sum of one f32 per thread over a 1024-thread workgroup, in a fixed order: xor
+// butterfly inside each wave, then the sixteen wave sums as a balanced pairwise tree.
+// This is the RMSNorm sum of squares of every kernel here (fused GEMV prologue and the
+// standalone RMSNorm), so they agree bit for bit.  `red`: 16 floats of LDS.  Every
+// thread of the workgroup must call it (it synchronises).
+SXQ_DEV float rmsnorm_sumsq_1024(float ss, float* red) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[i] = red[2 * i] + red[2 * i + 1];
+    return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
+// In-row DPP steps (lanes combine inside 16-lane rows): quad_perm xor1 = 0xB1,
+// xor2 = 0x4E, row_half_mirror = 0x141 (i <-> 7-i), row_mirror = 0x140 (i <-> 15-i).
+// After xor1 and xor2 every quad holds its quad total; the half mirror then pairs each
+// lane with the other quad of its 8, and the row mirror with the other 8 of its 16, so
+// for max/min/integer sums the four steps leave every lane with its 16-lane total.
+template <int CTRL>
+SXQ_DEV float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+SXQ_DEV int dpp_i32(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+
+// Quantize J chunks of 256 consecutive activations at once (lane i holds elements
+// 4i..4i+3 of chunk j in v[j]) to Q8_K blocks: k_quants.rs BlockQ8K::from_float.  The
+// chunks' reductions are interleaved so their cross-lane latencies overlap; chunk j is
+// written only if `valid[j]` (wave-uniform).  Writes the device layout (ActQ8K,
+// class-major qs) or the canonical BlockQ8K.
+template <int J, bool CANON>
+SXQ_DEV void wave_quantize_q8k_n(const float4 (&v)[J], int lane, void* const (&out)[J], const bool (&valid)[J]) {
+    float am[J], x[J][4];
+    int ix[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        x[j][0] = v[j].x; x[j][1] = v[j].y; x[j][2] = v[j].z; x[j][3] = v[j].w;
+        // first element of largest magnitude (Candle keeps the first on ties: `amax < |x|`)
+        am[j] = fabsf(x[j][0]);
+        ix[j] = 0;
+#pragma unroll
+        for (int r = 1; r < 4; ++r)
+            if (am[j] < fabsf(x[j][r])) { am[j] = fabsf(x[j][r]); ix[j] = r; }
+    }
+    float wmax[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(am[j], dpp_f32<0xB1>(am[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], dpp_f32<0x4E>(wmax[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], dpp_f32<0x141>(wmax[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], dpp_f32<0x140>(wmax[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], __shfl_xor(wmax[j], 16, 64));
+#pragma unroll
+    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], __shfl_xor(wmax[j], 32, 64));
+    int first[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) first[j] = am[j] == wmax[j] ? 4 * lane + ix[j] : 256;
+#pragma unroll
+    for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0xB1>(first[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0x4E>(first[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0x141>(first[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0x140>(first[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) first[j] = min(first[j], __shfl_xor(first[j], 16, 64));
+#pragma unroll
+    for (int j = 0; j < J; ++j) first[j] = min(first[j], __shfl_xor(first[j], 32, 64));
+    int q[J][4], s8[J], s4[J];
+    float d[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        // the max element itself (signed): its component, read from its lane
+        const int f = __builtin_amdgcn_readfirstlane(first[j]);
+        const int src = f >> 2, comp = f & 3;
+        const float mine = comp == 0 ? x[j][0] : comp == 1 ? x[j][1] : comp == 2 ? x[j][2] : x[j][3];
+        const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), src & 63));
+        q[j][0] = q[j][1] = q[j][2] = q[j][3] = 0;
+        d[j] = 0.0f;
+        if (wmax[j] != 0.0f) {
+            const float iscale = -128.0f / mx;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float t = roundf(iscale * x[j][r]);
+                t = (t != t || t > 127.0f) ? 127.0f : t;  // f32::min(t, 127.0) ignores NaN
+                q[j][r] = sat_i8(t);
+            }
+            d[j] = 1.0f / iscale;
+        }
+        // bsums: 16 elements = 4 lanes (a quad); bs2: 32 elements = 8 lanes.
+        s4[j] = q[j][0] + q[j][1] + q[j][2] + q[j][3];
+        s4[j] += dpp_i32<0xB1>(s4[j]);
+        s4[j] += dpp_i32<0x4E>(s4[j]);
+        s8[j] = s4[j] + dpp_i32<0x141>(s4[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        if (!valid[j]) continue;
+        if (CANON) {
+            BlockQ8K* b = (BlockQ8K*)out[j];
+            const uint32_t packed = (uint32_t)(q[j][0] & 0xFF) | ((uint32_t)(q[j][1] & 0xFF) << 8) |
+                                    ((uint32_t)(q[j][2] & 0xFF) << 16) | ((uint32_t)(q[j][3] & 0xFF) << 24);
+            ((uint32_t*)b->qs)[lane] = packed;
+            if ((lane & 3) == 0) b->bsums[lane >> 2] = (int16_t)s4[j];
+            if (lane == 0) b->d = d[j];
+        } else {
+            ActQ8K* b = (ActQ8K*)out[j];
+            // element e = 4*lane + r: sub-block jj = lane/8, class l = 4*(lane%2) + r, t = (lane%8)/2
+            const int jj = lane >> 3, t = (lane & 7) >> 1, l0 = 4 * (lane & 1);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) b->qs[4 * (8 * (l0 + r) + jj) + t] = (int8_t)q[j][r];
+            if ((lane & 7) == 0) b->bs2[jj] = s8[j];
+            if (lane == 0) b->d = d[j];
+        }
+    }
+}
+
+// One chunk: see wave_quantize_q8k_n.
 template <bool CANON>
 SXQ_DEV void wave_quantize_q8k(float4 v, int lane, void* out) {
-    const float x[4] = {v.x, v.y, v.z, v.w};
-    // first element of largest magnitude (Candle keeps the first on ties: `amax < |x|`)
-    float am = fabsf(x[0]);
-    int ix = 0;
-#pragma unroll
-    for (int r = 1; r < 4; ++r)
-        if (am < fabsf(x[r])) { am = fabsf(x[r]); ix = r; }
-    const float wmax = wave_max_f32(am);
-    const int first = wave_min_i32(am == wmax ? 4 * lane + ix : 256);
-    const int src = first >> 2, comp = first & 3;
-    const float c0 = __shfl(x[0], src, 64), c1 = __shfl(x[1], src, 64);
-    const float c2 = __shfl(x[2], src, 64), c3 = __shfl(x[3], src, 64);
-    const float mx = comp == 0 ? c0 : comp == 1 ? c1 : comp == 2 ? c2 : c3;
-    int q[4] = {0, 0, 0, 0};
-    float d = 0.0f;
-    if (wmax != 0.0f) {
-        const float iscale = -128.0f / mx;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float t = roundf(iscale * x[r]);
-            t = (t != t || t > 127.0f) ? 127.0f : t;  // f32::min(t, 127.0) ignores NaN
-            q[r] = sat_i8(t);
-        }
-        d = 1.0f / iscale;
-    }
-    // bsums: 16 elements = 4 lanes (a quad); bs2: 32 elements = 8 lanes.
-    int s4 = q[0] + q[1] + q[2] + q[3];
-    s4 += __shfl_xor(s4, 1, 64);
-    s4 += __shfl_xor(s4, 2, 64);
-    const int s8 = s4 + __shfl_xor(s4, 4, 64);
-    if (CANON) {
-        BlockQ8K* b = (BlockQ8K*)out;
-        uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                          ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-        ((uint32_t*)b->qs)[lane] = packed;
-        if ((lane & 3) == 0) b->bsums[lane >> 2] = (int16_t)s4;
-        if (lane == 0) b->d = d;
-    } else {
-        ActQ8K* b = (ActQ8K*)out;
-        // element e = 4*lane + r: j = lane/8, l = 4*(lane%2) + r, t = (lane%8)/2
-        const int j = lane >> 3, t = (lane & 7) >> 1, l0 = 4 * (lane & 1);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) b->qs[4 * (8 * (l0 + r) + j) + t] = (int8_t)q[r];
-        if ((lane & 7) == 0) b->bs2[j] = s8;
-        if (lane == 0) b->d = d;
-    }
+    const float4 vv[1] = {v};
+    void* const oo[1] = {out};
+    const bool ok[1] = {true};
+    wave_quantize_q8k_n<1, CANON>(vv, lane, oo, ok);
 }
 
 // Quantize 256 consecutive activations (8 Q8_0 blocks; lanes 8b..8b+7 own block b) to
