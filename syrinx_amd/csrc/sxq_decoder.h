@@ -13,11 +13,26 @@ hipError_t launch_qk_rope_append(const float* qkv, int B, int qkv_n, int nh, int
 // Attention splits: at most kMaxSplits partials per head are merged, so a stream holds
 // at most kMaxSplits * kAttnSplit positions.
 constexpr int kAttnSplit = 32;
+// Positions per split of the fused decode attention (fewer, larger splits: a cheaper merge).
+constexpr int kAttnSplitFused = 64;
 constexpr int kMaxSplits = 512;
 size_t attn_partial_lds(int nh, int nkv, int hd, int P);
 hipError_t launch_attention(int vdt, const float* q, const float* kc, const float* vc, const int* len, int B, int nh,
                             int nkv, int hd, int max_seq, int64_t kv_stream_stride, int P, int max_splits,
                             float* part, uint8_t* act, float* ctx_out, hipStream_t s);
+// Fused decode attention (QK-norm + RoPE + KV append + split partials + last-arriver
+// merge + quantization of the context); counter: [B * nkv] zero before the first call
+// (each call leaves it zero).  q_out / ctx_out optional (tests).  Returns
+// hipErrorInvalidValue when the head group is not a whole number of activation blocks
+// (attn_decode_fits); the caller then uses the three-kernel path.
+bool attn_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits);
+// Allow the fused kernel its dynamic LDS (above 64 KB); call once before launching.
+hipError_t attn_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits);
+hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, int nh, int nkv, int hd, const float* qn,
+                                   const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
+                                   const int* len, float* kc, float* vc, int64_t kv_stream_stride, int max_seq,
+                                   int max_splits, float* part, unsigned* counter, uint8_t* act, float* ctx_out,
+                                   float* q_out, hipStream_t s);
 hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s);
 hipError_t launch_embed_quant_table(const int* ids, int ids_per, int B, const QWeight& w, int dim, const float* cb,
                                     int n_cb, int cb_size, int sem_begin, int sem_end, float* h, hipStream_t s);

@@ -25,6 +25,34 @@ SXQ_DEV float wave_sum_f32(float v) {
     return v;
 }
 
+// Hand-off between the workgroups of one launch ("the last to arrive finishes the
+// job") without a device-wide fence: on this GPU an agent-scope fence writes back or
+// invalidates the whole L2 of an XCD, which costs far more than the work it guards.
+// Instead the data crosses through accesses that are themselves coherent at agent
+// scope -- relaxed agent-scope atomic stores and loads, which go to the coherent level
+// rather than a possibly stale L2 -- and the protocol is:
+//   writers:  store_agent(data...); publish_and_count() -> true in the last arriver
+//   last:     load_agent(data...)
+// publish_and_count waits until this thread's stores have completed (s_waitcnt 0),
+// joins the workgroup (so every thread's stores have), then thread 0 bumps the counter;
+// the last arriver only issues its loads after the counter returned.
+SXQ_DEV void store_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+SXQ_DEV void store_agent(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+SXQ_DEV float load_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+SXQ_DEV int load_agent(const int* p) { return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// Every thread of the workgroup calls it; `flag` is a workgroup-shared bool.  `total` =
+// number of workgroups that count on this counter.
+SXQ_DEV bool publish_and_count(unsigned* counter, unsigned total, bool* flag) {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
+    __syncthreads();                // ... and so are everyone else's in the workgroup
+    if (threadIdx.x == 0)
+        *flag = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+    __syncthreads();
+    return *flag;
+}
+
 // Quantize chunk c of a row of `dim` elements (elements c*256 .. c*256+255, whose
 // values start at `vals`) into the device activation layout `act_row` (row of blocks).
 template <int VDT>
@@ -82,30 +110,13 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float* __restrict_
 }
 
 // ---------------------------------------------------- QK-RMSNorm + RoPE + KV-cache append
-// grid (B, n_heads + 2 * n_kv), one wave per head of the fused qkv row
-// [q (nh*hd) | k (nkv*hd) | v (nkv*hd)].  Lane i owns rotation pairs i, i+64, ...
-__global__ __launch_bounds__(64) void k_qk_rope_append(const float* __restrict__ qkv, int qkv_n, int nh, int nkv,
-                                                       int hd, const float* __restrict__ qn,
-                                                       const float* __restrict__ kn, float eps, float inv_hd,
-                                                       int interleaved, const float* __restrict__ cos_t,
-                                                       const float* __restrict__ sin_t, const int* __restrict__ len,
-                                                       float* __restrict__ qout, float* __restrict__ kc,
-                                                       float* __restrict__ vc, int64_t kv_stream_stride,
-                                                       int max_seq) {
-    const int s = blockIdx.x, hid = blockIdx.y, lane = threadIdx.x;
-    const int pos = len[s];
-    const float* src = qkv + (int64_t)s * qkv_n + (int64_t)hid * hd;
-    const int half = hd / 2;
-    const bool is_q = hid < nh, is_k = !is_q && hid < nh + nkv;
-    if (!is_q && !is_k) {  // V: stored as projected
-        const int g = hid - nh - nkv;
-        float* dst = vc + (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + pos) * hd;
-        for (int d = lane; d < hd; d += 64) dst[d] = src[d];
-        return;
-    }
-    const float* nw = is_q ? qn : kn;
-    // pairs: interleaved (2i, 2i+1) or rotate-half (i, i + hd/2)
+// One head by one wave: optional per-head RMSNorm (QK-norm) then RoPE, src -> dst
+// (hd <= 256).  Pairs: interleaved (2i, 2i+1) or rotate-half (i, i + hd/2); lane i
+// owns pairs i and i + 64.  cos_row/sin_row: the RoPE tables at this position.
+SXQ_DEV void wave_norm_rope(const float* src, const float* nw, float eps, float inv_hd, int hd, int interleaved,
+                            const float* cos_row, const float* sin_row, float* dst, int lane) {
     constexpr int MAXP = 2;  // hd <= 256
+    const int half = hd / 2;
     float a[MAXP], b[MAXP];
     int ia[MAXP], ib[MAXP];
     float ss = 0.0f;
@@ -132,61 +143,121 @@ __global__ __launch_bounds__(64) void k_qk_rope_append(const float* __restrict__
             }
         }
     }
-    float* dst;
-    if (is_q) {
-        dst = qout + ((int64_t)s * nh + hid) * hd;
-    } else {
-        const int g = hid - nh;
-        dst = kc + (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + pos) * hd;
-    }
 #pragma unroll
     for (int t = 0; t < MAXP; ++t) {
         const int i = lane + 64 * t;
         if (i < half) {
-            const float c = cos_t[(int64_t)pos * half + i], sn = sin_t[(int64_t)pos * half + i];
+            const float c = cos_row[i], sn = sin_row[i];
             dst[ia[t]] = a[t] * c - b[t] * sn;
             dst[ib[t]] = b[t] * c + a[t] * sn;
         }
     }
 }
 
-// ------------------------------------------------------------- split-K decode attention
-// grid (B, n_kv, max_splits), 256 threads.  Each workgroup takes P consecutive cached
-// positions of one KV head for all G = nh/nkv query heads sharing it (GQA without
-// materialising repeat_kv), and writes per-head partials {m, l, acc[hd]}:
-//   m = max_j s_j, l = sum_j exp(s_j - m), acc = sum_j exp(s_j - m) v_j,
-// with s_j = (q . k_j) * scale.  The K and V tiles are fetched together up front.
-// k_attn_combine_quant merges the splits.
-__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ kc,
-                                                      const float* __restrict__ vc, const int* __restrict__ len,
-                                                      int nh, int nkv, int hd, int max_seq,
-                                                      int64_t kv_stream_stride, int P, float scale,
-                                                      float* __restrict__ part, int max_splits) {
-    extern __shared__ float smem[];
-    const int s = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
-    const int L = len[s] + 1;  // the token appended this step is attended too
-    const int p0 = sp * P;
-    if (p0 >= L) return;
-    const int np = min(P, L - p0);
-    const int G = nh / nkv, hdp = hd + 4;
-    float* qs = smem;               // [G][hd]
-    float* kt = qs + G * hd;        // [P][hd + 4]
-    float* vt = kt + P * hdp;       // [P][hd + 4]
-    float* sc = vt + P * hdp;       // [G][P]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t off = (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + p0) * hd;
-    const float* kb = kc + off;
-    const float* vb = vc + off;
-    const int hd4 = hd / 4, n4 = np * hd4;
-    for (int i = tid; i < G * hd; i += 256) qs[i] = q[((int64_t)s * nh + g * G) * hd + i];
-    for (int i = tid; i < n4; i += 256) {
-        const int p = i / hd4, d4 = i - p * hd4;
-        const float4 kv = *(const float4*)(kb + (int64_t)p * hd + 4 * d4);
-        const float4 vv = *(const float4*)(vb + (int64_t)p * hd + 4 * d4);
-        *(float4*)(kt + p * hdp + 4 * d4) = kv;
-        *(float4*)(vt + p * hdp + 4 * d4) = vv;
+// grid (B, n_heads + 2 * n_kv), one wave per head of the fused qkv row
+// [q (nh*hd) | k (nkv*hd) | v (nkv*hd)]: queries -> qout, keys and values -> the cache
+// at the stream's current length.
+__global__ __launch_bounds__(64) void k_qk_rope_append(const float* __restrict__ qkv, int qkv_n, int nh, int nkv,
+                                                       int hd, const float* __restrict__ qn,
+                                                       const float* __restrict__ kn, float eps, float inv_hd,
+                                                       int interleaved, const float* __restrict__ cos_t,
+                                                       const float* __restrict__ sin_t, const int* __restrict__ len,
+                                                       float* __restrict__ qout, float* __restrict__ kc,
+                                                       float* __restrict__ vc, int64_t kv_stream_stride,
+                                                       int max_seq) {
+    const int s = blockIdx.x, hid = blockIdx.y, lane = threadIdx.x;
+    const int pos = len[s];
+    const float* src = qkv + (int64_t)s * qkv_n + (int64_t)hid * hd;
+    const int half = hd / 2;
+    const bool is_q = hid < nh, is_k = !is_q && hid < nh + nkv;
+    if (!is_q && !is_k) {  // V: stored as projected
+        const int g = hid - nh - nkv;
+        float* dst = vc + (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + pos) * hd;
+        for (int d = lane; d < hd; d += 64) dst[d] = src[d];
+        return;
     }
-    __syncthreads();
+    float* dst = is_q ? qout + ((int64_t)s * nh + hid) * hd
+                      : kc + (int64_t)s * kv_stream_stride + ((int64_t)(hid - nh) * max_seq + pos) * hd;
+    wave_norm_rope(src, is_q ? qn : kn, eps, inv_hd, hd, interleaved, cos_t + (int64_t)pos * half,
+                   sin_t + (int64_t)pos * half, dst, lane);
+}
+
+// Split merge of one stream's attention partials part_s [nh][max_splits][hd + 4]
+// (record {m, l, 0, 0, acc[hd]}, 16-byte aligned):
+//   ctx = sum_i exp(m_i - M) acc_i / sum_i exp(m_i - M) l_i,  M = max_i m_i.
+// merge_weights (one wave per head, 4 waves) fills wts[hh][i] = exp(m_i - M) and
+// lsum[hh] for heads h0 .. h0 + nhc - 1; merge_elem then gives one context element.
+SXQ_DEV void merge_weights(const float* part_s, int h0, int nhc, int nsp, int hd, int max_splits, float* wts,
+                           float* lsum) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int hh = wave; hh < nhc; hh += 4) {
+        const float* ph = part_s + (int64_t)(h0 + hh) * max_splits * (hd + 4);
+        float M = -INFINITY;
+        for (int i = lane; i < nsp; i += 64) M = fmaxf(M, ph[i * (hd + 4)]);
+        M = wave_max_f32(M);
+        float Ls = 0.0f;
+        for (int i = lane; i < nsp; i += 64) {
+            const float w = expf(ph[i * (hd + 4)] - M);
+            wts[hh * kMaxSplits + i] = w;
+            Ls += ph[i * (hd + 4) + 1] * w;
+        }
+        Ls = wave_sum_f32(Ls);
+        if (lane == 0) lsum[hh] = Ls;
+    }
+}
+SXQ_DEV float merge_elem(const float* part_s, int h, int hh, int d, int nsp, int hd, int max_splits, const float* wts,
+                         const float* lsum) {
+    const float* ph = part_s + (int64_t)h * max_splits * (hd + 4) + 4 + d;
+    float acc = 0.0f;
+    for (int i = 0; i < nsp; ++i) acc += ph[i * (hd + 4)] * wts[hh * kMaxSplits + i];
+    return acc / lsum[hh];
+}
+
+// Copy rows [0, n) of a K and a V tile (row stride hd floats in global memory, hd + 4 in
+// LDS) with every thread's loads of a batch in flight together -- the LDS stores wait
+// for the whole batch rather than for each load in turn.  256 threads.
+SXQ_DEV void load_kv_tile(float* kt, float* vt, const float* kb, const float* vb, int n, int hd) {
+    constexpr int kBatch = 8;  // float4 of K and of V per thread per batch
+    const int hd4 = hd / 4, n4 = n * hd4, hdp = hd + 4;
+    for (int base = 0; base < n4; base += 256 * kBatch) {
+        float4 kv[kBatch], vv[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = min(base + j * 256 + (int)threadIdx.x, n4 - 1);  // clamped: in bounds
+            const int p = i / hd4, d4 = i - p * hd4;
+            kv[j] = *(const float4*)(kb + (int64_t)p * hd + 4 * d4);
+            vv[j] = *(const float4*)(vb + (int64_t)p * hd + 4 * d4);
+        }
+        // An empty asm reading every loaded register: the loads cannot be sunk to their
+        // stores (each would then wait for its own load); they are all issued first and
+        // the stores below wait once for the batch.  It emits no instruction.
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+            asm volatile("" ::"v"(kv[j].x), "v"(kv[j].y), "v"(kv[j].z), "v"(kv[j].w), "v"(vv[j].x), "v"(vv[j].y),
+                         "v"(vv[j].z), "v"(vv[j].w));
+        // clamped like the loads (unconditional, so no branch pulls a load down to its
+        // store): out-of-range threads rewrite the last row element with its own value
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = min(base + j * 256 + (int)threadIdx.x, n4 - 1);
+            const int p = i / hd4, d4 = i - p * hd4;
+            *(float4*)(kt + p * hdp + 4 * d4) = kv[j];
+            *(float4*)(vt + p * hdp + 4 * d4) = vv[j];
+        }
+    }
+}
+
+// ------------------------------------------------------------- split-K decode attention
+// One workgroup takes P consecutive cached positions of one KV head for all G = nh/nkv
+// query heads sharing it (GQA without materialising repeat_kv) and writes per-head
+// partials {m, l, 0, 0, acc[hd]} (records of hd + 4 floats):
+//   m = max_j s_j, l = sum_j exp(s_j - m), acc = sum_j exp(s_j - m) v_j,
+// with s_j = (q . k_j) * scale.  attn_tile_partials does that from LDS tiles: qs [G][hd],
+// kt/vt [P][hd + 4] (np valid rows), scratch sc [G][P]; pm points at head 0's partial of
+// this split, head_stride floats apart.  256 threads, all of which must call it.
+SXQ_DEV void attn_tile_partials(const float* qs, const float* kt, const float* vt, float* sc, int G, int P, int np,
+                                int hd, float scale, float* pm, int64_t head_stride) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hdp = hd + 4;
     // scores: a lane pair per (head, position), each lane half of the head dim
     for (int base = 0; base < 2 * G * P; base += 256) {
         const int i = base + tid;
@@ -209,8 +280,6 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ 
         if (i < 2 * G * P && half == 0 && p < np) sc[h * P + p] = acc * scale + 0.0f;
     }
     __syncthreads();
-    float* pm = part + (((int64_t)s * nh + g * G) * max_splits + sp) * (2 + hd);
-    const int64_t head_stride = (int64_t)max_splits * (2 + hd);
     for (int h = wave; h < G; h += 4) {
         float mx = -INFINITY;
         for (int p = lane; p < np; p += 64) mx = fmaxf(mx, sc[h * P + p]);
@@ -223,8 +292,8 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ 
         }
         l = wave_sum_f32(l);
         if (lane == 0) {
-            pm[h * head_stride] = mx;
-            pm[h * head_stride + 1] = l;
+            store_agent(&pm[h * head_stride], mx);
+            store_agent(&pm[h * head_stride + 1], l);
         }
     }
     __syncthreads();
@@ -233,50 +302,214 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ 
         const float* e = sc + h * P;
         float acc = 0.0f;
         for (int p = 0; p < np; ++p) acc += e[p] * vt[p * hdp + d];
-        pm[h * head_stride + 2 + d] = acc;
+        store_agent(&pm[h * head_stride + 4 + d], acc);
     }
 }
 
-// grid (B, ceil(nh*hd/256)), 256 threads: merge the splits of the heads covering
-// context elements [c*256, c*256 + 256), then quantize that chunk for the O projection:
-//   ctx = sum_i exp(m_i - M) acc_i / sum_i exp(m_i - M) l_i,  M = max_i m_i.
+// grid (B, n_kv, max_splits), 256 threads: the partials of split z over the cache
+// (keys/values already appended); k_attn_combine_quant merges the splits.
+__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ kc,
+                                                      const float* __restrict__ vc, const int* __restrict__ len,
+                                                      int nh, int nkv, int hd, int max_seq,
+                                                      int64_t kv_stream_stride, int P, float scale,
+                                                      float* __restrict__ part, int max_splits) {
+    extern __shared__ float4 smem4[];  // float4: 16-byte aligned after any static LDS
+    float* smem = (float*)smem4;
+    const int s = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+    const int L = len[s] + 1;  // the token appended this step is attended too
+    const int p0 = sp * P;
+    if (p0 >= L) return;
+    const int np = min(P, L - p0);
+    const int G = nh / nkv, hdp = hd + 4;
+    float* qs = smem;               // [G][hd]
+    float* kt = qs + G * hd;        // [P][hd + 4]
+    float* vt = kt + P * hdp;       // [P][hd + 4]
+    float* sc = vt + P * hdp;       // [G][P]
+    const int tid = threadIdx.x;
+    const int64_t off = (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + p0) * hd;
+    const float* kb = kc + off;
+    const float* vb = vc + off;
+    for (int i = tid; i < G * hd; i += 256) qs[i] = q[((int64_t)s * nh + g * G) * hd + i];
+    load_kv_tile(kt, vt, kb, vb, np, hd);
+    __syncthreads();
+    float* pm = part + (((int64_t)s * nh + g * G) * max_splits + sp) * (hd + 4);
+    attn_tile_partials(qs, kt, vt, sc, G, P, np, hd, scale, pm, (int64_t)max_splits * (hd + 4));
+}
+
+// Fused decode attention for one KV head group (grid (B, n_kv, max_splits), 256
+// threads): QK-norm + RoPE of the group's queries (every split, from the qkv row), the
+// new token's key/value (the split holding position len: norm + RoPE of k, appended to
+// the cache and to this tile), the split's partials, and -- in the last split of the
+// group to finish (a per-(stream, group) arrival counter, reset after use) -- the merge
+// of the group's G heads and the quantization of that G*hd slice of the context for the
+// O projection.  Same arithmetic as k_qk_rope_append + k_attn_partial +
+// k_attn_combine_quant; requires G*hd to be a whole number of activation blocks.
 template <int VDT>
-__global__ __launch_bounds__(256) void k_attn_combine_quant(const float* __restrict__ part, const int* __restrict__ len,
-                                                            int nh, int hd, int P, int max_splits,
-                                                            uint8_t* __restrict__ act, float* __restrict__ ctx_out) {
-    __shared__ float xs[256];
-    __shared__ float wts[8][kMaxSplits];
-    __shared__ float lsum[8];
-    const int s = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int dim = nh * hd;
-    const int L = len[s] + 1;
-    const int nsp = (L + P - 1) / P;
-    const int h0 = (c * 256) / hd;
-    const int nhc = min((256 + hd - 1) / hd, nh - h0);  // heads touching this chunk (<= 8)
-    // per-head split weights exp(m_i - M) and the normaliser, one wave per head
-    for (int hh = wave; hh < nhc; hh += 4) {
-        const float* ph = part + ((int64_t)s * nh + h0 + hh) * max_splits * (2 + hd);
+__global__ __launch_bounds__(256) void k_attn_decode(
+    const float* __restrict__ qkv, int qkv_n, int nh, int nkv, int hd, const float* __restrict__ qn,
+    const float* __restrict__ kn, float eps, float inv_hd, int interleaved, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, const int* __restrict__ len, float* __restrict__ kc, float* __restrict__ vc,
+    int64_t kv_stream_stride, int max_seq, int P, float scale, float* __restrict__ part, int max_splits,
+    unsigned* __restrict__ counter, uint8_t* __restrict__ act, float* __restrict__ ctx_out,
+    float* __restrict__ q_out) {
+    extern __shared__ float4 smem4[];  // float4: 16-byte aligned after any static LDS
+    float* smem = (float*)smem4;
+    __shared__ bool last;
+    const int s = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+    const int pos = len[s], L = pos + 1;
+    const int p0 = sp * P;
+    if (p0 >= L) return;
+    const int np = min(P, L - p0), nsp = (L + P - 1) / P;
+    const int G = nh / nkv, hdp = hd + 4, half = hd / 2;
+    float* qs = smem;               // [G][hd]
+    float* kt = qs + G * hd;        // [P][hd + 4]
+    float* vt = kt + P * hdp;       // [P][hd + 4]
+    float* sc = vt + P * hdp;       // [G][P]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* row = qkv + (int64_t)s * qkv_n;
+    const float* cos_row = cos_t + (int64_t)pos * half;
+    const float* sin_row = sin_t + (int64_t)pos * half;
+    const int64_t off = (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + p0) * hd;
+    // tile of the already cached positions p0 .. min(pos, p0 + np) - 1
+    if (pos > p0) load_kv_tile(kt, vt, kc + off, vc + off, min(np, pos - p0), hd);
+    // the group's queries
+    for (int h = wave; h < G; h += 4)
+        wave_norm_rope(row + (int64_t)(g * G + h) * hd, qn, eps, inv_hd, hd, interleaved, cos_row, sin_row,
+                       qs + h * hd, lane);
+    // the new token's key and value, in the split that holds position `pos`
+    const bool has_new = pos < p0 + np;
+    if (has_new) {
+        const int slot = pos - p0;
+        if (wave == 0)
+            wave_norm_rope(row + (int64_t)(nh + g) * hd, kn, eps, inv_hd, hd, interleaved, cos_row, sin_row,
+                           kt + slot * hdp, lane);
+        if (wave == 1)
+            for (int d = lane; d < hd; d += 64) vt[slot * hdp + d] = row[(int64_t)(nh + nkv + g) * hd + d];
+    }
+    __syncthreads();
+    if (has_new) {
+        const int slot = pos - p0;
+        const int64_t at = (int64_t)s * kv_stream_stride + ((int64_t)g * max_seq + pos) * hd;
+        for (int d = tid; d < hd; d += 256) {
+            kc[at + d] = kt[slot * hdp + d];
+            vc[at + d] = vt[slot * hdp + d];
+        }
+    }
+    if (q_out && sp == 0)
+        for (int i = tid; i < G * hd; i += 256) q_out[((int64_t)s * nh + g * G) * hd + i] = qs[i];
+    const float* part_s = part + (int64_t)s * nh * max_splits * (hd + 4);
+    float* pm = part + (((int64_t)s * nh + g * G) * max_splits + sp) * (hd + 4);
+    attn_tile_partials(qs, kt, vt, sc, G, P, np, hd, scale, pm, (int64_t)max_splits * (hd + 4));
+    // the last split of the group to arrive merges the group's heads
+    if (!publish_and_count(&counter[s * nkv + g], (unsigned)nsp, &last)) return;
+    // Merge, the arithmetic of merge_weights / merge_elem (same order, same bits), reading
+    // the partials with coherent loads issued kMergeBatch splits at a time so that each
+    // thread has many independent loads in flight.
+    const int gd = G * hd, PR = hd + 4, nchunk = (gd + 255) / 256, h0 = g * G;
+    float* wts = smem;                                   // [G][nsp]
+    float* lsum = wts + G * nsp;                         // [G]
+    float* xs = wts + ((G * nsp + G + 3) & ~3);          // [nchunk * 256]
+    constexpr int kElems = 4;       // context elements per thread: G*hd <= 1024
+    constexpr int kMergeBatch = 24; // splits per batch of loads
+    float acc[kElems];
+    const float* src[kElems];
+    int hk[kElems];
+#pragma unroll
+    for (int k = 0; k < kElems; ++k) {
+        const int e = min(tid + 256 * k, gd - 1);  // clamped: loads stay in bounds, results unused
+        hk[k] = e / hd;
+        src[k] = part_s + (int64_t)(h0 + hk[k]) * max_splits * PR + 4 + (e - hk[k] * hd);
+        acc[k] = 0.0f;
+    }
+    float v[kElems][kMergeBatch];
+    auto fetch = [&](int i0) {
+#pragma unroll
+        for (int k = 0; k < kElems; ++k)
+            if (256 * k < gd) {  // uniform
+#pragma unroll
+                for (int j = 0; j < kMergeBatch; ++j) v[k][j] = load_agent(src[k] + (int64_t)min(i0 + j, nsp - 1) * PR);
+#pragma unroll
+                for (int j = 0; j < kMergeBatch; ++j) asm volatile("" ::"v"(v[k][j]));  // keep the batch together
+            }
+    };
+    fetch(0);  // the first batch is in flight while the split weights are computed
+    for (int hh = wave; hh < G; hh += 4) {
+        const float* ph = part_s + (int64_t)(h0 + hh) * max_splits * PR;
         float M = -INFINITY;
-        for (int i = lane; i < nsp; i += 64) M = fmaxf(M, ph[i * (2 + hd)]);
+        for (int i = lane; i < nsp; i += 64) M = fmaxf(M, load_agent(ph + (int64_t)i * PR));
         M = wave_max_f32(M);
         float Ls = 0.0f;
         for (int i = lane; i < nsp; i += 64) {
-            const float w = expf(ph[i * (2 + hd)] - M);
-            wts[hh][i] = w;
-            Ls += ph[i * (2 + hd) + 1] * w;
+            const float w = expf(load_agent(ph + (int64_t)i * PR) - M);
+            wts[hh * nsp + i] = w;
+            Ls += load_agent(ph + (int64_t)i * PR + 1) * w;
         }
         Ls = wave_sum_f32(Ls);
         if (lane == 0) lsum[hh] = Ls;
     }
     __syncthreads();
+    for (int i0 = 0; i0 < nsp; i0 += kMergeBatch) {
+        if (i0 > 0) fetch(i0);
+#pragma unroll
+        for (int k = 0; k < kElems; ++k) {
+            if (256 * k < gd) {
+#pragma unroll
+                for (int j = 0; j < kMergeBatch; ++j)
+                    if (i0 + j < nsp) acc[k] += v[k][j] * wts[hk[k] * nsp + i0 + j];
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kElems; ++k) {
+        const int e = tid + 256 * k;
+        if (e < nchunk * 256) {
+            float v = 0.0f;
+            if (e < gd) {
+                v = acc[k] / lsum[hk[k]];
+                if (ctx_out) ctx_out[(int64_t)s * nh * hd + (int64_t)g * gd + e] = v;
+            }
+            xs[e] = v;
+        }
+    }
+    __syncthreads();
+    const int dim = nh * hd;
+    const int nb = VDT == kQ8K ? dim / 256 : dim / 32;
+    uint8_t* arow = act + (int64_t)s * nb * act_block_bytes(VDT);
+    for (int c = wave; c < nchunk; c += 4) {
+        const float4 v = *(const float4*)(xs + c * 256 + 4 * lane);
+        if (VDT == kQ8K) {
+            wave_quantize_q8k<false>(v, lane, arow + (size_t)((g * gd) / 256 + c) * sizeof(ActQ8K));
+        } else {
+            const int blk0 = (g * gd) / 32 + c * 8;  // first Q8_0 block of this chunk in the row
+            wave_quantize_q8_0<false>(v, lane, c * 8 + (lane >> 3) < gd / 32, arow + (size_t)blk0 * sizeof(ActQ8_0));
+        }
+    }
+    if (tid == 0) __hip_atomic_store(&counter[s * nkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// grid (B, ceil(nh*hd/256)), 256 threads: merge the splits of the heads covering
+// context elements [c*256, c*256 + 256), then quantize that chunk for the O projection.
+template <int VDT>
+__global__ __launch_bounds__(256) void k_attn_combine_quant(const float* __restrict__ part, const int* __restrict__ len,
+                                                            int nh, int hd, int P, int max_splits,
+                                                            uint8_t* __restrict__ act, float* __restrict__ ctx_out) {
+    __shared__ float xs[256];
+    __shared__ float wts[8 * kMaxSplits];
+    __shared__ float lsum[8];
+    const int s = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+    const int dim = nh * hd;
+    const int L = len[s] + 1;
+    const int nsp = (L + P - 1) / P;
+    const int h0 = (c * 256) / hd;
+    const int nhc = min((256 + hd - 1) / hd, nh - h0);  // heads touching this chunk (<= 8)
+    const float* part_s = part + (int64_t)s * nh * max_splits * (hd + 4);
+    merge_weights(part_s, h0, nhc, nsp, hd, max_splits, wts, lsum);
+    __syncthreads();
     const int e = c * 256 + tid;
     float v = 0.0f;
     if (e < dim) {
-        const int h = e / hd, d = e - h * hd, hh = h - h0;
-        const float* ph = part + ((int64_t)s * nh + h) * max_splits * (2 + hd) + 2 + d;
-        float acc = 0.0f;
-        for (int i = 0; i < nsp; ++i) acc += ph[i * (2 + hd)] * wts[hh][i];
-        v = acc / lsum[hh];
+        const int h = e / hd, d = e - h * hd;
+        v = merge_elem(part_s, h, h - h0, d, nsp, hd, max_splits, wts, lsum);
         if (ctx_out) ctx_out[(int64_t)s * dim + e] = v;
     }
     xs[tid] = v;
@@ -418,24 +651,20 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
     __syncthreads();
     if (tid == 0) {
         for (int w = 1; w < 4; ++w) argmax_merge(best, idx, bv[w], bi[w]);
-        pval[s * kArgmaxSlices + b] = best;
-        pidx[s * kArgmaxSlices + b] = idx;
-        __threadfence();  // publish the partial before counting it
-        last = atomicAdd(&counter[s], 1u) == kArgmaxSlices - 1;
+        store_agent(&pval[s * kArgmaxSlices + b], best);
+        store_agent(&pidx[s * kArgmaxSlices + b], idx);
     }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();  // see every other workgroup's partial
+    if (!publish_and_count(&counter[s], kArgmaxSlices, &last)) return;
     if (wave == 0) {
-        best = __builtin_nontemporal_load(&pval[s * kArgmaxSlices + lane]);
-        idx = __builtin_nontemporal_load(&pidx[s * kArgmaxSlices + lane]);
+        best = load_agent(&pval[s * kArgmaxSlices + lane]);
+        idx = load_agent(&pidx[s * kArgmaxSlices + lane]);
         for (int o = 32; o >= 1; o >>= 1) argmax_merge(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
         if (lane == 0) {
             if (idx == 0x7FFFFFFF) idx = 0;
             ids[(int64_t)s * ids_per] = idx;
             if (out_ids) out_ids[s] = idx;
             if (len) len[s] += 1;
-            counter[s] = 0u;
+            __hip_atomic_store(&counter[s], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -481,6 +710,49 @@ hipError_t launch_attention(int vdt, const float* q, const float* kc, const floa
     const int chunks = (nh * hd + 255) / 256;
     if (vdt == kQ8K) hipLaunchKernelGGL((k_attn_combine_quant<kQ8K>), dim3(B, chunks), dim3(256), 0, s, part, len, nh, hd, P, max_splits, act, ctx_out);
     else hipLaunchKernelGGL((k_attn_combine_quant<kQ8_0>), dim3(B, chunks), dim3(256), 0, s, part, len, nh, hd, P, max_splits, act, ctx_out);
+    return hipGetLastError();
+}
+
+// Fused attention LDS: the partial phase's tiles, or the merge phase's split weights and
+// context slice, whichever is larger (the partial phase, at the decode shapes).
+static size_t attn_decode_lds(int nh, int nkv, int hd, int P, int max_splits) {
+    const int G = nh / nkv;
+    const size_t partial = attn_partial_lds(nh, nkv, hd, P) / sizeof(float);
+    const size_t merge = (((size_t)G * max_splits + G + 3) & ~(size_t)3) + ((size_t)G * hd + 255) / 256 * 256;
+    return sizeof(float) * (partial > merge ? partial : merge);
+}
+
+bool attn_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits) {
+    const int G = nh / nkv;
+    return (G * hd) % (vdt == kQ8K ? 256 : 32) == 0 && G * hd <= 1024 &&
+           attn_decode_lds(nh, nkv, hd, kAttnSplitFused, max_splits) <= 160 * 1024;
+}
+
+hipError_t attn_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits) {
+    const int lds = (int)attn_decode_lds(nh, nkv, hd, kAttnSplitFused, max_splits);
+    if (vdt == kQ8K)
+        return hipFuncSetAttribute((const void*)k_attn_decode<kQ8K>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    return hipFuncSetAttribute((const void*)k_attn_decode<kQ8_0>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+}
+
+hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, int nh, int nkv, int hd, const float* qn,
+                                   const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
+                                   const int* len, float* kc, float* vc, int64_t kv_stream_stride, int max_seq,
+                                   int max_splits, float* part, unsigned* counter, uint8_t* act, float* ctx_out,
+                                   float* q_out, hipStream_t s) {
+    if (!attn_decode_fits(vdt, nh, nkv, hd, max_splits)) return hipErrorInvalidValue;
+    const float inv_hd = (float)(1.0 / (double)hd);
+    const float scale = (float)(1.0 / sqrt((double)hd));
+    const dim3 grid(B, nkv, (max_seq + kAttnSplitFused - 1) / kAttnSplitFused);  // partial records: max_splits per head
+    const size_t lds = attn_decode_lds(nh, nkv, hd, kAttnSplitFused, max_splits);
+    if (vdt == kQ8K)
+        hipLaunchKernelGGL((k_attn_decode<kQ8K>), grid, dim3(256), lds, s, qkv, qkv_n, nh, nkv, hd, qn, kn, eps, inv_hd,
+                           interleaved, cos_t, sin_t, len, kc, vc, kv_stream_stride, max_seq, kAttnSplitFused, scale, part,
+                           max_splits, counter, act, ctx_out, q_out);
+    else
+        hipLaunchKernelGGL((k_attn_decode<kQ8_0>), grid, dim3(256), lds, s, qkv, qkv_n, nh, nkv, hd, qn, kn, eps, inv_hd,
+                           interleaved, cos_t, sin_t, len, kc, vc, kv_stream_stride, max_seq, kAttnSplitFused, scale, part,
+                           max_splits, counter, act, ctx_out, q_out);
     return hipGetLastError();
 }
 

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -66,6 +67,8 @@ struct sxq_lm {
     float* am_val = nullptr;        // argmax partials [max_batch * kArgmaxSlices]
     int* am_idx = nullptr;
     unsigned* am_count = nullptr;   // per-stream arrival counters (zero between steps)
+    unsigned* attn_count = nullptr; // per-(stream, KV head) arrival counters of the fused attention
+    bool attn_fused = false;
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
     hipStream_t cap = nullptr;
     std::map<GraphKey, hipGraphExec_t> graphs;
@@ -182,14 +185,24 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
         STEP(launch_gemv_rmsnorm(L.wqkv.w, norm_in(lm->h, L.attn_norm, tr ? slot(nd) : nullptr), n, lm->act_a, lm->qkv,
                                  lm->qkv_n, L.bqkv, nullptr, 0, s));
         if (tr) STEP(record(lm->qkv, (size_t)n * lm->qkv_n));
-        STEP(launch_qk_rope_append(lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim,
-                                   c.qk_norm ? L.q_norm : nullptr, c.qk_norm ? L.k_norm : nullptr, c.norm_eps,
-                                   c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len, lm->qbuf, kc, vc,
-                                   lm->kv_stream_stride, c.max_seq, s));
-        if (tr) STEP(record(lm->qbuf, (size_t)n * lm->ctx));
-        STEP(launch_attention(lm->vdt, lm->qbuf, kc, vc, lm->d_len, n, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
-                              lm->kv_stream_stride, kAttnSplit, lm->max_splits, lm->part, lm->act_o,
-                              tr ? slot((size_t)n * lm->ctx) : nullptr, s));
+        const float* qn = c.qk_norm ? L.q_norm : nullptr;
+        const float* kn = c.qk_norm ? L.k_norm : nullptr;
+        if (lm->attn_fused) {
+            float* q_slot = tr ? slot((size_t)n * lm->ctx) : nullptr;
+            float* ctx_slot = tr ? slot((size_t)n * lm->ctx) : nullptr;
+            STEP(launch_attention_decode(lm->vdt, lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn, kn,
+                                         c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len, kc, vc,
+                                         lm->kv_stream_stride, c.max_seq, lm->max_splits, lm->part, lm->attn_count,
+                                         lm->act_o, ctx_slot, q_slot, s));
+        } else {
+            STEP(launch_qk_rope_append(lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn, kn, c.norm_eps,
+                                       c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len, lm->qbuf, kc, vc,
+                                       lm->kv_stream_stride, c.max_seq, s));
+            if (tr) STEP(record(lm->qbuf, (size_t)n * lm->ctx));
+            STEP(launch_attention(lm->vdt, lm->qbuf, kc, vc, lm->d_len, n, c.n_heads, c.n_kv_heads, c.head_dim,
+                                  c.max_seq, lm->kv_stream_stride, kAttnSplit, lm->max_splits, lm->part, lm->act_o,
+                                  tr ? slot((size_t)n * lm->ctx) : nullptr, s));
+        }
         STEP(launch_gemv(L.wo.w, lm->act_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
         if (tr) STEP(record(lm->h, nd));
         STEP(launch_gemv_rmsnorm(L.w13.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), n, lm->act_a, lm->gu,
@@ -290,7 +303,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->h, sizeof(float) * (size_t)MB * c.dim);
     A((void**)&lm->qkv, sizeof(float) * (size_t)MB * lm->qkv_n);
     A((void**)&lm->qbuf, sizeof(float) * (size_t)MB * lm->ctx);
-    A((void**)&lm->part, sizeof(float) * (size_t)MB * c.n_heads * lm->max_splits * (2 + hd));
+    A((void**)&lm->part, sizeof(float) * (size_t)MB * c.n_heads * lm->max_splits * (hd + 4));
     A((void**)&lm->gu, sizeof(float) * (size_t)MB * 2 * I);
     A((void**)&lm->logits, sizeof(float) * (size_t)MB * c.vocab);
     const size_t ab = act_block_bytes(lm->vdt), bs = block_size(lm->vdt);
@@ -302,6 +315,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->am_val, sizeof(float) * MB * kArgmaxSlices);
     A((void**)&lm->am_idx, sizeof(int) * MB * kArgmaxSlices);
     A((void**)&lm->am_count, sizeof(unsigned) * MB);
+    A((void**)&lm->attn_count, sizeof(unsigned) * MB * c.n_kv_heads);
     if (e != hipSuccess) {
         destroy_lm(lm);
         return hip_fail(e, "lm_create: allocation");
@@ -335,6 +349,13 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     if (e == hipSuccess) e = hipMemset(lm->d_len, 0, sizeof(int) * MB);
     if (e == hipSuccess) e = hipMemset(lm->d_ids, 0, sizeof(int) * MB * lm->ids_per);
     if (e == hipSuccess) e = hipMemset(lm->am_count, 0, sizeof(unsigned) * MB);
+    if (e == hipSuccess) e = hipMemset(lm->attn_count, 0, sizeof(unsigned) * MB * c.n_kv_heads);
+    lm->attn_fused = getenv("SXQ_ATTN_UNFUSED") == nullptr && attn_decode_fits(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits);
+    if (e == hipSuccess && lm->attn_fused &&
+        attn_decode_prepare(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits) != hipSuccess) {
+        (void)hipGetLastError();  // clear it: the three-kernel path needs no opt-in
+        lm->attn_fused = false;
+    }
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&lm->cap, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {

@@ -211,14 +211,24 @@ def _replay_step(ora, lm, cfg, W, tr, s, pos, frame=None):
     return logits
 
 
-@pytest.mark.parametrize("kind", ["fish_q4k", "fish_q8_0", "cv2_q8_0", "cv2_q4_0", "ragged"])
-def test_every_op_of_a_step_matches_oracle(cuda, ora, kind):
+# kinds ending in "_3k" force the three-kernel attention (RoPE/append, split partials,
+# merge) instead of the fused kernel; "long" has 51 attention splits, more than the
+# fused kernel stages in one chunk of its merge.
+@pytest.mark.parametrize("kind", ["fish_q4k", "fish_q8_0", "cv2_q8_0", "cv2_q4_0", "ragged", "fish_q4k_3k",
+                                  "ragged_3k", "cv2_q8_0_3k", "long"])
+def test_every_op_of_a_step_matches_oracle(cuda, ora, kind, monkeypatch):
+    if kind.endswith("_3k"):
+        monkeypatch.setenv("SXQ_ATTN_UNFUSED", "1")  # read when the engine is created
     if kind.startswith("fish"):
-        cfg = _fish_small(dtype=GgmlDType.Q4K if kind == "fish_q4k" else GgmlDType.Q8_0)
+        cfg = _fish_small(dtype=GgmlDType.Q8_0 if kind == "fish_q8_0" else GgmlDType.Q4K)
         lengths = [40]
     elif kind.startswith("cv2"):
-        cfg = D.cosyvoice2_lm_config(n_layers=2, max_seq=96, dtype=GgmlDType.Q8_0 if kind == "cv2_q8_0" else GgmlDType.Q4_0)
+        cfg = D.cosyvoice2_lm_config(n_layers=2, max_seq=96, dtype=GgmlDType.Q4_0 if kind == "cv2_q4_0" else GgmlDType.Q8_0)
         lengths = [70]  # two attention splits
+    elif kind == "long":
+        cfg = D.fish_s2_slow_ar_config(n_layers=1, max_seq=1664, vocab=4096, n_codebooks=10, codebook_size=64,
+                                       semantic_begin=3000, semantic_end=4095)
+        lengths = [1600]
     else:
         cfg = _fish_small(n_layers=1, max_batch=4)
         lengths = [5, 70, 17, 0]
