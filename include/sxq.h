@@ -51,6 +51,9 @@ typedef enum {
 /* sxq_qmm_forward flags */
 #define SXQ_DEVICE_PTRS 0u /* x, y, bias are device pointers; async on `stream` */
 #define SXQ_HOST_PTRS 1u   /* x, y, bias are host pointers; the call synchronises */
+#define SXQ_BIT_EXACT 2u   /* every row count through Candle's integer vec-dot (bit-identical); without it
+                              a Q4_K weight with >= 64 rows of x runs the f16 MFMA prefill GEMM, whose
+                              outputs differ from Candle's by less than 2^-10 * sum_k |w_k x_k| */
 
 /* Thread-local text of the last failure on this thread ("" if none). */
 const char *sxq_last_error(void);

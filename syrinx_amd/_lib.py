@@ -23,6 +23,7 @@ STATUS_NAMES = {
     ERR_OOM: "OOM",
 }
 HOST_PTRS = 1
+BIT_EXACT = 2  # SXQ_BIT_EXACT
 DEVICE_PTRS = 0
 
 

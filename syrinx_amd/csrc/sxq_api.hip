@@ -239,7 +239,7 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
                            float* y, const float* bias, unsigned flags, void* stream) {
     if (!q) return fail(SXQ_ERR_INVALID, "qmm_forward: null handle");
     if (!shape || ndim <= 0) return fail(SXQ_ERR_INVALID, "qmm_forward: missing input shape");
-    if (flags & ~SXQ_HOST_PTRS) return fail(SXQ_ERR_INVALID, "qmm_forward: unknown flags 0x%x", flags);
+    if (flags & ~(SXQ_HOST_PTRS | SXQ_BIT_EXACT)) return fail(SXQ_ERR_INVALID, "qmm_forward: unknown flags 0x%x", flags);
     const std::string ss = shape_str(shape, ndim);
     if (ndim < 2) return fail(SXQ_ERR_SHAPE, "input tensor has only one dimension %s", ss.c_str());
     if (strides) {
@@ -270,7 +270,10 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
     const int64_t k = q->w.k, n = q->w.n;
     const int vdt = vec_dot_type(q->w.dtype);
     const int64_t nbv = k / block_size(vdt);
-    const size_t act_bytes = (size_t)m * (size_t)nbv * act_block_bytes(vdt);
+    // Many rows of a Q4_K weight: the f16 MFMA GEMM (operands rounded to f16, error below
+    // 2^-10 * sum |w x| per output) unless SXQ_BIT_EXACT asks for Candle's integer vec-dot.
+    const bool gemm = q->w.dtype == kQ4K && m >= kGemmMinRows && !(flags & SXQ_BIT_EXACT);
+    const size_t act_bytes = gemm ? (size_t)m * (size_t)k * 2 : (size_t)m * (size_t)nbv * act_block_bytes(vdt);
 
     // One stream-ordered workspace: [act | x | y | bias] (the last three only for host pointers).
     const size_t xb = host ? (size_t)(m * k) * 4 : 0, yb = host ? (size_t)(m * n) * 4 : 0;
@@ -294,8 +297,13 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
             dbias = hb;
         }
     }
-    if (e == hipSuccess) e = launch_quantize_act(vdt, false, dx, k, (int)m, (int)k, act, s);
-    for (int64_t r0 = 0; r0 < m && e == hipSuccess; r0 += 16) {
+    if (gemm) {
+        if (e == hipSuccess) e = launch_x_to_f16_perm(dx, k, (int)m, (int)k, act, s);
+        if (e == hipSuccess) e = launch_gemm_q4k(q->w, act, (int)m, dy, n, dbias, nullptr, 0, s);
+    } else if (e == hipSuccess) {
+        e = launch_quantize_act(vdt, false, dx, k, (int)m, (int)k, act, s);
+    }
+    for (int64_t r0 = 0; !gemm && r0 < m && e == hipSuccess; r0 += 16) {
         const int mm = (int)(m - r0 < 16 ? m - r0 : 16);
         e = launch_gemv(q->w, (const uint8_t*)act + (size_t)r0 * nbv * act_block_bytes(vdt), mm, dy + r0 * n, n, dbias, nullptr, 0, s);
     }

@@ -47,6 +47,13 @@ struct NormIn {
 hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,
                                int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s);
 
+// Prefill GEMM for Q4_K weights (sxq_gemm.hip): rows of x rounded to f16 in the GEMM's
+// K order (xh: m * k halfs), then y = xh . dequant(W)^T on MFMA (+ bias, + res).
+constexpr int kGemmMinRows = 64;  // QMatMul::forward uses the GEMM from this many rows on
+hipError_t launch_x_to_f16_perm(const float* x, int64_t ldx, int m, int k, void* xh, hipStream_t s);
+hipError_t launch_gemm_q4k(const QWeight& w, const void* xh, int m, float* y, int64_t ldy, const float* bias,
+                           const float* res, int64_t ldr, hipStream_t s);
+
 }  // namespace sxq
 
 // The QMatMul handle behind the C-ABI's opaque sxq_qmm.

@@ -23,7 +23,7 @@ from typing import Sequence
 
 import torch
 
-from ._lib import HOST_PTRS, SxqError, check, lib
+from ._lib import BIT_EXACT, HOST_PTRS, SxqError, check, lib
 
 
 class GgmlDType(enum.IntEnum):
@@ -215,8 +215,12 @@ class QMatMul:
         """The sxq_qmm* pointer (for callers that drive the C-ABI directly)."""
         return self._h.value if self._h is not None else 0
 
-    def forward(self, xs: torch.Tensor, bias: torch.Tensor = None) -> torch.Tensor:
-        """Module::forward.  f32, contiguous, last dim == k, rank >= 2 (Candle's checks)."""
+    def forward(self, xs: torch.Tensor, bias: torch.Tensor = None, exact: bool = False) -> torch.Tensor:
+        """Module::forward.  f32, contiguous, last dim == k, rank >= 2 (Candle's checks).
+
+        Outputs equal Candle's CPU vec-dot bit for bit, except that a Q4_K weight applied
+        to 64 or more rows runs the f16 MFMA prefill GEMM (error below
+        2^-10 * sum |w x| per output); exact=True keeps the bit-identical path there too."""
         n, k = self._shape
         if self._dense is not None:
             w = self._dense
@@ -238,7 +242,8 @@ class QMatMul:
             if bias.numel() != n:
                 raise SxqError(4, f"bias of {bias.numel()} elements for {n} outputs")
         check(lib().sxq_qmm_forward(self._h, _ptr(xs), shape, xs.dim(), strides, _ptr(y),
-                                    _ptr(bias) if bias is not None else None, 0, _stream_ptr(xs.device)))
+                                    _ptr(bias) if bias is not None else None, BIT_EXACT if exact else 0,
+                                    _stream_ptr(xs.device)))
         return y
 
     __call__ = forward
@@ -258,7 +263,7 @@ class QMatMul:
         return out
 
 
-def qmatmul_host(qmm: QMatMul, x_np, bias_np=None):
+def qmatmul_host(qmm: QMatMul, x_np, bias_np=None, exact: bool = False):
     """forward() with host (numpy) buffers through SXQ_HOST_PTRS: the FFI path a Rust
     caller without device tensors would use."""
     import numpy as np
@@ -272,5 +277,5 @@ def qmatmul_host(qmm: QMatMul, x_np, bias_np=None):
         bias_np = np.ascontiguousarray(bias_np, dtype=np.float32)
         b = bias_np.ctypes.data_as(ctypes.c_void_p)
     check(lib().sxq_qmm_forward(qmm._h, x.ctypes.data_as(ctypes.c_void_p), shape, x.ndim, None,
-                                y.ctypes.data_as(ctypes.c_void_p), b, HOST_PTRS, None))
+                                y.ctypes.data_as(ctypes.c_void_p), b, HOST_PTRS | (BIT_EXACT if exact else 0), None))
     return y

@@ -2,7 +2,9 @@
 
 Bar: bit-exact.  Weight and activation blocks are byte-identical, dequantized weights
 bit-identical, and QMatMul outputs bit-identical to Candle's generic vec-dot order,
-for every row count (decode GEMV) -- integer and float steps replay Candle's order.
+for every row count of the decode GEMV -- integer and float steps replay Candle's order.
+The prefill GEMM (Q4_K, >= 64 rows) rounds both operands to f16 for MFMA: it is held to
+the rounding bound of that, against the f64 product of the exactly dequantized weight.
 """
 import threading
 
@@ -117,11 +119,11 @@ CASES = [
     (G.Q4K, 1003, 2560, 5),    # n not a multiple of the 8-row group
     (G.Q4K, 9728, 2560, 17),   # two 16-row slabs
     (G.Q8_0, 2560, 9728, 4),   # Q8_0 at the Qwen3-4B shape
-    # >= 16384 rows: the row-streaming Q4_K kernel; 16389 leaves a partial last row set
+    # tall matrices; 16389 rows leave a partial last workgroup of rows
     (G.Q4K, 16389, 1024, 1),
     (G.Q4K, 16389, 1024, 2),
     (G.Q4K, 16389, 512, 3),
-    (G.Q4K, 16384, 9728, 4),   # nb = 38: each wave's rounds span several row sets
+    (G.Q4K, 16384, 9728, 4),   # nb = 38 blocks per row, four activation rows
     (G.Q4K, 19456, 2560, 1),   # Qwen3-4B fused w1|w3
 ]
 
@@ -152,7 +154,7 @@ def test_bias_batch_shape_and_host_pointers(cuda, ora):
 
 
 def test_bias_on_tall_q4k(cuda, ora):
-    # bias epilogue of the row-streaming kernel, rows not a multiple of 8
+    # bias epilogue on a tall Q4_K matrix, rows not a multiple of 8
     n, k = 16395, 512
     w = _weights(n, k, 31)
     b = (np.random.default_rng(32).standard_normal(n) * 0.02).astype(np.float32)
@@ -228,3 +230,40 @@ def test_full_size_tied_head_q4k(cuda, ora):
     y = qmm.forward(torch.from_numpy(x).to(cuda)).cpu().numpy()
     blocks = qt.data().cpu().numpy().reshape(n, -1)
     _eq_bits(y, ora.matmul(ora.Q4K, x, blocks))
+
+
+# ------------------------------------------------------------------ prefill GEMM (MFMA)
+PREFILL = [
+    (300, 512, 200),     # rows and outputs not multiples of the 128 x 128 tile, with bias
+    (6144, 2560, 512),   # Qwen3-4B fused wqkv at a 512-token prompt
+    (2560, 9728, 128),   # down projection, K = 9728 (38 blocks)
+]
+
+
+@pytest.mark.parametrize("n,k,m", PREFILL)
+def test_prefill_gemm_within_f16_rounding_bound(cuda, ora, n, k, m):
+    w = _weights(n, k, 40 + n % 5)
+    x = _acts(m, k, 41)
+    b = (np.random.default_rng(42).standard_normal(n) * 0.02).astype(np.float32) if n == 300 else None
+    blocks = ora.quantize(ora.Q4K, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    xt = torch.from_numpy(x).to(cuda)
+    y = qmm.forward(xt, bias=None if b is None else torch.from_numpy(b).to(cuda)).cpu().numpy().astype(np.float64)
+    wd = ora.dequantize(ora.Q4K, blocks, k).reshape(n, k).astype(np.float64)  # Candle's to_float, exact
+    y64 = x.astype(np.float64) @ wd.T + (0.0 if b is None else b.astype(np.float64))
+    # Bound: each operand rounded to f16 (relative 2^-11, or 2^-25 absolute in the
+    # subnormal range), products and sums in f32.
+    S = np.abs(x).astype(np.float64) @ np.abs(wd).T
+    tol = (2.0 ** -10 + k * 2.0 ** -24) * S + 2.0 ** -24 * np.abs(x).sum(1, keepdims=True) + 1e-30
+    err = np.abs(y - y64)
+    assert (err <= tol).all(), f"{int((err > tol).sum())} outputs beyond the bound; worst ratio {float((err / tol).max()):.3g}"
+    # typical error, relative to the output scale
+    rel = float(np.sqrt(np.mean(err ** 2)) / np.sqrt(np.mean(y64 ** 2)))
+    assert rel < 2e-3, rel
+    # the exact path stays available and bit-identical for the same call
+    if m <= 200:
+        y_exact = qmm.forward(xt, bias=None if b is None else torch.from_numpy(b).to(cuda), exact=True).cpu().numpy()
+        want = ora.matmul(ora.Q4K, x, blocks)
+        if b is not None:
+            want = (want + b[None, :]).astype(np.float32)
+        _eq_bits(y_exact, want)
