@@ -47,9 +47,12 @@ def parse():
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--gemv-iters", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--mode", default="decode", choices=["decode", "gemv", "copy"],
+    ap.add_argument("--mode", default="decode", choices=["decode", "gemv", "copy", "prefill"],
                     help="decode: the benchmark; gemv: only the per-token GEMV pass (for counter runs); "
-                         "copy: a plain device copy of known size (the counter scale)")
+                         "copy: a plain device copy of known size (the counter scale); prefill: the "
+                         "512-token prefill GEMMs of one Qwen3-4B layer on MFMA")
+    ap.add_argument("--prefill-tokens", type=int, default=512)
+    ap.add_argument("--prefill-iters", type=int, default=20)
     return ap.parse_args()
 
 
@@ -156,6 +159,44 @@ def cpu_baseline(lm, torch, budget_s=12.0):
                       f"in {total:.1f} s"}
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA, MI355X
+
+
+def prefill_gemms(torch, tokens, iters):
+    """One Qwen3-4B layer's projections at a `tokens`-row prompt through QMatMul.forward
+    (Q4_K weights, the f16 MFMA prefill GEMM incl. its f16 conversion of x)."""
+    from syrinx_amd import GgmlDType, QMatMul, QTensor
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(3)
+    shapes = [(6144, 2560), (2560, 4096), (2 * 9728, 2560), (2560, 9728)]  # wqkv, wo, w1|w3, w2
+    mats, xs = [], []
+    for n, k in shapes:
+        w = torch.randn(n, k, device=dev, generator=g) * 0.02
+        mats.append(QMatMul.from_qtensor(QTensor.quantize(w, GgmlDType.Q4K)))
+        xs.append(torch.randn(tokens, k, device=dev, generator=g))
+        del w
+    flops = 2.0 * tokens * sum(n * k for n, k in shapes)
+    for _ in range(3):
+        for q, x in zip(mats, xs):
+            q.forward(x)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(iters):
+        for q, x in zip(mats, xs):
+            q.forward(x)
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": f"Qwen3-4B layer projections (wqkv, wo, w1|w3, w2) at M={tokens}, Q4_K weights, "
+                        "f16 MFMA with f32 accumulation",
+            "us_per_layer": round(ms * 1000.0, 2), "flops_per_layer": flops, "achieved": round(tflops, 1),
+            "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "ms_36_layers": round(36 * ms, 3)}
+
+
 def copy_calibration(torch, iters=8):
     """A plain device-to-device copy of 1 GiB: its counters give the FETCH/WRITE scale."""
     n = 1 << 30
@@ -176,6 +217,9 @@ def main():
     import torch
     if args.mode == "copy":
         copy_calibration(torch)
+        return
+    if args.mode == "prefill":
+        print(json.dumps({"mode": "prefill", "prefill": prefill_gemms(torch, args.prefill_tokens, args.prefill_iters)}))
         return
     from syrinx_amd import GgmlDType
     from syrinx_amd import decoder as D

@@ -11,9 +11,11 @@
  * host pointers with SXQ_HOST_PTRS (then it copies and synchronises).
  *
  * Threading: every function is safe to call concurrently from several host threads,
- * including sxq_qmm_forward on one handle (the handle is read-only after creation and
- * each call allocates its own stream-ordered workspace), mirroring the reference's
- * shared `Arc<Qwen2Lm>` use (tests/real_lm_hammer.rs:48-83).
+ * including sxq_qmm_forward on one handle (the handle is read-only after creation),
+ * mirroring the reference's shared `Arc<Qwen2Lm>` use (tests/real_lm_hammer.rs:48-83).
+ * sxq_qmm_forward's workspace is one buffer per device kept between calls (grown to the
+ * largest call so far, held until the process ends); calls take turns on it through an
+ * event, so concurrent calls on one device run one after another on the GPU.
  */
 #ifndef SXQ_H
 #define SXQ_H

@@ -3,8 +3,10 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/sxq.h"
@@ -38,6 +40,50 @@ sxq_status hip_fail(hipError_t e, const char* what) {
 using namespace sxq::abi;
 
 namespace {
+
+// QMatMul::forward's workspace: one buffer per device, kept between calls.  A call holds
+// it from acquire to release: it makes its stream wait for the previous user's event (so
+// calls on different streams, or from different threads, take turns on the buffer), grows
+// it stream-ordered when too small, and records the event after its last use.  Allocating
+// per call instead (hipMallocAsync / hipFreeAsync) made every call wait for the previous
+// one's kernels on the host.
+struct Workspace {
+    std::mutex mu;
+    void* buf = nullptr;
+    size_t size = 0;
+    hipEvent_t done = nullptr;
+};
+Workspace g_ws[64];
+
+struct WorkspaceLease {
+    Workspace* w = nullptr;
+    hipStream_t s = nullptr;
+    uint8_t* ptr = nullptr;
+    hipError_t err = hipSuccess;
+    WorkspaceLease(int dev, size_t need, hipStream_t st) : s(st) {
+        if (dev < 0 || dev >= 64) { err = hipErrorInvalidDevice; return; }
+        w = &g_ws[dev];
+        w->mu.lock();
+        if (!w->done) err = hipEventCreateWithFlags(&w->done, hipEventDisableTiming);
+        if (err == hipSuccess) err = hipStreamWaitEvent(s, w->done, 0);
+        if (err == hipSuccess && w->size < need) {
+            const size_t grow = (need + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+            if (w->buf) err = hipFreeAsync(w->buf, s);
+            w->buf = nullptr;
+            w->size = 0;
+            if (err == hipSuccess) err = hipMallocAsync(&w->buf, grow, s);
+            if (err == hipSuccess) w->size = grow;
+        }
+        ptr = (uint8_t*)w->buf;
+    }
+    ~WorkspaceLease() {
+        if (!w) return;
+        if (w->done) (void)hipEventRecord(w->done, s);
+        w->mu.unlock();
+    }
+    WorkspaceLease(const WorkspaceLease&) = delete;
+    WorkspaceLease& operator=(const WorkspaceLease&) = delete;
+};
 
 bool quant_weight_dtype(int dt) { return dt == kQ4_0 || dt == kQ8_0 || dt == kQ4K; }
 bool block_dtype(int dt) { return dt == kQ4_0 || dt == kQ8_0 || dt == kQ4K || dt == kQ8K; }
@@ -273,14 +319,16 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
     // Many rows of a Q4_K weight: the f16 MFMA GEMM (operands rounded to f16, error below
     // 2^-10 * sum |w x| per output) unless SXQ_BIT_EXACT asks for Candle's integer vec-dot.
     const bool gemm = q->w.dtype == kQ4K && m >= kGemmMinRows && !(flags & SXQ_BIT_EXACT);
-    const size_t act_bytes = gemm ? (size_t)m * (size_t)k * 2 : (size_t)m * (size_t)nbv * act_block_bytes(vdt);
+    const size_t act_bytes =
+        gemm ? gemm_q4k_workspace(n, (int)m, k) : (size_t)m * (size_t)nbv * act_block_bytes(vdt);
 
     // One stream-ordered workspace: [act | x | y | bias] (the last three only for host pointers).
     const size_t xb = host ? (size_t)(m * k) * 4 : 0, yb = host ? (size_t)(m * n) * 4 : 0;
     const size_t bb = (host && bias) ? (size_t)n * 4 : 0;
     auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    uint8_t* ws = nullptr;
-    HIP_TRY(hipMallocAsync((void**)&ws, up(act_bytes) + up(xb) + up(yb) + up(bb), s), "qmm_forward: workspace");
+    WorkspaceLease lease(q->device, up(act_bytes) + up(xb) + up(yb) + up(bb), s);
+    HIP_TRY(lease.err, "qmm_forward: workspace");
+    uint8_t* ws = lease.ptr;
     void* act = ws;
     const float* dx = x;
     float* dy = y;
@@ -298,7 +346,7 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
         }
     }
     if (gemm) {
-        if (e == hipSuccess) e = launch_x_to_f16_perm(dx, k, (int)m, (int)k, act, s);
+        if (e == hipSuccess) e = launch_gemm_q4k_prep(dx, k, (int)m, n, (int)k, act, s);
         if (e == hipSuccess) e = launch_gemm_q4k(q->w, act, (int)m, dy, n, dbias, nullptr, 0, s);
     } else if (e == hipSuccess) {
         e = launch_quantize_act(vdt, false, dx, k, (int)m, (int)k, act, s);
@@ -308,10 +356,8 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
         e = launch_gemv(q->w, (const uint8_t*)act + (size_t)r0 * nbv * act_block_bytes(vdt), mm, dy + r0 * n, n, dbias, nullptr, 0, s);
     }
     if (host && e == hipSuccess) e = hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, s);
-    hipError_t ef = hipFreeAsync(ws, s);
     if (host && e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "qmm_forward");
-    if (ef != hipSuccess) return hip_fail(ef, "qmm_forward: free");
     return SXQ_OK;
 }
 

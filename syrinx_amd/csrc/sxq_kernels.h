@@ -47,11 +47,14 @@ struct NormIn {
 hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,
                                int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s);
 
-// Prefill GEMM for Q4_K weights (sxq_gemm.hip): rows of x rounded to f16 in the GEMM's
-// K order (xh: m * k halfs), then y = xh . dequant(W)^T on MFMA (+ bias, + res).
+// Prefill GEMM for Q4_K weights (sxq_gemm.hip): y = x . dequant(W)^T on MFMA with f16
+// operands (+ bias, + res).  The workspace (gemm_q4k_workspace bytes) holds x rounded to
+// f16 in the GEMM's K order and, when K is split across workgroups, the partial tiles
+// and their counters; launch_gemm_q4k_prep fills it from x, then launch_gemm_q4k runs.
 constexpr int kGemmMinRows = 64;  // QMatMul::forward uses the GEMM from this many rows on
-hipError_t launch_x_to_f16_perm(const float* x, int64_t ldx, int m, int k, void* xh, hipStream_t s);
-hipError_t launch_gemm_q4k(const QWeight& w, const void* xh, int m, float* y, int64_t ldy, const float* bias,
+size_t gemm_q4k_workspace(int64_t n, int m, int64_t k);
+hipError_t launch_gemm_q4k_prep(const float* x, int64_t ldx, int m, int64_t n, int k, void* ws, hipStream_t s);
+hipError_t launch_gemm_q4k(const QWeight& w, const void* ws, int m, float* y, int64_t ldy, const float* bias,
                            const float* res, int64_t ldr, hipStream_t s);
 
 }  // namespace sxq

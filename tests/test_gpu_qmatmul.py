@@ -240,6 +240,33 @@ PREFILL = [
 ]
 
 
+def _prefill_check(ora, x, blocks, k, y, b=None):
+    wd = ora.dequantize(ora.Q4K, blocks, k).reshape(-1, k).astype(np.float64)  # Candle's to_float, exact
+    y64 = x.astype(np.float64) @ wd.T + (0.0 if b is None else b.astype(np.float64))
+    S = np.abs(x).astype(np.float64) @ np.abs(wd).T
+    tol = (2.0 ** -10 + k * 2.0 ** -24) * S + 2.0 ** -24 * np.abs(x).sum(1, keepdims=True) + 1e-30
+    err = np.abs(y - y64)
+    assert (err <= tol).all(), f"{int((err > tol).sum())} outputs beyond the bound; worst ratio {float((err / tol).max()):.3g}"
+
+
+@pytest.mark.parametrize("splits", ["1", "3"])
+def test_prefill_gemm_split_counts_agree(cuda, ora, monkeypatch, splits):
+    """The same product with K unsplit and split unevenly across workgroups (4 blocks
+    into 1 + 1 + 2): both within the f16 bound, and the split partials are added in a
+    fixed order, so repeated calls give identical bits."""
+    n, k, m = 600, 1024, 256
+    w = _weights(n, k, 43)
+    x = _acts(m, k, 44)
+    blocks = ora.quantize(ora.Q4K, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    xt = torch.from_numpy(x).to(cuda)
+    monkeypatch.setenv("SXQ_GEMM_SPLITS", splits)
+    y1 = qmm.forward(xt).cpu().numpy()
+    y2 = qmm.forward(xt).cpu().numpy()
+    _eq_bits(y1, y2)
+    _prefill_check(ora, x, blocks, k, y1.astype(np.float64))
+
+
 @pytest.mark.parametrize("n,k,m", PREFILL)
 def test_prefill_gemm_within_f16_rounding_bound(cuda, ora, n, k, m):
     w = _weights(n, k, 40 + n % 5)
