@@ -43,14 +43,15 @@ SXQ_HD int q4k_perm_elem(int p) {
     return 64 * s + 32 * (j & 1) + 2 * g + h + 8 * (j >> 1);
 }
 
-constexpr int kGemmBM = 128, kGemmBN = 256, kGemmStages = 4;
-constexpr int kGemmStageBytes = kGemmBM * 64 * 2;   // activations of one K group: 128 rows x 64 halfs
-constexpr int kGemmWStageBytes = kGemmBN * 2 * 16;  // weights of one K group: 256 rows x 2 segments
-constexpr int kGemmWOff = kGemmStages * kGemmStageBytes;
-constexpr int kGemmHdOff = kGemmWOff + kGemmStages * kGemmWStageBytes;  // 256 block headers
+constexpr int kGemmBM = 256, kGemmBN = 128;
+constexpr int kGemmAStage = kGemmBM * 64 * 2;  // activations of one K group: 256 rows x 64 halfs
+constexpr int kGemmWStage = kGemmBN * 2 * 16;  // weights of one K group: 128 rows x 2 segments
+constexpr int kGemmWOff = 2 * kGemmAStage;     // within one K half's region: 2 stages each
+constexpr int kGemmHdOff = kGemmWOff + 2 * kGemmWStage;  // block headers, 1 KB per wave
+constexpr int kGemmHalfBytes = kGemmHdOff + 4 * 1024;    // 77824
 
 int gemm_xh_rows(int m) { return (m + kGemmBM - 1) / kGemmBM * kGemmBM; }
-size_t gemm_q4k_lds() { return (size_t)kGemmHdOff + kGemmBN * 16; }
+size_t gemm_q4k_lds() { return 2 * (size_t)kGemmHalfBytes; }
 
 // x f32 [m][k] (row stride ldx) -> xh f16 [gemm_xh_rows(m)][k] in the GEMM K order,
 // xh[r][256b + p] = f16(x[r][256b + q4k_perm_elem(p)]), rows past m zero.  Each thread
@@ -157,13 +158,10 @@ SXQ_DEV f32x4 load16_agent(const float* p) {
     asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p));
     return r;
 }
-SXQ_DEV void vm_wait0(f32x4 (&v)[6][4]) {
+SXQ_DEV void vm_wait0(f32x4 (&v)[3][4]) {
     asm volatile("s_waitcnt vmcnt(0)" : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[0][2]), "+v"(v[0][3]), "+v"(v[1][0]),
                  "+v"(v[1][1]), "+v"(v[1][2]), "+v"(v[1][3]), "+v"(v[2][0]), "+v"(v[2][1]), "+v"(v[2][2]),
                  "+v"(v[2][3]));
-    asm volatile("s_waitcnt vmcnt(0)" : "+v"(v[3][0]), "+v"(v[3][1]), "+v"(v[3][2]), "+v"(v[3][3]), "+v"(v[4][0]),
-                 "+v"(v[4][1]), "+v"(v[4][2]), "+v"(v[4][3]), "+v"(v[5][0]), "+v"(v[5][1]), "+v"(v[5][2]),
-                 "+v"(v[5][3]));
 }
 
 // Workgroup barrier without the memory fence of __syncthreads(): the fence would make
@@ -173,34 +171,40 @@ SXQ_DEV void vm_wait0(f32x4 (&v)[6][4]) {
 SXQ_DEV void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
 
 // y[m][n] = x[m] . W[n] (+ bias[n], then res[m][n] + that), W Q4_K [n][k] in the device
-// layout, xh from k_x_to_f16_perm (rows padded to 128).  One workgroup of 256 threads
-// per tile or per split of a tile (see GemmPlan).  Wave w owns weight rows n0 + 64w .. +63 and all 128 token rows of
-// the tile: 4 x 2 MFMA tiles of 32 x 32 (128 accumulators per lane).
+// layout, xh from k_x_to_f16_perm (rows padded to 256).  One workgroup of 512 threads per
+// tile (256 token rows x 128 weight rows) or per split of a tile (see GemmPlan).
 //
-// K advances in groups of 64 (a quarter block).  Every operand reaches LDS by direct
-// global->LDS loads, issued 3 groups ahead into a ring of 4 stages, so no load lands in
-// registers and the loop's only waits are the explicit vmcnt counts below.
+// The 8 waves form two K halves of 4: half h takes the tile's K groups h, h+2, h+4, ...
+// (a group is 64 of K, a quarter block); two waves share each SIMD, so one's LDS latency
+// and VALU work hide under the other's MFMAs, and 8 waves draw twice the LDS read rate
+// of 4.  Wave w of a half owns weight rows 32w .. 32w+31 of the tile and all 256 token
+// rows: 8 MFMA tiles of 32 x 32 (128 accumulators per lane), so every dequantized B
+// operand feeds 8 MFMAs.  At the end the halves add their accumulators through LDS, half
+// 0's first, and each half finishes four of the eight 32-row tiles.
+//
+// Every operand reaches LDS by direct global->LDS loads one group ahead, into 2 stages per
+// half, so no load lands in registers and the loop's only waits are explicit vmcnt counts:
 //  - activations: within a stage row r's 16-byte chunk c sits at chunk slot
-//    8r + (c ^ (r & 7)), so the MFMA operand reads of 32 rows spread over all banks;
-//  - weights: lane (n, h) loads segment 2g + h of its two rows into its own slots and
-//    reads them back itself, dequantizing each dword straight into MFMA B registers;
-//  - block headers: one block ahead, decoded once per block into 16 floats per row.
-// One barrier per group (for the shared activation stages).
+//    8r + (c ^ ((r >> 1) & 7)): the MFMA operand reads of any 16 consecutive rows hit 16
+//    different 16-byte bank groups (64 banks of 4 bytes);
+//  - weights: lane (n, h) loads segment 2g + h of its row into its own slot and reads it
+//    back itself, dequantizing each dword straight into MFMA B registers;
+//  - block headers: one block ahead, decoded once per block into 16 floats.
+// One barrier per pair of groups (one per half, in lockstep).
 //
 // A tile split S ways: split z covers blocks [nb*z/S, nb*(z+1)/S); every split stores its
 // partial tile, and the last to arrive (per-tile counter) adds the partials in split order,
 // so the result does not depend on arrival order.
-__global__ __launch_bounds__(256) void k_gemm_q4k(const _Float16* __restrict__ xh, int M, int K,
+__global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ xh, int M, int K,
                                                   const uint4* __restrict__ hdr, const uint4* __restrict__ qs, int N,
                                                   float* __restrict__ y, int64_t ldy, const float* __restrict__ bias,
                                                   const float* res, int64_t ldr, float* part, unsigned* counters,
                                                   int tiles_m, int full, int splits) {
     extern __shared__ uint4 lds[];
-    lds_u8* lbase = (lds_u8*)lds;
     __shared__ bool last;
     const int nb = K >> 8;
     // Workgroups 0 .. full-1 take whole tiles; the rest split the remaining tiles' K range
-    // `splits` ways.  Tile t covers weight rows 256 * (t / tiles_m), token rows 128 * (t % tiles_m).
+    // `splits` ways.  Tile t covers weight rows 128 * (t / tiles_m), token rows 256 * (t % tiles_m).
     const int id = blockIdx.x;
     const int S = id < full ? 1 : splits;
     const int tile = id < full ? id : full + (id - full) / splits;
@@ -209,210 +213,212 @@ __global__ __launch_bounds__(256) void k_gemm_q4k(const _Float16* __restrict__ x
     const int b0 = (int)((int64_t)nb * sp / S), b1 = (int)((int64_t)nb * (sp + 1) / S);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = wave >> 2, wv = wave & 3;  // K half, weight-row slice
     const int ln = lane & 31, lh = lane >> 5;
+    lds_u8* hbase = (lds_u8*)lds + kh * kGemmHalfBytes;
 
-    // Activation loads: chunk slot (4 wave + u) * 64 + lane of a stage is row
-    // r = 32 wave + 8u + lane/8, chunk (lane % 8) ^ (r % 8) of the group.
-    const _Float16* asrc = xh + (int64_t)(m0 + 32 * wave + (lane >> 3)) * K + 8 * ((lane & 7) ^ ((lane >> 3) & 7));
+    // Activation loads: chunk slot (8 wv + u) * 64 + lane of a stage is row
+    // r = 64 wv + 8u + lane/8, chunk (lane % 8) ^ ((r >> 1) % 8) of the group.
+    // (Row r + 8u has (r >> 1) & 7 with bit 2 flipped when u is odd.)
+    const int ar = 64 * wv + (lane >> 3);
+    const int ac0 = (lane & 7) ^ ((ar >> 1) & 7);
+    const _Float16* asrc = xh + (int64_t)(m0 + ar) * K + 8 * ac0;
     const int64_t arow8 = (int64_t)8 * K;
-    // Weight rows of this lane (rows past N clamped: loaded, never stored).
-    const int64_t wr0 = min(n0 + 64 * wave + ln, N - 1), wr1 = min(n0 + 64 * wave + 32 + ln, N - 1);
-    const uint4* q0 = qs + wr0 * nb * 8 + lh;
-    const uint4* q1 = qs + wr1 * nb * 8 + lh;
-    const uint4* hsrc = hdr + (int64_t)min(n0 + 64 * wave + lane, N - 1) * nb;  // header of row 64 wave + lane
-    // LDS byte addresses of this lane's reads (stage, row tile and step offsets are
-    // immediates): activation chunk of step s for row tile 0, weight segments, headers.
+    const int aodd = 8 * ((ac0 ^ 4) - ac0);  // column shift of the odd-u rows, in halfs
+    // Weight row of this lane (rows past N clamped: loaded, never stored).
+    const int64_t wr = min(n0 + 32 * wv + ln, N - 1);
+    const uint4* q0 = qs + wr * nb * 8 + lh;
+    const uint4* hsrc = hdr + wr * nb;  // both halves of the wave load the row's header
+    // LDS byte addresses of this lane's reads (stage and row-tile offsets are immediates):
+    // activation chunk of step s for row tile 0 (rows ln and 32 mt + ln share (r >> 1) & 7).
     uint32_t aaddr[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) aaddr[s] = lds_addr(lbase) + 16 * (8 * ln + ((2 * s + lh) ^ (ln & 7)));
-    lds_u8* wlds = lbase + kGemmWOff + wave * 2048;  // + stage * kGemmWStageBytes + nt * 1024 + lane * 16
-    lds_u8* hlds = lbase + kGemmHdOff + wave * 1024;  // + row-in-wave * 16
+    for (int s = 0; s < 4; ++s) aaddr[s] = lds_addr(hbase) + 16 * (8 * ln + ((2 * s + lh) ^ ((ln >> 1) & 7)));
+    lds_u8* wlds = hbase + kGemmWOff + wv * 1024;  // + stage * kGemmWStage + lane * 16
+    lds_u8* hlds = hbase + kGemmHdOff + wv * 1024;  // + lane * 16
     const uint32_t waddr = lds_addr(wlds) + lane * 16, haddr = lds_addr(hlds) + ln * 16;
 
     auto dma = [](const void* src, lds_u8* dst) {
         __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
     };
-    // the 6 loads of group grp (from the start of K) into stage st
+    // the 9 loads of group grp (from the start of K) into stage st of this half
     auto load_group = [&](int grp, int st) {
         const _Float16* src = asrc + (int64_t)grp * 64;
-        lds_u8* dst = lbase + st * kGemmStageBytes + wave * 4096;
-        dma(src, dst);
-        dma(src + arow8, dst + 1024);
-        dma(src + 2 * arow8, dst + 2048);
-        dma(src + 3 * arow8, dst + 3072);
-        const int wo = (grp >> 2) * 8 + 2 * (grp & 3);
-        lds_u8* wd = wlds + st * kGemmWStageBytes;
-        dma(q0 + wo, wd);
-        dma(q1 + wo, wd + 1024);
+        lds_u8* dst = hbase + st * kGemmAStage + wv * 8192;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) dma(src + u * arow8 + (u & 1 ? aodd : 0), dst + 1024 * u);
+        dma(q0 + (grp >> 2) * 8 + 2 * (grp & 3), wlds + st * kGemmWStage);
     };
-    float sv0[8], nm0[8], sv1[8], nm1[8];
+    float sv[8], nm[8];
     auto scales = [&]() {
-        u32x4 hd0 = ds_read16<0>(haddr);
-        u32x4 hd1 = ds_read16<512>(haddr);
-        lgkm_wait<0>(hd0, hd1);
-        q4k_scales(make_uint4(hd0[0], hd0[1], hd0[2], hd0[3]), sv0, nm0);
-        q4k_scales(make_uint4(hd1[0], hd1[1], hd1[2], hd1[3]), sv1, nm1);
+        u32x4 hd = ds_read16<0>(haddr), hd2 = hd;
+        lgkm_wait<0>(hd, hd2);
+        q4k_scales(make_uint4(hd[0], hd[1], hd[2], hd[3]), sv, nm);
     };
-    floatx16 acc[4][2];
+    floatx16 acc[8];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 8; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
+        for (int i = 0; i < 16; ++i) acc[a][i] = 0.0f;
 
-    // One group on stage ST.  LDS reads run ahead of the MFMAs (the 2 weight reads and
-    // steps 0-1 first, step s + 2 once step s has arrived: at most 12 in flight, the lgkm
-    // counter holds 15), and the B operands of step s + 1 are dequantized between the
-    // MFMAs of step s, whose 32-cycle issue shadow covers about 8 VALU instructions.
+    // One group on stage ST: per step, 8 activation reads, the B operand dequantized
+    // meanwhile, then 8 MFMAs (the other wave of the SIMD covers the read latency).
     auto compute = [&](auto stc) {
         constexpr int ST = decltype(stc)::value;
-        constexpr int AO = ST * kGemmStageBytes, WO = ST * kGemmWStageBytes;
-        u32x4 w0 = ds_read16<WO>(waddr), w1 = ds_read16<WO + 1024>(waddr);
-        u32x4 a[4][4];
-        auto read_step = [&](int s) {
-            a[s][0] = ds_read16<AO>(aaddr[s]);
-            a[s][1] = ds_read16<AO + 4096>(aaddr[s]);
-            a[s][2] = ds_read16<AO + 8192>(aaddr[s]);
-            a[s][3] = ds_read16<AO + 12288>(aaddr[s]);
-        };
-        read_step(0);
-        read_step(1);
-        lgkm_wait<8>(w0, w1);
-        half8 b0 = q4k_bfrag(w0[0], sv0[0], nm0[0], sv0[1], nm0[1]);
-        half8 b1 = q4k_bfrag(w1[0], sv1[0], nm1[0], sv1[1], nm1[1]);
+        constexpr int AO = ST * kGemmAStage, WO = ST * kGemmWStage;
+        u32x4 w = ds_read16<WO>(waddr), w2 = w;
+        lgkm_wait<0>(w, w2);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            if (s < 3) lgkm_wait<4>(a[s][0], a[s][1], a[s][2], a[s][3]);
-            else lgkm_wait<0>(a[s][0], a[s][1], a[s][2], a[s][3]);
-            if (s < 2) read_step(s + 2);
-            half8 nb0 = b0, nb1 = b1;
-            if (s < 3) {
-                nb0 = q4k_bfrag(w0[s + 1], sv0[2 * s + 2], nm0[2 * s + 2], sv0[2 * s + 3], nm0[2 * s + 3]);
-                nb1 = q4k_bfrag(w1[s + 1], sv1[2 * s + 2], nm1[2 * s + 2], sv1[2 * s + 3], nm1[2 * s + 3]);
-            }
+            u32x4 a[8];
+            a[0] = ds_read16<AO>(aaddr[s]);
+            a[1] = ds_read16<AO + 4096>(aaddr[s]);
+            a[2] = ds_read16<AO + 8192>(aaddr[s]);
+            a[3] = ds_read16<AO + 12288>(aaddr[s]);
+            a[4] = ds_read16<AO + 16384>(aaddr[s]);
+            a[5] = ds_read16<AO + 20480>(aaddr[s]);
+            a[6] = ds_read16<AO + 24576>(aaddr[s]);
+            a[7] = ds_read16<AO + 28672>(aaddr[s]);
+            const half8 b = q4k_bfrag(w[s], sv[2 * s], nm[2 * s], sv[2 * s + 1], nm[2 * s + 1]);
+            lgkm_wait<0>(a[0], a[1], a[2], a[3]);
+            lgkm_wait<0>(a[4], a[5], a[6], a[7]);
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const half8 av = __builtin_bit_cast(half8, a[s][mt]);
-                acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b0, acc[mt][0], 0, 0, 0);
-                acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b1, acc[mt][1], 0, 0, 0);
-            }
-            if (s < 3) {
-                // 8 x (1 MFMA, 5 VALU)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-                }
-            }
-            b0 = nb0;
-            b1 = nb1;
+            for (int mt = 0; mt < 8; ++mt)
+                acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a[mt]), b, acc[mt], 0, 0, 0);
         }
     };
 
-    // Prologue: the first block's header, groups 0..2, the first block's scales.  Every
-    // group then issues exactly 6 loads and group 0 of a block also the next block's
-    // header (1 load); loads past the split's end are clamped to its last group / block
-    // (fetched again, never used), so the wait counts below are fixed.
+    // This half's groups: local group li is group 4 b0 + 2 li + kh from the start of K,
+    // li = 0 .. LG-1, in block b0 + li/2.  Prologue: the first block's header and local
+    // group 0.  Local group li then issues exactly 9 loads (local group li + 1, clamped to
+    // the half's last group: fetched again, never used) and, when li is even, the next
+    // block's header.  So when local group li starts, at most the header issued after its
+    // loads (li odd) may still be outstanding.
+    const int LG = 2 * (b1 - b0);
+    const int glast = 4 * (b1 - 1) + 2 + kh;
+    auto grp_of = [&](int li) { return min(4 * b0 + 2 * li + kh, glast); };
     dma(hsrc + b0, hlds);
-    load_group(4 * b0, 0);
-    load_group(4 * b0 + 1, 1);
-    load_group(4 * b0 + 2, 2);
-    SXQ_WAIT_VM(18);  // the header (the 18 group loads may still be in flight)
-    scales();
-
-    const int glast = 4 * b1 - 1;  // last group of the split, from the start of K
-    for (int blk = b0; blk < b1; ++blk) {
+    load_group(grp_of(0), 0);
+    for (int li0 = 0; li0 < LG; li0 += 2) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            // This group's loads are complete once at most the loads issued after them
-            // are outstanding: 6 for each of the next two groups, plus this block's
-            // header load when that came later.  The scheduling barriers keep every load
-            // in its section, so the counts stay exact.
+        for (int j = 0; j < 2; ++j) {
+            const int li = li0 + j;
             __builtin_amdgcn_sched_barrier(0);
-            if (g == 0) SXQ_WAIT_VM(12);
-            else SXQ_WAIT_VM(13);
-            barrier_nofence();  // stage g is filled everywhere; stage (g + 3) % 4 is free
+            if (j == 0) SXQ_WAIT_VM(0);
+            else SXQ_WAIT_VM(1);
+            barrier_nofence();  // stage j is filled everywhere; stage 1 - j is free
             __builtin_amdgcn_sched_barrier(0);
-            load_group(min(4 * (g == 0 ? blk : blk + 1) + ((g + 3) & 3), glast), (g + 3) & 3);
-            if (g == 0) dma(hsrc + min(blk + 1, b1 - 1), hlds);  // the header region is this wave's own
+            if (j == 0) scales();  // block b0 + li/2 (read before its region is reloaded)
+            load_group(grp_of(li + 1), 1 - j);
+            if (j == 0) dma(hsrc + min(b0 + li / 2 + 1, b1 - 1), hlds);
             __builtin_amdgcn_sched_barrier(0);
-            if (g == 0) compute(std::integral_constant<int, 0>());
-            if (g == 1) compute(std::integral_constant<int, 1>());
-            if (g == 2) compute(std::integral_constant<int, 2>());
-            if (g == 3) compute(std::integral_constant<int, 3>());
+            if (j == 0) compute(std::integral_constant<int, 0>());
+            else compute(std::integral_constant<int, 1>());
         }
-        // the next block's header, issued in group 0: 18 group loads came after it
-        __builtin_amdgcn_sched_barrier(0);
-        SXQ_WAIT_VM(18);
-        __builtin_amdgcn_sched_barrier(0);
-        scales();
     }
-    SXQ_WAIT_VM(0);  // no global->LDS load may still be in flight when the workgroup ends
+    SXQ_WAIT_VM(0);  // no global->LDS load may still be in flight past this point
+    __syncthreads();
 
-    if (S > 1) {
-        // Partial tile of split z of split tile st: float4 j of piece (mt, nt) of thread tid
-        // at part + 4 * ((((st * S + z) * 8 + piece) * 4 + j) * 256 + tid).
-        const int st = tile - full;
-        float* mine = part + (int64_t)(st * S + sp) * 32768 + 4 * tid;
+    // Add the halves, half 0's accumulator first: half 1 hands over its row tiles 0-3 and
+    // keeps 4-7, half 0 the reverse.  Values 4j .. 4j+3 of row tile t of lane `lane` of
+    // wave slice wv of the half that exports sit in float4 red[((half * 4 + wv) * 16 + 4t + j) * 64 + lane].
+    f32x4* red = (f32x4*)lds;
+    auto exchange = [&](auto keepc) {
+        constexpr int KEEP = decltype(keepc)::value, GIVE = 4 - KEEP;
+        f32x4* ex = red + ((kh * 4 + wv) * 16) * 64 + lane;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int j = 0; j < 4; ++j)
+                ex[(4 * t + j) * 64] = f32x4{acc[GIVE + t][4 * j], acc[GIVE + t][4 * j + 1], acc[GIVE + t][4 * j + 2],
+                                             acc[GIVE + t][4 * j + 3]};
+        __syncthreads();
+        const f32x4* im = red + (((1 - kh) * 4 + wv) * 16) * 64 + lane;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f32x4 v = {acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1], acc[mt][nt][4 * j + 2], acc[mt][nt][4 * j + 3]};
-                    store16_agent(mine + (((mt * 2 + nt) * 4 + j) * 256) * 4, v);
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 o = im[(4 * t + j) * 64];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float a = acc[KEEP + t][4 * j + e];
+                    acc[KEEP + t][4 * j + e] = KEEP == 0 ? a + o[e] : o[e] + a;
                 }
-        if (!publish_and_count(&counters[st], (unsigned)S, &last)) return;
-        // The last to arrive adds the S partials of each piece in split order (its own
-        // included, read back), loading up to 6 splits' worth at once.
-        const float* base = part + (int64_t)st * S * 32768 + 4 * tid;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const int piece = mt * 2 + nt;
-                f32x4 sum[4];
-                for (int z0 = 0; z0 < S; z0 += 6) {
-                    f32x4 t[6][4];
-#pragma unroll
-                    for (int dz = 0; dz < 6; ++dz)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            t[dz][j] = z0 + dz < S ? load16_agent(base + (int64_t)(z0 + dz) * 32768 + ((piece * 4 + j) * 256) * 4)
-                                                   : f32x4{0.f, 0.f, 0.f, 0.f};
-                    vm_wait0(t);
-#pragma unroll
-                    for (int dz = 0; dz < 6; ++dz)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            if (z0 + dz >= S) continue;
-                            if (z0 + dz == 0) sum[j] = t[0][j];
-                            else sum[j] = sum[j] + t[dz][j];
-                        }
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[mt][nt][4 * j + e] = sum[j][e];
             }
+    };
+    if (kh == 0) exchange(std::integral_constant<int, 0>());
+    else exchange(std::integral_constant<int, 4>());
+
+    // Split tiles: hand the partial over, the last split adds them (see above).  Row tile
+    // mt, float4 j, thread slot ts = 64 wv + lane of split z of split tile st sits at
+    // part + 4 * ((((st * S + z) * 8 + mt) * 4 + j) * 256 + ts).
+    auto split_reduce = [&](auto keepc) -> bool {
+        constexpr int KEEP = decltype(keepc)::value;
+        const int st = tile - full, ts = 64 * wv + lane;
+        float* mine = part + (int64_t)(st * S + sp) * 32768 + 4 * ts;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int mt = KEEP + t;
+                const f32x4 v = {acc[mt][4 * j], acc[mt][4 * j + 1], acc[mt][4 * j + 2], acc[mt][4 * j + 3]};
+                store16_agent(mine + ((mt * 4 + j) * 256) * 4, v);
+            }
+        if (!publish_and_count(&counters[st], (unsigned)S, &last)) return false;
+        // The last to arrive adds the S partials of each row tile in split order (its own
+        // included, read back), up to 3 splits (12 loads) at a time.
+        const float* base = part + (int64_t)st * S * 32768 + 4 * ts;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int mt = KEEP + t;
+            f32x4 sum[4];
+            for (int z0 = 0; z0 < S; z0 += 3) {
+                f32x4 tz[3][4];
+#pragma unroll
+                for (int dz = 0; dz < 3; ++dz)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        tz[dz][j] = z0 + dz < S ? load16_agent(base + (int64_t)(z0 + dz) * 32768 + ((mt * 4 + j) * 256) * 4)
+                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                vm_wait0(tz);
+#pragma unroll
+                for (int dz = 0; dz < 3; ++dz)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (z0 + dz >= S) continue;
+                        if (z0 + dz == 0) sum[j] = tz[0][j];
+                        else sum[j] = sum[j] + tz[dz][j];
+                    }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[mt][4 * j + e] = sum[j][e];
+        }
         if (tid == 0) __hip_atomic_store(&counters[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    };
+    if (S > 1) {
+        const bool mine = kh == 0 ? split_reduce(std::integral_constant<int, 0>())
+                                  : split_reduce(std::integral_constant<int, 4>());
+        if (!mine) return;
     }
+
     // D layout: acc[i] = D[8*(i/4) + 4*(lane/32) + i%4][lane%32].  Loads (bias, then the
     // residual 16 values at a time) come before the stores they feed, so no store has to
     // complete before the next one is issued.
+    const int col = n0 + 32 * wv + ln;
+    if (col >= N) return;
+    const float bv = bias ? bias[col] : 0.0f;
+    auto store = [&](auto keepc) {
+        constexpr int KEEP = decltype(keepc)::value;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int col = n0 + 64 * wave + 32 * nt + ln;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int t = 0; t < 4; ++t) {
+            const int mt = KEEP + t;
             const int row0 = m0 + 32 * mt + 4 * lh;
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = bias ? acc[mt][nt][i] + bv : acc[mt][nt][i];
+            for (int i = 0; i < 16; ++i) v[i] = bias ? acc[mt][i] + bv : acc[mt][i];
             if (res) {
                 float r[16];
                 const float* rp = res + (int64_t)row0 * ldr + col;
@@ -431,7 +437,9 @@ __global__ __launch_bounds__(256) void k_gemm_q4k(const _Float16* __restrict__ x
                 if (row0 + dr < M) yp[(int64_t)dr * ldy] = v[i];
             }
         }
-    }
+    };
+    if (kh == 0) store(std::integral_constant<int, 0>());
+    else store(std::integral_constant<int, 4>());
 }
 
 // Work split of one GEMM over the GPU's compute units: whole tiles first, as many as fill
@@ -506,7 +514,7 @@ hipError_t launch_gemm_q4k(const QWeight& w, const void* ws, int m, float* y, in
     const GemmPlan p = gemm_plan(w.n, m, w.k);
     float* part = (float*)((uint8_t*)ws + p.xh_bytes);
     unsigned* counters = (unsigned*)((uint8_t*)ws + p.xh_bytes + p.part_bytes);
-    hipLaunchKernelGGL(k_gemm_q4k, dim3((unsigned)p.grid), dim3(256), gemm_q4k_lds(), s, (const _Float16*)ws, m,
+    hipLaunchKernelGGL(k_gemm_q4k, dim3((unsigned)p.grid), dim3(512), gemm_q4k_lds(), s, (const _Float16*)ws, m,
                        (int)w.k, (const uint4*)w.hdr, (const uint4*)w.qs, (int)w.n, y, ldy, bias, res, ldr, part,
                        counters, p.tiles_m, p.full, p.splits);
     return hipGetLastError();
