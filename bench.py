@@ -19,9 +19,15 @@ plus the head, on this host's cores, and scales it to one token's GEMV work.
 WRITE_SIZE counters report for the same GEMV pass (read from the committed summary
 under profiles/, whose header gives the commands and the copy-kernel scale factor).
 
-Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtype q4k|q8_0]
+`prefill` is a second line in the same object: one Qwen3-4B layer's four projections
+(wqkv, wo, w1|w3, w2; Q4_K) applied to a 512-token prompt through QMatMul.forward, i.e.
+the f16 MFMA GEMM including its conversion of x, against the 2.5 PFLOP/s dense f16
+MFMA peak.
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtype q4k|q8_0] [--no-cpu] [--no-prefill]
        python bench.py --mode gemv [--gemv-iters N]   (GEMV pass only, for counter runs)
        python bench.py --mode copy                     (plain 1 GiB device copy, the counter scale)
+       python bench.py --mode prefill                  (the prefill line alone)
 """
 from __future__ import annotations
 
@@ -51,6 +57,7 @@ def parse():
                     help="decode: the benchmark; gemv: only the per-token GEMV pass (for counter runs); "
                          "copy: a plain device copy of known size (the counter scale); prefill: the "
                          "512-token prefill GEMMs of one Qwen3-4B layer on MFMA")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-GEMM line of the decode bench")
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--prefill-iters", type=int, default=20)
     return ap.parse_args()
@@ -265,6 +272,11 @@ def main():
     roof = gemv_roofline(lm, torch, args.gemv_iters)
     print(f"[bench] GEMV: {roof['gemv_us_per_token']} us/token, {roof['achieved']} GB/s", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(lm, torch)
+    prefill = None
+    if not args.no_prefill:
+        prefill = prefill_gemms(torch, args.prefill_tokens, args.prefill_iters)
+        print(f"[bench] prefill: {prefill['us_per_layer']} us/layer, {prefill['achieved']} TFLOP/s", file=sys.stderr,
+              flush=True)
     out = {
         "metric": "decode tok/s Qwen3-4B-shape Q4_K bs=1; quant-GEMV HBM GB/s as % of peak",
         "value": round(tok_s, 2),
@@ -286,6 +298,7 @@ def main():
                    "kv_len": args.kv, "batch": args.batch, "graph": True},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(out))
 
