@@ -270,12 +270,26 @@ SXQ_DEV void attn_tile_partials(const float* qs, const float* kt, const float* v
         }
     }
     __syncthreads();
-    for (int i = tid; i < G * hd; i += 256) {
-        const int h = i / hd, d = i - h * hd;
+    // Weighted values: a thread per 4 consecutive head-dim columns of a head (one 16-byte
+    // LDS read of V per position feeds 4 independent sums), each summed over the
+    // positions in order.
+    for (int i = tid; i < G * hd / 4; i += 256) {
+        const int h = (4 * i) / hd, d = 4 * i - h * hd;
         const float* e = sc + h * P;
-        float acc = 0.0f;
-        for (int p = 0; p < np; ++p) acc += e[p] * vt[p * hdp + d];
-        store_agent(&pm[h * head_stride + 4 + d], acc);
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+        for (int p = 0; p < np; ++p) {
+            const float w = e[p];
+            const float4 v = *(const float4*)(vt + p * hdp + d);
+            acc.x += w * v.x;
+            acc.y += w * v.y;
+            acc.z += w * v.z;
+            acc.w += w * v.w;
+        }
+        store_agent(&pm[h * head_stride + 4 + d], acc.x);
+        store_agent(&pm[h * head_stride + 5 + d], acc.y);
+        store_agent(&pm[h * head_stride + 6 + d], acc.z);
+        store_agent(&pm[h * head_stride + 7 + d], acc.w);
     }
 }
 
@@ -405,17 +419,39 @@ __global__ __launch_bounds__(256) void k_attn_decode(
                 for (int j = 0; j < kMergeBatch; ++j) asm volatile("" ::"v"(v[k][j]));  // keep the batch together
             }
     };
+    // Each split's m and l are read once, before the first batch of partials: loads
+    // complete in order, so the weights can be formed while that batch is still in
+    // flight.  Same arithmetic as merge_weights.  (A wave serves heads wave, wave + 4, ...;
+    // the m/l of its first head are loaded ahead, the others in the loop.)
+    constexpr int kSplitRounds = (kMaxSplits + 63) / 64;
+    float mv[kSplitRounds], lv[kSplitRounds];
+    auto load_ml = [&](int hh) {
+        const float* ph = part_s + (int64_t)(h0 + hh) * max_splits * PR;
+#pragma unroll
+        for (int c = 0; c < kSplitRounds; ++c) {
+            const int i = lane + 64 * c;
+            mv[c] = i < nsp ? load_agent(ph + (int64_t)i * PR) : -INFINITY;
+            lv[c] = i < nsp ? load_agent(ph + (int64_t)i * PR + 1) : 0.0f;
+        }
+    };
+    if (wave < G) load_ml(wave);
     fetch(0);  // the first batch is in flight while the split weights are computed
     for (int hh = wave; hh < G; hh += 4) {
-        const float* ph = part_s + (int64_t)(h0 + hh) * max_splits * PR;
+        if (hh != wave) load_ml(hh);
         float M = -INFINITY;
-        for (int i = lane; i < nsp; i += 64) M = fmaxf(M, load_agent(ph + (int64_t)i * PR));
+#pragma unroll
+        for (int c = 0; c < kSplitRounds; ++c)
+            if (lane + 64 * c < nsp) M = fmaxf(M, mv[c]);
         M = wave_max_f32(M);
         float Ls = 0.0f;
-        for (int i = lane; i < nsp; i += 64) {
-            const float w = expf(load_agent(ph + (int64_t)i * PR) - M);
-            wts[hh * nsp + i] = w;
-            Ls += load_agent(ph + (int64_t)i * PR + 1) * w;
+#pragma unroll
+        for (int c = 0; c < kSplitRounds; ++c) {
+            const int i = lane + 64 * c;
+            if (i < nsp) {
+                const float w = expf(mv[c] - M);
+                wts[hh * nsp + i] = w;
+                Ls += lv[c] * w;
+            }
         }
         Ls = wave_sum_f32(Ls);
         if (lane == 0) lsum[hh] = Ls;
