@@ -16,6 +16,9 @@ constexpr int kAttnSplit = 32;
 // Positions per split of the fused decode attention (fewer, larger splits: a cheaper merge).
 constexpr int kAttnSplitFused = 64;
 constexpr int kMaxSplits = 512;
+// The fused kernel: workgroup size and the most splits one of its merges takes.
+constexpr int kAttnThreads = 512;
+constexpr int kMaxSplitsFused = kMaxSplits * kAttnSplit / kAttnSplitFused;
 size_t attn_partial_lds(int nh, int nkv, int hd, int P);
 hipError_t launch_attention(int vdt, const float* q, const float* kc, const float* vc, const int* len, int B, int nh,
                             int nkv, int hd, int max_seq, int64_t kv_stream_stride, int P, int max_splits,
