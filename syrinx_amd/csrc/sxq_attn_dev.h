@@ -1,0 +1,355 @@
+// sxq_attn_dev.h -- fused GQA decode attention of one split as a device function:
+// QK-norm + RoPE + KV append + split partials + last-arriver merge + quantization of
+// the context (the kernel is k_attn_decode in sxq_decoder.hip).
+//
+// Reference: crates/syrinx-fish/src/s2/nn.rs:325-352 (QK-norm, RoPE, KV append,
+// attention), crates/syrinx-lm/src/cv2/attention.rs:67-88; f32 throughout as on the
+// reference CPU path.
+#pragma once
+#include "sxq_decoder.h"
+#include "sxq_quant_dev.h"
+#include "sxq_sync_dev.h"
+
+namespace sxq {
+
+struct RopeIn {
+    float a, b, wa, wb, c, sn;
+};
+// Loads for one head's norm + RoPE: lane i < HD/2 owns the pair (2i, 2i+1) interleaved or
+// (i, i + HD/2) rotate-half.  No branch around the loads (lanes past HD/2 repeat a pair,
+// masked in rope_finish; without norm weights the source is loaded in their place), so
+// the compiler's wait for them counts only the loads issued after them.
+template <int HD>
+SXQ_DEV RopeIn rope_load(const float* src, const float* nw, int interleaved, const float* cos_row,
+                         const float* sin_row, int lane) {
+    const int i = lane & (HD / 2 - 1);
+    const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + HD / 2;
+    const float* w = nw ? nw : src;
+    RopeIn r;
+    r.a = src[ia];
+    r.b = src[ib];
+    r.wa = w[ia];
+    r.wb = w[ib];
+    r.c = cos_row[i];
+    r.sn = sin_row[i];
+    return r;
+}
+// y = RoPE(norm(x)) for the pair loaded by rope_load, in registers: no LDS access and no
+// branch (without norm the scale is exactly 1), so it runs while the loads issued after
+// rope_load are still in flight.  Wave-uniform control flow (the norm's sum of squares
+// is a wave reduction).
+template <int HD>
+SXQ_DEV float2 rope_pair(const RopeIn& r, bool norm, float eps, float inv_hd, int lane) {
+    const bool own = lane < HD / 2;
+    float a = own ? r.a : 0.0f, b = own ? r.b : 0.0f;
+    const float ss = wave_sum_rows(a * a + b * b);
+    const float den = norm ? sqrtf((ss * inv_hd + 0.0f) * 1.0f + eps) : 1.0f;
+    a = (a / den) * (norm ? r.wa : 1.0f);
+    b = (b / den) * (norm ? r.wb : 1.0f);
+    return make_float2(a * r.c - b * r.sn, b * r.c + a * r.sn);
+}
+// Stores the pair from rope_pair (lanes < HD/2) to dst[] and, if non-null, gdst[].
+template <int HD>
+SXQ_DEV void rope_store(float2 y, int interleaved, float* dst, float* gdst, int lane) {
+    if (lane < HD / 2) {
+        const int ia = interleaved ? 2 * lane : lane, ib = interleaved ? 2 * lane + 1 : lane + HD / 2;
+        dst[ia] = y.x;
+        dst[ib] = y.y;
+        if (gdst) {
+            gdst[ia] = y.x;
+            gdst[ib] = y.y;
+        }
+    }
+}
+
+// Fused decode attention for split sp of KV head group g of stream s, NT threads:
+// P = NT/8 cached positions [sp*P, sp*P + P).  QK-norm + RoPE of the group's G queries
+// (from the qkv row), in the split holding position len also the new token's key/value
+// (norm + RoPE of k, appended to the cache), then the split's partials
+// {m, l, 0, 0, acc[hd]} per head
+//   m = max_j s_j, l = sum_j exp(s_j - m), acc = sum_j exp(s_j - m) v_j,  s_j = (q . k_j) * scale
+// and, in the last split of the group to finish (a per-(stream, group) arrival counter,
+// reset after use), the merge of the group's heads and the quantization of that G*hd
+// slice of the context for the O projection.
+//
+// Latency layout (a launch holds ~B * n_kv * L / P workgroups, about one per CU, so
+// every phase is a chain of dependent steps rather than a throughput problem):
+//   * the loads of each wave's norm + RoPE item (wave h: query head h; wave G: the new
+//     key) go first, then the key tile into registers (8 lanes per position, 16-byte
+//     pieces 32 floats apart: every load instruction reads whole 128-byte rows) and the
+//     value tile, so the norm + RoPE runs while the tile is in flight;
+//   * scores: each lane dots its key elements with the same elements of every query
+//     (LDS broadcast), reduced over its 8 lanes with DPP;
+//   * softmax: a wave per head, positions lane + 64 i, DPP reductions;
+//   * weighted values: nq = NT / (G*HD/4) position sets, a thread per (set, head, 4
+//     columns), the sets summed in order through LDS;
+//   * merge: the same (set, head, 4 columns) threads read their splits' partials with
+//     16-byte coherent loads issued together, the split weights formed meanwhile.
+// Requires HD in {64, 128}, G <= 8 and G*HD a whole number of activation blocks.
+template <int VDT, int HD, int NT>
+SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* smem, bool* last) {
+    constexpr int P = NT / 8, KJ = HD / 32, PR = HD + 4, NW = NT / 64;
+    typedef float v4f __attribute__((ext_vector_type(4)));  // (HIP's float4 array would go to scratch)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = A.len[s], L = pos + 1, p0 = sp * P;
+    if (p0 >= L) return;
+    const int nh = A.nh, nkv = A.nkv, max_splits = A.max_splits;
+    const int np = min(P, L - p0), nsp = (L + P - 1) / P;
+    const int G = nh / nkv, gd = G * HD, T = gd / 4, nq = NT / T;
+    const bool has_new = pos < p0 + np;  // position pos is then row np - 1 of the tile
+    const int slot = np - 1;
+    float* vt = smem;         // [P][HD]   value tile
+    float* qs = vt + P * HD;  // [G][HD]   queries after QK-norm + RoPE
+    float* knew = qs + gd;    // [HD]      the new key after QK-norm + RoPE
+    float* sc = knew + HD;    // [G][P]    scores, then exp(s - m)
+    float* red = sc + G * P;  // [nq][gd]  per-position-set weighted sums
+    const float* row = A.qkv + (int64_t)s * A.qkv_n;
+    const float* cos_row = A.cos_t + (int64_t)pos * (HD / 2);
+    const float* sin_row = A.sin_t + (int64_t)pos * (HD / 2);
+    const int64_t head_off = (int64_t)s * A.kv_stream_stride + (int64_t)g * A.max_seq * HD;
+    const float* kb = A.kc + head_off + (int64_t)p0 * HD;
+    const float* vb = A.vc + head_off + (int64_t)p0 * HD;
+    const float* vrow_new = row + (int64_t)(nh + nkv + g) * HD;
+
+    // 1. this wave's norm + RoPE item (every wave loads one; idle waves repeat the last)
+    const int nitem = G + (has_new ? 1 : 0);
+    const int item = min(wave, nitem - 1);
+    const bool isq = item < G;
+    const float* isrc = row + (int64_t)(isq ? g * G + item : nh + g) * HD;
+    const float* inw = isq ? A.qn : A.kn;
+    const RopeIn rin = rope_load<HD>(isrc, inw, A.interleaved, cos_row, sin_row, lane);
+    // 2. the key tile into registers (rows past np clamped to a cached row: loaded, never used)
+    const int kp = tid >> 3, kcol = 4 * (tid & 7);
+    const float* krow = kb + (int64_t)min(kp, slot) * HD + kcol;
+    float4 kr[KJ];
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) kr[j] = ld_global((const float4*)(krow + 32 * j));
+    // ... and the value tile, coalesced: round r holds floats [r*4NT, r*4NT + 4NT) of the
+    // tile, 4 per thread.  Row `slot` of the split holding the new token is the new value,
+    // read from the qkv row in that lane.  (Register loads, not direct-to-LDS ones: with a
+    // direct-to-LDS load in flight the compiler waits for every load before the first use
+    // of any, which would serialise the norm + RoPE below behind the tile.)
+    constexpr int VR = P * HD / (4 * NT);
+    v4f vr4[VR];
+#pragma unroll
+    for (int r = 0; r < VR; ++r) {
+        const int e = r * 4 * NT + 4 * tid;
+        const int vr = min(e / HD, slot), col = e - (e / HD) * HD;
+        const float* src = has_new && vr == slot ? vrow_new + col : vb + (int64_t)vr * HD + col;
+        vr4[r] = ld_global((const v4f*)src);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. norm + RoPE in registers while the tile is in flight; stored once it has landed
+    const float2 y = rope_pair<HD>(rin, inw != nullptr, A.eps, A.inv_hd, lane);
+    float2 y2 = make_float2(0.0f, 0.0f);
+    if (wave + NW < nitem) {  // G == NW: the new key is a second item of wave 0
+        const RopeIn r2 = rope_load<HD>(row + (int64_t)(nh + g) * HD, A.kn, A.interleaved, cos_row, sin_row, lane);
+        y2 = rope_pair<HD>(r2, A.kn != nullptr, A.eps, A.inv_hd, lane);
+    }
+#pragma unroll
+    for (int r = 0; r < VR; ++r) *(v4f*)(vt + r * 4 * NT + 4 * tid) = vr4[r];
+    float* kapp = A.kc + head_off + (int64_t)pos * HD;  // the new key's cache row
+    if (wave < nitem)
+        rope_store<HD>(y, A.interleaved, isq ? qs + item * HD : knew,
+                       isq ? (A.q_out && sp == 0 ? A.q_out + ((int64_t)s * nh + g * G + item) * HD : nullptr) : kapp,
+                       lane);
+    if (wave + NW < nitem) rope_store<HD>(y2, A.interleaved, knew, kapp, lane);
+    __syncthreads();
+    if (has_new) {
+        if (kp == slot)
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) kr[j] = *(const float4*)(knew + kcol + 32 * j);
+        if (wave == NW - 1)  // append the new value to the cache
+#pragma unroll
+            for (int t = 0; t < HD / 64; ++t)
+                A.vc[head_off + (int64_t)pos * HD + lane + 64 * t] = vt[slot * HD + lane + 64 * t];
+    }
+    // 4. scores: partial dots over this lane's key elements, summed over the 8 lanes of the
+    //    position; lane c of the 8 writes head c's score
+    float sv[8];
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+        float acc = 0.0f;
+        if (h < G) {
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) {
+                const float4 q = *(const float4*)(qs + h * HD + kcol + 32 * j);
+                acc += q.x * kr[j].x;
+                acc += q.y * kr[j].y;
+                acc += q.z * kr[j].z;
+                acc += q.w * kr[j].w;
+            }
+            acc += dpp_f32<0xB1>(acc);
+            acc += dpp_f32<0x4E>(acc);
+            acc += dpp_f32<0x141>(acc);
+        }
+        sv[h] = acc;
+    }
+    const int c8 = tid & 7;
+    float mine = sv[0];
+#pragma unroll
+    for (int h = 1; h < 8; ++h)
+        if (c8 == h) mine = sv[h];
+    if (c8 < G) sc[c8 * P + kp] = mine * A.scale + 0.0f;
+    __syncthreads();
+    // 5. softmax of head `wave` over the tile's positions (lane + 64 i)
+    float* part_s = A.part + (int64_t)s * nh * max_splits * PR;
+    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(part_s, (uint32_t)nh * (uint32_t)max_splits * PR * 4);
+    if (wave < G) {
+        constexpr int PL = P / 64;
+        float x[PL], mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            x[i] = lane + 64 * i < np ? sc[wave * P + lane + 64 * i] : -INFINITY;
+            mx = fmaxf(mx, x[i]);
+        }
+        const float m = wave_max_rows(mx);
+        float ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            const float e = lane + 64 * i < np ? expf(x[i] - m) : 0.0f;
+            sc[wave * P + lane + 64 * i] = e;
+            ls += e;
+        }
+        const float l = wave_sum_rows(ls);
+        if (lane == 0) {
+            float* pm = part_s + ((int64_t)(g * G + wave) * max_splits + sp) * PR;
+            store_agent(pm, m);
+            store_agent(pm + 1, l);
+        }
+    }
+    __syncthreads();
+    // 6. weighted values: thread (set qi, head h, columns d..d+3) over the set's positions
+    const int pps = (P + nq - 1) / nq;
+    const int qi = tid / T, rr = tid - qi * T, h = rr / (HD / 4), d = 4 * (rr - h * (HD / 4));
+    const bool mt = qi < nq;
+    if (mt) {
+        const int pa = qi * pps, pb = min(pa + pps, np);
+        const float* e = sc + h * P;
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+        for (int p = pa; p < pb; ++p) {
+            const float w = e[p];
+            const float4 v = *(const float4*)(vt + p * HD + d);
+            a.x += w * v.x;
+            a.y += w * v.y;
+            a.z += w * v.z;
+            a.w += w * v.w;
+        }
+        *(float4*)(red + qi * gd + h * HD + d) = a;
+    }
+    __syncthreads();
+    if (tid < T) {
+        float4 a = *(const float4*)(red + 4 * tid);
+        for (int q = 1; q < nq; ++q) {
+            const float4 b = *(const float4*)(red + q * gd + 4 * tid);
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
+        store16_coherent(prs, (uint32_t)(((g * G + h) * max_splits + sp) * PR + 4 + d) * 4, a);
+    }
+    // the last split of the group to arrive merges the group's heads
+    if (!publish_and_count(&A.counter[s * nkv + g], (unsigned)nsp, last)) return;
+
+    // 7. merge: ctx = sum_z exp(m_z - M) acc_z / sum_z exp(m_z - M) l_z, M = max_z m_z.
+    //    The tile LDS is free now: wts [G][nsp] | lsum [G] | red2 [nq][gd].
+    float* wts = smem;
+    float* lsum = wts + G * nsp;
+    float* red2 = smem + ((G * nsp + G + 3) & ~3);
+    // m and l of every split first (wave h < G, lane i: splits i, i + 64, ...)...
+    constexpr int kRounds = kMaxSplitsFused / 64;
+    float mv[kRounds], lv[kRounds];
+    if (wave < G) {
+        const float* ph = part_s + (int64_t)(g * G + wave) * max_splits * PR;
+#pragma unroll
+        for (int c = 0; c < kRounds; ++c) {
+            const int i = min(lane + 64 * c, nsp - 1);  // clamped: in bounds, masked below
+            mv[c] = load_agent(ph + (int64_t)i * PR);
+            lv[c] = load_agent(ph + (int64_t)i * PR + 1);
+        }
+    }
+    // ... then this thread's partials, splits z = qi + nq*b, kMergeBatch at a time
+    constexpr int kMergeBatch = 8;
+    const int zper = (nsp + nq - 1) / nq;  // splits per set, rounded up (uniform)
+    const uint32_t rec0 = (uint32_t)((g * G + h) * max_splits) * PR * 4 + (uint32_t)(4 + d) * 4;
+    float4 pv[kMergeBatch];
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; ++b) {
+        const int z = min(qi + nq * b, nsp - 1);
+        pv[b] = load16_coherent(prs, rec0 + (uint32_t)z * PR * 4);
+    }
+    if (wave < G) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < kRounds; ++c)
+            if (lane + 64 * c < nsp) M = fmaxf(M, mv[c]);
+        M = wave_max_rows(M);
+        float Ls = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kRounds; ++c) {
+            const int i = lane + 64 * c;
+            if (i < nsp) {
+                const float w = expf(mv[c] - M);
+                wts[wave * nsp + i] = w;
+                Ls += lv[c] * w;
+            }
+        }
+        Ls = wave_sum_rows(Ls);
+        if (lane == 0) lsum[wave] = Ls;
+    }
+    __syncthreads();
+    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int b0 = 0; b0 < zper; b0 += kMergeBatch) {
+        if (b0 > 0)
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) {
+                const int z = min(qi + nq * (b0 + b), nsp - 1);
+                pv[b] = load16_coherent(prs, rec0 + (uint32_t)z * PR * 4);
+            }
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) {
+            const int z = qi + nq * (b0 + b);
+            if (mt && z < nsp) {
+                const float w = wts[h * nsp + z];
+                a.x += pv[b].x * w;
+                a.y += pv[b].y * w;
+                a.z += pv[b].z * w;
+                a.w += pv[b].w * w;
+            }
+        }
+    }
+    if (mt) *(float4*)(red2 + qi * gd + h * HD + d) = a;
+    __syncthreads();
+    // 8. context: thread t < T holds elements 4t .. 4t + 3 of the group's slice, which is
+    //    the quantizers' lane layout (wave w: chunk w of 256 elements).
+    const int dim = nh * HD;
+    const int nbr = VDT == kQ8K ? dim / 256 : dim / 32;  // activation blocks per row
+    uint8_t* arow = A.act + (int64_t)s * nbr * act_block_bytes(VDT);
+    const int blk_first = VDT == kQ8K ? (g * gd) / 256 : (g * gd) / 32;  // the slice's first block
+    uint8_t* qdst = arow + (size_t)blk_first * act_block_bytes(VDT);
+    if (tid < ((T + 63) & ~63)) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (tid < T) {
+            float4 c = *(const float4*)(red2 + 4 * tid);
+            for (int q = 1; q < nq; ++q) {
+                const float4 b = *(const float4*)(red2 + q * gd + 4 * tid);
+                c.x += b.x;
+                c.y += b.y;
+                c.z += b.z;
+                c.w += b.w;
+            }
+            const float ls = lsum[(4 * tid) / HD];
+            v = make_float4(c.x / ls, c.y / ls, c.z / ls, c.w / ls);
+            if (A.ctx_out) *(float4*)(A.ctx_out + (int64_t)s * dim + (int64_t)g * gd + 4 * tid) = v;
+        }
+        if (VDT == kQ8K)
+            wave_quantize_q8k<false>(v, lane, qdst + (size_t)wave * sizeof(ActQ8K));
+        else
+            wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < gd / 32, qdst + (size_t)wave * 8 * sizeof(ActQ8_0));
+    }
+    if (tid == 0) __hip_atomic_store(&A.counter[s * nkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace sxq

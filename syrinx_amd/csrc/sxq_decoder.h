@@ -49,4 +49,23 @@ hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int id
                          float* pval, int* pidx, unsigned* counter, hipStream_t s);
 hipError_t launch_fill_value(float* y, int64_t n, float v, hipStream_t s);
 
+// Arguments of the fused decode attention over one step of B streams.
+struct AttnArgs {
+    const float* qkv;  // [B][qkv_n]: q (nh*hd) | k (nkv*hd) | v (nkv*hd)
+    int qkv_n, nh, nkv;
+    const float *qn, *kn;  // QK-norm weights [hd], or null
+    float eps, inv_hd, scale;
+    int interleaved;
+    const float *cos_t, *sin_t;  // RoPE tables [max_seq][hd/2]
+    const int* len;              // [B] cached positions before this step
+    float *kc, *vc;              // caches [B][nkv][max_seq][hd], stream stride kv_stream_stride
+    int64_t kv_stream_stride;
+    int max_seq;
+    float* part;  // partial records [B][nh][max_splits][hd + 4]
+    int max_splits;
+    unsigned* counter;       // [B][nkv] arrival counters, zero between launches
+    uint8_t* act;            // [B] quantized context rows (the O projection's input)
+    float *ctx_out, *q_out;  // optional f32 copies of the context and the roped queries
+};
+
 }  // namespace sxq

@@ -14,6 +14,7 @@
 //   MCF embedding      crates/syrinx-fish/src/s2/slow_ar.rs:101-161
 // The quantization kernels feed the next projection exactly what QMatMul::forward would
 // compute from the same f32 input (the wave quantizers of sxq_quant_dev.h).
+#include "sxq_attn_dev.h"
 #include "sxq_decoder.h"
 #include "sxq_sync_dev.h"
 #include "sxq_quant_dev.h"
@@ -24,25 +25,6 @@ SXQ_DEV float wave_sum_f32(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
-}
-
-// Wave-wide sum / max through DPP (xor 1, xor 2, the other quad of 8, the other 8 of 16:
-// every lane then holds its 16-lane row total) and the four row totals read as scalars,
-// (r0 + r1) + (r2 + r3).  Every lane gets the same value; wave-uniform control flow only.
-SXQ_DEV float row_total(float v, int r) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r)); }
-SXQ_DEV float wave_sum_rows(float v) {
-    v += dpp_f32<0xB1>(v);
-    v += dpp_f32<0x4E>(v);
-    v += dpp_f32<0x141>(v);
-    v += dpp_f32<0x140>(v);
-    return (row_total(v, 0) + row_total(v, 1)) + (row_total(v, 2) + row_total(v, 3));
-}
-SXQ_DEV float wave_max_rows(float v) {
-    v = fmaxf(v, dpp_f32<0xB1>(v));
-    v = fmaxf(v, dpp_f32<0x4E>(v));
-    v = fmaxf(v, dpp_f32<0x141>(v));
-    v = fmaxf(v, dpp_f32<0x140>(v));
-    return fmaxf(fmaxf(row_total(v, 0), row_total(v, 1)), fmaxf(row_total(v, 2), row_total(v, 3)));
 }
 
 // Quantize chunk c of a row of `dim` elements (elements c*256 .. c*256+255, whose
@@ -342,360 +324,13 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ 
     attn_tile_partials(qs, kt, vt, sc, G, P, np, hd, scale, pm, (int64_t)max_splits * (hd + 4));
 }
 
-// Fused decode attention for one KV head group: grid (B, n_kv, ceil(max_seq / P)),
-// kAttnThreads threads, split z covering cached positions [zP, zP + P).  Per split:
-// QK-norm + RoPE of the group's G queries (from the qkv row), in the split holding
-// position len also the new token's key/value (norm + RoPE of k, appended to the cache),
-// then the split's partials {m, l, 0, 0, acc[hd]} per head
-//   m = max_j s_j, l = sum_j exp(s_j - m), acc = sum_j exp(s_j - m) v_j,  s_j = (q . k_j) * scale
-// and, in the last split of the group to finish (a per-(stream, group) arrival counter,
-// reset after use), the merge of the group's heads and the quantization of that G*hd
-// slice of the context for the O projection.
-//
-// Latency layout (a launch holds ~B * n_kv * L / P workgroups, one per CU, so every
-// phase is a chain of dependent steps rather than a throughput problem):
-//   * each wave first issues the loads of its norm + RoPE item (wave h: query head h;
-//     wave G: the new key), then the key tile into registers (8 lanes per position,
-//     16-byte pieces 32 floats apart: every load instruction reads 8 whole 128-byte
-//     rows) and the value tile straight into LDS; the norm + RoPE runs while the tile
-//     is in flight;
-//   * scores: each lane dots its 4*HD/32 key elements with the same elements of every
-//     query (LDS broadcast), reduced over its 8 lanes with DPP;
-//   * softmax: a wave per head, a lane per position, DPP reductions;
-//   * weighted values: nq = kAttnThreads / (G*HD/4) position sets, a thread per (set,
-//     head, 4 columns), the sets summed in order through LDS;
-//   * merge: the same (set, head, 4 columns) threads read their splits' partials with
-//     16-byte coherent loads issued together, the split weights formed meanwhile.
-// Requires HD in {64, 128}, G <= 8 and G*HD a whole number of activation blocks.
-struct RopeIn {
-    float a, b, wa, wb, c, sn;
-};
-// Loads for one head's norm + RoPE: lane i < HD/2 owns the pair (2i, 2i+1) interleaved or
-// (i, i + HD/2) rotate-half.  No branch around the loads (lanes past HD/2 repeat a pair,
-// masked in rope_finish; without norm weights the source is loaded in their place), so
-// the compiler's wait for them counts only the loads issued after them.
-template <int HD>
-SXQ_DEV RopeIn rope_load(const float* src, const float* nw, int interleaved, const float* cos_row,
-                         const float* sin_row, int lane) {
-    const int i = lane & (HD / 2 - 1);
-    const int ia = interleaved ? 2 * i : i, ib = interleaved ? 2 * i + 1 : i + HD / 2;
-    const float* w = nw ? nw : src;
-    RopeIn r;
-    r.a = src[ia];
-    r.b = src[ib];
-    r.wa = w[ia];
-    r.wb = w[ib];
-    r.c = cos_row[i];
-    r.sn = sin_row[i];
-    return r;
-}
-// y = RoPE(norm(x)) for the pair loaded by rope_load, in registers: no LDS access and no
-// branch (without norm the scale is exactly 1), so it runs while the loads issued after
-// rope_load are still in flight.  Wave-uniform control flow (the norm's sum of squares
-// is a wave reduction).
-template <int HD>
-SXQ_DEV float2 rope_pair(const RopeIn& r, bool norm, float eps, float inv_hd, int lane) {
-    const bool own = lane < HD / 2;
-    float a = own ? r.a : 0.0f, b = own ? r.b : 0.0f;
-    const float ss = wave_sum_rows(a * a + b * b);
-    const float den = norm ? sqrtf((ss * inv_hd + 0.0f) * 1.0f + eps) : 1.0f;
-    a = (a / den) * (norm ? r.wa : 1.0f);
-    b = (b / den) * (norm ? r.wb : 1.0f);
-    return make_float2(a * r.c - b * r.sn, b * r.c + a * r.sn);
-}
-// Stores the pair from rope_pair (lanes < HD/2) to dst[] and, if non-null, gdst[].
-template <int HD>
-SXQ_DEV void rope_store(float2 y, int interleaved, float* dst, float* gdst, int lane) {
-    if (lane < HD / 2) {
-        const int ia = interleaved ? 2 * lane : lane, ib = interleaved ? 2 * lane + 1 : lane + HD / 2;
-        dst[ia] = y.x;
-        dst[ib] = y.y;
-        if (gdst) {
-            gdst[ia] = y.x;
-            gdst[ib] = y.y;
-        }
-    }
-}
-
-// 16-byte loads and stores coherent at agent scope (sc1), through a buffer resource over
-// `bytes` bytes at `base` (offsets in bytes; out-of-range loads return zeros).
-SXQ_DEV __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-SXQ_DEV float4 load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
-    return make_float4(v.x, v.y, v.z, v.w);
-}
-SXQ_DEV void store16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v) {
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-    const f4 w = {v.x, v.y, v.z, v.w};
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, w), r, off, 0, 16);
-}
-
+// The per-launch kernel: grid (B, n_kv, ceil(max_seq / kAttnSplitFused)), kAttnThreads threads.
 template <int VDT, int HD>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_decode(
-    const float* __restrict__ qkv, int qkv_n, int nh, int nkv, const float* __restrict__ qn,
-    const float* __restrict__ kn, float eps, float inv_hd, int interleaved, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, const int* __restrict__ len, float* __restrict__ kc, float* __restrict__ vc,
-    int64_t kv_stream_stride, int max_seq, float scale, float* __restrict__ part, int max_splits,
-    unsigned* __restrict__ counter, uint8_t* __restrict__ act, float* __restrict__ ctx_out,
-    float* __restrict__ q_out) {
-    constexpr int P = kAttnSplitFused, KJ = HD / 32, PR = HD + 4;
+__global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs A) {
+    static_assert(kAttnThreads / 8 == kAttnSplitFused, "a split is one position per 8 lanes");
     extern __shared__ float4 smem4[];  // float4: 16-byte aligned after any static LDS
-    float* smem = (float*)smem4;
     __shared__ bool last;
-    const int s = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
-    const int pos = len[s], L = pos + 1, p0 = sp * P;
-    if (p0 >= L) return;
-    const int np = min(P, L - p0), nsp = (L + P - 1) / P;
-    const int G = nh / nkv, gd = G * HD, T = gd / 4, nq = kAttnThreads / T;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool has_new = pos < p0 + np;  // position pos is then row np - 1 of the tile
-    float* vt = smem;         // [P][HD]   value tile
-    float* qs = vt + P * HD;  // [G][HD]   queries after QK-norm + RoPE
-    float* knew = qs + gd;    // [HD]      the new key after QK-norm + RoPE
-    float* sc = knew + HD;    // [G][P]    scores, then exp(s - m)
-    float* red = sc + G * P;  // [nq][gd]  per-position-set weighted sums
-    const float* row = qkv + (int64_t)s * qkv_n;
-    const float* cos_row = cos_t + (int64_t)pos * (HD / 2);
-    const float* sin_row = sin_t + (int64_t)pos * (HD / 2);
-    const int64_t head_off = (int64_t)s * kv_stream_stride + (int64_t)g * max_seq * HD;
-    const float* kb = kc + head_off + (int64_t)p0 * HD;
-    const float* vb = vc + head_off + (int64_t)p0 * HD;
-
-    // 1. loads of this wave's first norm + RoPE item, issued by every wave (idle waves
-    //    repeat the last item)
-    const int nitem = G + (has_new ? 1 : 0);
-    const int item = min(wave, nitem - 1);
-    const bool isq = item < G;
-    const RopeIn rin = rope_load<HD>(row + (int64_t)(isq ? g * G + item : nh + g) * HD, isq ? qn : kn, interleaved,
-                                     cos_row, sin_row, lane);
-    // 2. the key tile into registers (rows past np clamped to a cached row: loaded, never used)
-    const int kp = tid >> 3, kcol = 4 * (tid & 7);
-    const float* krow = kb + (int64_t)min(kp, np - 1) * HD + kcol;
-    float4 kr[KJ];
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) kr[j] = *(const float4*)(krow + 32 * j);
-    // ... and the value tile, coalesced: round r holds floats [r*2048, r*2048 + 2048) of
-    // the tile, 4 per thread.  Row np - 1 of the split holding the new token comes from
-    // the qkv row (its value).  (Register loads, not direct-to-LDS ones: with a
-    // direct-to-LDS load in flight the compiler waits for every load before the first use
-    // of any, which would serialise the norm + RoPE below behind the tile.)
-    const int slot = np - 1;
-    const float* vrow_new = row + (int64_t)(nh + nkv + g) * HD;
-    constexpr int VR = P * HD / (4 * kAttnThreads);
-    typedef float v4f __attribute__((ext_vector_type(4)));  // (HIP's float4 array would go to scratch)
-    v4f vr4[VR];
-#pragma unroll
-    for (int r = 0; r < VR; ++r) {
-        const int e = r * 4 * kAttnThreads + 4 * tid;
-        const int vr = min(e / HD, slot), col = e - (e / HD) * HD;
-        vr4[r] = *(const v4f*)(has_new && vr == slot ? vrow_new + col : vb + (int64_t)vr * HD + col);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // 3. norm + RoPE in registers while the tile is in flight; stored once it has landed
-    //    (an LDS store would wait for the tile's LDS writes anyway)
-    const float2 y = rope_pair<HD>(rin, (isq ? qn : kn) != nullptr, eps, inv_hd, lane);
-    float2 y2 = make_float2(0.0f, 0.0f);
-    if (wave + 8 < nitem) {  // G == 8: the new key is a second item of wave 0
-        const RopeIn r2 = rope_load<HD>(row + (int64_t)(nh + g) * HD, kn, interleaved, cos_row, sin_row, lane);
-        y2 = rope_pair<HD>(r2, kn != nullptr, eps, inv_hd, lane);
-    }
-#pragma unroll
-    for (int r = 0; r < VR; ++r) *(v4f*)(vt + r * 4 * kAttnThreads + 4 * tid) = vr4[r];
-    if (wave < nitem)
-        rope_store<HD>(y, interleaved, isq ? qs + item * HD : knew,
-                       isq ? (q_out && sp == 0 ? q_out + ((int64_t)s * nh + g * G + item) * HD : nullptr)
-                           : kc + head_off + (int64_t)pos * HD,
-                       lane);
-    if (wave + 8 < nitem) rope_store<HD>(y2, interleaved, knew, kc + head_off + (int64_t)pos * HD, lane);
-    __syncthreads();
-    if (has_new) {
-        if (kp == slot)
-#pragma unroll
-            for (int j = 0; j < KJ; ++j) kr[j] = *(const float4*)(knew + kcol + 32 * j);
-        if (wave == kAttnThreads / 64 - 1)  // append the new value to the cache
-#pragma unroll
-            for (int t = 0; t < HD / 64; ++t) vc[head_off + (int64_t)pos * HD + lane + 64 * t] = vt[slot * HD + lane + 64 * t];
-    }
-    // 4. scores: partial dots over this lane's key elements, summed over the 8 lanes of the
-    //    position; lane c of the 8 writes head c's score
-    float sv[8];
-#pragma unroll
-    for (int h = 0; h < 8; ++h) {
-        float acc = 0.0f;
-        if (h < G) {
-#pragma unroll
-            for (int j = 0; j < KJ; ++j) {
-                const float4 q = *(const float4*)(qs + h * HD + kcol + 32 * j);
-                acc += q.x * kr[j].x;
-                acc += q.y * kr[j].y;
-                acc += q.z * kr[j].z;
-                acc += q.w * kr[j].w;
-            }
-            acc += dpp_f32<0xB1>(acc);
-            acc += dpp_f32<0x4E>(acc);
-            acc += dpp_f32<0x141>(acc);
-        }
-        sv[h] = acc;
-    }
-    const int c8 = tid & 7;
-    float mine = sv[0];
-#pragma unroll
-    for (int h = 1; h < 8; ++h)
-        if (c8 == h) mine = sv[h];
-    if (c8 < G) sc[c8 * P + kp] = mine * scale + 0.0f;
-    __syncthreads();
-    // 5. softmax of head `wave` over the tile's positions (lane = position)
-    const uint32_t split_bytes = (uint32_t)max_splits * PR * 4;  // one head's records
-    float* part_s = part + (int64_t)s * nh * max_splits * PR;
-    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(part_s, (uint32_t)nh * split_bytes);
-    if (wave < G) {
-        const float x = lane < np ? sc[wave * P + lane] : -INFINITY;
-        const float m = wave_max_rows(x);
-        const float e = lane < np ? expf(x - m) : 0.0f;
-        const float l = wave_sum_rows(e);
-        sc[wave * P + lane] = e;
-        if (lane == 0) {
-            float* pm = part_s + ((int64_t)(g * G + wave) * max_splits + sp) * PR;
-            store_agent(pm, m);
-            store_agent(pm + 1, l);
-        }
-    }
-    __syncthreads();
-    // 6. weighted values: thread (set qi, head h, columns d..d+3) over the set's positions
-    const int pps = (P + nq - 1) / nq;
-    const int qi = tid / T, rr = tid - qi * T, h = rr / (HD / 4), d = 4 * (rr - h * (HD / 4));
-    const bool mt = qi < nq;
-    if (mt) {
-        const int pa = qi * pps, pb = min(pa + pps, np);
-        const float* e = sc + h * P;
-        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 8
-        for (int p = pa; p < pb; ++p) {
-            const float w = e[p];
-            const float4 v = *(const float4*)(vt + p * HD + d);
-            a.x += w * v.x;
-            a.y += w * v.y;
-            a.z += w * v.z;
-            a.w += w * v.w;
-        }
-        *(float4*)(red + qi * gd + h * HD + d) = a;
-    }
-    __syncthreads();
-    if (tid < T) {
-        float4 a = *(const float4*)(red + 4 * tid);
-        for (int q = 1; q < nq; ++q) {
-            const float4 b = *(const float4*)(red + q * gd + 4 * tid);
-            a.x += b.x;
-            a.y += b.y;
-            a.z += b.z;
-            a.w += b.w;
-        }
-        store16_coherent(prs, (uint32_t)(((g * G + h) * max_splits + sp) * PR + 4 + d) * 4, a);
-    }
-    // the last split of the group to arrive merges the group's heads
-    if (!publish_and_count(&counter[s * nkv + g], (unsigned)nsp, &last)) return;
-
-    // 7. merge: ctx = sum_z exp(m_z - M) acc_z / sum_z exp(m_z - M) l_z, M = max_z m_z.
-    //    The tile LDS is free now: wts [G][nsp] | lsum [G] | red2 [nq][gd].
-    float* wts = smem;
-    float* lsum = wts + G * nsp;
-    float* red2 = smem + ((G * nsp + G + 3) & ~3);
-    // m and l of every split first (wave h < G, lane i: splits i, i + 64, ...)...
-    constexpr int kRounds = kMaxSplitsFused / 64;
-    float mv[kRounds], lv[kRounds];
-    if (wave < G) {
-        const float* ph = part_s + (int64_t)(g * G + wave) * max_splits * PR;
-#pragma unroll
-        for (int c = 0; c < kRounds; ++c) {
-            const int i = min(lane + 64 * c, nsp - 1);  // clamped: in bounds, masked below
-            mv[c] = load_agent(ph + (int64_t)i * PR);
-            lv[c] = load_agent(ph + (int64_t)i * PR + 1);
-        }
-    }
-    // ... then this thread's partials, splits z = qi + nq*b, kMergeBatch at a time
-    constexpr int kMergeBatch = 8;
-    const int zper = (nsp + nq - 1) / nq;  // splits per set, rounded up (uniform)
-    const uint32_t rec0 = (uint32_t)((g * G + h) * max_splits) * PR * 4 + (uint32_t)(4 + d) * 4;
-    float4 pv[kMergeBatch];
-#pragma unroll
-    for (int b = 0; b < kMergeBatch; ++b) {
-        const int z = min(qi + nq * b, nsp - 1);
-        pv[b] = load16_coherent(prs, rec0 + (uint32_t)z * PR * 4);
-    }
-    if (wave < G) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int c = 0; c < kRounds; ++c)
-            if (lane + 64 * c < nsp) M = fmaxf(M, mv[c]);
-        M = wave_max_rows(M);
-        float Ls = 0.0f;
-#pragma unroll
-        for (int c = 0; c < kRounds; ++c) {
-            const int i = lane + 64 * c;
-            if (i < nsp) {
-                const float w = expf(mv[c] - M);
-                wts[wave * nsp + i] = w;
-                Ls += lv[c] * w;
-            }
-        }
-        Ls = wave_sum_rows(Ls);
-        if (lane == 0) lsum[wave] = Ls;
-    }
-    __syncthreads();
-    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int b0 = 0; b0 < zper; b0 += kMergeBatch) {
-        if (b0 > 0)
-#pragma unroll
-            for (int b = 0; b < kMergeBatch; ++b) {
-                const int z = min(qi + nq * (b0 + b), nsp - 1);
-                pv[b] = load16_coherent(prs, rec0 + (uint32_t)z * PR * 4);
-            }
-#pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b) {
-            const int z = qi + nq * (b0 + b);
-            if (mt && z < nsp) {
-                const float w = wts[h * nsp + z];
-                a.x += pv[b].x * w;
-                a.y += pv[b].y * w;
-                a.z += pv[b].z * w;
-                a.w += pv[b].w * w;
-            }
-        }
-    }
-    if (mt) *(float4*)(red2 + qi * gd + h * HD + d) = a;
-    __syncthreads();
-    // 8. context: thread t < T holds elements 4t .. 4t + 3 of the group's slice, which is
-    //    the quantizers' lane layout (wave w: chunk w of 256 elements)
-    if (tid < ((T + 63) & ~63)) {
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (tid < T) {
-            float4 c = *(const float4*)(red2 + 4 * tid);
-            for (int q = 1; q < nq; ++q) {
-                const float4 b = *(const float4*)(red2 + q * gd + 4 * tid);
-                c.x += b.x;
-                c.y += b.y;
-                c.z += b.z;
-                c.w += b.w;
-            }
-            const float ls = lsum[(4 * tid) / HD];
-            v = make_float4(c.x / ls, c.y / ls, c.z / ls, c.w / ls);
-            if (ctx_out) *(float4*)(ctx_out + (int64_t)s * nh * HD + (int64_t)g * gd + 4 * tid) = v;
-        }
-        const int dim = nh * HD;
-        const int nb = VDT == kQ8K ? dim / 256 : dim / 32;
-        uint8_t* arow = act + (int64_t)s * nb * act_block_bytes(VDT);
-        if (VDT == kQ8K) {
-            wave_quantize_q8k<false>(v, lane, arow + (size_t)((g * gd) / 256 + wave) * sizeof(ActQ8K));
-        } else {
-            const int blk0 = (g * gd) / 32 + wave * 8;  // first Q8_0 block of this chunk in the row
-            wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < gd / 32, arow + (size_t)blk0 * sizeof(ActQ8_0));
-        }
-    }
-    if (tid == 0) __hip_atomic_store(&counter[s * nkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    attn_decode_body<VDT, HD, kAttnThreads>(A, blockIdx.x, blockIdx.y, blockIdx.z, (float*)smem4, &last);
 }
 
 // grid (B, ceil(nh*hd/256)), 256 threads: merge the splits of the heads covering
@@ -924,10 +559,11 @@ hipError_t launch_attention(int vdt, const float* q, const float* kc, const floa
     return hipGetLastError();
 }
 
-// Fused attention LDS: the partial phase's tiles, or the merge phase's split weights and
-// per-set sums, whichever is larger (the partial phase, at the decode shapes).
+// Fused attention LDS (P = kAttnThreads/8 positions per split): the partial phase's
+// tiles, or the merge phase's split weights and per-set sums, whichever is larger (the
+// partial phase, at the decode shapes).
 static size_t attn_decode_lds(int nh, int nkv, int hd, int max_splits) {
-    const size_t G = nh / nkv, gd = G * hd, nq = kAttnThreads / (gd / 4), P = kAttnSplitFused;
+    const size_t G = nh / nkv, gd = G * hd, nq = kAttnThreads / (gd / 4), P = kAttnThreads / 8;
     const size_t nspf = (size_t)max_splits < (size_t)kMaxSplitsFused ? max_splits : kMaxSplitsFused;
     const size_t partial = P * hd + gd + hd + G * P + nq * gd;
     const size_t merge = ((G * nspf + G + 3) & ~(size_t)3) + nq * gd;
@@ -961,12 +597,33 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
                                    float* q_out, hipStream_t s) {
     if (!attn_decode_fits(vdt, nh, nkv, hd, max_splits) || max_seq > kMaxSplitsFused * kAttnSplitFused)
         return hipErrorInvalidValue;
-    float inv_hd = (float)(1.0 / (double)hd);
-    float scale = (float)(1.0 / sqrt((double)hd));
+    AttnArgs A;
+    A.qkv = qkv;
+    A.qkv_n = qkv_n;
+    A.nh = nh;
+    A.nkv = nkv;
+    A.qn = qn;
+    A.kn = kn;
+    A.eps = eps;
+    A.inv_hd = (float)(1.0 / (double)hd);
+    A.scale = (float)(1.0 / sqrt((double)hd));
+    A.interleaved = interleaved;
+    A.cos_t = cos_t;
+    A.sin_t = sin_t;
+    A.len = len;
+    A.kc = kc;
+    A.vc = vc;
+    A.kv_stream_stride = kv_stream_stride;
+    A.max_seq = max_seq;
+    A.part = part;
+    A.max_splits = max_splits;
+    A.counter = counter;
+    A.act = act;
+    A.ctx_out = ctx_out;
+    A.q_out = q_out;
     const dim3 grid(B, nkv, (max_seq + kAttnSplitFused - 1) / kAttnSplitFused);  // partial records: max_splits per head
     const size_t lds = attn_decode_lds(nh, nkv, hd, max_splits);
-    void* args[] = {&qkv, &qkv_n, &nh, &nkv, &qn, &kn, &eps, &inv_hd, &interleaved, &cos_t, &sin_t, &len, &kc, &vc,
-                    &kv_stream_stride, &max_seq, &scale, &part, &max_splits, &counter, &act, &ctx_out, &q_out};
+    void* args[] = {&A};
     return hipLaunchKernel(attn_decode_kernel(vdt, hd), grid, dim3(kAttnThreads), args, lds, s);
 }
 

@@ -164,11 +164,10 @@ SXQ_DEV void vm_wait0(f32x4 (&v)[3][4]) {
                  "+v"(v[2][3]));
 }
 
-// Workgroup barrier without the memory fence of __syncthreads(): the fence would make
+// barrier_nofence (sxq_sync_dev.h) between stages: __syncthreads()'s fence would make
 // the compiler wait for every outstanding global->LDS load, including the ones issued
 // for later groups.  The caller waits for the loads it needs (SXQ_WAIT_VM); the memory
 // clobber keeps the compiler from moving LDS accesses across the barrier.
-SXQ_DEV void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
 
 // y[m][n] = x[m] . W[n] (+ bias[n], then res[m][n] + that), W Q4_K [n][k] in the device
 // layout, xh from k_x_to_f16_perm (rows padded to 256).  One workgroup of 512 threads per

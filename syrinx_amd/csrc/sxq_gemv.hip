@@ -18,14 +18,12 @@
 #include <stdlib.h>
 
 #include "sxq_decoder.h"
+#include "sxq_gemv_dev.h"
 #include "sxq_kernels.h"
-#include "sxq_quant_dev.h"
 
 namespace sxq {
 
 static constexpr int kLdsBudget = 48 * 1024;
-
-SXQ_DEV float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
 
 // Copy act blocks [m][c0, c0+cb) (global, row stride nb blocks) into LDS [m][cb].
 template <int ABYTES>
@@ -210,8 +208,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_q80(const uint16_t* __restr
 // product(s) in LDS: Q4_K the eight lane terms (d_w*d_a)*(f32)aux32[l] and the min term
 // (dmin_w*d_a)*(f32)sumi; Q8_0/Q4_0 the term ((f32)isum*d_w)*d_a.  The epilogue folds
 // them in block order per (row, lane) -- the only order-dependent part -- so results
-// stay bit-identical to Candle's generic vec-dot.
-constexpr int kTmax = 8;
+// stay bit-identical to Candle's generic vec-dot.  The Q4_K tile (loads, products,
+// fold) is in sxq_gemv_dev.h.
 
 // Activation staging in two halves so the caller can put its weight loads between
 // them: act_fetch issues a thread's first 16-byte loads (clamped, so all are
@@ -235,50 +233,6 @@ SXQ_DEV void act_store(const uint4 (&v)[Stage<NT>::kPer], uint4* lds, const uint
     for (int i = Stage<NT>::kPer * NT + threadIdx.x; i < total_u4; i += NT) lds[i] = ((const uint4*)act)[i];
 }
 
-// RMSNorm + activation quantization as the prologue of a 1024-thread GEMV (one row of
-// dim <= 4096): thread t holds float4 t of the row and of the norm weight, i.e. lane
-// t%64's share of 256-element chunk t/64, so wave w normalises and quantizes chunk w
-// straight from registers into the LDS activation blocks.  The row's sum of squares is
-// rmsnorm_sumsq_1024 -- the same function and order as k_rmsnorm_quant -- so both paths
-// produce the same bits.
-SXQ_DEV void norm_fetch(float4& xv, float4& wv, const NormIn& ni, int dim) {
-    const int i = min((int)threadIdx.x, dim / 4 - 1);  // clamped: every load in bounds
-    xv = ((const float4*)ni.x)[i];
-    wv = ((const float4*)ni.w)[i];
-    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
-}
-template <int VDT>
-SXQ_DEV void norm_quant_store(const float4& xv, const float4& wv, const NormIn& ni, int dim, uint8_t* lds_act,
-                              float* red) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool mine = tid < dim / 4;
-    float ss = 0.0f;
-    if (mine) {
-        ss += xv.x * xv.x;
-        ss += xv.y * xv.y;
-        ss += xv.z * xv.z;
-        ss += xv.w * xv.w;
-    }
-    ss = rmsnorm_sumsq_1024(ss, red);
-    const float var = ss * (float)(1.0 / (double)dim) + 0.0f;
-    const float den = sqrtf(var * 1.0f + ni.eps);
-    const int nchunks = (dim + 255) / 256;
-    if (wave >= nchunks) return;  // uniform per wave
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (mine) {
-        v.x = (xv.x / den) * wv.x;
-        v.y = (xv.y / den) * wv.y;
-        v.z = (xv.z / den) * wv.z;
-        v.w = (xv.w / den) * wv.w;
-        if (ni.normed && blockIdx.x == 0) ((float4*)ni.normed)[tid] = v;
-    }
-    if (VDT == kQ8K) {
-        wave_quantize_q8k<false>(v, lane, lds_act + (size_t)wave * sizeof(ActQ8K));
-    } else {
-        wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < dim / 32, lds_act + (size_t)wave * 8 * sizeof(ActQ8_0));
-    }
-}
-
 // Q4_K task-split GEMV, NT threads (256 or 1024) per workgroup: NT/8 eight-lane groups.
 template <int MMAX, bool NORM, int NT>
 __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, int n,
@@ -294,22 +248,14 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     const int tasks = rows * nb;
     const int TS = (tasks + SLOTS - 1) / SLOTS * SLOTS;  // product slots: whole rounds
     float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8K) / 16));  // [m][TS][9]
-    const int lane = threadIdx.x & 63, l = lane & 7, grp = threadIdx.x >> 3;
     const uint32_t blk0 = (uint32_t)row0 * (uint32_t)nb;
-    const char* qbase = (const char*)qs + (l << 4);
-    const char* hbase = (const char*)hdr;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8K) / 16);
     uint4 av[Stage<NT>::kPer];
     float4 xv, wv;
     if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 256);
     else act_fetch<NT>(av, act, act_u4);
     uint4 q[kTmax], h[kTmax];
-#pragma unroll
-    for (int u = 0; u < kTmax; ++u) {
-        const uint32_t blk = blk0 + (uint32_t)min(u * SLOTS + grp, tasks - 1);
-        q[u] = *(const uint4*)(qbase + (blk << 7));
-        h[u] = *(const uint4*)(hbase + (blk << 4));
-    }
+    q4k_tile_load<NT>(hdr, qs, blk0, tasks, q, h);
     if constexpr (NORM) {
         __shared__ float red[16];
         norm_quant_store<kQ8K>(xv, wv, ni, nb * 256, (uint8_t*)lds, red);
@@ -317,68 +263,15 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
         act_store<NT>(av, lds, act, act_u4);
     }
     __syncthreads();
-    // Block index of task u*SLOTS + grp: grp mod nb, stepped by SLOTS mod nb each round.
-    // Tasks past the end (last round) compute on clamped loads into their own spare
-    // slots, which the epilogue never reads.
-    const uint32_t step = (uint32_t)SLOTS % (uint32_t)nb;
-    uint32_t b = (uint32_t)grp % (uint32_t)nb;
-#pragma unroll
-    for (int u = 0; u < kTmax; ++u) {
-        if (u * SLOTS >= tasks) break;  // uniform: no group has a task in this round
-        const uint32_t sc_lo = h[u].y & 0x3F3F3F3Fu;
-        const uint32_t sc_hi = (h[u].w & 0x0F0F0F0Fu) | (((h[u].y >> 6) & 0x03030303u) << 4);
-        const uint32_t mn_lo = h[u].z & 0x3F3F3F3Fu;
-        const uint32_t mn_hi = ((h[u].w >> 4) & 0x0F0F0F0Fu) | (((h[u].z >> 6) & 0x03030303u) << 4);
-        const int ml = (int)(((l < 4 ? mn_lo : mn_hi) >> (8 * (l & 3))) & 0xFF);
-        const uint32_t w4[8] = {q[u].x & 0x0F0F0F0Fu, (q[u].x >> 4) & 0x0F0F0F0Fu, q[u].y & 0x0F0F0F0Fu,
-                                (q[u].y >> 4) & 0x0F0F0F0Fu, q[u].z & 0x0F0F0F0Fu, (q[u].z >> 4) & 0x0F0F0F0Fu,
-                                q[u].w & 0x0F0F0F0Fu, (q[u].w >> 4) & 0x0F0F0F0Fu};
-        int sc[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            sc[j] = (int)((sc_lo >> (8 * j)) & 0xFF);
-            sc[4 + j] = (int)((sc_hi >> (8 * j)) & 0xFF);
-        }
-        const float dw = h2f(h[u].x & 0xFFFF), dminw = h2f(h[u].x >> 16);
-#pragma unroll
-        for (int r = 0; r < MMAX; ++r) {
-            if (r < m) {
-                const ActQ8K& a = la[r * nb + (int)b];
-                const uint4 A0 = ((const uint4*)a.qs)[2 * l];
-                const uint4 A1 = ((const uint4*)a.qs)[2 * l + 1];
-                const int Aj[8] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w,
-                                   (int)A1.x, (int)A1.y, (int)A1.z, (int)A1.w};
-                int aux = 0;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) aux += __mul24(__builtin_amdgcn_sdot4((int)w4[j], Aj[j], 0, false), sc[j]);
-                const int sumi = sum8_i32(__mul24(ml, a.bs2[l]));
-                const float ad = a.d;
-                float* p = pr + (r * TS + u * SLOTS + grp) * 9;
-                p[l] = (dw * ad) * (float)aux;
-                p[8] = (dminw * ad) * (float)sumi;  // same value from all eight lanes
-            }
-        }
-        b += step;
-        b = min(b, b - (uint32_t)nb);  // unsigned: subtracts nb only when b >= nb
-    }
+    q4k_tile_products<MMAX, NT>(q, h, la, nb, m, tasks, TS, pr);
     __syncthreads();
     // epilogue: thread (row r, lane class l) folds its chain in block order
-    const int r = threadIdx.x >> 3;
-    const bool act_row = r < rows;
+    const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
     for (int rr = 0; rr < m; ++rr) {
-        float sl = 0.0f, sf = 0.0f;
-        if (act_row) {
-            const float* p = pr + (rr * TS + r * nb) * 9;
-            for (int b = 0; b < nb; ++b) sl += p[b * 9 + l];
-            if (l == 0)
-                for (int b = 0; b < nb; ++b) sf -= p[b * 9 + 8];
-        }
-        float tot = -0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) tot += __shfl(sl, (lane & ~7) + j, 64);
-        if (act_row && l == 0) {
+        const float v0 = q4k_tile_fold(pr, TS, nb, rr, rows);
+        if (r < rows && l == 0) {
             const int row = row0 + r;
-            float v = sf + tot;
+            float v = v0;
             if (bias) v = v + bias[row];
             if (res) v = res[(int64_t)rr * ldr + row] + v;
             y[(int64_t)rr * ldy + row] = v;

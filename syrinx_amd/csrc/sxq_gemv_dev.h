@@ -1,0 +1,155 @@
+// sxq_gemv_dev.h -- one tile of the Q4_K x Q8_K task-split GEMV as device functions:
+// the per-launch GEMV kernels (sxq_gemv.hip) and the persistent decode kernel
+// (sxq_pipeline.hip) run the same code, so both give Candle's vec-dot bit for bit.
+//
+// A tile is `rows` consecutive weight rows starting at block index blk0 (row-major,
+// nb blocks per row); its rows*nb (row, block) tasks are dealt round-robin to the NT/8
+// eight-lane groups of the workgroup, at most kTmax tasks each.  Lane l of a group
+// loads the 16 bytes holding class l (elements = l mod 8) of a block's four 32-byte
+// chunks (the device layout of sxq_common.h) and produces Candle's aux32[l] directly.
+#pragma once
+#include "sxq_kernels.h"
+#include "sxq_quant_dev.h"
+#include "sxq_sync_dev.h"
+
+namespace sxq {
+
+constexpr int kTmax = 8;
+
+SXQ_DEV float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
+
+// Issue the weight loads of every task of this thread's group, TM rounds (clamped to
+// the last task, so all TM loads are unconditional and in flight together; the tile
+// must have at most TM * NT/8 tasks).
+template <int NT, int TM = kTmax>
+SXQ_DEV void q4k_tile_load(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, uint32_t blk0, int tasks,
+                           uint4 (&q)[TM], uint4 (&h)[TM]) {
+    constexpr int SLOTS = NT / 8;
+    const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
+    const char* qbase = (const char*)qs + (l << 4);
+    const char* hbase = (const char*)hdr;
+#pragma unroll
+    for (int u = 0; u < TM; ++u) {
+        const uint32_t blk = blk0 + (uint32_t)min(u * SLOTS + grp, tasks - 1);
+        q[u] = ld_global((const uint4*)(qbase + (blk << 7)));
+        h[u] = ld_global((const uint4*)(hbase + (blk << 4)));
+    }
+}
+
+// Per-task float products into pr [m][TS][9] (TS = tasks rounded up to whole rounds):
+// the eight lane terms (d_w*d_a)*(f32)aux32[l] and the min term (dmin_w*d_a)*(f32)sumi
+// of Candle's Q4_K vec-dot, against the LDS activation blocks la [m][nb].  Tasks past
+// the end (last round) compute on clamped loads into their own spare slots.
+template <int MMAX, int NT, int TM = kTmax>
+SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const ActQ8K* la, int nb, int m,
+                               int tasks, int TS, float* pr) {
+    constexpr int SLOTS = NT / 8;
+    const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
+    // Block index of task u*SLOTS + grp: grp mod nb, stepped by SLOTS mod nb each round.
+    const uint32_t step = (uint32_t)SLOTS % (uint32_t)nb;
+    uint32_t b = (uint32_t)grp % (uint32_t)nb;
+#pragma unroll
+    for (int u = 0; u < TM; ++u) {
+        if (u * SLOTS >= tasks) break;  // uniform: no group has a task in this round
+        const uint32_t sc_lo = h[u].y & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (h[u].w & 0x0F0F0F0Fu) | (((h[u].y >> 6) & 0x03030303u) << 4);
+        const uint32_t mn_lo = h[u].z & 0x3F3F3F3Fu;
+        const uint32_t mn_hi = ((h[u].w >> 4) & 0x0F0F0F0Fu) | (((h[u].z >> 6) & 0x03030303u) << 4);
+        const int ml = (int)(((l < 4 ? mn_lo : mn_hi) >> (8 * (l & 3))) & 0xFF);
+        const uint32_t w4[8] = {q[u].x & 0x0F0F0F0Fu, (q[u].x >> 4) & 0x0F0F0F0Fu, q[u].y & 0x0F0F0F0Fu,
+                                (q[u].y >> 4) & 0x0F0F0F0Fu, q[u].z & 0x0F0F0F0Fu, (q[u].z >> 4) & 0x0F0F0F0Fu,
+                                q[u].w & 0x0F0F0F0Fu, (q[u].w >> 4) & 0x0F0F0F0Fu};
+        int sc[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sc[j] = (int)((sc_lo >> (8 * j)) & 0xFF);
+            sc[4 + j] = (int)((sc_hi >> (8 * j)) & 0xFF);
+        }
+        const float dw = h2f(h[u].x & 0xFFFF), dminw = h2f(h[u].x >> 16);
+#pragma unroll
+        for (int r = 0; r < MMAX; ++r) {
+            if (r < m) {
+                const ActQ8K& a = la[r * nb + (int)b];
+                const uint4 A0 = ((const uint4*)a.qs)[2 * l];
+                const uint4 A1 = ((const uint4*)a.qs)[2 * l + 1];
+                const int Aj[8] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w,
+                                   (int)A1.x, (int)A1.y, (int)A1.z, (int)A1.w};
+                int aux = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) aux += __mul24(__builtin_amdgcn_sdot4((int)w4[j], Aj[j], 0, false), sc[j]);
+                const int sumi = sum8_i32(__mul24(ml, a.bs2[l]));
+                const float ad = a.d;
+                float* p = pr + (r * TS + u * SLOTS + grp) * 9;
+                p[l] = (dw * ad) * (float)aux;
+                p[8] = (dminw * ad) * (float)sumi;  // same value from all eight lanes
+            }
+        }
+        b += step;
+        b = min(b, b - (uint32_t)nb);  // unsigned: subtracts nb only when b >= nb
+    }
+}
+
+// Fold of activation row rr: thread (tile row r = tid/8, lane class l) sums its lane
+// chain in block order, lane 0 also the min terms; the eight lane sums are then added
+// in Candle's order.  Every thread calls it; the result (sumf + (-0.0 + sums[0] + ...
+// + sums[7])) is valid in lane class 0 of rows < rows.
+SXQ_DEV float q4k_tile_fold(const float* pr, int TS, int nb, int rr, int rows) {
+    const int lane = threadIdx.x & 63, l = lane & 7, r = threadIdx.x >> 3;
+    float sl = 0.0f, sf = 0.0f;
+    if (r < rows) {
+        const float* p = pr + (rr * TS + r * nb) * 9;
+        for (int b = 0; b < nb; ++b) sl += p[b * 9 + l];
+        if (l == 0)
+            for (int b = 0; b < nb; ++b) sf -= p[b * 9 + 8];
+    }
+    float tot = -0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tot += __shfl(sl, (lane & ~7) + j, 64);
+    return sf + tot;
+}
+
+// RMSNorm + activation quantization as the prologue of a 1024-thread GEMV (one row of
+// dim <= 4096): thread t holds float4 t of the row and of the norm weight, i.e. lane
+// t%64's share of 256-element chunk t/64, so wave w normalises and quantizes chunk w
+// straight from registers into the LDS activation blocks.  The row's sum of squares is
+// rmsnorm_sumsq_1024 -- the same function and order as k_rmsnorm_quant -- so both paths
+// produce the same bits.
+SXQ_DEV void norm_fetch(float4& xv, float4& wv, const NormIn& ni, int dim) {
+    const int i = min((int)threadIdx.x, dim / 4 - 1);  // clamped: every load in bounds
+    xv = ((const float4*)ni.x)[i];
+    wv = ((const float4*)ni.w)[i];
+    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
+}
+template <int VDT>
+SXQ_DEV void norm_quant_store(const float4& xv, const float4& wv, const NormIn& ni, int dim, uint8_t* lds_act,
+                              float* red) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool mine = tid < dim / 4;
+    float ss = 0.0f;
+    if (mine) {
+        ss += xv.x * xv.x;
+        ss += xv.y * xv.y;
+        ss += xv.z * xv.z;
+        ss += xv.w * xv.w;
+    }
+    ss = rmsnorm_sumsq_1024(ss, red);
+    const float var = ss * (float)(1.0 / (double)dim) + 0.0f;
+    const float den = sqrtf(var * 1.0f + ni.eps);
+    const int nchunks = (dim + 255) / 256;
+    if (wave >= nchunks) return;  // uniform per wave
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (mine) {
+        v.x = (xv.x / den) * wv.x;
+        v.y = (xv.y / den) * wv.y;
+        v.z = (xv.z / den) * wv.z;
+        v.w = (xv.w / den) * wv.w;
+        if (ni.normed && blockIdx.x == 0) ((float4*)ni.normed)[tid] = v;
+    }
+    if (VDT == kQ8K) {
+        wave_quantize_q8k<false>(v, lane, lds_act + (size_t)wave * sizeof(ActQ8K));
+    } else {
+        wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < dim / 32, lds_act + (size_t)wave * 8 * sizeof(ActQ8_0));
+    }
+}
+
+}  // namespace sxq

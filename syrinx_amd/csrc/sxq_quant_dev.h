@@ -50,6 +50,25 @@ SXQ_DEV float dpp_f32(float v) {
 template <int CTRL>
 SXQ_DEV int dpp_i32(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
 
+// Wave-wide sum / max through DPP (xor 1, xor 2, the other quad of 8, the other 8 of 16:
+// every lane then holds its 16-lane row total) and the four row totals read as scalars,
+// (r0 + r1) + (r2 + r3).  Every lane gets the same value; wave-uniform control flow only.
+SXQ_DEV float row_total(float v, int r) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16 * r)); }
+SXQ_DEV float wave_sum_rows(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    return (row_total(v, 0) + row_total(v, 1)) + (row_total(v, 2) + row_total(v, 3));
+}
+SXQ_DEV float wave_max_rows(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    return fmaxf(fmaxf(row_total(v, 0), row_total(v, 1)), fmaxf(row_total(v, 2), row_total(v, 3)));
+}
+
 // Quantize J chunks of 256 consecutive activations at once (lane i holds elements
 // 4i..4i+3 of chunk j in v[j]) to Q8_K blocks: k_quants.rs BlockQ8K::from_float.  The
 // chunks' reductions are interleaved so their cross-lane latencies overlap; chunk j is

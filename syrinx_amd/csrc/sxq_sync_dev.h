@@ -1,5 +1,5 @@
 // sxq_sync_dev.h -- device helpers for handing data from the workgroups of one launch
-// to the last of them to arrive.
+// to the last of them to arrive, and for controlling which loads a wait covers.
 #pragma once
 #include "sxq_common.h"
 
@@ -32,5 +32,40 @@ SXQ_DEV bool publish_and_count(unsigned* counter, unsigned total, bool* flag) {
     __syncthreads();
     return *flag;
 }
+
+// 16-byte loads and stores coherent at agent scope (sc1), through a buffer resource over
+// `bytes` bytes at `base` (offsets in bytes; out-of-range loads return zeros).  The
+// compiler tracks their completion like any other load.
+SXQ_DEV __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+SXQ_DEV float4 load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+SXQ_DEV void store16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const f4 w = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, w), r, off, 0, 16);
+}
+
+// A 16-byte load through the global address space, whatever the pointer's type: a
+// generic pointer (one read from memory rather than passed as a kernel argument) would
+// give a flat load, which also counts against the LDS counter, so that every later LDS
+// wait would wait for it too.  Loaded as a native vector: HIP's uint4/float4 copy
+// through a generic reference, which would drop the address space again.
+template <typename T>
+SXQ_DEV T ld_global(const T* p) {
+    static_assert(sizeof(T) == 16, "16-byte loads");
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const v4u v = *(const __attribute__((address_space(1))) v4u*)(const void*)p;
+    return __builtin_bit_cast(T, v);
+}
+
+// Workgroup barrier without __syncthreads()'s memory fence: loads in flight stay in
+// flight (the fence would wait for all of them).
+SXQ_DEV void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
 
 }  // namespace sxq
