@@ -262,7 +262,9 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     } else {
         act_store<NT>(av, lds, act, act_u4);
     }
-    __syncthreads();
+    // The activations are in LDS; the weight loads may still be in flight: each round of
+    // products waits only for its own.
+    lds_barrier();
     q4k_tile_products<MMAX, NT>(q, h, la, nb, m, tasks, TS, pr);
     __syncthreads();
     // epilogue: thread (row r, lane class l) folds its chain in block order

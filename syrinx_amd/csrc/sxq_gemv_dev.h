@@ -1,6 +1,6 @@
-// sxq_gemv_dev.h -- one tile of the Q4_K x Q8_K task-split GEMV as device functions:
-// the per-launch GEMV kernels (sxq_gemv.hip) and the persistent decode kernel
-// (sxq_pipeline.hip) run the same code, so both give Candle's vec-dot bit for bit.
+// sxq_gemv_dev.h -- one tile of the Q4_K x Q8_K task-split GEMV (k_gemv2_q4k,
+// sxq_gemv.hip) as device functions: weight loads, per-task products, in-order fold.
+// The results are Candle's vec-dot bit for bit.
 //
 // A tile is `rows` consecutive weight rows starting at block index blk0 (row-major,
 // nb blocks per row); its rows*nb (row, block) tasks are dealt round-robin to the NT/8
@@ -17,6 +17,39 @@ namespace sxq {
 constexpr int kTmax = 8;
 
 SXQ_DEV float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
+
+// The integer part of a Q4_K task, aux32[l] = sum_j sc_j * dot_j over the eight
+// sub-blocks (exact in any order), as the instructions it should be: the compiler turns
+// sdot4(w, a, 0) into an accumulating v_dot4c plus a move of 0 into its destination,
+// and extracts each scale byte before multiplying.  Here: eight v_dot4_i32_i8 with c = 0,
+// then eight 24-bit multiplies whose scale operand is an SDWA byte select of the packed
+// scale word (scale j: byte j of slo for j < 4, byte j - 4 of shi).  One asm block, all
+// dots ahead of all multiplies: a dot's result may be read only some cycles after it
+// is written (the compiler pads with s_nop when it schedules them), and here each is
+// read eight instructions later.  |dot_j| <= 4 * 15 * 128 < 2^23, scales < 2^6.
+SXQ_DEV int q4k_aux(const int (&w)[8], const int (&a)[8], int slo, int shi) {
+    int d0, d1, d2, d3, d4, d5, d6, d7;
+    asm("v_dot4_i32_i8 %0, %8, %16, 0\n\t"
+        "v_dot4_i32_i8 %1, %9, %17, 0\n\t"
+        "v_dot4_i32_i8 %2, %10, %18, 0\n\t"
+        "v_dot4_i32_i8 %3, %11, %19, 0\n\t"
+        "v_dot4_i32_i8 %4, %12, %20, 0\n\t"
+        "v_dot4_i32_i8 %5, %13, %21, 0\n\t"
+        "v_dot4_i32_i8 %6, %14, %22, 0\n\t"
+        "v_dot4_i32_i8 %7, %15, %23, 0\n\t"
+        "v_mul_i32_i24_sdwa %0, %0, %24 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
+        "v_mul_i32_i24_sdwa %1, %1, %24 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
+        "v_mul_i32_i24_sdwa %2, %2, %24 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
+        "v_mul_i32_i24_sdwa %3, %3, %24 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3\n\t"
+        "v_mul_i32_i24_sdwa %4, %4, %25 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0\n\t"
+        "v_mul_i32_i24_sdwa %5, %5, %25 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1\n\t"
+        "v_mul_i32_i24_sdwa %6, %6, %25 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2\n\t"
+        "v_mul_i32_i24_sdwa %7, %7, %25 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=&v"(d0), "=&v"(d1), "=&v"(d2), "=&v"(d3), "=&v"(d4), "=&v"(d5), "=&v"(d6), "=&v"(d7)
+        : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]), "v"(a[0]),
+          "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]), "v"(slo), "v"(shi));
+    return ((d0 + d1) + (d2 + d3)) + ((d4 + d5) + (d6 + d7));
+}
 
 // Issue the weight loads of every task of this thread's group, TM rounds (clamped to
 // the last task, so all TM loads are unconditional and in flight together; the tile
@@ -56,15 +89,11 @@ SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const
         const uint32_t mn_lo = h[u].z & 0x3F3F3F3Fu;
         const uint32_t mn_hi = ((h[u].w >> 4) & 0x0F0F0F0Fu) | (((h[u].z >> 6) & 0x03030303u) << 4);
         const int ml = (int)(((l < 4 ? mn_lo : mn_hi) >> (8 * (l & 3))) & 0xFF);
-        const uint32_t w4[8] = {q[u].x & 0x0F0F0F0Fu, (q[u].x >> 4) & 0x0F0F0F0Fu, q[u].y & 0x0F0F0F0Fu,
-                                (q[u].y >> 4) & 0x0F0F0F0Fu, q[u].z & 0x0F0F0F0Fu, (q[u].z >> 4) & 0x0F0F0F0Fu,
-                                q[u].w & 0x0F0F0F0Fu, (q[u].w >> 4) & 0x0F0F0F0Fu};
-        int sc[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            sc[j] = (int)((sc_lo >> (8 * j)) & 0xFF);
-            sc[4 + j] = (int)((sc_hi >> (8 * j)) & 0xFF);
-        }
+        const int w4[8] = {(int)(q[u].x & 0x0F0F0F0Fu), (int)((q[u].x >> 4) & 0x0F0F0F0Fu),
+                           (int)(q[u].y & 0x0F0F0F0Fu), (int)((q[u].y >> 4) & 0x0F0F0F0Fu),
+                           (int)(q[u].z & 0x0F0F0F0Fu), (int)((q[u].z >> 4) & 0x0F0F0F0Fu),
+                           (int)(q[u].w & 0x0F0F0F0Fu), (int)((q[u].w >> 4) & 0x0F0F0F0Fu)};
+        const int slo = (int)sc_lo, shi = (int)sc_hi;  // scale of sub-block j: byte j of slo, j - 4 of shi
         const float dw = h2f(h[u].x & 0xFFFF), dminw = h2f(h[u].x >> 16);
 #pragma unroll
         for (int r = 0; r < MMAX; ++r) {
@@ -74,9 +103,7 @@ SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const
                 const uint4 A1 = ((const uint4*)a.qs)[2 * l + 1];
                 const int Aj[8] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w,
                                    (int)A1.x, (int)A1.y, (int)A1.z, (int)A1.w};
-                int aux = 0;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) aux += __mul24(__builtin_amdgcn_sdot4((int)w4[j], Aj[j], 0, false), sc[j]);
+                const int aux = q4k_aux(w4, Aj, slo, shi);
                 const int sumi = sum8_i32(__mul24(ml, a.bs2[l]));
                 const float ad = a.d;
                 float* p = pr + (r * TS + u * SLOTS + grp) * 9;
@@ -90,21 +117,41 @@ SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const
 }
 
 // Fold of activation row rr: thread (tile row r = tid/8, lane class l) sums its lane
-// chain in block order, lane 0 also the min terms; the eight lane sums are then added
-// in Candle's order.  Every thread calls it; the result (sumf + (-0.0 + sums[0] + ...
-// + sums[7])) is valid in lane class 0 of rows < rows.
+// chain in block order, and (every lane, the same values) the min terms; the eight lane
+// sums are then added in Candle's order.  The chains are sequential float adds, so the
+// terms are loaded eight blocks at a time ahead of them, and the lane sums reach lane
+// class 0 by DPP row shifts (lane j of the group -> lane 0) rather than LDS permutes.
+// Every thread calls it; the result (sumf + (-0.0 + sums[0] + ... + sums[7])) is valid
+// in lane class 0 of rows < rows.
 SXQ_DEV float q4k_tile_fold(const float* pr, int TS, int nb, int rr, int rows) {
-    const int lane = threadIdx.x & 63, l = lane & 7, r = threadIdx.x >> 3;
+    const int l = threadIdx.x & 7, r = threadIdx.x >> 3;
     float sl = 0.0f, sf = 0.0f;
     if (r < rows) {
         const float* p = pr + (rr * TS + r * nb) * 9;
-        for (int b = 0; b < nb; ++b) sl += p[b * 9 + l];
-        if (l == 0)
-            for (int b = 0; b < nb; ++b) sf -= p[b * 9 + 8];
-    }
-    float tot = -0.0f;
+        for (int b0 = 0; b0 < nb; b0 += 8) {
+            float t[8], mt[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) tot += __shfl(sl, (lane & ~7) + j, 64);
+            for (int k = 0; k < 8; ++k) {
+                const int b = min(b0 + k, nb - 1);  // clamped: in bounds, not added
+                t[k] = p[b * 9 + l];
+                mt[k] = p[b * 9 + 8];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (b0 + k < nb) {  // uniform
+                    sl += t[k];
+                    sf -= mt[k];
+                }
+        }
+    }
+    float tot = -0.0f + sl;
+    tot += dpp_f32<0x101>(sl);  // row_shl:j -- lane i reads lane i + j of its row of 16
+    tot += dpp_f32<0x102>(sl);
+    tot += dpp_f32<0x103>(sl);
+    tot += dpp_f32<0x104>(sl);
+    tot += dpp_f32<0x105>(sl);
+    tot += dpp_f32<0x106>(sl);
+    tot += dpp_f32<0x107>(sl);
     return sf + tot;
 }
 

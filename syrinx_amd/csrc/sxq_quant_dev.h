@@ -27,11 +27,19 @@ SXQ_DEV int wave_min_i32(int v) {
 // This is the RMSNorm sum of squares of every kernel here (fused GEMV prologue and the
 // standalone RMSNorm), so they agree bit for bit.  `red`: 16 floats of LDS.  Every
 // thread of the workgroup must call it (it synchronises).
+// Workgroup barrier that waits only for this wave's LDS accesses (lgkmcnt(0)), not for
+// its global loads: __syncthreads() waits for every outstanding load, so a GEMV's
+// weight loads issued ahead of it would all have to land before anything after it ran.
+SXQ_DEV void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
+    asm volatile("s_barrier" ::: "memory");
+}
+
 SXQ_DEV float rmsnorm_sumsq_1024(float ss, float* red) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
+    lds_barrier();
     float t[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) t[i] = red[2 * i] + red[2 * i + 1];
