@@ -22,28 +22,12 @@ SXQ_DEV int wave_min_i32(int v) {
     return v;
 }
 
-// Sum of one f32 per thread over a 1024-thread workgroup, in a fixed order: xor
-// butterfly inside each wave, then the sixteen wave sums as a balanced pairwise tree.
-// This is the RMSNorm sum of squares of every kernel here (fused GEMV prologue and the
-// standalone RMSNorm), so they agree bit for bit.  `red`: 16 floats of LDS.  Every
-// thread of the workgroup must call it (it synchronises).
 // Workgroup barrier that waits only for this wave's LDS accesses (lgkmcnt(0)), not for
 // its global loads: __syncthreads() waits for every outstanding load, so a GEMV's
 // weight loads issued ahead of it would all have to land before anything after it ran.
 SXQ_DEV void lds_barrier() {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited for
     asm volatile("s_barrier" ::: "memory");
-}
-
-SXQ_DEV float rmsnorm_sumsq_1024(float ss, float* red) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    lds_barrier();
-    float t[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) t[i] = red[2 * i] + red[2 * i + 1];
-    return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
 }
 
 // In-row DPP steps (lanes combine inside 16-lane rows): quad_perm xor1 = 0xB1,
@@ -77,6 +61,21 @@ SXQ_DEV float wave_max_rows(float v) {
     return fmaxf(fmaxf(row_total(v, 0), row_total(v, 1)), fmaxf(row_total(v, 2), row_total(v, 3)));
 }
 
+// Sum of one f32 per thread over a 1024-thread workgroup, in a fixed order: each wave's
+// sum as wave_sum_rows, then the sixteen wave sums as a balanced pairwise tree.  This
+// is the RMSNorm sum of squares of every kernel here (fused GEMV prologue and the
+// standalone RMSNorm), so they agree bit for bit.  `red`: 16 floats of LDS.  Every
+// thread of the workgroup must call it (it synchronises, on LDS only).
+SXQ_DEV float rmsnorm_sumsq_1024(float ss, float* red) {
+    ss = wave_sum_rows(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    lds_barrier();
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[i] = red[2 * i] + red[2 * i + 1];
+    return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
 // Quantize J chunks of 256 consecutive activations at once (lane i holds elements
 // 4i..4i+3 of chunk j in v[j]) to Q8_K blocks: k_quants.rs BlockQ8K::from_float.  The
 // chunks' reductions are interleaved so their cross-lane latencies overlap; chunk j is
@@ -105,10 +104,11 @@ SXQ_DEV void wave_quantize_q8k_n(const float4 (&v)[J], int lane, void* const (&o
     for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], dpp_f32<0x141>(wmax[j]));
 #pragma unroll
     for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], dpp_f32<0x140>(wmax[j]));
+    // the four 16-lane row maxima, read as scalars (max is exact in any order)
 #pragma unroll
-    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], __shfl_xor(wmax[j], 16, 64));
-#pragma unroll
-    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], __shfl_xor(wmax[j], 32, 64));
+    for (int j = 0; j < J; ++j)
+        wmax[j] = fmaxf(fmaxf(row_total(wmax[j], 0), row_total(wmax[j], 1)),
+                        fmaxf(row_total(wmax[j], 2), row_total(wmax[j], 3)));
     int first[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) first[j] = am[j] == wmax[j] ? 4 * lane + ix[j] : 256;
@@ -121,9 +121,9 @@ SXQ_DEV void wave_quantize_q8k_n(const float4 (&v)[J], int lane, void* const (&o
 #pragma unroll
     for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0x140>(first[j]));
 #pragma unroll
-    for (int j = 0; j < J; ++j) first[j] = min(first[j], __shfl_xor(first[j], 16, 64));
-#pragma unroll
-    for (int j = 0; j < J; ++j) first[j] = min(first[j], __shfl_xor(first[j], 32, 64));
+    for (int j = 0; j < J; ++j)
+        first[j] = min(min(__builtin_amdgcn_readlane(first[j], 0), __builtin_amdgcn_readlane(first[j], 16)),
+                       min(__builtin_amdgcn_readlane(first[j], 32), __builtin_amdgcn_readlane(first[j], 48)));
     int q[J][4], s8[J], s4[J];
     float d[J];
 #pragma unroll
@@ -190,9 +190,9 @@ SXQ_DEV void wave_quantize_q8_0(float4 v, int lane, bool valid, void* out) {
     float am = 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) am = fmaxf(am, fabsf(x[r]));
-    am = fmaxf(am, __shfl_xor(am, 1, 64));
-    am = fmaxf(am, __shfl_xor(am, 2, 64));
-    am = fmaxf(am, __shfl_xor(am, 4, 64));
+    am = fmaxf(am, dpp_f32<0xB1>(am));   // xor 1
+    am = fmaxf(am, dpp_f32<0x4E>(am));   // xor 2
+    am = fmaxf(am, dpp_f32<0x141>(am));  // the other quad of the 8: the 8-lane max
     const float d = am / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     int q[4];
@@ -200,9 +200,9 @@ SXQ_DEV void wave_quantize_q8_0(float4 v, int lane, bool valid, void* out) {
     for (int r = 0; r < 4; ++r) q[r] = sat_i8(roundf(x[r] * id));
     const uint16_t dh = f32_to_f16_bits(d);
     int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
+    s += dpp_i32<0xB1>(s);
+    s += dpp_i32<0x4E>(s);
+    s += dpp_i32<0x141>(s);
     if (!valid) return;
     const int blk = lane >> 3, w = lane & 7;
     const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
