@@ -281,6 +281,87 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     }
 }
 
+// ------------------------------------------------- SwiGLU pair around the down projection
+// One decode row (m = 1, 1024 threads), Q4_K weights.  k_gemv2_q4k_swiglu is the fused
+// RMSNorm GEMV of the gate|up weight [2I][nb] (gate rows 0..I-1, up rows I..2I-1) whose
+// tile t holds gate rows [tB, tB + Bt) and the same up rows [I + tB, I + tB + Bt), so its
+// epilogue has both halves of each pair: it stores gu (both halves, canonical order) and
+// a = silu(g) * u -- k_silu_mul_quant's arithmetic -- as f32.  k_gemv2_q4k_quant is the
+// down projection whose prologue quantizes that f32 row to Q8_K in LDS (chunk c by wave
+// c mod 16, the quantizer of k_silu_mul_quant), so the two leave the same bits as the
+// GEMV + SiLU*mul kernel + GEMV sequence, one launch and one quantized row fewer.
+__global__ __launch_bounds__(1024) void k_gemv2_q4k_swiglu(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
+                                                           int I, int nb, int B, NormIn ni, float* __restrict__ gu,
+                                                           float* __restrict__ act_f32) {
+    constexpr int NT = 1024, SLOTS = NT / 8;
+    extern __shared__ uint4 lds[];
+    __shared__ float sw[NT / 8];  // the tile's row results: gate [0, Bt), up [Bt, 2Bt)
+    __shared__ float red[16];
+    const ActQ8K* la = (const ActQ8K*)lds;
+    const int t = blockIdx.x, g0 = t * B, Bt = min(B, I - g0);
+    const int rows = 2 * Bt, tasks = rows * nb, seg = Bt * nb;
+    const int TS = (tasks + SLOTS - 1) / SLOTS * SLOTS;
+    float* pr = (float*)(lds + (size_t)nb * (sizeof(ActQ8K) / 16));  // [TS][9]
+    float4 xv, wv;
+    norm_fetch(xv, wv, ni, nb * 256);
+    uint4 q[kTmax], h[kTmax];
+    q4k_tile_load2<NT>(hdr, qs, (uint32_t)g0 * (uint32_t)nb, (uint32_t)(I + g0) * (uint32_t)nb, seg, tasks, q, h);
+    norm_quant_store<kQ8K>(xv, wv, ni, nb * 256, (uint8_t*)lds, red);
+    lds_barrier();
+    q4k_tile_products<1, NT>(q, h, la, nb, 1, tasks, TS, pr);
+    __syncthreads();
+    const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
+    const float v = q4k_tile_fold(pr, TS, nb, 0, rows);
+    if (r < rows && l == 0) {
+        sw[r] = v;
+        gu[r < Bt ? g0 + r : I + g0 + (r - Bt)] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < Bt) {
+        const float gv = sw[threadIdx.x], uv = sw[Bt + threadIdx.x];
+        act_f32[g0 + threadIdx.x] = (gv / (1.0f + expf(-gv))) * uv;
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
+                                                          int n, int nb, int R, const float* __restrict__ x,
+                                                          float* y, const float* res) {
+    constexpr int NT = 1024, SLOTS = NT / 8, J = 3;
+    extern __shared__ uint4 lds[];
+    ActQ8K* la = (ActQ8K*)lds;
+    const int row0 = blockIdx.x * R, rows = min(R, n - row0), tasks = rows * nb;
+    const int TS = (tasks + SLOTS - 1) / SLOTS * SLOTS;
+    float* pr = (float*)(lds + (size_t)nb * (sizeof(ActQ8K) / 16));  // [TS][9]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // wave w quantizes chunks w, w + 16, w + 32 (nb <= 48); their loads go ahead of the
+    // weight loads, which return after them
+    float4 v[J];
+    void* out[J];
+    bool valid[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = wave + 16 * j, cc = min(c, nb - 1);
+        valid[j] = c < nb;
+        out[j] = la + cc;
+        v[j] = *(const float4*)(x + cc * 256 + 4 * lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 q[kTmax], h[kTmax];
+    q4k_tile_load<NT>(hdr, qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
+    if (wave < nb) wave_quantize_q8k_n<J, false>(v, lane, out, valid);  // uniform per wave
+    lds_barrier();
+    q4k_tile_products<1, NT>(q, h, la, nb, 1, tasks, TS, pr);
+    __syncthreads();
+    const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
+    const float v0 = q4k_tile_fold(pr, TS, nb, 0, rows);
+    if (r < rows && l == 0) {
+        const int row = row0 + r;
+        float v = v0;
+        if (res) v = res[row] + v;
+        y[row] = v;
+    }
+}
+
 // Q8_0 / Q4_0 task-split GEMV: a lane pair per Q8_0 task (16 bytes each), one lane per
 // Q4_0 task; NT threads per workgroup.
 template <int MMAX, bool Q4, bool NORM, int NT>
@@ -495,6 +576,41 @@ hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64
     if (m <= 8) return gemv_dispatch<8>(w, act, m, y, ldy, bias, res, ldr, s);
     if (m <= 16) return gemv_dispatch<16>(w, act, m, y, ldy, bias, res, ldr, s);
     return hipErrorInvalidValue;
+}
+
+// SwiGLU pair sizing: B gate rows per tile so that the tiles spread over one
+// workgroup per CU, within the tile limits (2B rows <= NT/8, 2B*nb tasks <= kTmax rounds).
+static int swiglu_rows(int I, int nb) {
+    int B = (I + 255) / 256;
+    B = min(B, 1024 / 16);
+    B = min(B, max(1, (1024 / 8) * kTmax / (2 * nb)));
+    return max(B, 1);
+}
+
+bool swiglu_pair_fits(const QWeight& gate_up, const QWeight& down) {
+    const int I = (int)(gate_up.n / 2), nb = (int)gate_up.nb;
+    return gate_up.dtype == kQ4K && down.dtype == kQ4K && gate_up.n == 2 * (int64_t)I && down.k == I &&
+           gate_up.k <= kNormMaxDim && I % 256 == 0 && I / 256 <= 48 &&
+           gemv2_fits((int)down.n, (int)down.nb, 1, kQ4K, 1024) &&
+           2 * swiglu_rows(I, nb) * nb <= (1024 / 8) * kTmax;
+}
+
+hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const NormIn& ni, float* gu, float* act_f32,
+                              float* y, const float* res, hipStream_t s) {
+    if (!swiglu_pair_fits(gate_up, down)) return hipErrorInvalidValue;
+    const int I = (int)(gate_up.n / 2), nb = (int)gate_up.nb;
+    const int B = swiglu_rows(I, nb);
+    const size_t lds1 = gemv2_lds(nb, 1, 2 * B, kQ4K, 1024);
+    hipLaunchKernelGGL(k_gemv2_q4k_swiglu, dim3((I + B - 1) / B), dim3(1024), lds1, s, (const uint4*)gate_up.hdr,
+                       (const uint4*)gate_up.qs, I, nb, B, ni, gu, act_f32);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int n = (int)down.n, nb2 = (int)down.nb;
+    const int R = gemv2_rows(n, nb2, 1, kQ4K, 1024);
+    const size_t lds2 = gemv2_lds(nb2, 1, R, kQ4K, 1024);
+    hipLaunchKernelGGL(k_gemv2_q4k_quant, dim3((n + R - 1) / R), dim3(1024), lds2, s, (const uint4*)down.hdr,
+                       (const uint4*)down.qs, n, nb2, R, act_f32, y, res);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,

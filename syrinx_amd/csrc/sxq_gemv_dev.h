@@ -69,6 +69,25 @@ SXQ_DEV void q4k_tile_load(const uint4* __restrict__ hdr, const uint4* __restric
     }
 }
 
+// The same for a tile of two row segments: tasks [0, seg) are blocks blkA + t, tasks
+// [seg, tasks) blocks blkB + (t - seg) (seg a whole number of rows: a multiple of nb,
+// so a task's block index within its row is still t mod nb).
+template <int NT, int TM = kTmax>
+SXQ_DEV void q4k_tile_load2(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, uint32_t blkA, uint32_t blkB,
+                            int seg, int tasks, uint4 (&q)[TM], uint4 (&h)[TM]) {
+    constexpr int SLOTS = NT / 8;
+    const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
+    const char* qbase = (const char*)qs + (l << 4);
+    const char* hbase = (const char*)hdr;
+#pragma unroll
+    for (int u = 0; u < TM; ++u) {
+        const int t = min(u * SLOTS + grp, tasks - 1);
+        const uint32_t blk = t < seg ? blkA + (uint32_t)t : blkB + (uint32_t)(t - seg);
+        q[u] = ld_global((const uint4*)(qbase + (blk << 7)));
+        h[u] = ld_global((const uint4*)(hbase + (blk << 4)));
+    }
+}
+
 // Per-task float products into pr [m][TS][9] (TS = tasks rounded up to whole rounds):
 // the eight lane terms (d_w*d_a)*(f32)aux32[l] and the min term (dmin_w*d_a)*(f32)sumi
 // of Candle's Q4_K vec-dot, against the LDS activation blocks la [m][nb].  Tasks past

@@ -47,6 +47,15 @@ struct NormIn {
 hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,
                                int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s);
 
+// The feed-forward of one decode row (m = 1) around SwiGLU, Q4_K weights: the fused
+// RMSNorm GEMV of the gate|up weight [2I][k] (gate rows first) writes gu [2I] and
+// act_f32 = silu(gate) * up [I]; the down GEMV [n][I] quantizes act_f32 in its prologue
+// and writes y = res + down . act (res may be null).  Two launches; the same bits as the
+// GEMV + SiLU*mul + quantize + GEMV sequence.
+bool swiglu_pair_fits(const QWeight& gate_up, const QWeight& down);
+hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const NormIn& ni, float* gu, float* act_f32,
+                              float* y, const float* res, hipStream_t s);
+
 // Prefill GEMM for Q4_K weights (sxq_gemm.hip): y = x . dequant(W)^T on MFMA with f16
 // operands (+ bias, + res).  The workspace (gemm_q4k_workspace bytes) holds x rounded to
 // f16 in the GEMM's K order and, when K is split across workgroups, the partial tiles

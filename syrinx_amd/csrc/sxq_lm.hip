@@ -69,6 +69,8 @@ struct sxq_lm {
     unsigned* am_count = nullptr;   // per-stream arrival counters (zero between steps)
     unsigned* attn_count = nullptr; // per-(stream, KV head) arrival counters of the fused attention
     bool attn_fused = false;
+    bool swiglu = false;        // one decode row: gate|up GEMV with SwiGLU epilogue + quantizing down GEMV
+    float* act_f32 = nullptr;   // SwiGLU output row of that pair [max_batch][intermediate]
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
     hipStream_t cap = nullptr;
     std::map<GraphKey, hipGraphExec_t> graphs;
@@ -205,11 +207,18 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
         }
         STEP(launch_gemv(L.wo.w, lm->act_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
         if (tr) STEP(record(lm->h, nd));
-        STEP(launch_gemv_rmsnorm(L.w13.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), n, lm->act_a, lm->gu,
-                                 2 * I, nullptr, nullptr, 0, s));
-        if (tr) STEP(record(lm->gu, (size_t)n * 2 * I));
-        STEP(launch_silu_mul_quant(lm->vdt, lm->gu, n, I, lm->act_d, tr ? slot((size_t)n * I) : nullptr, s));
-        STEP(launch_gemv(L.w2.w, lm->act_d, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+        if (lm->swiglu && n == 1) {
+            STEP(launch_swiglu_pair(L.w13.w, L.w2.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), lm->gu,
+                                    lm->act_f32, lm->h, lm->h, s));
+            if (tr) STEP(record(lm->gu, (size_t)2 * I));
+            if (tr) STEP(record(lm->act_f32, (size_t)I));
+        } else {
+            STEP(launch_gemv_rmsnorm(L.w13.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), n, lm->act_a,
+                                     lm->gu, 2 * I, nullptr, nullptr, 0, s));
+            if (tr) STEP(record(lm->gu, (size_t)n * 2 * I));
+            STEP(launch_silu_mul_quant(lm->vdt, lm->gu, n, I, lm->act_d, tr ? slot((size_t)n * I) : nullptr, s));
+            STEP(launch_gemv(L.w2.w, lm->act_d, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+        }
         if (tr) STEP(record(lm->h, nd));
     }
     STEP(launch_gemv_rmsnorm(lm->head.w, norm_in(lm->h, lm->final_norm, tr ? slot(nd) : nullptr), n, lm->act_a,
@@ -305,6 +314,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->qbuf, sizeof(float) * (size_t)MB * lm->ctx);
     A((void**)&lm->part, sizeof(float) * (size_t)MB * c.n_heads * lm->max_splits * (hd + 4));
     A((void**)&lm->gu, sizeof(float) * (size_t)MB * 2 * I);
+    A((void**)&lm->act_f32, sizeof(float) * (size_t)MB * I);
     A((void**)&lm->logits, sizeof(float) * (size_t)MB * c.vocab);
     const size_t ab = act_block_bytes(lm->vdt), bs = block_size(lm->vdt);
     A((void**)&lm->act_a, ab * MB * (c.dim / bs));
@@ -351,6 +361,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     if (e == hipSuccess) e = hipMemset(lm->am_count, 0, sizeof(unsigned) * MB);
     if (e == hipSuccess) e = hipMemset(lm->attn_count, 0, sizeof(unsigned) * MB * c.n_kv_heads);
     lm->attn_fused = getenv("SXQ_ATTN_UNFUSED") == nullptr && attn_decode_fits(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits);
+    lm->swiglu = getenv("SXQ_SWIGLU_UNFUSED") == nullptr && swiglu_pair_fits(lm->layers[0].w13.w, lm->layers[0].w2.w);
     if (e == hipSuccess && lm->attn_fused &&
         attn_decode_prepare(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits) != hipSuccess) {
         (void)hipGetLastError();  // clear it: the three-kernel path needs no opt-in

@@ -337,6 +337,29 @@ def test_graph_replay_equals_eager_and_feeds_back_argmax(cuda):
         np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("graph", [False, True])
+def test_swiglu_pair_equals_three_launches(cuda, monkeypatch, graph):
+    """One decode row: the gate|up GEMV with the SwiGLU epilogue and the down GEMV that
+    quantizes in its prologue give the bits of GEMV + SiLU*mul kernel + GEMV."""
+    cfg = _fish_small(n_layers=2)
+    res = {}
+    for mode in ("pair", "three"):
+        if mode == "three":
+            monkeypatch.setenv("SXQ_SWIGLU_UNFUSED", "1")  # read when the engine is created
+        lm = D.DecoderLM(cfg, device=cuda)
+        lm.init_random(seed=41, std=0.02)
+        lm.kv_fill_random([33], seed=42)
+        fr = _frames(np.random.default_rng(43), 1, cfg)
+        logits, _ = lm.step(ids=torch.from_numpy(fr), graph=graph)
+        outs = [logits.cpu().numpy()]
+        for _ in range(3):
+            logits, _ = lm.step(n=1, graph=graph)
+            outs.append(logits.cpu().numpy())
+        res[mode] = outs
+    for a, b in zip(res["pair"], res["three"]):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_full_cache_is_an_error(cuda):
     cfg = _fish_small(n_layers=1)
     cfg.max_seq = 8
