@@ -9,8 +9,9 @@ Weights are random N(0, 0.02) quantized with Candle's from_float (synthetic data
 A step is one decode token (embedding -> 36 layers -> head -> argmax fed back on the
 device), replayed as a captured HIP graph.  `value` is tokens per second over the
 timed steps.  `roofline` is the Q4_K GEMV family (every projection of a token,
-launched back to back over 2.27 GB of weights) timed with HIP events on the stream
-the kernels run on: algorithmic bytes (weight blocks + activations + outputs) per
+launched back to back over 2.27 GB of weights, captured as a HIP graph like the decode
+step and replayed; the eager-launch time is reported beside it) timed with HIP events
+on the stream the kernels run on: algorithmic bytes (weight blocks + activations + outputs) per
 launch over the average launch duration, against 8 TB/s.  `cpu_baseline` times the
 oracle (the CPU restatement of Candle's quantized matmul) on one layer's projections
 plus the head, on this host's cores, and scales it to one token's GEMV work.
@@ -98,9 +99,27 @@ def gemv_roofline(lm, torch, iters):
         check(lib().sxq_lm_gemv_pass(lm._h, 1, 1, ctypes.c_void_p(s.cuda_stream)))
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # eager launches (reported alongside): each launch adds the host-queue dispatch cost
     e0.record(s)
     for _ in range(iters):
         check(lib().sxq_lm_gemv_pass(lm._h, 1, 1, ctypes.c_void_p(s.cuda_stream)))
+    e1.record(s)
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / iters
+    # the measured pass: the same launches captured once as a HIP graph and replayed, as
+    # the decode step runs them
+    graph = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream(dev)
+    cs.wait_stream(s)
+    with torch.cuda.graph(graph, stream=cs):
+        check(lib().sxq_lm_gemv_pass(lm._h, 1, 1, ctypes.c_void_p(cs.cuda_stream)))
+    s.wait_stream(cs)
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0.record(s)
+    for _ in range(iters):
+        graph.replay()
     e1.record(s)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / iters
@@ -113,7 +132,8 @@ def gemv_roofline(lm, torch, iters):
             "algorithmic_bytes_per_launch": round(algo / n_launch),
             "kernel": "k_gemv2_q4k" if c.weight_dtype == 12 else "k_gemv2_q80",
             "bytes_per_token": algo, "launches_per_token": n_launch, "avg_launch_us": round(avg_us, 3),
-            "gemv_us_per_token": round(ms * 1000.0, 2)}
+            "gemv_us_per_token": round(ms * 1000.0, 2), "replay": "hip graph",
+            "eager_gemv_us_per_token": round(eager_ms * 1000.0, 2)}
 
 
 def cpu_threads():
@@ -242,7 +262,7 @@ def main():
     print(f"[bench] model ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     if args.mode == "gemv":
         roof = gemv_roofline(lm, torch, args.gemv_iters)
-        print(json.dumps({"mode": "gemv", "passes": args.gemv_iters + 2, "roofline": roof}))
+        print(json.dumps({"mode": "gemv", "passes": 2 * (args.gemv_iters + 2), "roofline": roof}))
         return
     rng_frame = torch.zeros((args.batch, 1 + cfg.n_codebooks), dtype=torch.int32)
     rng_frame[:, 0] = 151700

@@ -45,10 +45,7 @@ SXQ_HD int q4k_perm_elem(int p) {
 
 constexpr int kGemmBM = 256, kGemmBN = 128;
 constexpr int kGemmAStage = kGemmBM * 64 * 2;  // activations of one K group: 256 rows x 64 halfs
-constexpr int kGemmWStage = kGemmBN * 2 * 16;  // weights of one K group: 128 rows x 2 segments
-constexpr int kGemmWOff = 2 * kGemmAStage;     // within one K half's region: 2 stages each
-constexpr int kGemmHdOff = kGemmWOff + 2 * kGemmWStage;  // block headers, 1 KB per wave
-constexpr int kGemmHalfBytes = kGemmHdOff + 4 * 1024;    // 77824
+constexpr int kGemmHalfBytes = 2 * kGemmAStage;  // one K half's region: 2 activation stages
 
 int gemm_xh_rows(int m) { return (m + kGemmBM - 1) / kGemmBM * kGemmBM; }
 size_t gemm_q4k_lds() { return 2 * (size_t)kGemmHalfBytes; }
@@ -81,27 +78,23 @@ __global__ __launch_bounds__(256) void k_x_to_f16_perm(const float* __restrict__
 
 // The 8 (scale, min) pairs of a Q4_K block header (get_scale_min_k4), times d and dmin:
 // sv[j] = d * sc_j, nm[j] = -(dmin * m_j), both exact in f32 (11-bit times 6-bit
-// significands).  The 12 scale bytes are header bytes 4..15 (dwords y, z, w), taken
-// with shifts so the header stays in registers; d and dmin convert in hardware.
+// significands).  The 12 scale bytes are header bytes 4..15 (dwords y, z, w = q[0..3],
+// q[4..7], q[8..11]); the four 6-bit values of each kind are assembled a dword at a time
+// (sc_j = q[j] & 63, m_j = q[j+4] & 63 for j < 4; sc_{j+4} = (q[j+8] & 15) | (q[j] >> 6) << 4,
+// m_{j+4} = (q[j+8] >> 4) | (q[j+4] >> 6) << 4) and each byte converts with one
+// v_cvt_f32_ubyte<t>.
 SXQ_DEV void q4k_scales(const uint4& h, float sv[8], float nm[8]) {
-    auto sc = [&](int i) -> int {
-        const uint32_t d = i < 4 ? h.y : (i < 8 ? h.z : h.w);
-        return (int)((d >> (8 * (i & 3))) & 0xFF);
-    };
+    const uint32_t s03 = h.y & 0x3F3F3F3Fu, m03 = h.z & 0x3F3F3F3Fu;
+    const uint32_t s47 = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m47 = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
     const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFF));
     const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16));
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        int scv, m;
-        if (j < 4) {
-            scv = sc(j) & 63;
-            m = sc(j + 4) & 63;
-        } else {
-            scv = (sc(j + 4) & 0xF) | ((sc(j - 4) >> 6) << 4);
-            m = (sc(j + 4) >> 4) | ((sc(j) >> 6) << 4);
-        }
-        sv[j] = d * (float)scv;
-        nm[j] = -(dmin * (float)m);
+    for (int t = 0; t < 4; ++t) {
+        sv[t] = d * (float)((s03 >> (8 * t)) & 0xFF);
+        sv[t + 4] = d * (float)((s47 >> (8 * t)) & 0xFF);
+        nm[t] = -(dmin * (float)((m03 >> (8 * t)) & 0xFF));
+        nm[t + 4] = -(dmin * (float)((m47 >> (8 * t)) & 0xFF));
     }
 }
 
@@ -149,20 +142,12 @@ SXQ_DEV void lgkm_wait(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
 }
 SXQ_DEV uint32_t lds_addr(const lds_u8* p) { return (uint32_t)(uintptr_t)p; }
 
-// 16-byte global accesses coherent at agent scope (sc1: past the XCD's own L2), for the
-// partial tiles one workgroup hands to another; the load's value is ready after vm_wait.
+// Buffer resource over `bytes` bytes at `base` (raw offsets in bytes, no swizzle).
+SXQ_DEV __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-SXQ_DEV void store16_agent(float* p, f32x4 v) { asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory"); }
-SXQ_DEV f32x4 load16_agent(const float* p) {
-    f32x4 r;
-    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(r) : "v"(p));
-    return r;
-}
-SXQ_DEV void vm_wait0(f32x4 (&v)[3][4]) {
-    asm volatile("s_waitcnt vmcnt(0)" : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[0][2]), "+v"(v[0][3]), "+v"(v[1][0]),
-                 "+v"(v[1][1]), "+v"(v[1][2]), "+v"(v[1][3]), "+v"(v[2][0]), "+v"(v[2][1]), "+v"(v[2][2]),
-                 "+v"(v[2][3]));
-}
 
 // barrier_nofence (sxq_sync_dev.h) between stages: __syncthreads()'s fence would make
 // the compiler wait for every outstanding global->LDS load, including the ones issued
@@ -181,15 +166,18 @@ SXQ_DEV void vm_wait0(f32x4 (&v)[3][4]) {
 // operand feeds 8 MFMAs.  At the end the halves add their accumulators through LDS, half
 // 0's first, and each half finishes four of the eight 32-row tiles.
 //
-// Every operand reaches LDS by direct global->LDS loads one group ahead, into 2 stages per
-// half, so no load lands in registers and the loop's only waits are explicit vmcnt counts:
-//  - activations: within a stage row r's 16-byte chunk c sits at chunk slot
-//    8r + (c ^ ((r >> 1) & 7)): the MFMA operand reads of any 16 consecutive rows hit 16
-//    different 16-byte bank groups (64 banks of 4 bytes);
-//  - weights: lane (n, h) loads segment 2g + h of its row into its own slot and reads it
-//    back itself, dequantizing each dword straight into MFMA B registers;
-//  - block headers: one block ahead, decoded once per block into 16 floats.
-// One barrier per pair of groups (one per half, in lockstep).
+// Every operand is loaded one group ahead, by buffer loads whose per-group offsets sit in
+// scalar registers (no per-lane address arithmetic in the loop), and the loop's only
+// memory waits are explicit vmcnt counts:
+//  - activations go straight to LDS (buffer_load ... lds), 2 stages per half; within a
+//    stage row r's 16-byte chunk c sits at chunk slot 8r + (c ^ ((r >> 1) & 7)): the MFMA
+//    operand reads of any 16 consecutive rows hit 16 different 16-byte bank groups (64
+//    banks of 4 bytes);
+//  - weights go to registers: lane (n, h) loads segment 2g + h of its row and dequantizes
+//    each dword straight into MFMA B registers;
+//  - block headers go to registers one block ahead and are decoded into 16 floats at the
+//    block's first group, while that group's first activation reads are in flight.
+// One barrier per group (both halves in lockstep).
 //
 // A tile split S ways: split z covers blocks [nb*z/S, nb*(z+1)/S); every split stores its
 // partial tile, and the last to arrive (per-tile counter) adds the partials in split order,
@@ -216,57 +204,60 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
     const int ln = lane & 31, lh = lane >> 5;
     lds_u8* hbase = (lds_u8*)lds + kh * kGemmHalfBytes;
 
+    // Buffer resources over this tile's operands (activation rows m0 .., weight rows n0 ..),
+    // so that every load of the loop takes its per-group offset from a scalar register.
+    const int nrows = min(kGemmBN, N - n0);
+    const __amdgpu_buffer_rsrc_t arsrc = tile_rsrc(xh + (int64_t)m0 * K, (uint32_t)kGemmBM * (uint32_t)K * 2u);
+    const __amdgpu_buffer_rsrc_t wrsrc = tile_rsrc(qs + (int64_t)n0 * nb * 8, (uint32_t)nrows * (uint32_t)nb * 128u);
+    const __amdgpu_buffer_rsrc_t hrsrc = tile_rsrc(hdr + (int64_t)n0 * nb, (uint32_t)nrows * (uint32_t)nb * 16u);
     // Activation loads: chunk slot (8 wv + u) * 64 + lane of a stage is row
-    // r = 64 wv + 8u + lane/8, chunk (lane % 8) ^ ((r >> 1) % 8) of the group.
-    // (Row r + 8u has (r >> 1) & 7 with bit 2 flipped when u is odd.)
+    // r = 64 wv + 8u + lane/8, chunk (lane % 8) ^ ((r >> 1) % 8) of the group.  Row r + 8u has
+    // (r >> 1) & 7 with bit 2 flipped when u is odd, so two lane offsets serve all 8 loads.
     const int ar = 64 * wv + (lane >> 3);
     const int ac0 = (lane & 7) ^ ((ar >> 1) & 7);
-    const _Float16* asrc = xh + (int64_t)(m0 + ar) * K + 8 * ac0;
-    const int64_t arow8 = (int64_t)8 * K;
-    const int aodd = 8 * ((ac0 ^ 4) - ac0);  // column shift of the odd-u rows, in halfs
-    // Weight row of this lane (rows past N clamped: loaded, never stored).
-    const int64_t wr = min(n0 + 32 * wv + ln, N - 1);
-    const uint4* q0 = qs + wr * nb * 8 + lh;
-    const uint4* hsrc = hdr + wr * nb;  // both halves of the wave load the row's header
+    const uint32_t aoff_even = (uint32_t)ar * (uint32_t)K * 2u + 16u * ac0;
+    const uint32_t aoff_odd = (uint32_t)ar * (uint32_t)K * 2u + 16u * (ac0 ^ 4);
+    const uint32_t arow8 = 16u * (uint32_t)K;  // 8 rows, in bytes
+    // Weight row of this lane relative to n0 (rows past N clamped: loaded, never stored).
+    const int wrel = min(32 * wv + ln, nrows - 1);
+    const uint32_t woff = ((uint32_t)wrel * nb * 8u + lh) * 16u, hoff = (uint32_t)wrel * nb * 16u;
     // LDS byte addresses of this lane's reads (stage and row-tile offsets are immediates):
     // activation chunk of step s for row tile 0 (rows ln and 32 mt + ln share (r >> 1) & 7).
     uint32_t aaddr[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) aaddr[s] = lds_addr(hbase) + 16 * (8 * ln + ((2 * s + lh) ^ ((ln >> 1) & 7)));
-    lds_u8* wlds = hbase + kGemmWOff + wv * 1024;  // + stage * kGemmWStage + lane * 16
-    lds_u8* hlds = hbase + kGemmHdOff + wv * 1024;  // + lane * 16
-    const uint32_t waddr = lds_addr(wlds) + lane * 16, haddr = lds_addr(hlds) + ln * 16;
 
-    auto dma = [](const void* src, lds_u8* dst) {
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
-    };
-    // the 9 loads of group grp (from the start of K) into stage st of this half
+    // The 8 activation loads of group grp (from the start of K) into stage st of this half.
     auto load_group = [&](int grp, int st) {
-        const _Float16* src = asrc + (int64_t)grp * 64;
         lds_u8* dst = hbase + st * kGemmAStage + wv * 8192;
+        const uint32_t g = (uint32_t)grp * 128u;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) dma(src + u * arow8 + (u & 1 ? aodd : 0), dst + 1024 * u);
-        dma(q0 + (grp >> 2) * 8 + 2 * (grp & 3), wlds + st * kGemmWStage);
+        for (int u = 0; u < 8; ++u)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void*)(dst + 1024 * u), 16,
+                                                     u & 1 ? aoff_odd : aoff_even, g + u * arow8, 0, 0);
+    };
+    // This lane's 16 weight bytes of group grp: segment 2 (grp % 4) + lh of block grp / 4.
+    auto load_w = [&](int grp) -> u32x4 {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             wrsrc, woff, (uint32_t)(grp >> 2) * 128u + (uint32_t)(grp & 3) * 32u, 0));
+    };
+    auto load_h = [&](int blk) -> u32x4 {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(hrsrc, hoff, (uint32_t)blk * 16u, 0));
     };
     float sv[8], nm[8];
-    auto scales = [&]() {
-        u32x4 hd = ds_read16<0>(haddr), hd2 = hd;
-        lgkm_wait<0>(hd, hd2);
-        q4k_scales(make_uint4(hd[0], hd[1], hd[2], hd[3]), sv, nm);
-    };
     floatx16 acc[8];
 #pragma unroll
     for (int a = 0; a < 8; ++a)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[a][i] = 0.0f;
 
-    // One group on stage ST: per step, 8 activation reads, the B operand dequantized
-    // meanwhile, then 8 MFMAs (the other wave of the SIMD covers the read latency).
-    auto compute = [&](auto stc) {
+    // One group on stage ST with weight dwords w: per step, 8 activation reads, the B
+    // operand dequantized meanwhile, then 8 MFMAs (the other wave of the SIMD covers the
+    // read latency).  At a block's first group the block's scales are decoded from its
+    // header while the first step's reads are in flight.
+    auto compute = [&](auto stc, const u32x4& w, const u32x4* h) {
         constexpr int ST = decltype(stc)::value;
-        constexpr int AO = ST * kGemmAStage, WO = ST * kGemmWStage;
-        u32x4 w = ds_read16<WO>(waddr), w2 = w;
-        lgkm_wait<0>(w, w2);
+        constexpr int AO = ST * kGemmAStage;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             u32x4 a[8];
@@ -278,6 +269,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
             a[5] = ds_read16<AO + 20480>(aaddr[s]);
             a[6] = ds_read16<AO + 24576>(aaddr[s]);
             a[7] = ds_read16<AO + 28672>(aaddr[s]);
+            if (s == 0 && h) q4k_scales(make_uint4((*h)[0], (*h)[1], (*h)[2], (*h)[3]), sv, nm);
             const half8 b = q4k_bfrag(w[s], sv[2 * s], nm[2 * s], sv[2 * s + 1], nm[2 * s + 1]);
             lgkm_wait<0>(a[0], a[1], a[2], a[3]);
             lgkm_wait<0>(a[4], a[5], a[6], a[7]);
@@ -288,32 +280,38 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
     };
 
     // This half's groups: local group li is group 4 b0 + 2 li + kh from the start of K,
-    // li = 0 .. LG-1, in block b0 + li/2.  Prologue: the first block's header and local
-    // group 0.  Local group li then issues exactly 9 loads (local group li + 1, clamped to
-    // the half's last group: fetched again, never used) and, when li is even, the next
-    // block's header.  So when local group li starts, at most the header issued after its
-    // loads (li odd) may still be outstanding.
+    // li = 0 .. LG-1, in block b0 + li/2.  Prologue: the first block's header, local group
+    // 0's activations and weights.  Local group li then issues its successor's 8 activation
+    // loads and weight load (local group li + 1, clamped to the half's last group: fetched
+    // again, never used) and, when li is even, the next block's header.  So when local
+    // group li starts, at most the header issued after its loads (li odd) may still be
+    // outstanding.
     const int LG = 2 * (b1 - b0);
     const int glast = 4 * (b1 - 1) + 2 + kh;
     auto grp_of = [&](int li) { return min(4 * b0 + 2 * li + kh, glast); };
-    dma(hsrc + b0, hlds);
+    u32x4 hnext = load_h(b0);
+    u32x4 w0 = load_w(grp_of(0)), w1;
     load_group(grp_of(0), 0);
-    for (int li0 = 0; li0 < LG; li0 += 2) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int li = li0 + j;
-            __builtin_amdgcn_sched_barrier(0);
-            if (j == 0) SXQ_WAIT_VM(0);
-            else SXQ_WAIT_VM(1);
-            barrier_nofence();  // stage j is filled everywhere; stage 1 - j is free
-            __builtin_amdgcn_sched_barrier(0);
-            if (j == 0) scales();  // block b0 + li/2 (read before its region is reloaded)
-            load_group(grp_of(li + 1), 1 - j);
-            if (j == 0) dma(hsrc + min(b0 + li / 2 + 1, b1 - 1), hlds);
-            __builtin_amdgcn_sched_barrier(0);
-            if (j == 0) compute(std::integral_constant<int, 0>());
-            else compute(std::integral_constant<int, 1>());
-        }
+    for (int li = 0; li < LG; li += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        SXQ_WAIT_VM(0);
+        barrier_nofence();  // stage 0 is filled everywhere; stage 1 is free
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 h = hnext;
+        load_group(grp_of(li + 1), 1);
+        w1 = load_w(grp_of(li + 1));
+        hnext = load_h(min(b0 + li / 2 + 1, b1 - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(std::integral_constant<int, 0>(), w0, &h);
+
+        __builtin_amdgcn_sched_barrier(0);
+        SXQ_WAIT_VM(1);
+        barrier_nofence();  // stage 1 is filled everywhere; stage 0 is free
+        __builtin_amdgcn_sched_barrier(0);
+        load_group(grp_of(li + 2), 0);
+        w0 = load_w(grp_of(li + 2));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(std::integral_constant<int, 1>(), w1, nullptr);
     }
     SXQ_WAIT_VM(0);  // no global->LDS load may still be in flight past this point
     __syncthreads();
@@ -354,45 +352,52 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
     auto split_reduce = [&](auto keepc) -> bool {
         constexpr int KEEP = decltype(keepc)::value;
         const int st = tile - full, ts = 64 * wv + lane;
-        float* mine = part + (int64_t)(st * S + sp) * 32768 + 4 * ts;
+        // The partials cross between workgroups through 16-byte buffer accesses coherent
+        // at agent scope (sc1), which the compiler sees (waits and register hazards are
+        // its own).  Byte offsets within this tile's S partials.
+        const __amdgpu_buffer_rsrc_t prsrc = coherent_rsrc(part + (int64_t)st * S * 32768, (uint32_t)S * 131072u);
+        const uint32_t mine = (uint32_t)sp * 131072u + 16u * ts;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int mt = KEEP + t;
-                const f32x4 v = {acc[mt][4 * j], acc[mt][4 * j + 1], acc[mt][4 * j + 2], acc[mt][4 * j + 3]};
-                store16_agent(mine + ((mt * 4 + j) * 256) * 4, v);
+                store16_coherent(prsrc, mine + (uint32_t)((mt * 4 + j) * 256) * 16u,
+                                 make_float4(acc[mt][4 * j], acc[mt][4 * j + 1], acc[mt][4 * j + 2], acc[mt][4 * j + 3]));
             }
         if (!publish_and_count(&counters[st], (unsigned)S, &last)) return false;
         // The last to arrive adds the S partials of each row tile in split order (its own
         // included, read back), up to 3 splits (12 loads) at a time.
-        const float* base = part + (int64_t)st * S * 32768 + 4 * ts;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int mt = KEEP + t;
-            f32x4 sum[4];
+            float4 sum[4];
             for (int z0 = 0; z0 < S; z0 += 3) {
-                f32x4 tz[3][4];
+                float4 tz[3][4];
 #pragma unroll
                 for (int dz = 0; dz < 3; ++dz)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        tz[dz][j] = z0 + dz < S ? load16_agent(base + (int64_t)(z0 + dz) * 32768 + ((mt * 4 + j) * 256) * 4)
-                                                : f32x4{0.f, 0.f, 0.f, 0.f};
-                vm_wait0(tz);
+                        tz[dz][j] = z0 + dz < S ? load16_coherent(prsrc, (uint32_t)(z0 + dz) * 131072u + 16u * ts +
+                                                                             (uint32_t)((mt * 4 + j) * 256) * 16u)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
                 for (int dz = 0; dz < 3; ++dz)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         if (z0 + dz >= S) continue;
                         if (z0 + dz == 0) sum[j] = tz[0][j];
-                        else sum[j] = sum[j] + tz[dz][j];
+                        else sum[j] = make_float4(sum[j].x + tz[dz][j].x, sum[j].y + tz[dz][j].y, sum[j].z + tz[dz][j].z,
+                                                  sum[j].w + tz[dz][j].w);
                     }
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[mt][4 * j + e] = sum[j][e];
+            for (int j = 0; j < 4; ++j) {
+                acc[mt][4 * j] = sum[j].x;
+                acc[mt][4 * j + 1] = sum[j].y;
+                acc[mt][4 * j + 2] = sum[j].z;
+                acc[mt][4 * j + 3] = sum[j].w;
+            }
         }
         if (tid == 0) __hip_atomic_store(&counters[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return true;
