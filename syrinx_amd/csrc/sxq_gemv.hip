@@ -17,6 +17,8 @@
 // workgroup (in K chunks when m * K does not fit).
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "sxq_decoder.h"
 #include "sxq_gemv_dev.h"
 #include "sxq_kernels.h"
@@ -233,8 +235,11 @@ SXQ_DEV void act_store(const uint4 (&v)[Stage<NT>::kPer], uint4* lds, const uint
     for (int i = Stage<NT>::kPer * NT + threadIdx.x; i < total_u4; i += NT) lds[i] = ((const uint4*)act)[i];
 }
 
-// Q4_K task-split GEMV, NT threads (256 or 1024) per workgroup: NT/8 eight-lane groups.
-template <int MMAX, bool NORM, int NT>
+// Q4_K task-split GEMV, NT threads (256 or 1024) per workgroup: NT/8 eight-lane groups,
+// TM rounds of tasks (the launch's tiles need no more; a round that held no task would
+// still issue its loads, and the epilogue would wait for them before reusing their
+// registers).
+template <int MMAX, bool NORM, int NT, int TM>
 __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, int n,
                                                   int nb, const uint8_t* __restrict__ act, int m, int R, float* y,
                                                   int64_t ldy, const float* __restrict__ bias, const float* res,
@@ -254,8 +259,8 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     float4 xv, wv;
     if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 256);
     else act_fetch<NT>(av, act, act_u4);
-    uint4 q[kTmax], h[kTmax];
-    q4k_tile_load<NT>(hdr, qs, blk0, tasks, q, h);
+    uint4 q[TM], h[TM];
+    q4k_tile_load<NT, TM>(hdr, qs, blk0, tasks, q, h);
     if constexpr (NORM) {
         __shared__ float red[16];
         norm_quant_store<kQ8K>(xv, wv, ni, nb * 256, (uint8_t*)lds, red);
@@ -265,7 +270,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     // The activations are in LDS; the weight loads may still be in flight: each round of
     // products waits only for its own.
     lds_barrier();
-    q4k_tile_products<MMAX, NT>(q, h, la, nb, m, tasks, TS, pr);
+    q4k_tile_products<MMAX, NT, TM>(q, h, la, nb, m, tasks, TS, pr);
     __syncthreads();
     // epilogue: thread (row r, lane class l) folds its chain in block order
     const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
@@ -290,6 +295,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
 // down projection whose prologue quantizes that f32 row to Q8_K in LDS (chunk c by wave
 // c mod 16, the quantizer of k_silu_mul_quant), so the two leave the same bits as the
 // GEMV + SiLU*mul kernel + GEMV sequence, one launch and one quantized row fewer.
+template <int TM>
 __global__ __launch_bounds__(1024) void k_gemv2_q4k_swiglu(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
                                                            int I, int nb, int B, NormIn ni, float* __restrict__ gu,
                                                            float* __restrict__ act_f32) {
@@ -304,11 +310,11 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_swiglu(const uint4* __restri
     float* pr = (float*)(lds + (size_t)nb * (sizeof(ActQ8K) / 16));  // [TS][9]
     float4 xv, wv;
     norm_fetch(xv, wv, ni, nb * 256);
-    uint4 q[kTmax], h[kTmax];
-    q4k_tile_load2<NT>(hdr, qs, (uint32_t)g0 * (uint32_t)nb, (uint32_t)(I + g0) * (uint32_t)nb, seg, tasks, q, h);
+    uint4 q[TM], h[TM];
+    q4k_tile_load2<NT, TM>(hdr, qs, (uint32_t)g0 * (uint32_t)nb, (uint32_t)(I + g0) * (uint32_t)nb, seg, tasks, q, h);
     norm_quant_store<kQ8K>(xv, wv, ni, nb * 256, (uint8_t*)lds, red);
     lds_barrier();
-    q4k_tile_products<1, NT>(q, h, la, nb, 1, tasks, TS, pr);
+    q4k_tile_products<1, NT, TM>(q, h, la, nb, 1, tasks, TS, pr);
     __syncthreads();
     const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
     const float v = q4k_tile_fold(pr, TS, nb, 0, rows);
@@ -323,6 +329,7 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_swiglu(const uint4* __restri
     }
 }
 
+template <int TM>
 __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
                                                           int n, int nb, int R, const float* __restrict__ x,
                                                           float* y, const float* res) {
@@ -346,11 +353,11 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restric
         v[j] = *(const float4*)(x + cc * 256 + 4 * lane);
     }
     __builtin_amdgcn_sched_barrier(0);
-    uint4 q[kTmax], h[kTmax];
-    q4k_tile_load<NT>(hdr, qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
+    uint4 q[TM], h[TM];
+    q4k_tile_load<NT, TM>(hdr, qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
     if (wave < nb) wave_quantize_q8k_n<J, false>(v, lane, out, valid);  // uniform per wave
     lds_barrier();
-    q4k_tile_products<1, NT>(q, h, la, nb, 1, tasks, TS, pr);
+    q4k_tile_products<1, NT, TM>(q, h, la, nb, 1, tasks, TS, pr);
     __syncthreads();
     const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
     const float v0 = q4k_tile_fold(pr, TS, nb, 0, rows);
@@ -364,7 +371,7 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restric
 
 // Q8_0 / Q4_0 task-split GEMV: a lane pair per Q8_0 task (16 bytes each), one lane per
 // Q4_0 task; NT threads per workgroup.
-template <int MMAX, bool Q4, bool NORM, int NT>
+template <int MMAX, bool Q4, bool NORM, int NT, int TM>
 __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ dw16, const uint4* __restrict__ qs,
                                                   int n, int nb, const uint8_t* __restrict__ act, int m, int R,
                                                   float* y, int64_t ldy, const float* __restrict__ bias,
@@ -386,10 +393,10 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
     float4 xv, wv;
     if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 32);
     else act_fetch<NT>(av, act, act_u4);
-    uint4 w[kTmax];
-    float dw[kTmax];
+    uint4 w[TM];
+    float dw[TM];
 #pragma unroll
-    for (int u = 0; u < kTmax; ++u) {
+    for (int u = 0; u < TM; ++u) {
         const int t = min(u * TPI + slot, tasks - 1);
         w[u] = qs[(base + t) * QU4 + half];
         dw[u] = h2f(dw16[base + t]);
@@ -406,7 +413,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
     const uint32_t step = (uint32_t)TPI % (uint32_t)nb;
     uint32_t b = (uint32_t)slot % (uint32_t)nb;
 #pragma unroll
-    for (int u = 0; u < kTmax; ++u) {
+    for (int u = 0; u < TM; ++u) {
         if (u * TPI >= tasks) break;
 #pragma unroll
         for (int r = 0; r < MMAX; ++r) {
@@ -502,6 +509,23 @@ static int gemv2_nt(int n, int nb, int m, int dtype) {
     return env_nt == 1024 && gemv2_fits(n, nb, m, dtype, 1024) ? 1024 : 256;
 }
 
+// Calls f(std::integral_constant<int, TM>()) for TM = rounds (1 .. kTmax).
+template <typename F>
+static hipError_t with_rounds(int rounds, F&& f) {
+    switch (rounds) {
+        case 1: return f(std::integral_constant<int, 1>());
+        case 2: return f(std::integral_constant<int, 2>());
+        case 3: return f(std::integral_constant<int, 3>());
+        case 4: return f(std::integral_constant<int, 4>());
+        case 5: return f(std::integral_constant<int, 5>());
+        case 6: return f(std::integral_constant<int, 6>());
+        case 7: return f(std::integral_constant<int, 7>());
+        case 8: return f(std::integral_constant<int, 8>());
+        default: return hipErrorInvalidValue;
+    }
+}
+static_assert(kTmax == 8, "with_rounds covers 1 .. kTmax");
+
 template <int MMAX, bool NORM, int NT>
 static hipError_t gemv2_launch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                                const float* res, int64_t ldr, hipStream_t s, const NormIn& ni) {
@@ -510,14 +534,21 @@ static hipError_t gemv2_launch(const QWeight& w, const void* act, int m, float* 
     const size_t lds = gemv2_lds(nb, m, R, w.dtype, NT);
     const dim3 grid((n + R - 1) / R), block(NT);
     const uint8_t* a = (const uint8_t*)act;
-    if (w.dtype == kQ4K)
-        hipLaunchKernelGGL((k_gemv2_q4k<MMAX, NORM, NT>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
-    else if (w.dtype == kQ8_0)
-        hipLaunchKernelGGL((k_gemv2_q80<MMAX, false, NORM, NT>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
-    else if (w.dtype == kQ4_0)
-        hipLaunchKernelGGL((k_gemv2_q80<MMAX, true, NORM, NT>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
-    else
-        return hipErrorInvalidValue;
+    const int tpr = tasks_per_round(w.dtype, NT);
+    const int rounds = (R * nb + tpr - 1) / tpr;
+    const hipError_t e = with_rounds(rounds, [&](auto tmc) -> hipError_t {
+        constexpr int TM = decltype(tmc)::value;
+        if (w.dtype == kQ4K)
+            hipLaunchKernelGGL((k_gemv2_q4k<MMAX, NORM, NT, TM>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+        else if (w.dtype == kQ8_0)
+            hipLaunchKernelGGL((k_gemv2_q80<MMAX, false, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+        else if (w.dtype == kQ4_0)
+            hipLaunchKernelGGL((k_gemv2_q80<MMAX, true, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+        else
+            return hipErrorInvalidValue;
+        return hipSuccess;
+    });
+    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 
@@ -601,15 +632,22 @@ hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const
     const int I = (int)(gate_up.n / 2), nb = (int)gate_up.nb;
     const int B = swiglu_rows(I, nb);
     const size_t lds1 = gemv2_lds(nb, 1, 2 * B, kQ4K, 1024);
-    hipLaunchKernelGGL(k_gemv2_q4k_swiglu, dim3((I + B - 1) / B), dim3(1024), lds1, s, (const uint4*)gate_up.hdr,
-                       (const uint4*)gate_up.qs, I, nb, B, ni, gu, act_f32);
-    hipError_t e = hipGetLastError();
+    hipError_t e = with_rounds((2 * B * nb + 127) / 128, [&](auto tmc) -> hipError_t {
+        hipLaunchKernelGGL(k_gemv2_q4k_swiglu<decltype(tmc)::value>, dim3((I + B - 1) / B), dim3(1024), lds1, s,
+                           (const uint4*)gate_up.hdr, (const uint4*)gate_up.qs, I, nb, B, ni, gu, act_f32);
+        return hipSuccess;
+    });
+    if (e == hipSuccess) e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int n = (int)down.n, nb2 = (int)down.nb;
     const int R = gemv2_rows(n, nb2, 1, kQ4K, 1024);
     const size_t lds2 = gemv2_lds(nb2, 1, R, kQ4K, 1024);
-    hipLaunchKernelGGL(k_gemv2_q4k_quant, dim3((n + R - 1) / R), dim3(1024), lds2, s, (const uint4*)down.hdr,
-                       (const uint4*)down.qs, n, nb2, R, act_f32, y, res);
+    e = with_rounds((R * nb2 + 127) / 128, [&](auto tmc) -> hipError_t {
+        hipLaunchKernelGGL(k_gemv2_q4k_quant<decltype(tmc)::value>, dim3((n + R - 1) / R), dim3(1024), lds2, s,
+                           (const uint4*)down.hdr, (const uint4*)down.qs, n, nb2, R, act_f32, y, res);
+        return hipSuccess;
+    });
+    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 
