@@ -251,8 +251,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     const int row0 = blockIdx.x * R;
     const int rows = min(R, n - row0);
     const int tasks = rows * nb;
-    const int TS = (tasks + SLOTS - 1) / SLOTS * SLOTS;  // product slots: whole rounds
-    float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8K) / 16));  // [m][TS][9]
+    float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8K) / 16));  // product chains [m][R + 1][9][CS]
     const uint32_t blk0 = (uint32_t)row0 * (uint32_t)nb;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8K) / 16);
     uint4 av[Stage<NT>::kPer];
@@ -270,12 +269,12 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     // The activations are in LDS; the weight loads may still be in flight: each round of
     // products waits only for its own.
     lds_barrier();
-    q4k_tile_products<MMAX, NT, TM>(q, h, la, nb, m, tasks, TS, pr);
+    q4k_tile_products<MMAX, NT, TM>(q, h, la, nb, m, rows, R, pr);
     __syncthreads();
     // epilogue: thread (row r, lane class l) folds its chain in block order
     const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
     for (int rr = 0; rr < m; ++rr) {
-        const float v0 = q4k_tile_fold(pr, TS, nb, rr, rows);
+        const float v0 = q4k_tile_fold(pr, nb, R, rr, rows);
         if (r < rows && l == 0) {
             const int row = row0 + r;
             float v = v0;
@@ -306,18 +305,17 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_swiglu(const uint4* __restri
     const ActQ8K* la = (const ActQ8K*)lds;
     const int t = blockIdx.x, g0 = t * B, Bt = min(B, I - g0);
     const int rows = 2 * Bt, tasks = rows * nb, seg = Bt * nb;
-    const int TS = (tasks + SLOTS - 1) / SLOTS * SLOTS;
-    float* pr = (float*)(lds + (size_t)nb * (sizeof(ActQ8K) / 16));  // [TS][9]
+    float* pr = (float*)(lds + (size_t)nb * (sizeof(ActQ8K) / 16));  // product chains [2B + 1][9][CS]
     float4 xv, wv;
     norm_fetch(xv, wv, ni, nb * 256);
     uint4 q[TM], h[TM];
     q4k_tile_load2<NT, TM>(hdr, qs, (uint32_t)g0 * (uint32_t)nb, (uint32_t)(I + g0) * (uint32_t)nb, seg, tasks, q, h);
     norm_quant_store<kQ8K>(xv, wv, ni, nb * 256, (uint8_t*)lds, red);
     lds_barrier();
-    q4k_tile_products<1, NT, TM>(q, h, la, nb, 1, tasks, TS, pr);
+    q4k_tile_products<1, NT, TM>(q, h, la, nb, 1, rows, 2 * B, pr);
     __syncthreads();
     const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
-    const float v = q4k_tile_fold(pr, TS, nb, 0, rows);
+    const float v = q4k_tile_fold(pr, nb, 2 * B, 0, rows);
     if (r < rows && l == 0) {
         sw[r] = v;
         gu[r < Bt ? g0 + r : I + g0 + (r - Bt)] = v;
@@ -337,8 +335,7 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restric
     extern __shared__ uint4 lds[];
     ActQ8K* la = (ActQ8K*)lds;
     const int row0 = blockIdx.x * R, rows = min(R, n - row0), tasks = rows * nb;
-    const int TS = (tasks + SLOTS - 1) / SLOTS * SLOTS;
-    float* pr = (float*)(lds + (size_t)nb * (sizeof(ActQ8K) / 16));  // [TS][9]
+    float* pr = (float*)(lds + (size_t)nb * (sizeof(ActQ8K) / 16));  // product chains [R + 1][9][CS]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // wave w quantizes chunks w, w + 16, w + 32 (nb <= 48); their loads go ahead of the
     // weight loads, which return after them
@@ -357,10 +354,10 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restric
     q4k_tile_load<NT, TM>(hdr, qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
     if (wave < nb) wave_quantize_q8k_n<J, false>(v, lane, out, valid);  // uniform per wave
     lds_barrier();
-    q4k_tile_products<1, NT, TM>(q, h, la, nb, 1, tasks, TS, pr);
+    q4k_tile_products<1, NT, TM>(q, h, la, nb, 1, rows, R, pr);
     __syncthreads();
     const int r = threadIdx.x >> 3, l = threadIdx.x & 7;
-    const float v0 = q4k_tile_fold(pr, TS, nb, 0, rows);
+    const float v0 = q4k_tile_fold(pr, nb, R, 0, rows);
     if (r < rows && l == 0) {
         const int row = row0 + r;
         float v = v0;
@@ -468,10 +465,10 @@ static int tasks_per_round(int dtype, int nt) { return dtype == kQ4K ? nt / 8 : 
 
 size_t gemv2_lds(int nb, int m, int R, int dtype, int nt) {
     const size_t ab = act_block_bytes(vec_dot_type(dtype));
-    const size_t per_task = dtype == kQ4K ? 36 : 4;
+    if (dtype == kQ4K) return (size_t)m * nb * ab + (size_t)m * (R + 1) * 9 * q4k_chain_stride(nb) * 4;
     const int tpi = tasks_per_round(dtype, nt);
     const size_t slots = ((size_t)R * nb + tpi - 1) / tpi * tpi;
-    return (size_t)m * nb * ab + slots * m * per_task;
+    return (size_t)m * nb * ab + slots * m * 4;
 }
 
 int gemv2_rows(int n, int nb, int m, int dtype, int nt) {

@@ -88,18 +88,31 @@ SXQ_DEV void q4k_tile_load2(const uint4* __restrict__ hdr, const uint4* __restri
     }
 }
 
-// Per-task float products into pr [m][TS][9] (TS = tasks rounded up to whole rounds):
-// the eight lane terms (d_w*d_a)*(f32)aux32[l] and the min term (dmin_w*d_a)*(f32)sumi
-// of Candle's Q4_K vec-dot, against the LDS activation blocks la [m][nb].  Tasks past
-// the end (last round) compute on clamped loads into their own spare slots.
+// Layout of the per-block float products: one chain per (activation row rr, tile row
+// r, lane class c = 0..7, plus c = 8 for the min terms), nb floats in block order, at
+// pr + ((rr * (RC + 1) + r) * 9 + c) * CS (RC = the tile's row capacity; row RC of each
+// activation row is a spare that takes the writes of tasks past the end).  The chain stride CS
+// is nb rounded up to 4 floats and then to an odd number of 16-byte units, so that
+// chains start 16-byte aligned (the fold reads them as float4) and the eight lane
+// classes' writes of one task fall in eight different LDS banks.
+SXQ_HD int q4k_chain_stride(int nb) {
+    const int q = (nb + 3) >> 2;
+    return 4 * (q | 1);
+}
+
+// Per-task float products into the chains: the eight lane terms (d_w*d_a)*(f32)aux32[l]
+// and the min term (dmin_w*d_a)*(f32)sumi of Candle's Q4_K vec-dot, against the LDS
+// activation blocks la [m][nb].  Task t is tile row t / nb, block t % nb; tasks past the
+// end (last round) compute on clamped loads and write into the spare row.
 template <int MMAX, int NT, int TM = kTmax>
 SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const ActQ8K* la, int nb, int m,
-                               int tasks, int TS, float* pr) {
+                               int rows, int RC, float* pr) {
     constexpr int SLOTS = NT / 8;
     const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
-    // Block index of task u*SLOTS + grp: grp mod nb, stepped by SLOTS mod nb each round.
-    const uint32_t step = (uint32_t)SLOTS % (uint32_t)nb;
-    uint32_t b = (uint32_t)grp % (uint32_t)nb;
+    const int CS = q4k_chain_stride(nb), tasks = rows * nb;
+    // Tile row and block of task u*SLOTS + grp, stepped by SLOTS each round.
+    const uint32_t bstep = (uint32_t)SLOTS % (uint32_t)nb, rstep = (uint32_t)SLOTS / (uint32_t)nb;
+    uint32_t b = (uint32_t)grp % (uint32_t)nb, row = (uint32_t)grp / (uint32_t)nb;
 #pragma unroll
     for (int u = 0; u < TM; ++u) {
         if (u * SLOTS >= tasks) break;  // uniform: no group has a task in this round
@@ -114,6 +127,7 @@ SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const
                            (int)(q[u].w & 0x0F0F0F0Fu), (int)((q[u].w >> 4) & 0x0F0F0F0Fu)};
         const int slo = (int)sc_lo, shi = (int)sc_hi;  // scale of sub-block j: byte j of slo, j - 4 of shi
         const float dw = h2f(h[u].x & 0xFFFF), dminw = h2f(h[u].x >> 16);
+        const bool live = row < (uint32_t)rows;
 #pragma unroll
         for (int r = 0; r < MMAX; ++r) {
             if (r < m) {
@@ -125,42 +139,62 @@ SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const
                 const int aux = q4k_aux(w4, Aj, slo, shi);
                 const int sumi = sum8_i32(__mul24(ml, a.bs2[l]));
                 const float ad = a.d;
-                float* p = pr + (r * TS + u * SLOTS + grp) * 9;
-                p[l] = (dw * ad) * (float)aux;
-                p[8] = (dminw * ad) * (float)sumi;  // same value from all eight lanes
+                // a task past the end writes into the spare row RC (never folded)
+                float* p = pr + ((r * (RC + 1) + (live ? (int)row : RC)) * 9) * CS + (int)b;
+                p[l * CS] = (dw * ad) * (float)aux;
+                if (l == 0) p[8 * CS] = (dminw * ad) * (float)sumi;  // the same in all eight lanes
             }
         }
-        b += step;
-        b = min(b, b - (uint32_t)nb);  // unsigned: subtracts nb only when b >= nb
+        b += bstep;
+        row += rstep;
+        if (b >= (uint32_t)nb) {
+            b -= (uint32_t)nb;
+            row += 1;
+        }
     }
 }
 
 // Fold of activation row rr: thread (tile row r = tid/8, lane class l) sums its lane
 // chain in block order, and (every lane, the same values) the min terms; the eight lane
-// sums are then added in Candle's order.  The chains are sequential float adds, so the
-// terms are loaded eight blocks at a time ahead of them, and the lane sums reach lane
+// sums are then added in Candle's order.  The chains are sequential float adds: each is
+// read as float4s, sixteen blocks ahead of their adds, and the lane sums reach lane
 // class 0 by DPP row shifts (lane j of the group -> lane 0) rather than LDS permutes.
-// Every thread calls it; the result (sumf + (-0.0 + sums[0] + ... + sums[7])) is valid
-// in lane class 0 of rows < rows.
-SXQ_DEV float q4k_tile_fold(const float* pr, int TS, int nb, int rr, int rows) {
+// Blocks past nb in a chain's last step are added as +0.0: adding +0.0
+// leaves both chains' bits unchanged (the lane chain starts at +0.0, and a
+// round-to-nearest sum that starts at +0.0 is never -0.0; x - (+0.0) is x).  Every
+// thread calls it; the result (sumf + (-0.0 + sums[0] + ... + sums[7])) is valid in lane
+// class 0 of rows < rows.
+SXQ_DEV float q4k_tile_fold(const float* pr, int nb, int RC, int rr, int rows) {
     const int l = threadIdx.x & 7, r = threadIdx.x >> 3;
+    const int CS = q4k_chain_stride(nb), nv = (nb + 3) >> 2;
     float sl = 0.0f, sf = 0.0f;
     if (r < rows) {
-        const float* p = pr + (rr * TS + r * nb) * 9;
-        for (int b0 = 0; b0 < nb; b0 += 8) {
-            float t[8], mt[8];
+        const float4* cl = (const float4*)(pr + ((rr * (RC + 1) + r) * 9 + l) * CS);
+        const float4* cm = (const float4*)(pr + ((rr * (RC + 1) + r) * 9 + 8) * CS);
+        // sixteen blocks per step; only a step that runs past nb needs its blocks masked
+        for (int v0 = 0; v0 < nv; v0 += 4) {
+            float ta[16], tm[16];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int b = min(b0 + k, nb - 1);  // clamped: in bounds, not added
-                t[k] = p[b * 9 + l];
-                mt[k] = p[b * 9 + 8];
+            for (int j = 0; j < 4; ++j) {
+                const int v = min(v0 + j, nv - 1);  // clamped: read, not added
+                const float4 x = cl[v], y = cm[v];
+                ta[4 * j] = x.x, ta[4 * j + 1] = x.y, ta[4 * j + 2] = x.z, ta[4 * j + 3] = x.w;
+                tm[4 * j] = y.x, tm[4 * j + 1] = y.y, tm[4 * j + 2] = y.z, tm[4 * j + 3] = y.w;
             }
+            if (4 * v0 + 16 <= nb) {  // uniform
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (b0 + k < nb) {  // uniform
-                    sl += t[k];
-                    sf -= mt[k];
+                for (int k = 0; k < 16; ++k) {
+                    sl += ta[k];
+                    sf -= tm[k];
                 }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const bool in = 4 * v0 + k < nb;  // uniform
+                    sl += in ? ta[k] : 0.0f;
+                    sf -= in ? tm[k] : 0.0f;
+                }
+            }
         }
     }
     float tot = -0.0f + sl;
