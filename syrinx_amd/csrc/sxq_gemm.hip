@@ -52,13 +52,10 @@ size_t gemm_q4k_lds() { return 2 * (size_t)kGemmHalfBytes; }
 
 // x f32 [m][k] (row stride ldx) -> xh f16 [gemm_xh_rows(m)][k] in the GEMM K order,
 // xh[r][256b + p] = f16(x[r][256b + q4k_perm_elem(p)]), rows past m zero.  Each thread
-// writes 8 consecutive halfs (one MFMA operand chunk).  The first `ncount` threads also
-// clear the GEMM's split counters.
+// writes 8 consecutive halfs (one MFMA operand chunk).
 __global__ __launch_bounds__(256) void k_x_to_f16_perm(const float* __restrict__ x, int64_t ldx, int m, int k,
-                                                       int rows, _Float16* __restrict__ xh, unsigned* counters,
-                                                       int ncount) {
+                                                       int rows, _Float16* __restrict__ xh) {
     const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;  // chunk of 8 halfs
-    if (c < ncount) counters[c] = 0u;
     const int kc = k >> 3;
     if (c >= (int64_t)rows * kc) return;
     const int64_t r = c / kc;
@@ -180,15 +177,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // One barrier per group (both halves in lockstep).
 //
 // A tile split S ways: split z covers blocks [nb*z/S, nb*(z+1)/S); every split stores its
-// partial tile, and the last to arrive (per-tile counter) adds the partials in split order,
-// so the result does not depend on arrival order.
+// partial tile, and k_gemm_splitk_sum, launched after this kernel, adds the partials in
+// split order across the whole GPU.
 __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ xh, int M, int K,
                                                   const uint4* __restrict__ hdr, const uint4* __restrict__ qs, int N,
                                                   float* __restrict__ y, int64_t ldy, const float* __restrict__ bias,
-                                                  const float* res, int64_t ldr, float* part, unsigned* counters,
-                                                  int tiles_m, int full, int splits) {
+                                                  const float* res, int64_t ldr, float* part, int tiles_m,
+                                                  int full, int splits) {
     extern __shared__ uint4 lds[];
-    __shared__ bool last;
     const int nb = K >> 8;
     // Workgroups 0 .. full-1 take whole tiles; the rest split the remaining tiles' K range
     // `splits` ways.  Tile t covers weight rows 128 * (t / tiles_m), token rows 256 * (t % tiles_m).
@@ -346,66 +342,25 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
     if (kh == 0) exchange(std::integral_constant<int, 0>());
     else exchange(std::integral_constant<int, 4>());
 
-    // Split tiles: hand the partial over, the last split adds them (see above).  Row tile
-    // mt, float4 j, thread slot ts = 64 wv + lane of split z of split tile st sits at
-    // part + 4 * ((((st * S + z) * 8 + mt) * 4 + j) * 256 + ts).
-    auto split_reduce = [&](auto keepc) -> bool {
-        constexpr int KEEP = decltype(keepc)::value;
-        const int st = tile - full, ts = 64 * wv + lane;
-        // The partials cross between workgroups through 16-byte buffer accesses coherent
-        // at agent scope (sc1), which the compiler sees (waits and register hazards are
-        // its own).  Byte offsets within this tile's S partials.
-        const __amdgpu_buffer_rsrc_t prsrc = coherent_rsrc(part + (int64_t)st * S * 32768, (uint32_t)S * 131072u);
-        const uint32_t mine = (uint32_t)sp * 131072u + 16u * ts;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int mt = KEEP + t;
-                store16_coherent(prsrc, mine + (uint32_t)((mt * 4 + j) * 256) * 16u,
-                                 make_float4(acc[mt][4 * j], acc[mt][4 * j + 1], acc[mt][4 * j + 2], acc[mt][4 * j + 3]));
-            }
-        if (!publish_and_count(&counters[st], (unsigned)S, &last)) return false;
-        // The last to arrive adds the S partials of each row tile in split order (its own
-        // included, read back), up to 3 splits (12 loads) at a time.
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int mt = KEEP + t;
-            float4 sum[4];
-            for (int z0 = 0; z0 < S; z0 += 3) {
-                float4 tz[3][4];
-#pragma unroll
-                for (int dz = 0; dz < 3; ++dz)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        tz[dz][j] = z0 + dz < S ? load16_coherent(prsrc, (uint32_t)(z0 + dz) * 131072u + 16u * ts +
-                                                                             (uint32_t)((mt * 4 + j) * 256) * 16u)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                for (int dz = 0; dz < 3; ++dz)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        if (z0 + dz >= S) continue;
-                        if (z0 + dz == 0) sum[j] = tz[0][j];
-                        else sum[j] = make_float4(sum[j].x + tz[dz][j].x, sum[j].y + tz[dz][j].y, sum[j].z + tz[dz][j].z,
-                                                  sum[j].w + tz[dz][j].w);
-                    }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[mt][4 * j] = sum[j].x;
-                acc[mt][4 * j + 1] = sum[j].y;
-                acc[mt][4 * j + 2] = sum[j].z;
-                acc[mt][4 * j + 3] = sum[j].w;
-            }
-        }
-        if (tid == 0) __hip_atomic_store(&counters[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return true;
-    };
+    // A split tile stores its partial and is done: k_gemm_splitk_sum adds the S partials.
+    // Row tile mt, float4 j, thread slot ts = 64 wv + lane of split z of split tile st sits
+    // at float4 index ((st * S + z) * 8 + mt) * 1024 + j * 256 + ts of part.
     if (S > 1) {
-        const bool mine = kh == 0 ? split_reduce(std::integral_constant<int, 0>())
-                                  : split_reduce(std::integral_constant<int, 4>());
-        if (!mine) return;
+        float4* mine = (float4*)part + (int64_t)((tile - full) * S + sp) * 8192 + 64 * wv + lane;
+        auto store_part = [&](auto keepc) {
+            constexpr int KEEP = decltype(keepc)::value;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int mt = KEEP + t;
+                    mine[(mt * 4 + j) * 256] =
+                        make_float4(acc[mt][4 * j], acc[mt][4 * j + 1], acc[mt][4 * j + 2], acc[mt][4 * j + 3]);
+                }
+        };
+        if (kh == 0) store_part(std::integral_constant<int, 0>());
+        else store_part(std::integral_constant<int, 4>());
+        return;
     }
 
     // D layout: acc[i] = D[8*(i/4) + 4*(lane/32) + i%4][lane%32].  Loads (bias, then the
@@ -446,12 +401,49 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
     else store(std::integral_constant<int, 4>());
 }
 
+// Second pass for split tiles: one thread per float4 slot (row tile mt, float4 j, slot
+// ts) of a split tile adds the tile's S partials in split order -- the result does not
+// depend on which split finished first -- and writes y like the whole-tile store:
+// (sum + bias), then res + that.  Slot ts = 64 wv + lane holds D[32 mt + 8 j + 4 (lane/32)
+// + e][32 wv + lane % 32], e = 0..3, of the tile (the MFMA D layout above).
+__global__ __launch_bounds__(256) void k_gemm_splitk_sum(const float* __restrict__ part, int S, int full,
+                                                         int tiles_m, int M, int N, float* y, int64_t ldy,
+                                                         const float* __restrict__ bias, const float* res, int64_t ldr,
+                                                         int nslots) {
+    const int g = blockIdx.x * 256 + threadIdx.x;
+    if (g >= nslots) return;
+    const int st = g >> 13, q = g & 8191;
+    const int ts = q & 255, mt = q >> 10, j = (q >> 8) & 3;
+    const int wv = ts >> 6, lane = ts & 63;
+    const int tile = full + st;
+    const int n0 = (tile / tiles_m) * kGemmBN, m0 = (tile % tiles_m) * kGemmBM;
+    const float4* p = (const float4*)part + (int64_t)st * S * 8192 + q;
+    float4 sum = p[0];
+    for (int z = 1; z < S; ++z) {
+        const float4 t = p[(int64_t)z * 8192];
+        sum = make_float4(sum.x + t.x, sum.y + t.y, sum.z + t.z, sum.w + t.w);
+    }
+    const int col = n0 + 32 * wv + (lane & 31);
+    if (col >= N) return;
+    const float bv = bias ? bias[col] : 0.0f;
+    const int row0 = m0 + 32 * mt + 8 * j + 4 * (lane >> 5);
+    const float e[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = row0 + i;
+        if (row >= M) break;
+        float v = bias ? e[i] + bv : e[i];
+        if (res) v = res[(int64_t)row * ldr + col] + v;
+        y[(int64_t)row * ldy + col] = v;
+    }
+}
+
 // Work split of one GEMM over the GPU's compute units: whole tiles first, as many as fill
 // every unit a whole number of times, then the remaining tiles each split along K so that
 // the last round still occupies (nearly) every unit.
 struct GemmPlan {
     int tiles_n = 0, tiles_m = 0, tiles = 0, full = 0, splits = 1, grid = 0;
-    size_t xh_bytes = 0, part_bytes = 0, count_bytes = 0;
+    size_t xh_bytes = 0, part_bytes = 0;
 };
 
 static int device_cus() {
@@ -486,7 +478,6 @@ static GemmPlan gemm_plan(int64_t n, int m, int64_t k) {
     p.xh_bytes = ((size_t)gemm_xh_rows(m) * (size_t)k * 2 + 255) & ~(size_t)255;
     const size_t split_tiles = (size_t)(p.tiles - p.full);
     p.part_bytes = split_tiles * p.splits * 128 * 256 * 4;
-    p.count_bytes = split_tiles * 4;
     return p;
 }
 
@@ -494,18 +485,15 @@ int gemm_q4k_splits(int64_t n, int m, int64_t k) { return gemm_plan(n, m, k).spl
 
 size_t gemm_q4k_workspace(int64_t n, int m, int64_t k) {
     const GemmPlan p = gemm_plan(n, m, k);
-    return p.xh_bytes + p.part_bytes + p.count_bytes;
+    return p.xh_bytes + p.part_bytes;
 }
 
 hipError_t launch_gemm_q4k_prep(const float* x, int64_t ldx, int m, int64_t n, int k, void* ws, hipStream_t s) {
     const GemmPlan p = gemm_plan(n, m, k);
     const int rows = gemm_xh_rows(m);
-    unsigned* counters = (unsigned*)((uint8_t*)ws + p.xh_bytes + p.part_bytes);
-    const int ncount = p.tiles - p.full;
     const int64_t chunks = (int64_t)rows * (k / 8);
-    const int64_t threads = chunks > ncount ? chunks : ncount;
-    hipLaunchKernelGGL(k_x_to_f16_perm, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, ldx, m, k, rows,
-                       (_Float16*)ws, counters, ncount);
+    hipLaunchKernelGGL(k_x_to_f16_perm, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s, x, ldx, m, k, rows,
+                       (_Float16*)ws);
     return hipGetLastError();
 }
 
@@ -517,10 +505,14 @@ hipError_t launch_gemm_q4k(const QWeight& w, const void* ws, int m, float* y, in
     if (attr != hipSuccess) return attr;
     const GemmPlan p = gemm_plan(w.n, m, w.k);
     float* part = (float*)((uint8_t*)ws + p.xh_bytes);
-    unsigned* counters = (unsigned*)((uint8_t*)ws + p.xh_bytes + p.part_bytes);
     hipLaunchKernelGGL(k_gemm_q4k, dim3((unsigned)p.grid), dim3(512), gemm_q4k_lds(), s, (const _Float16*)ws, m,
                        (int)w.k, (const uint4*)w.hdr, (const uint4*)w.qs, (int)w.n, y, ldy, bias, res, ldr, part,
-                       counters, p.tiles_m, p.full, p.splits);
+                       p.tiles_m, p.full, p.splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.full == p.tiles) return e;
+    const int nslots = (p.tiles - p.full) * 8192;
+    hipLaunchKernelGGL(k_gemm_splitk_sum, dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, s, (const float*)part,
+                       p.splits, p.full, p.tiles_m, m, (int)w.n, y, ldy, bias, res, ldr, nslots);
     return hipGetLastError();
 }
 
