@@ -51,26 +51,30 @@ int gemm_xh_rows(int m) { return (m + kGemmBM - 1) / kGemmBM * kGemmBM; }
 size_t gemm_q4k_lds() { return 2 * (size_t)kGemmHalfBytes; }
 
 // x f32 [m][k] (row stride ldx) -> xh f16 [gemm_xh_rows(m)][k] in the GEMM K order,
-// xh[r][256b + p] = f16(x[r][256b + q4k_perm_elem(p)]), rows past m zero.  Each thread
-// writes 8 consecutive halfs (one MFMA operand chunk).
+// xh[r][256b + p] = f16(x[r][256b + q4k_perm_elem(p)]), rows past m zero.  One wave per
+// (row, 256-element block): it reads the block as 64 float4s (one contiguous 1 KB read),
+// passes it through LDS, and lane l < 32 writes positions 8l .. 8l+7 (one MFMA operand
+// chunk; one contiguous 512-byte write per wave); position 8l + j is element
+// q4k_perm_elem(8l) + 32 (j & 1) + 8 (j >> 1).
 __global__ __launch_bounds__(256) void k_x_to_f16_perm(const float* __restrict__ x, int64_t ldx, int m, int k,
                                                        int rows, _Float16* __restrict__ xh) {
-    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;  // chunk of 8 halfs
-    const int kc = k >> 3;
-    if (c >= (int64_t)rows * kc) return;
-    const int64_t r = c / kc;
-    const int p0 = (int)(c - r * kc) << 3;  // first position of the chunk within the row
-    half8 v;
-    if (r < m) {
-        const float* src = x + r * ldx + (p0 & ~255) + q4k_perm_elem(p0 & 255);
-        // j = 0..7 -> element offsets 0, 32, 8, 40, 16, 48, 24, 56 from the chunk's first
+    __shared__ float4 blk[4][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nb = k >> 8;
+    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // unit: row * nb + block
+    const bool live = u < (int64_t)rows * nb;
+    const int64_t r = live ? u / nb : 0;
+    const int b = live ? (int)(u - r * nb) : 0;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live && r < m) v = ((const float4*)(x + r * ldx + 256 * b))[lane];
+    blk[wave][lane] = v;
+    __syncthreads();
+    if (!live || lane >= 32) return;
+    const float* e = (const float*)blk[wave] + q4k_perm_elem(8 * lane);
+    half8 h;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (_Float16)src[32 * (j & 1) + 8 * (j >> 1)];
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (_Float16)0.0f;
-    }
-    *(half8*)(xh + (c << 3)) = v;
+    for (int j = 0; j < 8; ++j) h[j] = (_Float16)e[32 * (j & 1) + 8 * (j >> 1)];
+    *(half8*)(xh + r * k + 256 * b + 8 * lane) = h;
 }
 
 // The 8 (scale, min) pairs of a Q4_K block header (get_scale_min_k4), times d and dmin:
@@ -491,8 +495,8 @@ size_t gemm_q4k_workspace(int64_t n, int m, int64_t k) {
 hipError_t launch_gemm_q4k_prep(const float* x, int64_t ldx, int m, int64_t n, int k, void* ws, hipStream_t s) {
     const GemmPlan p = gemm_plan(n, m, k);
     const int rows = gemm_xh_rows(m);
-    const int64_t chunks = (int64_t)rows * (k / 8);
-    hipLaunchKernelGGL(k_x_to_f16_perm, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s, x, ldx, m, k, rows,
+    const int64_t units = (int64_t)rows * (k / 256);  // one wave each, four per workgroup
+    hipLaunchKernelGGL(k_x_to_f16_perm, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, s, x, ldx, m, k, rows,
                        (_Float16*)ws);
     return hipGetLastError();
 }
