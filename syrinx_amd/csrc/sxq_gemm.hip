@@ -282,8 +282,8 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
     // This half's groups: local group li is group 4 b0 + 2 li + kh from the start of K,
     // li = 0 .. LG-1, in block b0 + li/2.  Prologue: the first block's header, local group
     // 0's activations and weights.  Local group li then issues its successor's 8 activation
-    // loads and weight load (local group li + 1, clamped to the half's last group: fetched
-    // again, never used) and, when li is even, the next block's header.  So when local
+    // loads and weight load (none after the last group) and, when li is even, the next
+    // block's header (clamped to the last block: fetched again, never used).  So when local
     // group li starts, at most the header issued after its loads (li odd) may still be
     // outstanding.
     const int LG = 2 * (b1 - b0);
@@ -308,8 +308,10 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
         SXQ_WAIT_VM(1);
         barrier_nofence();  // stage 1 is filled everywhere; stage 0 is free
         __builtin_amdgcn_sched_barrier(0);
-        load_group(grp_of(li + 2), 0);
-        w0 = load_w(grp_of(li + 2));
+        if (li + 2 < LG) {  // uniform: the last pair prefetches nothing
+            load_group(grp_of(li + 2), 0);
+            w0 = load_w(grp_of(li + 2));
+        }
         __builtin_amdgcn_sched_barrier(0);
         compute(std::integral_constant<int, 1>(), w1, nullptr);
     }
