@@ -597,6 +597,23 @@ hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64
         if (fits && m == 1) return gemv2_dispatch<1>(w, act, m, y, ldy, bias, res, ldr, s);
         if (fits && m == 2) return gemv2_dispatch<2>(w, act, m, y, ldy, bias, res, ldr, s);
         if (fits && m <= 4) return gemv2_dispatch<4>(w, act, m, y, ldy, bias, res, ldr, s);
+        // 5..16 rows: the task-split kernel four activation rows at a time (each launch
+        // streams the weights again; per row this is still well ahead of the
+        // one-group-per-row kernel, whose few waves leave most of the GPU idle).
+        if (m <= 16 && gemv2_fits((int)w.n, nb, 4, w.dtype, 256)) {
+            const size_t row_bytes = (size_t)nb * act_block_bytes(vec_dot_type(w.dtype));
+            for (int r0 = 0; r0 < m; r0 += 4) {
+                const int mc = min(4, m - r0);
+                const void* a = (const uint8_t*)act + (size_t)r0 * row_bytes;
+                float* yc = y + (int64_t)r0 * ldy;
+                const float* rc = res ? res + (int64_t)r0 * ldr : nullptr;
+                const hipError_t e = mc == 1   ? gemv2_dispatch<1>(w, a, mc, yc, ldy, bias, rc, ldr, s)
+                                     : mc == 2 ? gemv2_dispatch<2>(w, a, mc, yc, ldy, bias, rc, ldr, s)
+                                               : gemv2_dispatch<4>(w, a, mc, yc, ldy, bias, rc, ldr, s);
+                if (e != hipSuccess) return e;
+            }
+            return hipSuccess;
+        }
     }
     if (m == 1) return gemv_dispatch<1>(w, act, m, y, ldy, bias, res, ldr, s);
     if (m == 2) return gemv_dispatch<2>(w, act, m, y, ldy, bias, res, ldr, s);

@@ -125,6 +125,8 @@ CASES = [
     (G.Q4K, 16389, 512, 3),
     (G.Q4K, 16384, 9728, 4),   # nb = 38 blocks per row, four activation rows
     (G.Q4K, 19456, 2560, 1),   # Qwen3-4B fused w1|w3
+    (G.Q4K, 2560, 9728, 10),   # skinny batch in chunks of four rows: 4 + 4 + 2
+    (G.Q8_0, 896, 4864, 7),    # Q8_0 in chunks: 4 + 3
 ]
 
 
