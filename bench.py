@@ -25,7 +25,11 @@ under profiles/, whose header gives the commands and the copy-kernel scale facto
 the f16 MFMA GEMM including its conversion of x, against the 2.5 PFLOP/s dense f16
 MFMA peak.
 
-Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtype q4k|q8_0] [--no-cpu] [--no-prefill]
+`skinny_batch` is a third line: 16 concurrent streams decoding at once with ragged
+KV lengths drawn uniformly from 256..2048 (the GEMVs run 16 activation rows, attention
+and the KV append run per stream), tokens per second over all streams.
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtype q4k|q8_0] [--no-cpu] [--no-prefill] [--skinny-batch 16|0]
        python bench.py --mode gemv [--gemv-iters N]   (GEMV pass only, for counter runs)
        python bench.py --mode copy                     (plain 1 GiB device copy, the counter scale)
        python bench.py --mode prefill                  (the prefill line alone)
@@ -61,6 +65,9 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-GEMM line of the decode bench")
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--prefill-iters", type=int, default=20)
+    ap.add_argument("--skinny-batch", type=int, default=16,
+                    help="streams of the skinny-batch line (ragged KV lengths uniform over 256..2048); 0 skips it")
+    ap.add_argument("--skinny-steps", type=int, default=64)
     return ap.parse_args()
 
 
@@ -224,6 +231,41 @@ def prefill_gemms(torch, tokens, iters):
             "ms_36_layers": round(36 * ms, 3)}
 
 
+SKINNY_KV = (256, 2048)
+
+
+def skinny_batch(lm, torch, n, steps, warmup):
+    """Greedy decode of n concurrent streams whose KV caches hold ragged lengths drawn
+    uniformly from 256..2048 (seeded): the GEMVs see n activation rows, attention and the
+    KV append run per stream at its own position."""
+    import random
+    rng = random.Random(5)
+    lengths = [rng.randint(*SKINNY_KV) for _ in range(n)]
+    lm.kv_fill_random([SKINNY_KV[1]] * n, seed=2)
+    frame = torch.zeros((n, 1 + lm.cfg.n_codebooks), dtype=torch.int32)
+    frame[:, 0] = 151700
+    frame[:, 1:] = (torch.arange(n, dtype=torch.int32)[:, None] * 11 + torch.arange(lm.cfg.n_codebooks)) * 37 % 4096
+    lm.set_lengths(lengths)
+    lm.step(ids=frame, graph=True, want_logits=False)  # captures the n-stream graph
+    for _ in range(warmup):
+        lm.step(n=n, graph=True, want_logits=False)
+    lm.set_lengths(lengths)
+    lm.step(ids=frame, graph=True, want_logits=False)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream(lm.device)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        lm.step(n=n, graph=True, want_logits=False)
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    return {"workload": f"{n} concurrent streams, Qwen3-4B shape, Q4_K, ragged KV lengths uniform over "
+                        f"{SKINNY_KV[0]}..{SKINNY_KV[1]} (seed 5), {steps} steps",
+            "value": round(n * steps / (ms / 1000.0), 2), "unit": "tok/s (all streams)",
+            "ms_per_step": round(ms / steps, 4), "kv_lengths": lengths}
+
+
 def copy_calibration(torch, iters=8):
     """A plain device-to-device copy of 1 GiB: its counters give the FETCH/WRITE scale."""
     n = 1 << 30
@@ -253,8 +295,9 @@ def main():
 
     dev = torch.device("cuda:0")
     dt = GgmlDType.Q4K if args.dtype == "q4k" else GgmlDType.Q8_0
-    max_seq = args.kv + args.steps + args.warmup + 8
-    cfg = D.fish_s2_slow_ar_config(n_layers=36, max_seq=max_seq, max_batch=args.batch, dtype=dt)
+    skinny = args.skinny_batch if args.mode == "decode" else 0
+    max_seq = max(args.kv, SKINNY_KV[1] if skinny else 0) + max(args.steps, args.skinny_steps) + args.warmup + 8
+    cfg = D.fish_s2_slow_ar_config(n_layers=36, max_seq=max_seq, max_batch=max(args.batch, skinny), dtype=dt)
     t0 = time.time()
     lm = D.SlowAr(cfg, device=dev)
     lm.init_random(seed=0, std=0.02)
@@ -291,6 +334,7 @@ def main():
           file=sys.stderr, flush=True)
     roof = gemv_roofline(lm, torch, args.gemv_iters)
     print(f"[bench] GEMV: {roof['gemv_us_per_token']} us/token, {roof['achieved']} GB/s", file=sys.stderr, flush=True)
+    skinny_line = skinny_batch(lm, torch, skinny, args.skinny_steps, args.warmup) if skinny else None
     cpu = None if args.no_cpu else cpu_baseline(lm, torch)
     prefill = None
     if not args.no_prefill:
@@ -319,6 +363,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "skinny_batch": skinny_line,
     }
     print(json.dumps(out))
 

@@ -216,23 +216,26 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_q80(const uint16_t* __restr
 // Activation staging in two halves so the caller can put its weight loads between
 // them: act_fetch issues a thread's first 16-byte loads (clamped, so all are
 // unconditional and in flight together); act_store writes them to LDS and copies any
-// remainder (only when m * nb blocks exceed 1024 uint4 = 16 KB).
-template <int NT>
+// remainder (only when m * nb blocks exceed kPer * NT uint4).
+template <int NT, int MMAX>
 struct Stage {
-    static constexpr int kPer = 1024 / NT;
+    // 16 KB first; 16 KB per activation row for 1024 threads, whose multi-row launches
+    // stage up to 46 KB
+    static constexpr int kPer = NT == 1024 ? MMAX : 1024 / NT;
 };
-template <int NT>
-SXQ_DEV void act_fetch(uint4 (&v)[Stage<NT>::kPer], const uint8_t* __restrict__ act, int total_u4) {
+template <int NT, int MMAX, int KP = Stage<NT, MMAX>::kPer>
+SXQ_DEV void act_fetch(uint4 (&v)[KP], const uint8_t* __restrict__ act, int total_u4) {
 #pragma unroll
-    for (int k = 0; k < Stage<NT>::kPer; ++k) v[k] = ((const uint4*)act)[min(k * NT + (int)threadIdx.x, total_u4 - 1)];
+    for (int k = 0; k < KP; ++k)
+        v[k] = ((const uint4*)act)[min(k * NT + (int)threadIdx.x, total_u4 - 1)];
     __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
 }
-template <int NT>
-SXQ_DEV void act_store(const uint4 (&v)[Stage<NT>::kPer], uint4* lds, const uint8_t* __restrict__ act, int total_u4) {
+template <int NT, int MMAX, int KP = Stage<NT, MMAX>::kPer>
+SXQ_DEV void act_store(const uint4 (&v)[KP], uint4* lds, const uint8_t* __restrict__ act, int total_u4) {
     // clamped like the loads: out-of-range threads rewrite the last element with its own value
 #pragma unroll
-    for (int k = 0; k < Stage<NT>::kPer; ++k) lds[min(k * NT + (int)threadIdx.x, total_u4 - 1)] = v[k];
-    for (int i = Stage<NT>::kPer * NT + threadIdx.x; i < total_u4; i += NT) lds[i] = ((const uint4*)act)[i];
+    for (int k = 0; k < KP; ++k) lds[min(k * NT + (int)threadIdx.x, total_u4 - 1)] = v[k];
+    for (int i = KP * NT + threadIdx.x; i < total_u4; i += NT) lds[i] = ((const uint4*)act)[i];
 }
 
 // Q4_K task-split GEMV, NT threads (256 or 1024) per workgroup: NT/8 eight-lane groups,
@@ -254,17 +257,17 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8K) / 16));  // product chains [m][R + 1][9][CS]
     const uint32_t blk0 = (uint32_t)row0 * (uint32_t)nb;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8K) / 16);
-    uint4 av[Stage<NT>::kPer];
+    uint4 av[Stage<NT, MMAX>::kPer];
     float4 xv, wv;
     if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 256);
-    else act_fetch<NT>(av, act, act_u4);
+    else act_fetch<NT, MMAX>(av, act, act_u4);
     uint4 q[TM], h[TM];
     q4k_tile_load<NT, TM>(hdr, qs, blk0, tasks, q, h);
     if constexpr (NORM) {
         __shared__ float red[16];
         norm_quant_store<kQ8K>(xv, wv, ni, nb * 256, (uint8_t*)lds, red);
     } else {
-        act_store<NT>(av, lds, act, act_u4);
+        act_store<NT, MMAX>(av, lds, act, act_u4);
     }
     // The activations are in LDS; the weight loads may still be in flight: each round of
     // products waits only for its own.
@@ -386,10 +389,10 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
     const int slot = threadIdx.x / LPT;
     const int64_t base = (int64_t)row0 * nb;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8_0) / 16);
-    uint4 av[Stage<NT>::kPer];
+    uint4 av[Stage<NT, MMAX>::kPer];
     float4 xv, wv;
     if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 32);
-    else act_fetch<NT>(av, act, act_u4);
+    else act_fetch<NT, MMAX>(av, act, act_u4);
     uint4 w[TM];
     float dw[TM];
 #pragma unroll
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
         __shared__ float red[16];
         norm_quant_store<kQ8_0>(xv, wv, ni, nb * 32, (uint8_t*)lds, red);
     } else {
-        act_store<NT>(av, lds, act, act_u4);
+        act_store<NT, MMAX>(av, lds, act, act_u4);
     }
     __syncthreads();
     // Block index of task u*TPI + slot, stepped by TPI mod nb each round; tasks past the
@@ -460,7 +463,8 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
 // rows over one full wave of workgroups -- 256 (one 1024-thread workgroup per CU) or
 // 1024 (four 256-thread workgroups per CU), overridable with SXQ_GEMV_WG -- capped so
 // every lane group holds at most kTmax tasks, the epilogue has a thread per (row, lane
-// class), and LDS fits in 60 KB.
+// class), and LDS fits the workgroup's share of a CU's 160 KB: 60 KB for 256 threads,
+// 144 KB for 1024 (one workgroup per CU).
 static int tasks_per_round(int dtype, int nt) { return dtype == kQ4K ? nt / 8 : (dtype == kQ8_0 ? nt / 2 : nt); }
 
 size_t gemv2_lds(int nb, int m, int R, int dtype, int nt) {
@@ -471,6 +475,8 @@ size_t gemv2_lds(int nb, int m, int R, int dtype, int nt) {
     return (size_t)m * nb * ab + slots * m * 4;
 }
 
+static size_t gemv2_lds_cap(int nt) { return nt == 1024 ? 144 * 1024 : 60 * 1024; }
+
 int gemv2_rows(int n, int nb, int m, int dtype, int nt) {
     static const int env_wg = [] {
         const char* e = getenv("SXQ_GEMV_WG");
@@ -480,7 +486,7 @@ int gemv2_rows(int n, int nb, int m, int dtype, int nt) {
     int R = (n + target_wg - 1) / target_wg;
     R = min(R, nt / 8);
     R = min(R, max(1, tasks_per_round(dtype, nt) * kTmax / nb));
-    while (R > 1 && gemv2_lds(nb, m, R, dtype, nt) > 60 * 1024) --R;
+    while (R > 1 && gemv2_lds(nb, m, R, dtype, nt) > gemv2_lds_cap(nt)) --R;
     return max(R, 1);
 }
 
@@ -488,22 +494,37 @@ int gemv2_rows(int n, int nb, int m, int dtype, int nt) {
 // within kTmax rounds and LDS within 60 KB; for NT = 1024 also no more workgroups than
 // the one-per-CU target (otherwise the 256-thread kernel is the better fit).
 bool gemv2_fits(int n, int nb, int m, int dtype, int nt) {
-    if (nb > tasks_per_round(dtype, nt) * kTmax || gemv2_lds(nb, m, 1, dtype, nt) > 60 * 1024) return false;
+    if (nb > tasks_per_round(dtype, nt) * kTmax || gemv2_lds(nb, m, 1, dtype, nt) > gemv2_lds_cap(nt)) return false;
     if (nt == 256) return true;
     const int R = gemv2_rows(n, nb, m, dtype, nt);
     return (n + R - 1) / R <= 256;
 }
 
-// Threads per workgroup.  Plain launches use 256 (measured at least as fast as 1024 at
-// every decode shape, and faster for w1|w3); SXQ_GEMV_NT=1024 selects the larger one
-// where it fits.  The fused RMSNorm prologue always runs with 1024 threads, so the row
-// is normalised and quantized once per CU rather than four times.
+// Threads per workgroup.  One activation row: 256 (measured at least as fast as 1024 at
+// every decode shape, and faster for w1|w3).  Two or more rows: 1024 where it fits --
+// every workgroup stages all m rows of activation blocks in LDS, and with 256 threads
+// the LDS cap leaves so few weight rows per workgroup that the staging outweighs the
+// weights (the 9728-wide down projection at m = 4: one row per workgroup, 2560
+// workgroups each staging 46 KB).  SXQ_GEMV_NT=256 or 1024 forces one size where it fits.
+// The fused RMSNorm prologue always runs with 1024 threads, so the row is normalised
+// and quantized once per CU rather than four times.
 static int gemv2_nt(int n, int nb, int m, int dtype) {
     static const int env_nt = [] {
         const char* e = getenv("SXQ_GEMV_NT");
-        return e ? atoi(e) : 256;
+        return e ? atoi(e) : 0;
     }();
-    return env_nt == 1024 && gemv2_fits(n, nb, m, dtype, 1024) ? 1024 : 256;
+    const bool wide = env_nt ? env_nt == 1024 : m >= 2;
+    return wide && gemv2_fits(n, nb, m, dtype, 1024) ? 1024 : 256;
+}
+
+// A launch with more than 64 KB of dynamic LDS needs the kernel's limit raised first;
+// raised once per kernel, to the largest cap any launch of it asks for.
+template <auto K>
+static hipError_t allow_lds(size_t lds) {
+    if (lds <= 64 * 1024) return hipSuccess;
+    static const hipError_t e =
+        hipFuncSetAttribute((const void*)K, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemv2_lds_cap(1024));
+    return e;
 }
 
 // Calls f(std::integral_constant<int, TM>()) for TM = rounds (1 .. kTmax).
@@ -535,14 +556,18 @@ static hipError_t gemv2_launch(const QWeight& w, const void* act, int m, float* 
     const int rounds = (R * nb + tpr - 1) / tpr;
     const hipError_t e = with_rounds(rounds, [&](auto tmc) -> hipError_t {
         constexpr int TM = decltype(tmc)::value;
-        if (w.dtype == kQ4K)
+        if (w.dtype == kQ4K) {
+            if (const hipError_t e_ = allow_lds<k_gemv2_q4k<MMAX, NORM, NT, TM>>(lds); e_ != hipSuccess) return e_;
             hipLaunchKernelGGL((k_gemv2_q4k<MMAX, NORM, NT, TM>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
-        else if (w.dtype == kQ8_0)
+        } else if (w.dtype == kQ8_0) {
+            if (const hipError_t e_ = allow_lds<k_gemv2_q80<MMAX, false, NORM, NT, TM>>(lds); e_ != hipSuccess) return e_;
             hipLaunchKernelGGL((k_gemv2_q80<MMAX, false, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
-        else if (w.dtype == kQ4_0)
+        } else if (w.dtype == kQ4_0) {
+            if (const hipError_t e_ = allow_lds<k_gemv2_q80<MMAX, true, NORM, NT, TM>>(lds); e_ != hipSuccess) return e_;
             hipLaunchKernelGGL((k_gemv2_q80<MMAX, true, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
-        else
+        } else {
             return hipErrorInvalidValue;
+        }
         return hipSuccess;
     });
     if (e != hipSuccess) return e;
