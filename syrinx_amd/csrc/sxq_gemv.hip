@@ -491,11 +491,12 @@ int gemv2_rows(int n, int nb, int m, int dtype, int nt) {
 }
 
 // Whether the task-split kernel with NT threads covers this shape: one row's tasks
-// within kTmax rounds and LDS within 60 KB; for NT = 1024 also no more workgroups than
-// the one-per-CU target (otherwise the 256-thread kernel is the better fit).
+// within kTmax rounds and LDS within the cap; for NT = 1024 and one activation row also
+// no more workgroups than the one-per-CU target (otherwise the 256-thread kernel is the
+// better fit; with more rows the larger LDS share wins at any workgroup count).
 bool gemv2_fits(int n, int nb, int m, int dtype, int nt) {
     if (nb > tasks_per_round(dtype, nt) * kTmax || gemv2_lds(nb, m, 1, dtype, nt) > gemv2_lds_cap(nt)) return false;
-    if (nt == 256) return true;
+    if (nt == 256 || m > 1) return true;
     const int R = gemv2_rows(n, nb, m, dtype, nt);
     return (n + R - 1) / R <= 256;
 }
