@@ -628,45 +628,30 @@ static hipError_t gemv_dispatch(const QWeight& w, const void* act, int m, float*
 // A workgroup of 4 waves owns 16 weight rows and all their blocks; wave w runs classes
 // 2w and 2w + 1 (wave 0 also the min term) over the blocks in order, so every chain
 // stays in one lane's registers in block order, and only at the end do the eight class
-// sums of each (activation row, weight row) meet in LDS, added in class order.
-// Activation blocks go through LDS in chunks of four as f16 in the MFMA operand order
-// (double-buffered: loaded two chunks ahead, stored one chunk ahead, one barrier per
-// chunk; 69 KB, two workgroups per CU); each wave loads its two class dwords and the
-// block headers two chunks ahead (clamped, unconditional loads).  MFMA k-slots: lane
-// group g (lane / 16) of a class-l operand holds dword g of the weight's class-l 16
-// bytes (device layout: byte 16l + 4c + t holds elements 64c + l + 8t and
-// 64c + 32 + l + 8t), as the eight values (t, nibble) = (0,lo) (2,lo) (1,lo) (3,lo)
-// (0,hi) (2,hi) (1,hi) (3,hi); the activation operand holds the same elements, which
-// sit at qs[32l + 8g + {0,2,1,3,4,6,5,7}] of the class-major Q8_K block.
+// sums of each (activation row, weight row) meet in LDS, added in class order.  The
+// operands go through LDS in chunks of four blocks, copied with contiguous 16-byte loads
+// (whole cache lines; each lane's own pieces are 4- to 16-byte scraps of many lines)
+// into row-padded tiles that the lanes then read without bank conflicts: weights
+// 16 rows x 512 B (+16), headers, and activations 16 rows x 4 x 304 B (+16); double-
+// buffered, loaded one chunk ahead, one barrier per chunk (57 KB: two workgroups per
+// CU).  Activation rows past m and weight rows past n use clamped copies and are never
+// stored.  MFMA k-slots: lane group g (lane / 16) of a class-l operand holds dword g of
+// the weight's class-l 16 bytes (device layout: byte 16l + 4c + t holds elements
+// 64c + l + 8t and 64c + 32 + l + 8t), as the eight values (t, nibble) = (0,lo) (2,lo)
+// (1,lo) (3,lo) (0,hi) (2,hi) (1,hi) (3,hi); the activation operand holds the same
+// elements, which sit at qs[32l + 8g + {0,2,1,3,4,6,5,7}] of the class-major Q8_K block.
 constexpr int kMmaRows = 16;
-constexpr int kMmaChunk = 4;                   // blocks per staged chunk
-constexpr int kMmaA = kMmaChunk * 8 * 4 * 16;  // half8 per chunk: [block][class][g][m]
-constexpr int kMmaS = kMmaChunk * 16 * 8;      // floats per chunk: bs2 [block][m][s]
-constexpr int kMmaD = kMmaChunk * 16;          // floats per chunk: d_a [block][m]
-constexpr size_t kMmaLds = 2 * (kMmaA * 16 + (kMmaS + kMmaD) * 4);
-static_assert(kMmaA * 16 >= 9 * 256 * 4, "the final class sums reuse the activation buffer");
+constexpr int kMmaChunk = 4;                          // blocks per chunk
+constexpr int kMmaWRow = kMmaChunk * 32 + 4;          // dwords per weight row of a chunk (padded)
+constexpr int kMmaARow = kMmaChunk * 76 + 4;          // dwords per activation row of a chunk (padded)
+constexpr int kMmaBuf = 16 * kMmaWRow + 16 * kMmaChunk * 4 + 16 * kMmaARow;  // dwords per chunk buffer
+constexpr size_t kMmaLds = 2 * (size_t)kMmaBuf * 4;
+static_assert(kMmaBuf >= 9 * 256, "the final class sums reuse a chunk buffer");
+static_assert(sizeof(ActQ8K) == 76 * 4, "activation rows are copied as 19 uint4 per block");
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-struct MmaW {  // one lane's share of a chunk: per block its two class dwords (g) and the header
-    uint32_t q[kMmaChunk][2];
-    uint4 h[kMmaChunk];
-};
-
-SXQ_DEV MmaW mma_load_w(const uint4* __restrict__ hdr, const uint32_t* __restrict__ qs32, uint32_t rb0, int c, int nb,
-                        int w, int g) {
-    MmaW r;
-#pragma unroll
-    for (int j = 0; j < kMmaChunk; ++j) {
-        const uint32_t blk = rb0 + (uint32_t)min(c * kMmaChunk + j, nb - 1);
-        r.h[j] = hdr[blk];
-        r.q[j][0] = qs32[blk * 32 + 8 * w + g];      // class 2w: bytes 32w + 4g
-        r.q[j][1] = qs32[blk * 32 + 8 * w + 4 + g];  // class 2w + 1
-    }
-    return r;
-}
 
 // (1024 + hi16, 1024 + lo16) f16 pair of two 16-bit integers below 1024
 SXQ_DEV half2_t mma_magic(uint32_t v) { return __builtin_bit_cast(half2_t, v | 0x64006400u); }
@@ -682,8 +667,8 @@ SXQ_DEV half8_t mma_weight8(uint32_t v, half2_t sc0, half2_t ns0, half2_t sc1, h
     return half8_t{x0.x, x0.y, x1.x, x1.y, x2.x, x2.y, x3.x, x3.y};
 }
 
-// eight int8 (two dwords) -> f16 in slot order {0,2,1,3,4,6,5,7}; zero when !live
-SXQ_DEV half8_t mma_act8(uint2 v, bool live) {
+// eight int8 (two dwords) -> f16 in slot order {0,2,1,3,4,6,5,7}
+SXQ_DEV half8_t mma_act8(uint2 v) {
     const half2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     const uint32_t x0 = v.x ^ 0x80808080u, x1 = v.y ^ 0x80808080u;  // u = q + 128
     // byte select: (u0, 0x64, u2, 0x64) = f16 pair (1024 + u0, 1024 + u2)
@@ -691,93 +676,76 @@ SXQ_DEV half8_t mma_act8(uint2 v, bool live) {
     const half2_t p1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030401u)) + off;
     const half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, x1, 0x04020400u)) + off;
     const half2_t p3 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030401u)) + off;
-    const half8_t r = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-    const half8_t z = {};
-    return live ? r : z;
+    return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-__global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ hdr, const uint32_t* __restrict__ qs32,
+__global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
                                                       int n, int nb, const uint8_t* __restrict__ act, int m, float* y,
                                                       int64_t ldy, const float* __restrict__ bias, const float* res,
                                                       int64_t ldr) {
     extern __shared__ uint4 lds[];
-    half8_t* abuf = (half8_t*)lds;              // [2][kMmaA]
-    float* sbuf = (float*)(lds + 2 * kMmaA);    // [2][kMmaS]
-    float* dbuf = sbuf + 2 * kMmaS;             // [2][kMmaD]
+    uint32_t* l32 = (uint32_t*)lds;  // [2][kMmaBuf]: weights [16][kMmaWRow], headers [16][4] uint4, act [16][kMmaARow]
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, nl = lane & 15;
     const int row0 = blockIdx.x * kMmaRows;
-    const uint32_t rb0 = (uint32_t)min(row0 + nl, n - 1) * (uint32_t)nb;  // clamped: loads only
     const int nc = (nb + kMmaChunk - 1) / kMmaChunk;
 
-    // activation staging of chunk c: thread t converts units u = t + 256k (k < 8) of
-    // (block, class, g, m) = (u >> 9, (u >> 6) & 7, (u >> 4) & 3, u & 15) into LDS slot u;
-    // threads < 64 also copy d and bs2 of (block, m) = (t >> 4, t & 15)
-    struct Staged {
-        uint2 v[8];
-        float d;
-        int4 b0, b1;
-    };
-    auto stage_load = [&](int c) {  // unconditional loads (clamped), so the waits stay counted
-        Staged st;
-        c = min(c, nc - 1);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int u = tid + 256 * k;
-            const int b = min(c * kMmaChunk + (u >> 9), nb - 1), mr = min(u & 15, m - 1);
-            const uint8_t* blk = act + ((size_t)mr * nb + b) * sizeof(ActQ8K);
-            st.v[k] = *(const uint2*)(blk + 32 * ((u >> 6) & 7) + 8 * ((u >> 4) & 3));
-        }
-        const int b = min(c * kMmaChunk + ((tid >> 4) & 3), nb - 1), mr = min(tid & 15, m - 1);
-        const ActQ8K* blk = (const ActQ8K*)(act + ((size_t)mr * nb + b) * sizeof(ActQ8K));
-        st.d = blk->d;
-        st.b0 = *(const int4*)&blk->bs2[0];
-        st.b1 = *(const int4*)&blk->bs2[4];
-        return st;
-    };
-    auto stage_store = [&](int c, const Staged& st) {
-        half8_t* a = abuf + (c & 1) * kMmaA;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int u = tid + 256 * k;
-            const bool live = (u & 15) < m && c * kMmaChunk + (u >> 9) < nb;
-            a[u] = mma_act8(st.v[k], live);
-        }
-        if (tid < 64) {
-            const int bb = tid >> 4, mr = tid & 15;
-            const bool live = mr < m && c * kMmaChunk + bb < nb;
-            float* sp = sbuf + (c & 1) * kMmaS + (bb * 16 + mr) * 8;
-            sp[0] = live ? (float)st.b0.x : 0.0f, sp[1] = live ? (float)st.b0.y : 0.0f;
-            sp[2] = live ? (float)st.b0.z : 0.0f, sp[3] = live ? (float)st.b0.w : 0.0f;
-            sp[4] = live ? (float)st.b1.x : 0.0f, sp[5] = live ? (float)st.b1.y : 0.0f;
-            sp[6] = live ? (float)st.b1.z : 0.0f, sp[7] = live ? (float)st.b1.w : 0.0f;
-            dbuf[(c & 1) * kMmaD + bb * 16 + mr] = live ? st.d : 0.0f;
-        }
-    };
-
-    // Prefetch buffers in registers: weights W[c & 1] hold chunk c; staged activations
-    // S[(c + 1) & 1] hold chunk c + 1.  The loop is unrolled by two so each buffer is
-    // refilled in place after its use (no register copies, which would wait for the
-    // loads just issued), and runs an even number of steps with every load clamped and
-    // unconditional, so the compiler's load counters stay exact.
-    MmaW w0 = mma_load_w(hdr, qs32, rb0, 0, nb, w, g);
-    MmaW w1 = mma_load_w(hdr, qs32, rb0, 1, nb, w, g);
-    {
-        const Staged st0 = stage_load(0);
-        stage_store(0, st0);
+    // chunk copy: weight pieces u = tid, tid + 256 of (row u >> 5, 16-byte piece u & 31);
+    // header (row tid >> 2, block tid & 3) for tid < 64; activation pieces u = tid + 256k
+    // (k < 5, clamped to the 1216 pieces) of (row u / 76, piece u % 76)
+    uint4 swq0, swq1, sh, sa0, sa1, sa2, sa3, sa4;  // the chunk in flight
+#define SXQ_MMA_WQ(K, V)                                                                   \
+    {                                                                                      \
+        const int u = tid + 256 * (K), r = min(row0 + (u >> 5), n - 1), p = u & 31;        \
+        const int b = min(cc * kMmaChunk + (p >> 3), nb - 1);                             \
+        V = qs[((size_t)r * nb + b) * 8 + (p & 7)];                                        \
     }
-    Staged s1 = stage_load(1);
-    Staged s0 = stage_load(2);
-    __syncthreads();
+#define SXQ_MMA_A(K, V)                                                                    \
+    {                                                                                      \
+        const int u = min(tid + 256 * (K), 16 * 76 - 1), r = min(u / 76, m - 1), p = u % 76; \
+        const int b = min(cc * kMmaChunk + p / 19, nb - 1);                              \
+        V = ((const uint4*)(act + ((size_t)r * nb + b) * sizeof(ActQ8K)))[p % 19];        \
+    }
+    auto stage_load = [&](int c) {  // unconditional loads (clamped)
+        const int cc = min(c, nc - 1);
+        SXQ_MMA_WQ(0, swq0) SXQ_MMA_WQ(1, swq1)
+        {
+            const int r = min(row0 + ((tid >> 2) & 15), n - 1), b = min(cc * kMmaChunk + (tid & 3), nb - 1);
+            sh = hdr[(size_t)r * nb + b];
+        }
+        SXQ_MMA_A(0, sa0) SXQ_MMA_A(1, sa1) SXQ_MMA_A(2, sa2) SXQ_MMA_A(3, sa3) SXQ_MMA_A(4, sa4)
+    };
+#undef SXQ_MMA_WQ
+#undef SXQ_MMA_A
+    auto stage_store = [&](int c) {
+        uint32_t* bw = l32 + (c & 1) * kMmaBuf;
+        *(uint4*)(bw + (tid >> 5) * kMmaWRow + (tid & 31) * 4) = swq0;
+        *(uint4*)(bw + ((tid + 256) >> 5) * kMmaWRow + (tid & 31) * 4) = swq1;
+        if (tid < 64) *(uint4*)(bw + 16 * kMmaWRow + tid * 4) = sh;
+        uint32_t* ba = bw + 16 * kMmaWRow + 16 * kMmaChunk * 4;
+        const uint4 v[5] = {sa0, sa1, sa2, sa3, sa4};
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const int u = min(tid + 256 * k, 16 * 76 - 1);
+            *(uint4*)(ba + (u / 76) * kMmaARow + (u % 76) * 4) = v[k];
+        }
+    };
 
-    // chains of lane (nl, g), accumulator element j: activation row 4g + j, weight row nl
+    // chains of lane (nl, g), accumulator element e: activation row 4g + e, weight row nl
     float s0c[4] = {0.f, 0.f, 0.f, 0.f}, s1c[4] = {0.f, 0.f, 0.f, 0.f}, sf[4] = {0.f, 0.f, 0.f, 0.f};
-    auto step = [&](int c, MmaW& wb, Staged& sb) {
-        const int par = c & 1, live = min(kMmaChunk, nb - c * kMmaChunk);  // live <= 0 past the end
+    stage_load(0);
+    stage_store(0);
+    stage_load(1);
+    __syncthreads();
+    for (int c = 0; c < nc; ++c) {
+        const uint32_t* bw = l32 + (c & 1) * kMmaBuf;
+        const uint4* bh = (const uint4*)(bw + 16 * kMmaWRow);
+        const uint32_t* ba = bw + 16 * kMmaWRow + 16 * kMmaChunk * 4;
+        const int live = min(kMmaChunk, nb - c * kMmaChunk);
 #pragma unroll
         for (int j = 0; j < kMmaChunk; ++j) {
             if (j < live) {  // uniform
-                const uint4 h = wb.h[j];
+                const uint4 h = bh[nl * 4 + j];
                 const uint32_t sc_lo = h.y & 0x3F3F3F3Fu;
                 const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | (((h.y >> 6) & 0x03030303u) << 4);
                 const uint32_t scw = (g < 2 ? sc_lo : sc_hi) >> (16 * (g & 1));  // scales 2g, 2g + 1
@@ -785,46 +753,44 @@ __global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ 
                 const half2_t sc0 = {(_Float16)f0, (_Float16)f0}, sc1 = {(_Float16)f1, (_Float16)f1};
                 const half2_t ns0 = {(_Float16)(-1024.0f * f0), (_Float16)(-1024.0f * f0)};
                 const half2_t ns1 = {(_Float16)(-1024.0f * f1), (_Float16)(-1024.0f * f1)};
-                const half8_t* a = abuf + par * kMmaA + j * 512 + (2 * w) * 64 + lane;
+                const uint32_t* wr = bw + nl * kMmaWRow + j * 32 + 8 * w + g;  // class 2w dword g
+                const uint32_t* ar = ba + nl * kMmaARow + j * 76 + 16 * w + 2 * g;  // qs[64w + 8g]
                 const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
                 const f32x4_t c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    a[0], mma_weight8(wb.q[j][0], sc0, ns0, sc1, ns1), z, 0, 0, 0);
+                    mma_act8(*(const uint2*)ar), mma_weight8(wr[0], sc0, ns0, sc1, ns1), z, 0, 0, 0);
                 const f32x4_t c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    a[64], mma_weight8(wb.q[j][1], sc0, ns0, sc1, ns1), z, 0, 0, 0);
-                const float4 ad = *(const float4*)(dbuf + par * kMmaD + j * 16 + 4 * g);
-                const float adv[4] = {ad.x, ad.y, ad.z, ad.w};
+                    mma_act8(*(const uint2*)(ar + 8)), mma_weight8(wr[4], sc0, ns0, sc1, ns1), z, 0, 0, 0);
                 const float dw = h2f(h.x & 0xFFFF);
+                float ad[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ad[e] = __builtin_bit_cast(float, ba[(4 * g + e) * kMmaARow + j * 76 + 64]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float d = dw * adv[e];
+                    const float d = dw * ad[e];
                     s0c[e] += d * c0[e];
                     s1c[e] += d * c1[e];
                 }
-                if (w == 0) {  // the min term: mins g and g + 4 against bs2 of row nl
+                if (w == 0) {  // the min term: mins g and g + 4 against bs2 of activation row nl
                     const uint32_t mn_lo = h.z & 0x3F3F3F3Fu;
                     const uint32_t mn_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | (((h.z >> 6) & 0x03030303u) << 4);
-                    const float* sp = sbuf + par * kMmaS + (j * 16 + nl) * 8;
+                    const int* bs = (const int*)(ba + nl * kMmaARow + j * 76 + 68);  // bs2 at byte 272
                     f32x4_t mi = z;
-                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32(sp[g], (float)((mn_lo >> (8 * g)) & 0xFF), mi, 0, 0, 0);
-                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32(sp[g + 4], (float)((mn_hi >> (8 * g)) & 0xFF), mi, 0, 0,
-                                                              0);
+                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32((float)bs[g], (float)((mn_lo >> (8 * g)) & 0xFF), mi, 0,
+                                                              0, 0);
+                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32((float)bs[g + 4], (float)((mn_hi >> (8 * g)) & 0xFF), mi,
+                                                              0, 0, 0);
                     const float dminw = h2f(h.x >> 16);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) sf[e] -= (dminw * adv[e]) * mi[e];
+                    for (int e = 0; e < 4; ++e) sf[e] -= (dminw * ad[e]) * mi[e];
                 }
             }
         }
-        wb = mma_load_w(hdr, qs32, rb0, c + 2, nb, w, g);
-        if (c + 1 < nc) stage_store(c + 1, sb);
-        sb = stage_load(c + 3);
+        if (c + 1 < nc) stage_store(c + 1);
+        stage_load(c + 2);
         __syncthreads();
-    };
-    for (int c = 0; c < nc; c += 2) {
-        step(c, w0, s1);
-        step(c + 1, w1, s0);
     }
-    // the class sums meet in LDS (the activation buffer: every read of it is behind the
-    // last barrier): xb[chain][m][n], chain 0..7 = class, 8 = min
+    // the class sums meet in LDS (chunk buffer 0: every read of it is behind the last
+    // barrier): xb[chain][activation row][weight row], chain 0..7 = class, 8 = min
     float* xb = (float*)lds;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -848,13 +814,9 @@ __global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ 
 
 static hipError_t gemv_mma_launch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                                   const float* res, int64_t ldr, hipStream_t s) {
-    static const hipError_t attr =
-        hipFuncSetAttribute((const void*)k_gemv_mma_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMmaLds);
-    if (attr != hipSuccess) return attr;
     const int n = (int)w.n, nb = (int)w.nb;
     hipLaunchKernelGGL(k_gemv_mma_q4k, dim3((unsigned)((n + kMmaRows - 1) / kMmaRows)), dim3(256), kMmaLds, s,
-                       (const uint4*)w.hdr, (const uint32_t*)w.qs, n, nb, (const uint8_t*)act, m, y, ldy, bias, res,
-                       ldr);
+                       (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, (const uint8_t*)act, m, y, ldy, bias, res, ldr);
     return hipGetLastError();
 }
 
