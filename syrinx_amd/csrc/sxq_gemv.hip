@@ -625,16 +625,16 @@ static hipError_t gemv_dispatch(const QWeight& w, const void* act, int m, float*
 // sums[l] += (d_w * d_a) * aux32[l] and sumf -= (dmin_w * d_a) * sumi, chains in
 // block order, then sumf + (-0.0 + sums[0] + ... + sums[7]).
 //
-// A workgroup of 4 waves owns 16 weight rows and all their blocks; wave w runs classes
-// 2w and 2w + 1 (wave 0 also the min term) over the blocks in order, so every chain
+// A workgroup of 8 waves owns 16 weight rows and all their blocks; wave w runs class w
+// (wave 0 also the min term) over the blocks in order, so every chain
 // stays in one lane's registers in block order, and only at the end do the eight class
 // sums of each (activation row, weight row) meet in LDS, added in class order.  The
 // operands go through LDS in chunks of four blocks, copied with contiguous 16-byte loads
 // (whole cache lines; each lane's own pieces are 4- to 16-byte scraps of many lines)
 // into row-padded tiles that the lanes then read without bank conflicts: weights
 // 16 rows x 512 B (+16), headers, and activations 16 rows x 4 x 304 B (+16); double-
-// buffered, loaded one chunk ahead, one barrier per chunk (57 KB: two workgroups per
-// CU).  Activation rows past m and weight rows past n use clamped copies and are never
+// buffered, loaded one chunk ahead, one barrier per chunk (57 KB: two workgroups, 16
+// waves, per CU).  Activation rows past m and weight rows past n use clamped copies and are never
 // stored.  MFMA k-slots: lane group g (lane / 16) of a class-l operand holds dword g of
 // the weight's class-l 16 bytes (device layout: byte 16l + 4c + t holds elements
 // 64c + l + 8t and 64c + 32 + l + 8t), as the eight values (t, nibble) = (0,lo) (2,lo)
@@ -679,7 +679,7 @@ SXQ_DEV half8_t mma_act8(uint2 v) {
     return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-__global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
+__global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
                                                       int n, int nb, const uint8_t* __restrict__ act, int m, float* y,
                                                       int64_t ldy, const float* __restrict__ bias, const float* res,
                                                       int64_t ldr) {
@@ -693,46 +693,45 @@ __global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ 
     // chunk copy: weight pieces u = tid, tid + 256 of (row u >> 5, 16-byte piece u & 31);
     // header (row tid >> 2, block tid & 3) for tid < 64; activation pieces u = tid + 256k
     // (k < 5, clamped to the 1216 pieces) of (row u / 76, piece u % 76)
-    uint4 swq0, swq1, sh, sa0, sa1, sa2, sa3, sa4;  // the chunk in flight
+    uint4 swq0, sh, sa0, sa1, sa2;  // the chunk in flight
 #define SXQ_MMA_WQ(K, V)                                                                   \
     {                                                                                      \
-        const int u = tid + 256 * (K), r = min(row0 + (u >> 5), n - 1), p = u & 31;        \
+        const int u = tid + 512 * (K), r = min(row0 + (u >> 5), n - 1), p = u & 31;        \
         const int b = min(cc * kMmaChunk + (p >> 3), nb - 1);                             \
         V = qs[((size_t)r * nb + b) * 8 + (p & 7)];                                        \
     }
 #define SXQ_MMA_A(K, V)                                                                    \
     {                                                                                      \
-        const int u = min(tid + 256 * (K), 16 * 76 - 1), r = min(u / 76, m - 1), p = u % 76; \
+        const int u = min(tid + 512 * (K), 16 * 76 - 1), r = min(u / 76, m - 1), p = u % 76; \
         const int b = min(cc * kMmaChunk + p / 19, nb - 1);                              \
         V = ((const uint4*)(act + ((size_t)r * nb + b) * sizeof(ActQ8K)))[p % 19];        \
     }
     auto stage_load = [&](int c) {  // unconditional loads (clamped)
         const int cc = min(c, nc - 1);
-        SXQ_MMA_WQ(0, swq0) SXQ_MMA_WQ(1, swq1)
+        SXQ_MMA_WQ(0, swq0)
         {
             const int r = min(row0 + ((tid >> 2) & 15), n - 1), b = min(cc * kMmaChunk + (tid & 3), nb - 1);
             sh = hdr[(size_t)r * nb + b];
         }
-        SXQ_MMA_A(0, sa0) SXQ_MMA_A(1, sa1) SXQ_MMA_A(2, sa2) SXQ_MMA_A(3, sa3) SXQ_MMA_A(4, sa4)
+        SXQ_MMA_A(0, sa0) SXQ_MMA_A(1, sa1) SXQ_MMA_A(2, sa2)
     };
 #undef SXQ_MMA_WQ
 #undef SXQ_MMA_A
     auto stage_store = [&](int c) {
         uint32_t* bw = l32 + (c & 1) * kMmaBuf;
         *(uint4*)(bw + (tid >> 5) * kMmaWRow + (tid & 31) * 4) = swq0;
-        *(uint4*)(bw + ((tid + 256) >> 5) * kMmaWRow + (tid & 31) * 4) = swq1;
         if (tid < 64) *(uint4*)(bw + 16 * kMmaWRow + tid * 4) = sh;
         uint32_t* ba = bw + 16 * kMmaWRow + 16 * kMmaChunk * 4;
-        const uint4 v[5] = {sa0, sa1, sa2, sa3, sa4};
+        const uint4 v[3] = {sa0, sa1, sa2};
 #pragma unroll
-        for (int k = 0; k < 5; ++k) {
-            const int u = min(tid + 256 * k, 16 * 76 - 1);
+        for (int k = 0; k < 3; ++k) {
+            const int u = min(tid + 512 * k, 16 * 76 - 1);
             *(uint4*)(ba + (u / 76) * kMmaARow + (u % 76) * 4) = v[k];
         }
     };
 
     // chains of lane (nl, g), accumulator element e: activation row 4g + e, weight row nl
-    float s0c[4] = {0.f, 0.f, 0.f, 0.f}, s1c[4] = {0.f, 0.f, 0.f, 0.f}, sf[4] = {0.f, 0.f, 0.f, 0.f};
+    float s0c[4] = {0.f, 0.f, 0.f, 0.f}, sf[4] = {0.f, 0.f, 0.f, 0.f};
     stage_load(0);
     stage_store(0);
     stage_load(1);
@@ -753,13 +752,11 @@ __global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ 
                 const half2_t sc0 = {(_Float16)f0, (_Float16)f0}, sc1 = {(_Float16)f1, (_Float16)f1};
                 const half2_t ns0 = {(_Float16)(-1024.0f * f0), (_Float16)(-1024.0f * f0)};
                 const half2_t ns1 = {(_Float16)(-1024.0f * f1), (_Float16)(-1024.0f * f1)};
-                const uint32_t* wr = bw + nl * kMmaWRow + j * 32 + 8 * w + g;  // class 2w dword g
-                const uint32_t* ar = ba + nl * kMmaARow + j * 76 + 16 * w + 2 * g;  // qs[64w + 8g]
+                const uint32_t wq = bw[nl * kMmaWRow + j * 32 + 4 * w + g];             // class w dword g
+                const uint2 aq = *(const uint2*)(ba + nl * kMmaARow + j * 76 + 8 * w + 2 * g);  // qs[32w + 8g]
                 const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
                 const f32x4_t c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    mma_act8(*(const uint2*)ar), mma_weight8(wr[0], sc0, ns0, sc1, ns1), z, 0, 0, 0);
-                const f32x4_t c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    mma_act8(*(const uint2*)(ar + 8)), mma_weight8(wr[4], sc0, ns0, sc1, ns1), z, 0, 0, 0);
+                    mma_act8(aq), mma_weight8(wq, sc0, ns0, sc1, ns1), z, 0, 0, 0);
                 const float dw = h2f(h.x & 0xFFFF);
                 float ad[4];
 #pragma unroll
@@ -768,7 +765,6 @@ __global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ 
                 for (int e = 0; e < 4; ++e) {
                     const float d = dw * ad[e];
                     s0c[e] += d * c0[e];
-                    s1c[e] += d * c1[e];
                 }
                 if (w == 0) {  // the min term: mins g and g + 4 against bs2 of activation row nl
                     const uint32_t mn_lo = h.z & 0x3F3F3F3Fu;
@@ -795,13 +791,12 @@ __global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ 
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int i = (4 * g + e) * 16 + nl;
-        xb[(2 * w) * 256 + i] = s0c[e];
-        xb[(2 * w + 1) * 256 + i] = s1c[e];
+        xb[w * 256 + i] = s0c[e];
         if (w == 0) xb[8 * 256 + i] = sf[e];
     }
     __syncthreads();
     const int mr = tid >> 4, row = row0 + (tid & 15);
-    if (mr < m && row < n) {
+    if (tid < 256 && mr < m && row < n) {
         float tot = -0.0f;
 #pragma unroll
         for (int cl = 0; cl < 8; ++cl) tot += xb[cl * 256 + tid];
@@ -815,7 +810,7 @@ __global__ __launch_bounds__(256) void k_gemv_mma_q4k(const uint4* __restrict__ 
 static hipError_t gemv_mma_launch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                                   const float* res, int64_t ldr, hipStream_t s) {
     const int n = (int)w.n, nb = (int)w.nb;
-    hipLaunchKernelGGL(k_gemv_mma_q4k, dim3((unsigned)((n + kMmaRows - 1) / kMmaRows)), dim3(256), kMmaLds, s,
+    hipLaunchKernelGGL(k_gemv_mma_q4k, dim3((unsigned)((n + kMmaRows - 1) / kMmaRows)), dim3(512), kMmaLds, s,
                        (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, (const uint8_t*)act, m, y, ldy, bias, res, ldr);
     return hipGetLastError();
 }
