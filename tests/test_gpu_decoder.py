@@ -298,21 +298,23 @@ def test_cosyvoice2_lm_step_matches_oracle(cuda, model_oracle, dtype):
     _check(logits.cpu().numpy()[0], orc, orc.step_one(0, frame=tok[0]), f"cv2 {dtype.name} token step")
 
 
-def test_ragged_batch_matches_per_stream_oracle(cuda, model_oracle):
-    cfg = _fish_small(n_layers=1, max_batch=4)
-    lm, W = _build(cfg, cuda, 7, 4)
-    orc = model_oracle.OracleDecoder(cfg, W, 4)
-    lengths = [5, 70, 17, 0]
+# 4 streams: the task-split GEMV; 7 streams: Q4_K projections on the matrix-core GEMV
+@pytest.mark.parametrize("lengths", [[5, 70, 17, 0], [5, 70, 17, 0, 33, 1, 48]])
+def test_ragged_batch_matches_per_stream_oracle(cuda, model_oracle, lengths):
+    B = len(lengths)
+    cfg = _fish_small(n_layers=1, max_batch=B)
+    lm, W = _build(cfg, cuda, 7, B)
+    orc = model_oracle.OracleDecoder(cfg, W, B)
     _prefill(lm, orc, cfg, lengths, seed=8)
     rng = np.random.default_rng(9)
     for step in range(2):
-        fr = _frames(rng, 4, cfg)
+        fr = _frames(rng, B, cfg)
         logits, _ = lm.step(ids=torch.from_numpy(fr))
         got = logits.cpu().numpy()
-        for s in range(4):
+        for s in range(B):
             want = orc.step_one(s, frame=fr[s])
             _check(got[s], orc, want, f"ragged step {step} stream {s} (len {lengths[s] + step})")
-    assert lm.lengths(4) == [L + 2 for L in lengths]
+    assert lm.lengths(B) == [L + 2 for L in lengths]
 
 
 def test_graph_replay_equals_eager_and_feeds_back_argmax(cuda):

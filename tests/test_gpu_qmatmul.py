@@ -167,6 +167,18 @@ def test_bias_on_tall_q4k(cuda, ora):
     _eq_bits(y, (ora.matmul(ora.Q4K, x, blocks) + b[None, :]).astype(np.float32))
 
 
+def test_bias_on_q4k_matrix_core_rows(cuda, ora):
+    # 5..16 rows of Q4_K take the matrix-core GEMV: bias epilogue, ragged n, 9 rows
+    n, k = 1003, 2560
+    w = _weights(n, k, 34)
+    b = (np.random.default_rng(35).standard_normal(n) * 0.02).astype(np.float32)
+    x = _acts(9, k, 36)
+    blocks = ora.quantize(ora.Q4K, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    y = qmm.forward(torch.from_numpy(x).to(cuda), bias=torch.from_numpy(b).to(cuda)).cpu().numpy()
+    _eq_bits(y, (ora.matmul(ora.Q4K, x, blocks) + b[None, :]).astype(np.float32))
+
+
 def test_export_and_dequantize_round_trip(cuda, ora):
     w = _weights(300, 2560, 8)
     blocks = ora.quantize(ora.Q4K, w)
