@@ -632,9 +632,10 @@ static hipError_t gemv_dispatch(const QWeight& w, const void* act, int m, float*
 // operands go through LDS in chunks of four blocks, copied with contiguous 16-byte loads
 // (whole cache lines; each lane's own pieces are 4- to 16-byte scraps of many lines)
 // into row-padded tiles that the lanes then read without bank conflicts: weights
-// 16 rows x 512 B (+16), headers, and activations 16 rows x 4 x 304 B (+16); double-
-// buffered, loaded one chunk ahead, one barrier per chunk (57 KB: two workgroups, 16
-// waves, per CU).  Activation rows past m and weight rows past n use clamped copies and are never
+// 16 rows x 512 B (+16), headers decoded once per (block, lane group, row) into the
+// f16 scale pairs of the W' FMA and d, dmin, mins as floats, and activations
+// 16 rows x 4 x 304 B (+16); double-buffered, loaded one chunk ahead, one barrier per
+// chunk (71 KB: two workgroups, 16 waves, per CU).  Activation rows past m and weight rows past n use clamped copies and are never
 // stored.  MFMA k-slots: lane group g (lane / 16) of a class-l operand holds dword g of
 // the weight's class-l 16 bytes (device layout: byte 16l + 4c + t holds elements
 // 64c + l + 8t and 64c + 32 + l + 8t), as the eight values (t, nibble) = (0,lo) (2,lo)
@@ -644,7 +645,8 @@ constexpr int kMmaRows = 16;
 constexpr int kMmaChunk = 4;                          // blocks per chunk
 constexpr int kMmaWRow = kMmaChunk * 32 + 4;          // dwords per weight row of a chunk (padded)
 constexpr int kMmaARow = kMmaChunk * 76 + 4;          // dwords per activation row of a chunk (padded)
-constexpr int kMmaBuf = 16 * kMmaWRow + 16 * kMmaChunk * 4 + 16 * kMmaARow;  // dwords per chunk buffer
+constexpr int kMmaHdr = kMmaChunk * 4 * 16 * 8;     // decoded headers: [block][g][row] x 2 uint4
+constexpr int kMmaBuf = 16 * kMmaWRow + kMmaHdr + 16 * kMmaARow;  // dwords per chunk buffer
 constexpr size_t kMmaLds = 2 * (size_t)kMmaBuf * 4;
 static_assert(kMmaBuf >= 9 * 256, "the final class sums reuse a chunk buffer");
 static_assert(sizeof(ActQ8K) == 76 * 4, "activation rows are copied as 19 uint4 per block");
@@ -709,8 +711,8 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
     auto stage_load = [&](int c) {  // unconditional loads (clamped)
         const int cc = min(c, nc - 1);
         SXQ_MMA_WQ(0, swq0)
-        {
-            const int r = min(row0 + ((tid >> 2) & 15), n - 1), b = min(cc * kMmaChunk + (tid & 3), nb - 1);
+        {  // header of (row tid & 15, block (tid >> 6) & 3), decoded for g = (tid >> 4) & 3
+            const int r = min(row0 + (tid & 15), n - 1), b = min(cc * kMmaChunk + ((tid >> 6) & 3), nb - 1);
             sh = hdr[(size_t)r * nb + b];
         }
         SXQ_MMA_A(0, sa0) SXQ_MMA_A(1, sa1) SXQ_MMA_A(2, sa2)
@@ -720,8 +722,27 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
     auto stage_store = [&](int c) {
         uint32_t* bw = l32 + (c & 1) * kMmaBuf;
         *(uint4*)(bw + (tid >> 5) * kMmaWRow + (tid & 31) * 4) = swq0;
-        if (tid < 64) *(uint4*)(bw + 16 * kMmaWRow + tid * 4) = sh;
-        uint32_t* ba = bw + 16 * kMmaWRow + 16 * kMmaChunk * 4;
+        if (tid < 256) {  // one decode per (block, g, row) for every wave: scales 2g, 2g + 1 as the
+                          // f16 pairs of the W' FMA, d, dmin, mins g and g + 4
+            const int gg = (tid >> 4) & 3;
+            const uint32_t sc_lo = sh.y & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (sh.w & 0x0F0F0F0Fu) | (((sh.y >> 6) & 0x03030303u) << 4);
+            const uint32_t mn_lo = sh.z & 0x3F3F3F3Fu;
+            const uint32_t mn_hi = ((sh.w >> 4) & 0x0F0F0F0Fu) | (((sh.z >> 6) & 0x03030303u) << 4);
+            const uint32_t scw = (gg < 2 ? sc_lo : sc_hi) >> (16 * (gg & 1));
+            const float f0 = (float)(scw & 0xFF), f1 = (float)((scw >> 8) & 0xFF);
+            const half2_t sc0 = {(_Float16)f0, (_Float16)f0}, sc1 = {(_Float16)f1, (_Float16)f1};
+            const half2_t ns0 = {(_Float16)(-1024.0f * f0), (_Float16)(-1024.0f * f0)};
+            const half2_t ns1 = {(_Float16)(-1024.0f * f1), (_Float16)(-1024.0f * f1)};
+            uint4* hd = (uint4*)(bw + 16 * kMmaWRow);
+            hd[tid] = make_uint4(__builtin_bit_cast(uint32_t, sc0), __builtin_bit_cast(uint32_t, ns0),
+                                 __builtin_bit_cast(uint32_t, sc1), __builtin_bit_cast(uint32_t, ns1));
+            hd[256 + tid] = make_uint4(__builtin_bit_cast(uint32_t, h2f(sh.x & 0xFFFF)),
+                                       __builtin_bit_cast(uint32_t, h2f(sh.x >> 16)),
+                                       __builtin_bit_cast(uint32_t, (float)((mn_lo >> (8 * gg)) & 0xFF)),
+                                       __builtin_bit_cast(uint32_t, (float)((mn_hi >> (8 * gg)) & 0xFF)));
+        }
+        uint32_t* ba = bw + 16 * kMmaWRow + kMmaHdr;
         const uint4 v[3] = {sa0, sa1, sa2};
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
@@ -739,25 +760,20 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
     for (int c = 0; c < nc; ++c) {
         const uint32_t* bw = l32 + (c & 1) * kMmaBuf;
         const uint4* bh = (const uint4*)(bw + 16 * kMmaWRow);
-        const uint32_t* ba = bw + 16 * kMmaWRow + 16 * kMmaChunk * 4;
+        const uint32_t* ba = bw + 16 * kMmaWRow + kMmaHdr;
         const int live = min(kMmaChunk, nb - c * kMmaChunk);
 #pragma unroll
         for (int j = 0; j < kMmaChunk; ++j) {
             if (j < live) {  // uniform
-                const uint4 h = bh[nl * 4 + j];
-                const uint32_t sc_lo = h.y & 0x3F3F3F3Fu;
-                const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | (((h.y >> 6) & 0x03030303u) << 4);
-                const uint32_t scw = (g < 2 ? sc_lo : sc_hi) >> (16 * (g & 1));  // scales 2g, 2g + 1
-                const float f0 = (float)(scw & 0xFF), f1 = (float)((scw >> 8) & 0xFF);
-                const half2_t sc0 = {(_Float16)f0, (_Float16)f0}, sc1 = {(_Float16)f1, (_Float16)f1};
-                const half2_t ns0 = {(_Float16)(-1024.0f * f0), (_Float16)(-1024.0f * f0)};
-                const half2_t ns1 = {(_Float16)(-1024.0f * f1), (_Float16)(-1024.0f * f1)};
+                const uint4 ha = bh[j * 64 + lane], hb = bh[256 + j * 64 + lane];  // decoded header
+                const half2_t sc0 = __builtin_bit_cast(half2_t, ha.x), ns0 = __builtin_bit_cast(half2_t, ha.y);
+                const half2_t sc1 = __builtin_bit_cast(half2_t, ha.z), ns1 = __builtin_bit_cast(half2_t, ha.w);
                 const uint32_t wq = bw[nl * kMmaWRow + j * 32 + 4 * w + g];             // class w dword g
                 const uint2 aq = *(const uint2*)(ba + nl * kMmaARow + j * 76 + 8 * w + 2 * g);  // qs[32w + 8g]
                 const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
                 const f32x4_t c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     mma_act8(aq), mma_weight8(wq, sc0, ns0, sc1, ns1), z, 0, 0, 0);
-                const float dw = h2f(h.x & 0xFFFF);
+                const float dw = __builtin_bit_cast(float, hb.x);
                 float ad[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) ad[e] = __builtin_bit_cast(float, ba[(4 * g + e) * kMmaARow + j * 76 + 64]);
@@ -767,15 +783,12 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
                     s0c[e] += d * c0[e];
                 }
                 if (w == 0) {  // the min term: mins g and g + 4 against bs2 of activation row nl
-                    const uint32_t mn_lo = h.z & 0x3F3F3F3Fu;
-                    const uint32_t mn_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | (((h.z >> 6) & 0x03030303u) << 4);
                     const int* bs = (const int*)(ba + nl * kMmaARow + j * 76 + 68);  // bs2 at byte 272
                     f32x4_t mi = z;
-                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32((float)bs[g], (float)((mn_lo >> (8 * g)) & 0xFF), mi, 0,
-                                                              0, 0);
-                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32((float)bs[g + 4], (float)((mn_hi >> (8 * g)) & 0xFF), mi,
-                                                              0, 0, 0);
-                    const float dminw = h2f(h.x >> 16);
+                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32((float)bs[g], __builtin_bit_cast(float, hb.z), mi, 0, 0, 0);
+                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32((float)bs[g + 4], __builtin_bit_cast(float, hb.w), mi, 0, 0,
+                                                              0);
+                    const float dminw = __builtin_bit_cast(float, hb.y);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) sf[e] -= (dminw * ad[e]) * mi[e];
                 }
@@ -809,6 +822,9 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
 
 static hipError_t gemv_mma_launch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                                   const float* res, int64_t ldr, hipStream_t s) {
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)k_gemv_mma_q4k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMmaLds);
+    if (attr != hipSuccess) return attr;
     const int n = (int)w.n, nb = (int)w.nb;
     hipLaunchKernelGGL(k_gemv_mma_q4k, dim3((unsigned)((n + kMmaRows - 1) / kMmaRows)), dim3(512), kMmaLds, s,
                        (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, (const uint8_t*)act, m, y, ldy, bias, res, ldr);
