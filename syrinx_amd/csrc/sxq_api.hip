@@ -46,7 +46,11 @@ namespace {
 // calls on different streams, or from different threads, take turns on the buffer), grows
 // it stream-ordered when too small, and records the event after its last use.  Allocating
 // per call instead (hipMallocAsync / hipFreeAsync) made every call wait for the previous
-// one's kernels on the host.
+// one's kernels on the host.  On a stream that is being captured into a graph the lease
+// neither waits nor records (an event recorded outside the capture cannot be waited on
+// inside it) and cannot grow the buffer: an eager call of the same or a larger shape
+// must come first, and replays of the graph share the buffer with every other call on
+// the device, so they must not overlap them.
 struct Workspace {
     std::mutex mu;
     void* buf = nullptr;
@@ -60,10 +64,20 @@ struct WorkspaceLease {
     hipStream_t s = nullptr;
     uint8_t* ptr = nullptr;
     hipError_t err = hipSuccess;
+    bool capturing = false;
     WorkspaceLease(int dev, size_t need, hipStream_t st) : s(st) {
         if (dev < 0 || dev >= 64) { err = hipErrorInvalidDevice; return; }
         w = &g_ws[dev];
         w->mu.lock();
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        err = hipStreamIsCapturing(s, &cs);
+        if (err != hipSuccess) return;
+        if (cs != hipStreamCaptureStatusNone) {
+            capturing = true;
+            if (w->size < need) err = hipErrorStreamCaptureUnsupported;  // grow it eagerly first
+            ptr = (uint8_t*)w->buf;
+            return;
+        }
         if (!w->done) err = hipEventCreateWithFlags(&w->done, hipEventDisableTiming);
         if (err == hipSuccess) err = hipStreamWaitEvent(s, w->done, 0);
         if (err == hipSuccess && w->size < need) {
@@ -78,7 +92,7 @@ struct WorkspaceLease {
     }
     ~WorkspaceLease() {
         if (!w) return;
-        if (w->done) (void)hipEventRecord(w->done, s);
+        if (w->done && !capturing) (void)hipEventRecord(w->done, s);
         w->mu.unlock();
     }
     WorkspaceLease(const WorkspaceLease&) = delete;

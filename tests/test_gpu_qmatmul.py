@@ -308,3 +308,28 @@ def test_prefill_gemm_within_f16_rounding_bound(cuda, ora, n, k, m):
         if b is not None:
             want = (want + b[None, :]).astype(np.float32)
         _eq_bits(y_exact, want)
+
+
+def test_forward_captured_in_a_graph(cuda, ora):
+    # QMatMul.forward captured into a HIP graph after one eager call of the same shape (the
+    # workspace cannot grow during capture): GEMV, matrix-core GEMV and the split-K
+    # prefill GEMM, each replayed several times with eager work between the replays
+    cases = [(G.Q4K, 2560, 2560, 1), (G.Q4K, 1003, 2560, 9), (G.Q8_0, 896, 896, 3), (G.Q4K, 2560, 4096, 128)]
+    for dt, n, k, m in cases:
+        w = _weights(n, k, 40 + m)
+        blocks = ora.quantize(ora.Q4K if dt == G.Q4K else ora.Q8_0, w)
+        qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), dt, device=cuda))
+        x = torch.from_numpy(_acts(m, k, 41 + m)).to(cuda)
+        want = qmm.forward(x).cpu().numpy()
+        s = torch.cuda.Stream(device=cuda)
+        s.wait_stream(torch.cuda.current_stream(cuda))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            y = qmm.forward(x)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            _ = torch.zeros(1000, device=cuda).sum().item()  # eager work between replays
+            y.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(y.cpu().numpy(), want, err_msg=f"{dt} m={m} replay {rep}")
