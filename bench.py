@@ -31,6 +31,7 @@ KV lengths drawn uniformly from 256..2048 (the GEMVs run 16 activation rows, att
 and the KV append run per stream), tokens per second over all streams.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtype q4k|q8_0] [--no-cpu] [--no-prefill] [--skinny-batch 16|0]
+       python bench.py --model cv2 --dtype q8_0 --kv 512   (the CosyVoice2 Qwen2-0.5B LM decode step)
        python bench.py --mode gemv [--gemv-iters N]   (GEMV pass only, for counter runs)
        python bench.py --mode copy                     (plain 1 GiB device copy, the counter scale)
        python bench.py --mode prefill                  (the prefill line alone)
@@ -55,6 +56,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--dtype", default="q4k", choices=["q4k", "q8_0"])
+    ap.add_argument("--model", default="fish", choices=["fish", "cv2"],
+                    help="fish: the Qwen3-4B-shaped slow AR (the headline); cv2: the CosyVoice2 Qwen2-0.5B LM "
+                         "(24 layers, dim 896; pass --dtype q8_0 --kv 512 for its configuration)")
     ap.add_argument("--kv", type=int, default=1024)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--gemv-iters", type=int, default=20)
@@ -315,11 +319,15 @@ def main():
 
     dev = torch.device("cuda:0")
     dt = GgmlDType.Q4K if args.dtype == "q4k" else GgmlDType.Q8_0
-    skinny = args.skinny_batch if args.mode == "decode" else 0
+    skinny = args.skinny_batch if args.mode == "decode" and args.model == "fish" else 0
     max_seq = max(args.kv, SKINNY_KV[1] if skinny else 0) + max(args.steps, args.skinny_steps) + args.warmup + 8
-    cfg = D.fish_s2_slow_ar_config(n_layers=36, max_seq=max_seq, max_batch=max(args.batch, skinny), dtype=dt)
     t0 = time.time()
-    lm = D.SlowAr(cfg, device=dev)
+    if args.model == "cv2":
+        cfg = D.cosyvoice2_lm_config(n_layers=24, max_seq=max_seq, max_batch=args.batch, dtype=dt)
+        lm = D.Qwen2Lm(cfg, device=dev)
+    else:
+        cfg = D.fish_s2_slow_ar_config(n_layers=36, max_seq=max_seq, max_batch=max(args.batch, skinny), dtype=dt)
+        lm = D.SlowAr(cfg, device=dev)
     lm.init_random(seed=0, std=0.02)
     lm.kv_fill_random([args.kv] * args.batch, seed=1)
     print(f"[bench] model ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
@@ -327,9 +335,9 @@ def main():
         roof = gemv_roofline(lm, torch, args.gemv_iters)
         print(json.dumps({"mode": "gemv", "passes": 2 * (args.gemv_iters + 2), "roofline": roof}))
         return
-    rng_frame = torch.zeros((args.batch, 1 + cfg.n_codebooks), dtype=torch.int32)
-    rng_frame[:, 0] = 151700
-    rng_frame[:, 1:] = torch.arange(cfg.n_codebooks, dtype=torch.int32) * 37 % 4096
+    rng_frame = torch.zeros((args.batch, lm.ids_per), dtype=torch.int32)
+    rng_frame[:, 0] = 151700 if args.model == "fish" else 100
+    rng_frame[:, 1:] = torch.arange(lm.ids_per - 1, dtype=torch.int32) * 37 % 4096
     lm.step(ids=rng_frame, graph=True)  # captures the graph
     for _ in range(args.warmup):
         lm.step(n=args.batch, graph=True, want_logits=False)
@@ -357,7 +365,7 @@ def main():
     skinny_line = skinny_batch(lm, torch, skinny, args.skinny_steps, args.warmup) if skinny else None
     cpu = None if args.no_cpu else cpu_baseline(lm, torch)
     prefill = None
-    if not args.no_prefill:
+    if not args.no_prefill and args.model == "fish":
         prefill = prefill_gemms(torch, args.prefill_tokens, args.prefill_iters)
         print(f"[bench] prefill: {prefill['us_per_layer']} us/layer, {prefill['achieved']} TFLOP/s", file=sys.stderr,
               flush=True)
@@ -375,11 +383,13 @@ def main():
         "dtype": ("q4k-weight x q8k-activation int dot, f32" if dt == GgmlDType.Q4K
                   else "q8_0-weight x q8_0-activation int dot, f32"),
         "data": "synthetic (random N(0,0.02) weights quantized by from_float; KV N(0,1))",
-        "config": {"workload": f"Fish s2-pro slow AR (Qwen3-4B shape) greedy decode, {args.dtype.upper()} "
-                               f"projections, batch {args.batch}, f32 KV prefilled to {args.kv}, "
-                               f"{args.steps} tokens",
-                   "n_layers": 36, "dim": 2560, "heads": "32/8x128", "intermediate": 9728, "vocab": 155776,
-                   "kv_len": args.kv, "batch": args.batch, "graph": True},
+        "config": {"workload": (f"Fish s2-pro slow AR (Qwen3-4B shape) greedy decode" if args.model == "fish" else
+                                f"CosyVoice2 LM (Qwen2-0.5B shape) greedy decode") +
+                               f", {args.dtype.upper()} projections, batch {args.batch}, f32 KV prefilled to "
+                               f"{args.kv}, {args.steps} tokens",
+                   "n_layers": cfg.n_layers, "dim": cfg.dim,
+                   "heads": f"{cfg.n_heads}/{cfg.n_kv_heads}x{cfg.head_dim}", "intermediate": cfg.intermediate,
+                   "vocab": cfg.vocab, "kv_len": args.kv, "batch": args.batch, "graph": True},
         "roofline": roof,
         "cpu_baseline": cpu,
         "prefill": prefill,
