@@ -165,7 +165,7 @@ def cpu_baseline(lm, torch, budget_s=12.0):
     `budget_s` seconds have passed (at least one)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
-    import oracle  # the checker / CPU baseline
+    import oracle  # the CPU oracle, timed as the CPU baseline
     from syrinx_amd import GgmlDType, QTensor
     c = lm.cfg
     dt = GgmlDType(c.weight_dtype)

@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/sxq_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()`` and by
-``bench.py``'s cpu_baseline leg, as the checker (or the timed CPU baseline).  The
+``bench.py``'s cpu_baseline leg, to check results (or as the timed CPU baseline).  The
 product package ``syrinx_amd`` never imports it.
 
 The C file restates candle-core 0.8's quantized CPU path (third-party, absent from

@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product (syrinx_amd/, include/) links,
  * loads or calls this code.  Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg use it, and only as the checker / the timed CPU baseline.
+ * cpu_baseline leg use it, and only to check results / as the timed CPU baseline.
  *
  * What it restates.  The reference (syrinx) calls the third-party crate
  * `candle-core` 0.8 (crates.io; version requirement "0.8", no Cargo.lock, so the

@@ -16,7 +16,7 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def ora():
-    import oracle  # noqa: WPS433 (test-only import of the checker)
+    import oracle  # noqa: WPS433 (test-only import of the CPU oracle)
 
     oracle.lib()
     return oracle

@@ -51,7 +51,7 @@ def cuda():
 
 @pytest.fixture(scope="module")
 def model_oracle():
-    import model  # oracle/model.py, the checker
+    import model  # oracle/model.py, the CPU oracle of a decode step
     return model
 
 

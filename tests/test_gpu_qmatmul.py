@@ -108,7 +108,7 @@ def test_activation_blocks_bit_exact(cuda, ora, vdt, k):
 
 # ------------------------------------------------------------------ QMatMul forward
 CASES = [
-    (G.Q8_0, 4864, 896, 1),    # BASELINE config 1 (Qwen2-0.5B MLP up-proj)
+    (G.Q8_0, 4864, 896, 1),    # Qwen2-0.5B MLP up-projection, one row
     (G.Q8_0, 896, 4864, 1),    # down-proj
     (G.Q8_0, 128, 896, 3),     # k/v proj, ragged rows
     (G.Q4_0, 896, 896, 2),     # the dtype the reference ships

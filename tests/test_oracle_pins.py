@@ -28,8 +28,9 @@ def test_block_sizes_match_ggml_layout(ora):
     assert [L.ora_block_size(t) for t in (ora.Q4_0, ora.Q8_0, ora.Q4K, ora.Q8K)] == [32, 32, 256, 256]
 
 
-def test_storage_accounting_matches_baseline_figures(ora):
-    # storage_size_in_bytes = N*K/bs*type_size (cv2/load.rs:103); figures from BASELINE.
+def test_storage_accounting_matches_published_figures(ora):
+    # storage_size_in_bytes = N*K/bs*type_size (cv2/load.rs:103): the Qwen2-0.5B up-projection
+    # in Q8_0 and the 36 Qwen3-4B layers in Q4_K
     assert 4864 * ora.row_bytes(ora.Q8_0, 896) == 4_630_528
     layer = (6144 * ora.row_bytes(ora.Q4K, 2560) + 2560 * ora.row_bytes(ora.Q4K, 4096)
              + 2 * 9728 * ora.row_bytes(ora.Q4K, 2560) + 2560 * ora.row_bytes(ora.Q4K, 9728))
