@@ -127,6 +127,8 @@ CASES = [
     (G.Q4K, 19456, 2560, 1),   # Qwen3-4B fused w1|w3
     (G.Q4K, 2560, 9728, 10),   # skinny batch in chunks of four rows: 4 + 4 + 2
     (G.Q8_0, 896, 4864, 7),    # Q8_0 in chunks: 4 + 3
+    (G.Q4K, 7, 256, 12),       # matrix-core GEMV: fewer weight rows than a tile, one block
+    (G.Q4K, 40, 1536, 16),     # matrix-core GEMV: 6 blocks = a full and a partial chunk
 ]
 
 
