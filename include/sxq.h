@@ -13,9 +13,13 @@
  * Threading: every function is safe to call concurrently from several host threads,
  * including sxq_qmm_forward on one handle (the handle is read-only after creation),
  * mirroring the reference's shared `Arc<Qwen2Lm>` use (tests/real_lm_hammer.rs:48-83).
- * sxq_qmm_forward's workspace is one buffer per device kept between calls (grown to the
- * largest call so far, held until the process ends); calls take turns on it through an
- * event, so concurrent calls on one device run one after another on the GPU.
+ * sxq_qmm_forward's workspace is one buffer per device kept between calls (grown to at
+ * least the largest call so far, held until the process ends); calls take turns on it
+ * through an event, so concurrent calls on one device run one after another on the GPU.
+ * A forward on a stream that is being captured into a graph must not use that shared
+ * buffer (a replay could overlap any later eager call): sxq_qmm_forward refuses it, and
+ * the caller passes a workspace of its own to sxq_qmm_forward_ws, which the graph then
+ * keeps alive.
  */
 #ifndef SXQ_H
 #define SXQ_H
@@ -111,6 +115,20 @@ sxq_status sxq_qmm_create(int device, int dtype, int64_t n, int64_t k, const voi
  * f16 MFMA prefill GEMM (error bound at SXQ_BIT_EXACT above). */
 sxq_status sxq_qmm_forward(const sxq_qmm *qmm, const float *x, const int64_t *x_shape, int x_ndim,
                            const int64_t *x_strides, float *y, const float *bias, unsigned flags, void *stream);
+
+/* Device workspace bytes sxq_qmm_forward_ws needs for m rows of x (with `flags` as the
+ * forward will get them).  No reference counterpart: Candle allocates inside forward. */
+sxq_status sxq_qmm_workspace_size(const sxq_qmm *qmm, int64_t m, unsigned flags, size_t *bytes);
+
+/* QMatMul::forward exactly as sxq_qmm_forward (same checks, kernels and bits), on device
+ * pointers, with a caller-provided device workspace (`workspace_bytes` >=
+ * sxq_qmm_workspace_size, 256-byte aligned) instead of the library's shared one: for
+ * code under graph capture (the graph owns the workspace, so replays never alias other
+ * calls) and callers that manage their own memory.  Calls that share one workspace
+ * must not overlap.  flags: SXQ_BIT_EXACT only. */
+sxq_status sxq_qmm_forward_ws(const sxq_qmm *qmm, const float *x, const int64_t *x_shape, int x_ndim,
+                              const int64_t *x_strides, float *y, const float *bias, unsigned flags,
+                              void *workspace, size_t workspace_bytes, void *stream);
 
 /* QTensor::{dtype, shape, storage_size_in_bytes} (storage accounting: load.rs:103). */
 sxq_status sxq_qmm_info(const sxq_qmm *qmm, int *dtype, int64_t *n, int64_t *k, size_t *storage_bytes);
@@ -223,10 +241,15 @@ sxq_status sxq_lm_get_lengths(const sxq_lm *lm, int32_t *lengths, int n_streams)
  *            codes), or NULL to reuse the previous step's argmax (codes kept);
  *   embeds   f32 [n_streams, dim] input embeddings instead of ids (CosyVoice2 passes
  *            embeddings to forward_logits_cached), or NULL;
- *   logits   f32 [n_streams, vocab] output, or NULL;  next_ids int32 [n_streams], or NULL.
+ *   logits   f32 [n_streams, vocab] output, or NULL;
+ *   hidden   f32 [n_streams, dim] output, or NULL: the post-final-RMSNorm hidden state the
+ *            head multiplies (the `hidden` SlowAr::head returns for the fast AR,
+ *            crates/syrinx-fish/src/s2/slow_ar.rs:207-246, consumed at
+ *            crates/syrinx-fish/src/common/dualar.rs:196);
+ *   next_ids int32 [n_streams] greedy argmax of the logits, or NULL.
  * Each stream's token is placed at its current length, which then advances by one. */
 sxq_status sxq_lm_step(sxq_lm *lm, int n_streams, const int32_t *ids, const float *embeds, float *logits,
-                       int32_t *next_ids, unsigned flags, void *stream);
+                       float *hidden, int32_t *next_ids, unsigned flags, void *stream);
 /* Enqueue only the projection GEMVs of one step (every layer's fused QKV, O, gate|up
  * and down, plus the head if with_head) on the step's current activations: the
  * GEMV share of a token, for bandwidth measurement.  No reference counterpart. */

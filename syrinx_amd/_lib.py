@@ -51,6 +51,8 @@ _SIGS = {
     "sxq_act_quantize": (_I, [_I, _I, _P, _I64, _I64, _P, _P]),
     "sxq_qmm_create": (_I, [_I, _I, _I64, _I64, _P, _SZ, _I, _P]),
     "sxq_qmm_forward": (_I, [_P, _P, _P, _I, _P, _P, _P, _U, _P]),
+    "sxq_qmm_workspace_size": (_I, [_P, _I64, _U, _P]),
+    "sxq_qmm_forward_ws": (_I, [_P, _P, _P, _I, _P, _P, _P, _U, _P, _SZ, _P]),
     "sxq_qmm_info": (_I, [_P, _P, _P, _P, _P]),
     "sxq_qmm_dequantize": (_I, [_P, _P, _P]),
     "sxq_qmm_export": (_I, [_P, _P, _P]),
@@ -63,7 +65,7 @@ _SIGS = {
     "sxq_lm_kv_fill_random": (_I, [_P, _P, _I, _U64]),
     "sxq_lm_set_lengths": (_I, [_P, _P, _I]),
     "sxq_lm_get_lengths": (_I, [_P, _P, _I]),
-    "sxq_lm_step": (_I, [_P, _I, _P, _P, _P, _P, _U, _P]),
+    "sxq_lm_step": (_I, [_P, _I, _P, _P, _P, _P, _P, _U, _P]),
     "sxq_lm_read_kv": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "sxq_lm_gemv_pass": (_I, [_P, _I, _I, _P]),
     "sxq_lm_read_state": (_I, [_P, _I, _I, _P, _P]),

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include "../../include/sxq.h"
+#include "sxq_kernels.h"
 
 namespace sxq {
 namespace abi {
@@ -11,6 +12,25 @@ namespace abi {
 sxq_status fail(sxq_status code, const char* fmt, ...);
 // Map a HIP error to SXQ_ERR_OOM / SXQ_ERR_DEVICE with its text.
 sxq_status hip_fail(hipError_t e, const char* what);
+
+inline size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// One QMatMul::forward, checked: m rows of x, which kernel family, workspace bytes.
+struct FwdPlan {
+    int64_t m = 0;
+    bool gemm = false;  // the MFMA prefill GEMM (else quantized activations + GEMV)
+    int vdt = 0;
+    int64_t nbv = 0;    // activation blocks per row
+    size_t ws = 0;      // device workspace: activation blocks, or the GEMM's staging
+};
+// Candle's argument checks of QMatMul::forward (its error texts), then the plan; flags
+// outside `allowed` are rejected.
+sxq_status plan_forward(const sxq_qmm* q, const int64_t* shape, int ndim, const int64_t* strides, unsigned flags,
+                        unsigned allowed, FwdPlan* p);
+// The kernels of one planned forward on device pointers, with `ws` (p.ws bytes, 256-byte
+// aligned) as workspace.  Nothing in `ws` needs to hold anything on entry.
+hipError_t run_forward(const sxq_qmm* q, const FwdPlan& p, const float* x, float* y, const float* bias, uint8_t* ws,
+                       hipStream_t s);
 
 #define HIP_TRY(expr, what)                                      \
     do {                                                         \

@@ -41,16 +41,16 @@ using namespace sxq::abi;
 
 namespace {
 
-// QMatMul::forward's workspace: one buffer per device, kept between calls.  A call holds
-// it from acquire to release: it makes its stream wait for the previous user's event (so
-// calls on different streams, or from different threads, take turns on the buffer), grows
-// it stream-ordered when too small, and records the event after its last use.  Allocating
-// per call instead (hipMallocAsync / hipFreeAsync) made every call wait for the previous
-// one's kernels on the host.  On a stream that is being captured into a graph the lease
-// neither waits nor records (an event recorded outside the capture cannot be waited on
-// inside it) and cannot grow the buffer: an eager call of the same or a larger shape
-// must come first, and replays of the graph share the buffer with every other call on
-// the device, so they must not overlap them.
+// QMatMul::forward's workspace for sxq_qmm_forward: one buffer per device, kept between
+// calls.  A call holds it from acquire to release: it makes its stream wait for the
+// previous user's event (so calls on different streams, or from different threads, take
+// turns on the buffer), grows it stream-ordered when too small, and records the event
+// after its last use.  Allocating per call instead (hipMallocAsync / hipFreeAsync) made
+// every call wait for the previous one's kernels on the host.  Growth at least doubles
+// the size, so a process sees few regrowths.  A stream that is being captured into a
+// graph never touches this buffer: a captured forward gets its workspace from the caller
+// (sxq_qmm_forward_ws), which the graph then owns, so no replay can alias an eager call
+// and no regrowth can free memory a graph still uses.
 struct Workspace {
     std::mutex mu;
     void* buf = nullptr;
@@ -64,24 +64,15 @@ struct WorkspaceLease {
     hipStream_t s = nullptr;
     uint8_t* ptr = nullptr;
     hipError_t err = hipSuccess;
-    bool capturing = false;
     WorkspaceLease(int dev, size_t need, hipStream_t st) : s(st) {
         if (dev < 0 || dev >= 64) { err = hipErrorInvalidDevice; return; }
         w = &g_ws[dev];
         w->mu.lock();
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        err = hipStreamIsCapturing(s, &cs);
-        if (err != hipSuccess) return;
-        if (cs != hipStreamCaptureStatusNone) {
-            capturing = true;
-            if (w->size < need) err = hipErrorStreamCaptureUnsupported;  // grow it eagerly first
-            ptr = (uint8_t*)w->buf;
-            return;
-        }
         if (!w->done) err = hipEventCreateWithFlags(&w->done, hipEventDisableTiming);
         if (err == hipSuccess) err = hipStreamWaitEvent(s, w->done, 0);
         if (err == hipSuccess && w->size < need) {
-            const size_t grow = (need + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+            size_t grow = need > 2 * w->size ? need : 2 * w->size;
+            grow = (grow + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
             if (w->buf) err = hipFreeAsync(w->buf, s);
             w->buf = nullptr;
             w->size = 0;
@@ -92,7 +83,7 @@ struct WorkspaceLease {
     }
     ~WorkspaceLease() {
         if (!w) return;
-        if (w->done && !capturing) (void)hipEventRecord(w->done, s);
+        if (w->done) (void)hipEventRecord(w->done, s);
         w->mu.unlock();
     }
     WorkspaceLease(const WorkspaceLease&) = delete;
@@ -295,11 +286,16 @@ sxq_status sxq_qmm_destroy(sxq_qmm* q) {
     return SXQ_OK;
 }
 
-sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shape, int ndim, const int64_t* strides,
-                           float* y, const float* bias, unsigned flags, void* stream) {
+}  // extern "C"
+
+namespace sxq {
+namespace abi {
+
+sxq_status plan_forward(const sxq_qmm* q, const int64_t* shape, int ndim, const int64_t* strides, unsigned flags,
+                        unsigned allowed, FwdPlan* p) {
     if (!q) return fail(SXQ_ERR_INVALID, "qmm_forward: null handle");
     if (!shape || ndim <= 0) return fail(SXQ_ERR_INVALID, "qmm_forward: missing input shape");
-    if (flags & ~(SXQ_HOST_PTRS | SXQ_BIT_EXACT)) return fail(SXQ_ERR_INVALID, "qmm_forward: unknown flags 0x%x", flags);
+    if (flags & ~allowed) return fail(SXQ_ERR_INVALID, "qmm_forward: unsupported flags 0x%x", flags & ~allowed);
     const std::string ss = shape_str(shape, ndim);
     if (ndim < 2) return fail(SXQ_ERR_SHAPE, "input tensor has only one dimension %s", ss.c_str());
     if (strides) {
@@ -319,59 +315,115 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
         if (shape[i] < 0) return fail(SXQ_ERR_INVALID, "qmm_forward: negative dim in %s", ss.c_str());
         m *= shape[i];
     }
-    if (m == 0) return SXQ_OK;
     if (m > 65535) return fail(SXQ_ERR_INVALID, "qmm_forward: %lld rows exceed the 65535-row limit", (long long)m);
+    p->m = m;
+    p->vdt = vec_dot_type(q->w.dtype);
+    p->nbv = q->w.k / block_size(p->vdt);
+    // Many rows of a Q4_K weight: the f16 MFMA GEMM (operands rounded to f16, error below
+    // 2^-10 * sum |w x| per output) unless SXQ_BIT_EXACT asks for Candle's integer vec-dot.
+    p->gemm = q->w.dtype == kQ4K && m >= kGemmMinRows && !(flags & SXQ_BIT_EXACT);
+    p->ws = m == 0 ? 0
+                   : up256(p->gemm ? gemm_q4k_workspace(q->w.n, (int)m, q->w.k)
+                                   : (size_t)m * (size_t)p->nbv * act_block_bytes(p->vdt));
+    return SXQ_OK;
+}
+
+hipError_t run_forward(const sxq_qmm* q, const FwdPlan& p, const float* x, float* y, const float* bias, uint8_t* ws,
+                       hipStream_t s) {
+    const int64_t k = q->w.k, n = q->w.n, m = p.m;
+    if (p.gemm) {
+        hipError_t e = launch_gemm_q4k_prep(x, k, (int)m, n, (int)k, ws, s);
+        if (e == hipSuccess) e = launch_gemm_q4k(q->w, ws, (int)m, y, n, bias, nullptr, 0, s);
+        return e;
+    }
+    hipError_t e = launch_quantize_act(p.vdt, false, x, k, (int)m, (int)k, ws, s);
+    for (int64_t r0 = 0; r0 < m && e == hipSuccess; r0 += 16) {
+        const int mm = (int)(m - r0 < 16 ? m - r0 : 16);
+        e = launch_gemv(q->w, ws + (size_t)r0 * p.nbv * act_block_bytes(p.vdt), mm, y + r0 * n, n, bias, nullptr, 0, s);
+    }
+    return e;
+}
+
+}  // namespace abi
+}  // namespace sxq
+
+extern "C" {
+
+sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shape, int ndim, const int64_t* strides,
+                           float* y, const float* bias, unsigned flags, void* stream) {
+    FwdPlan p;
+    sxq_status st = plan_forward(q, shape, ndim, strides, flags, SXQ_HOST_PTRS | SXQ_BIT_EXACT, &p);
+    if (st != SXQ_OK) return st;
+    if (p.m == 0) return SXQ_OK;
     if (!x || !y) return fail(SXQ_ERR_INVALID, "qmm_forward: null x or y");
 
     DeviceGuard g(q->device);
     HIP_TRY(g.err, "hipSetDevice");
     hipStream_t s = (hipStream_t)stream;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &cs), "qmm_forward: capture status");
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(SXQ_ERR_INVALID,
+                    "qmm_forward: the stream is being captured into a graph; a captured forward needs its own "
+                    "workspace (sxq_qmm_forward_ws) or the fixed scratch (sxq_qmm_forward_noalloc)");
     const bool host = (flags & SXQ_HOST_PTRS) != 0;
-    const int64_t k = q->w.k, n = q->w.n;
-    const int vdt = vec_dot_type(q->w.dtype);
-    const int64_t nbv = k / block_size(vdt);
-    // Many rows of a Q4_K weight: the f16 MFMA GEMM (operands rounded to f16, error below
-    // 2^-10 * sum |w x| per output) unless SXQ_BIT_EXACT asks for Candle's integer vec-dot.
-    const bool gemm = q->w.dtype == kQ4K && m >= kGemmMinRows && !(flags & SXQ_BIT_EXACT);
-    const size_t act_bytes =
-        gemm ? gemm_q4k_workspace(n, (int)m, k) : (size_t)m * (size_t)nbv * act_block_bytes(vdt);
+    const int64_t k = q->w.k, n = q->w.n, m = p.m;
 
-    // One stream-ordered workspace: [act | x | y | bias] (the last three only for host pointers).
+    // One stream-ordered workspace: [plan | x | y | bias] (the last three only for host pointers).
     const size_t xb = host ? (size_t)(m * k) * 4 : 0, yb = host ? (size_t)(m * n) * 4 : 0;
     const size_t bb = (host && bias) ? (size_t)n * 4 : 0;
-    auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    WorkspaceLease lease(q->device, up(act_bytes) + up(xb) + up(yb) + up(bb), s);
+    WorkspaceLease lease(q->device, p.ws + up256(xb) + up256(yb) + up256(bb), s);
     HIP_TRY(lease.err, "qmm_forward: workspace");
     uint8_t* ws = lease.ptr;
-    void* act = ws;
     const float* dx = x;
     float* dy = y;
     const float* dbias = bias;
     hipError_t e = hipSuccess;
     if (host) {
-        float* hx = (float*)(ws + up(act_bytes));
-        dy = (float*)(ws + up(act_bytes) + up(xb));
+        float* hx = (float*)(ws + p.ws);
+        dy = (float*)(ws + p.ws + up256(xb));
         e = hipMemcpyAsync(hx, x, xb, hipMemcpyHostToDevice, s);
         dx = hx;
         if (e == hipSuccess && bias) {
-            float* hb = (float*)(ws + up(act_bytes) + up(xb) + up(yb));
+            float* hb = (float*)(ws + p.ws + up256(xb) + up256(yb));
             e = hipMemcpyAsync(hb, bias, bb, hipMemcpyHostToDevice, s);
             dbias = hb;
         }
     }
-    if (gemm) {
-        if (e == hipSuccess) e = launch_gemm_q4k_prep(dx, k, (int)m, n, (int)k, act, s);
-        if (e == hipSuccess) e = launch_gemm_q4k(q->w, act, (int)m, dy, n, dbias, nullptr, 0, s);
-    } else if (e == hipSuccess) {
-        e = launch_quantize_act(vdt, false, dx, k, (int)m, (int)k, act, s);
-    }
-    for (int64_t r0 = 0; !gemm && r0 < m && e == hipSuccess; r0 += 16) {
-        const int mm = (int)(m - r0 < 16 ? m - r0 : 16);
-        e = launch_gemv(q->w, (const uint8_t*)act + (size_t)r0 * nbv * act_block_bytes(vdt), mm, dy + r0 * n, n, dbias, nullptr, 0, s);
-    }
+    if (e == hipSuccess) e = run_forward(q, p, dx, dy, dbias, ws, s);
     if (host && e == hipSuccess) e = hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, s);
     if (host && e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "qmm_forward");
+    return SXQ_OK;
+}
+
+sxq_status sxq_qmm_workspace_size(const sxq_qmm* q, int64_t m, unsigned flags, size_t* bytes) {
+    if (!bytes) return fail(SXQ_ERR_INVALID, "qmm_workspace_size: null output");
+    if (!q) return fail(SXQ_ERR_INVALID, "qmm_workspace_size: null handle");
+    if (m < 0) return fail(SXQ_ERR_INVALID, "qmm_workspace_size: negative row count");
+    const int64_t shape[2] = {m, q->w.k};
+    FwdPlan p;
+    sxq_status st = plan_forward(q, shape, 2, nullptr, flags, SXQ_BIT_EXACT, &p);
+    if (st != SXQ_OK) return st;
+    *bytes = p.ws;
+    return SXQ_OK;
+}
+
+sxq_status sxq_qmm_forward_ws(const sxq_qmm* q, const float* x, const int64_t* shape, int ndim,
+                              const int64_t* strides, float* y, const float* bias, unsigned flags, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+    FwdPlan p;
+    sxq_status st = plan_forward(q, shape, ndim, strides, flags, SXQ_BIT_EXACT, &p);
+    if (st != SXQ_OK) return st;
+    if (p.m == 0) return SXQ_OK;
+    if (!x || !y) return fail(SXQ_ERR_INVALID, "qmm_forward_ws: null x or y");
+    if (workspace_bytes < p.ws || !workspace)
+        return fail(SXQ_ERR_INVALID, "qmm_forward_ws: the workspace holds %zu bytes, this call needs %zu",
+                    workspace ? workspace_bytes : (size_t)0, p.ws);
+    if ((uintptr_t)workspace & 255) return fail(SXQ_ERR_INVALID, "qmm_forward_ws: workspace not 256-byte aligned");
+    DeviceGuard g(q->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    HIP_TRY(run_forward(q, p, x, y, bias, (uint8_t*)workspace, (hipStream_t)stream), "qmm_forward_ws");
     return SXQ_OK;
 }
 

@@ -10,7 +10,10 @@
 // the activations are rounded to f16; v_mfma_f32_32x32x16_f16 accumulates in f32.  (f16
 // rather than bf16: the same MFMA rate on gfx950, with 3 more mantissa bits.)  The
 // result therefore differs from Candle's integer Q8_K vec-dot by the f16 rounding of
-// both operands, bounded by 2^-10 * sum_k |w_k x_k| per output.
+// both operands, bounded by 2^-10 * sum_k |w_k x_k| per output (plus the f16 subnormal
+// floor, 2^-25 per operand value).  A row of x with values beyond f16's range is scaled
+// by a power of two 2^-e before the rounding and its results by 2^e after the
+// accumulation (exact), so it stays finite; its subnormal floor becomes 2^(e-25).
 //
 // K order.  Inside each 256-element block the GEMM runs over K in an order chosen so that
 // every lane of the kernel dequantizes whole dwords of the Q4_K device layout
@@ -50,31 +53,63 @@ constexpr int kGemmHalfBytes = 2 * kGemmAStage;  // one K half's region: 2 activ
 int gemm_xh_rows(int m) { return (m + kGemmBM - 1) / kGemmBM * kGemmBM; }
 size_t gemm_q4k_lds() { return 2 * (size_t)kGemmHalfBytes; }
 
+// Rows whose largest magnitude reaches kF16Safe are scaled by a power of two 2^-e before
+// the f16 rounding, so that no value overflows f16 (max 65504); the GEMM multiplies the
+// row's f32 result by 2^e, which is exact.  Rows below it keep e = 0: the scale is 1 and
+// the bits are those of the unscaled product.
+constexpr float kF16Safe = 32768.0f;
+
 // x f32 [m][k] (row stride ldx) -> xh f16 [gemm_xh_rows(m)][k] in the GEMM K order,
-// xh[r][256b + p] = f16(x[r][256b + q4k_perm_elem(p)]), rows past m zero.  One wave per
-// (row, 256-element block): it reads the block as 64 float4s (one contiguous 1 KB read),
-// passes it through LDS, and lane l < 32 writes positions 8l .. 8l+7 (one MFMA operand
-// chunk; one contiguous 512-byte write per wave); position 8l + j is element
-// q4k_perm_elem(8l) + 32 (j & 1) + 8 (j >> 1).
+// xh[r][256b + p] = f16(x[r][256b + q4k_perm_elem(p)] * 2^-e_r), rows past m zero, and
+// rs[r] = 2^e_r.  One workgroup per row: first the row's max |x| (e_r = 0 below
+// kF16Safe), then wave w converts blocks w, w + 4, ...: it reads a block as 64 float4s
+// (one contiguous 1 KB read, an L2 hit after the first pass), passes it through LDS, and
+// lane l < 32 writes positions 8l .. 8l+7 (one MFMA operand chunk; one contiguous
+// 512-byte write per wave); position 8l + j is element q4k_perm_elem(8l) + 32 (j & 1) +
+// 8 (j >> 1).
 __global__ __launch_bounds__(256) void k_x_to_f16_perm(const float* __restrict__ x, int64_t ldx, int m, int k,
-                                                       int rows, _Float16* __restrict__ xh) {
+                                                       _Float16* __restrict__ xh, float* __restrict__ rs) {
     __shared__ float4 blk[4][64];
+    __shared__ float wmax[4];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nb = k >> 8;
-    const int64_t u = (int64_t)blockIdx.x * 4 + wave;  // unit: row * nb + block
-    const bool live = u < (int64_t)rows * nb;
-    const int64_t r = live ? u / nb : 0;
-    const int b = live ? (int)(u - r * nb) : 0;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (live && r < m) v = ((const float4*)(x + r * ldx + 256 * b))[lane];
-    blk[wave][lane] = v;
-    __syncthreads();
-    if (!live || lane >= 32) return;
-    const float* e = (const float*)blk[wave] + q4k_perm_elem(8 * lane);
-    half8 h;
+    const int64_t r = blockIdx.x;
+    const bool live = r < m;
+    const float4* xr = (const float4*)(x + r * ldx);
+    float amax = 0.0f;
+    if (live)
+        for (int i = threadIdx.x; i < (k >> 2); i += 256) {
+            const float4 v = xr[i];
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) h[j] = (_Float16)e[32 * (j & 1) + 8 * (j >> 1)];
-    *(half8*)(xh + r * k + 256 * b + 8 * lane) = h;
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if (lane == 0) wmax[wave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int e = 0;
+    if (amax >= kF16Safe && amax <= 3.0e38f) {  // inf / NaN rows stay unscaled (they propagate either way)
+        int ex = 0;
+        (void)frexpf(amax, &ex);                // amax < 2^ex
+        e = ex - 15;                             // amax * 2^-e < 2^15
+    }
+    const float sc = ldexpf(1.0f, -e);
+    if (threadIdx.x == 0) rs[r] = ldexpf(1.0f, e);
+    for (int b0 = 0; b0 < nb; b0 += 4) {  // uniform trip count: every wave reaches each barrier
+        const int b = b0 + wave;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (live && b < nb) v = xr[64 * b + lane];
+        blk[wave][lane] = v;
+        __syncthreads();
+        if (b < nb && lane < 32) {
+            const float* el = (const float*)blk[wave] + q4k_perm_elem(8 * lane);
+            half8 h;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) h[j] = (_Float16)(el[32 * (j & 1) + 8 * (j >> 1)] * sc);
+            *(half8*)(xh + r * k + 256 * b + 8 * lane) = h;
+        }
+        __syncthreads();
+    }
 }
 
 // The 8 (scale, min) pairs of a Q4_K block header (get_scale_min_k4), times d and dmin:
@@ -186,8 +221,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ xh, int M, int K,
                                                   const uint4* __restrict__ hdr, const uint4* __restrict__ qs, int N,
                                                   float* __restrict__ y, int64_t ldy, const float* __restrict__ bias,
-                                                  const float* res, int64_t ldr, float* part, int tiles_m,
-                                                  int full, int splits) {
+                                                  const float* res, int64_t ldr, const float* __restrict__ rs,
+                                                  float* part, int tiles_m, int full, int splits) {
     extern __shared__ uint4 lds[];
     const int nb = K >> 8;
     // Workgroups 0 .. full-1 take whole tiles; the rest split the remaining tiles' K range
@@ -369,9 +404,9 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
         return;
     }
 
-    // D layout: acc[i] = D[8*(i/4) + 4*(lane/32) + i%4][lane%32].  Loads (bias, then the
-    // residual 16 values at a time) come before the stores they feed, so no store has to
-    // complete before the next one is issued.
+    // D layout: acc[i] = D[8*(i/4) + 4*(lane/32) + i%4][lane%32].  Loads (bias, the row
+    // scales, then the residual 16 values at a time) come before the stores they feed, so
+    // no store has to complete before the next one is issued.  y = acc * 2^e_row (+ bias).
     const int col = n0 + 32 * wv + ln;
     if (col >= N) return;
     const float bv = bias ? bias[col] : 0.0f;
@@ -383,7 +418,15 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
             const int row0 = m0 + 32 * mt + 4 * lh;
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = bias ? acc[mt][i] + bv : acc[mt][i];
+            for (int q = 0; q < 4; ++q) {  // rows row0 + 8q .. +3 (rs covers the padded rows)
+                const float4 sc = *(const float4*)(rs + row0 + 8 * q);
+                const float scs[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float a = acc[mt][4 * q + e] * scs[e];
+                    v[4 * q + e] = bias ? a + bv : a;
+                }
+            }
             if (res) {
                 float r[16];
                 const float* rp = res + (int64_t)row0 * ldr + col;
@@ -410,12 +453,12 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
 // Second pass for split tiles: one thread per float4 slot (row tile mt, float4 j, slot
 // ts) of a split tile adds the tile's S partials in split order -- the result does not
 // depend on which split finished first -- and writes y like the whole-tile store:
-// (sum + bias), then res + that.  Slot ts = 64 wv + lane holds D[32 mt + 8 j + 4 (lane/32)
+// (sum * 2^e_row + bias), then res + that.  Slot ts = 64 wv + lane holds D[32 mt + 8 j + 4 (lane/32)
 // + e][32 wv + lane % 32], e = 0..3, of the tile (the MFMA D layout above).
 __global__ __launch_bounds__(256) void k_gemm_splitk_sum(const float* __restrict__ part, int S, int full,
                                                          int tiles_m, int M, int N, float* y, int64_t ldy,
                                                          const float* __restrict__ bias, const float* res, int64_t ldr,
-                                                         int nslots) {
+                                                         const float* __restrict__ rs, int nslots) {
     const int g = blockIdx.x * 256 + threadIdx.x;
     if (g >= nslots) return;
     const int st = g >> 13, q = g & 8191;
@@ -438,7 +481,8 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_sum(const float* __restrict
     for (int i = 0; i < 4; ++i) {
         const int row = row0 + i;
         if (row >= M) break;
-        float v = bias ? e[i] + bv : e[i];
+        const float a = e[i] * rs[row];
+        float v = bias ? a + bv : a;
         if (res) v = res[(int64_t)row * ldr + col] + v;
         y[(int64_t)row * ldy + col] = v;
     }
@@ -449,7 +493,7 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_sum(const float* __restrict
 // the last round still occupies (nearly) every unit.
 struct GemmPlan {
     int tiles_n = 0, tiles_m = 0, tiles = 0, full = 0, splits = 1, grid = 0;
-    size_t xh_bytes = 0, part_bytes = 0;
+    size_t xh_bytes = 0, rs_bytes = 0, part_bytes = 0;
 };
 
 static int device_cus() {
@@ -482,6 +526,7 @@ static GemmPlan gemm_plan(int64_t n, int m, int64_t k) {
     if (p.splits == 1) p.full = p.tiles;
     p.grid = p.full + (p.tiles - p.full) * p.splits;
     p.xh_bytes = ((size_t)gemm_xh_rows(m) * (size_t)k * 2 + 255) & ~(size_t)255;
+    p.rs_bytes = ((size_t)gemm_xh_rows(m) * 4 + 255) & ~(size_t)255;
     const size_t split_tiles = (size_t)(p.tiles - p.full);
     p.part_bytes = split_tiles * p.splits * 128 * 256 * 4;
     return p;
@@ -491,15 +536,14 @@ int gemm_q4k_splits(int64_t n, int m, int64_t k) { return gemm_plan(n, m, k).spl
 
 size_t gemm_q4k_workspace(int64_t n, int m, int64_t k) {
     const GemmPlan p = gemm_plan(n, m, k);
-    return p.xh_bytes + p.part_bytes;
+    return p.xh_bytes + p.rs_bytes + p.part_bytes;
 }
 
 hipError_t launch_gemm_q4k_prep(const float* x, int64_t ldx, int m, int64_t n, int k, void* ws, hipStream_t s) {
     const GemmPlan p = gemm_plan(n, m, k);
     const int rows = gemm_xh_rows(m);
-    const int64_t units = (int64_t)rows * (k / 256);  // one wave each, four per workgroup
-    hipLaunchKernelGGL(k_x_to_f16_perm, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, s, x, ldx, m, k, rows,
-                       (_Float16*)ws);
+    hipLaunchKernelGGL(k_x_to_f16_perm, dim3((unsigned)rows), dim3(256), 0, s, x, ldx, m, k, (_Float16*)ws,
+                       (float*)((uint8_t*)ws + p.xh_bytes));
     return hipGetLastError();
 }
 
@@ -510,15 +554,16 @@ hipError_t launch_gemm_q4k(const QWeight& w, const void* ws, int m, float* y, in
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_q4k_lds());
     if (attr != hipSuccess) return attr;
     const GemmPlan p = gemm_plan(w.n, m, w.k);
-    float* part = (float*)((uint8_t*)ws + p.xh_bytes);
+    const float* rs = (const float*)((const uint8_t*)ws + p.xh_bytes);
+    float* part = (float*)((uint8_t*)ws + p.xh_bytes + p.rs_bytes);
     hipLaunchKernelGGL(k_gemm_q4k, dim3((unsigned)p.grid), dim3(512), gemm_q4k_lds(), s, (const _Float16*)ws, m,
-                       (int)w.k, (const uint4*)w.hdr, (const uint4*)w.qs, (int)w.n, y, ldy, bias, res, ldr, part,
+                       (int)w.k, (const uint4*)w.hdr, (const uint4*)w.qs, (int)w.n, y, ldy, bias, res, ldr, rs, part,
                        p.tiles_m, p.full, p.splits);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.full == p.tiles) return e;
     const int nslots = (p.tiles - p.full) * 8192;
     hipLaunchKernelGGL(k_gemm_splitk_sum, dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, s, (const float*)part,
-                       p.splits, p.full, p.tiles_m, m, (int)w.n, y, ldy, bias, res, ldr, nslots);
+                       p.splits, p.full, p.tiles_m, m, (int)w.n, y, ldy, bias, res, ldr, rs, nslots);
     return hipGetLastError();
 }
 

@@ -35,10 +35,12 @@ struct LmLayer {
     float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *bqkv = nullptr;
 };
 
+// A captured step is specific to its stream count, its input (ids or embeddings) and the
+// trace buffer it records into (a graph keeps the pointer it was captured with).
 struct GraphKey {
     int n;
     bool embeds;
-    bool trace;
+    const float* trace;
     bool operator<(const GraphKey& o) const {
         if (n != o.n) return n < o.n;
         if (embeds != o.embeds) return embeds < o.embeds;
@@ -62,6 +64,7 @@ struct sxq_lm {
     int* d_len = nullptr;
     std::vector<int> h_len;
     float *h = nullptr, *qkv = nullptr, *qbuf = nullptr, *part = nullptr, *gu = nullptr, *logits = nullptr;
+    float* hn = nullptr;  // post-final-RMSNorm hidden of the step [max_batch][dim] (SlowAr::head's `hidden`)
     uint8_t *act_a = nullptr, *act_o = nullptr, *act_d = nullptr;
     int *d_ids = nullptr, *d_next = nullptr;
     float* am_val = nullptr;        // argmax partials [max_batch * kArgmaxSlices]
@@ -221,8 +224,9 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
         }
         if (tr) STEP(record(lm->h, nd));
     }
-    STEP(launch_gemv_rmsnorm(lm->head.w, norm_in(lm->h, lm->final_norm, tr ? slot(nd) : nullptr), n, lm->act_a,
-                             lm->logits, c.vocab, c.head_bias ? lm->head_bias : nullptr, nullptr, 0, s));
+    STEP(launch_gemv_rmsnorm(lm->head.w, norm_in(lm->h, lm->final_norm, lm->hn), n, lm->act_a, lm->logits, c.vocab,
+                             c.head_bias ? lm->head_bias : nullptr, nullptr, 0, s));
+    if (tr) STEP(record(lm->hn, nd));
     STEP(launch_argmax(lm->logits, n, c.vocab, lm->d_ids, lm->ids_per, lm->d_next, lm->d_len, lm->am_val, lm->am_idx,
                        lm->am_count, s));
 #undef STEP
@@ -310,6 +314,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->vc, sizeof(float) * (size_t)lm->kv_layer_stride * c.n_layers);
     A((void**)&lm->d_len, sizeof(int) * MB);
     A((void**)&lm->h, sizeof(float) * (size_t)MB * c.dim);
+    A((void**)&lm->hn, sizeof(float) * (size_t)MB * c.dim);
     A((void**)&lm->qkv, sizeof(float) * (size_t)MB * lm->qkv_n);
     A((void**)&lm->qbuf, sizeof(float) * (size_t)MB * lm->ctx);
     A((void**)&lm->part, sizeof(float) * (size_t)MB * c.n_heads * lm->max_splits * (hd + 4));
@@ -541,8 +546,8 @@ sxq_status sxq_lm_kv_fill_random(sxq_lm* lm, const int32_t* lengths, int n, uint
     return lengths ? sxq_lm_set_lengths(lm, lengths, n) : SXQ_OK;
 }
 
-sxq_status sxq_lm_step(sxq_lm* lm, int n, const int32_t* ids, const float* embeds, float* logits, int32_t* next_ids,
-                       unsigned flags, void* stream) {
+sxq_status sxq_lm_step(sxq_lm* lm, int n, const int32_t* ids, const float* embeds, float* logits, float* hidden,
+                       int32_t* next_ids, unsigned flags, void* stream) {
     if (!lm) return fail(SXQ_ERR_INVALID, "lm_step: null handle");
     if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_step: %d streams (max %d)", n, lm->c.max_batch);
     if (flags & ~SXQ_LM_GRAPH) return fail(SXQ_ERR_INVALID, "lm_step: unknown flags 0x%x", flags);
@@ -557,7 +562,7 @@ sxq_status sxq_lm_step(sxq_lm* lm, int n, const int32_t* ids, const float* embed
     if (ids) HIP_TRY(hipMemcpyAsync(lm->d_ids, ids, sizeof(int) * n * lm->ids_per, hipMemcpyDeviceToDevice, st), "lm_step: ids");
     if (emb) HIP_TRY(hipMemcpyAsync(lm->h, embeds, sizeof(float) * n * lm->c.dim, hipMemcpyDeviceToDevice, st), "lm_step: embeds");
     if (flags & SXQ_LM_GRAPH) {
-        const GraphKey key{n, emb, lm->trace != nullptr};
+        const GraphKey key{n, emb, lm->trace};
         auto it = lm->graphs.find(key);
         if (it == lm->graphs.end()) {
             // Capture on the library's own stream (the legacy default stream cannot capture).
@@ -580,6 +585,8 @@ sxq_status sxq_lm_step(sxq_lm* lm, int n, const int32_t* ids, const float* embed
     for (int s = 0; s < n; ++s) lm->h_len[s] += 1;
     if (logits)
         HIP_TRY(hipMemcpyAsync(logits, lm->logits, sizeof(float) * n * lm->c.vocab, hipMemcpyDeviceToDevice, st), "lm_step: logits");
+    if (hidden)
+        HIP_TRY(hipMemcpyAsync(hidden, lm->hn, sizeof(float) * n * lm->c.dim, hipMemcpyDeviceToDevice, st), "lm_step: hidden");
     if (next_ids) HIP_TRY(hipMemcpyAsync(next_ids, lm->d_next, sizeof(int) * n, hipMemcpyDeviceToDevice, st), "lm_step: next ids");
     return SXQ_OK;
 }

@@ -13,9 +13,14 @@ namespace sxq {
 // rather than a possibly stale L2 -- and the protocol is:
 //   writers:  store_agent(data...); publish_and_count() -> true in the last arriver
 //   last:     load_agent(data...)
-// publish_and_count waits until this thread's stores have completed (s_waitcnt 0),
-// joins the workgroup (so every thread's stores have), then thread 0 bumps the counter;
-// the last arriver only issues its loads after the counter returned.
+// publish_and_count waits until this thread's stores have completed (vmcnt 0, as an asm
+// statement with a memory clobber, so the compiler can neither sink a store below it nor
+// hoist a later access above it), joins the workgroup (so every thread's stores have),
+// then thread 0 bumps the counter; the last arriver only issues its loads after the
+// counter returned.  What this relies on beyond the HIP memory model: agent-scope
+// relaxed accesses reach the device-coherent level in program order once their vmcnt
+// wait has passed, and the last arriver's loads, which depend on the counter's value
+// through control flow and the memory clobbers, are not issued before it returns.
 SXQ_DEV void store_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 SXQ_DEV void store_agent(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 SXQ_DEV float load_agent(const float* p) {
@@ -25,7 +30,7 @@ SXQ_DEV int load_agent(const int* p) { return __hip_atomic_load(const_cast<int*>
 // Every thread of the workgroup calls it; `flag` is a workgroup-shared bool.  `total` =
 // number of workgroups that count on this counter.
 SXQ_DEV bool publish_and_count(unsigned* counter, unsigned total, bool* flag) {
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores are complete
     __syncthreads();                // ... and so are everyone else's in the workgroup
     if (threadIdx.x == 0)
         *flag = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;

@@ -157,9 +157,10 @@ class DecoderLM:
 
     # -- step ---------------------------------------------------------------------------
     def step(self, ids: torch.Tensor = None, embeds: torch.Tensor = None, n: int = None, graph: bool = False,
-             want_logits: bool = True):
+             want_logits: bool = True, want_hidden: bool = False):
         """One token for n streams.  ids int32 [n, 1 + n_codebooks] (or [n]) or embeds
-        f32 [n, dim]; None for both reuses the previous argmax.  Returns (logits, next_ids)."""
+        f32 [n, dim]; None for both reuses the previous argmax.  Returns (logits, next_ids),
+        or (logits, next_ids, hidden) with want_hidden (the post-final-RMSNorm state)."""
         if ids is not None:
             ids = ids.to(device=self.device, dtype=torch.int32).reshape(-1, self.ids_per).contiguous()
             n = ids.shape[0]
@@ -170,10 +171,11 @@ class DecoderLM:
             raise ValueError("step: give ids, embeds or n")
         logits = torch.empty((n, self.cfg.vocab), dtype=torch.float32, device=self.device) if want_logits else None
         nxt = torch.empty((n,), dtype=torch.int32, device=self.device)
+        hidden = torch.empty((n, self.cfg.dim), dtype=torch.float32, device=self.device) if want_hidden else None
         P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
-        check(lib().sxq_lm_step(self._h, n, P(ids), P(embeds), P(logits), P(nxt), LM_GRAPH if graph else 0,
+        check(lib().sxq_lm_step(self._h, n, P(ids), P(embeds), P(logits), P(hidden), P(nxt), LM_GRAPH if graph else 0,
                                 torch.cuda.current_stream(self.device).cuda_stream))
-        return logits, nxt
+        return (logits, nxt, hidden) if want_hidden else (logits, nxt)
 
     TRACE_SEGMENTS = ("hn_attn", "qkv", "q", "ctx", "h_mid", "hn_ffn", "gu", "act", "h_out")
 
@@ -236,16 +238,26 @@ class SlowAr(DecoderLM):
 
     def slow_step(self, frame, pos: int = None, graph: bool = True):
         """frame: [1 + num_codebooks] ids of the previous frame; pos must equal the cache
-        length (slow_ar.rs:259-271).  Returns (semantic_logits [vocab], next argmax id)."""
+        length (slow_ar.rs:259-271).  Returns (semantic_logits [vocab], hidden [1, 1, dim]),
+        as SlowAr::slow_step does; the greedy argmax of the logits is kept on the device
+        and read with last_argmax()."""
         if pos is not None and pos != self.lengths(1)[0]:
             raise ValueError(f"slow_step pos {pos} must equal the current cache length {self.lengths(1)[0]}")
         ids = torch.as_tensor(frame, dtype=torch.int32).reshape(1, -1)
-        logits, nxt = self.step(ids=ids, graph=graph)
-        return logits[0], nxt[0]
+        logits, nxt, hidden = self.step(ids=ids, graph=graph, want_hidden=True)
+        self._last_argmax = nxt
+        return logits[0], hidden.reshape(1, 1, -1)
 
     def slow_step_batch(self, frames, graph: bool = True):
-        """frames: [n, 1 + num_codebooks]; ragged cache lengths need no left padding."""
-        return self.step(ids=torch.as_tensor(frames, dtype=torch.int32), graph=graph)
+        """frames: [n, 1 + num_codebooks]; ragged cache lengths need no left padding
+        (slow_ar.rs:456-499).  Returns (semantic_logits [n, vocab], hidden [n, 1, dim])."""
+        logits, nxt, hidden = self.step(ids=torch.as_tensor(frames, dtype=torch.int32), graph=graph, want_hidden=True)
+        self._last_argmax = nxt
+        return logits, hidden.reshape(hidden.shape[0], 1, -1)
+
+    def last_argmax(self) -> torch.Tensor:
+        """Greedy argmax ids [n] of the last step's logits (device int32)."""
+        return self._last_argmax
 
 
 class Qwen2Lm(DecoderLM):

@@ -161,6 +161,7 @@ class QMatMul:
         self._shape = None
         self._dtype = None
         self._device = None
+        self._graph_ws = []  # workspaces of captured forwards, alive as long as this QMatMul
 
     @staticmethod
     def from_qtensor(qt: QTensor) -> "QMatMul":
@@ -241,9 +242,21 @@ class QMatMul:
             bias = bias.to(device=xs.device, dtype=torch.float32).contiguous()
             if bias.numel() != n:
                 raise SxqError(4, f"bias of {bias.numel()} elements for {n} outputs")
-        check(lib().sxq_qmm_forward(self._h, _ptr(xs), shape, xs.dim(), strides, _ptr(y),
-                                    _ptr(bias) if bias is not None else None, BIT_EXACT if exact else 0,
-                                    _stream_ptr(xs.device)))
+        flags = BIT_EXACT if exact else 0
+        bptr = _ptr(bias) if bias is not None else None
+        if torch.cuda.is_current_stream_capturing():
+            # Under graph capture the forward takes a workspace of its own from torch's
+            # graph memory pool, which the graph keeps: replays never share the library's
+            # eager workspace with other calls.
+            need = ctypes.c_size_t()
+            check(lib().sxq_qmm_workspace_size(self._h, xs.numel() // k, flags, ctypes.byref(need)))
+            ws = torch.empty(max(int(need.value), 1), dtype=torch.uint8, device=xs.device)
+            check(lib().sxq_qmm_forward_ws(self._h, _ptr(xs), shape, xs.dim(), strides, _ptr(y), bptr, flags,
+                                           _ptr(ws), ws.numel(), _stream_ptr(xs.device)))
+            self._graph_ws.append(ws)
+        else:
+            check(lib().sxq_qmm_forward(self._h, _ptr(xs), shape, xs.dim(), strides, _ptr(y), bptr, flags,
+                                        _stream_ptr(xs.device)))
         return y
 
     __call__ = forward

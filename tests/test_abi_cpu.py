@@ -59,6 +59,16 @@ def test_forward_argument_checks_need_no_gpu():
     assert L.sxq_act_quantize(0, 12, None, 1, 256, None, None) == _lib.ERR_DTYPE
 
 
+def test_workspace_entry_points_check_arguments_without_a_gpu():
+    L = _lib.lib()
+    shape = (ctypes.c_int64 * 2)(1, 896)
+    sz = ctypes.c_size_t(123)
+    assert L.sxq_qmm_workspace_size(None, 1, 0, ctypes.byref(sz)) == _lib.ERR_INVALID
+    assert L.sxq_qmm_workspace_size(None, 1, 0, None) == _lib.ERR_INVALID
+    assert L.sxq_qmm_forward_ws(None, None, shape, 2, None, None, None, 0, None, 0, None) == _lib.ERR_INVALID
+    assert "null handle" in L.sxq_last_error().decode()
+
+
 def test_python_mirror_rejects_misaligned_quantize():
     import torch
     with pytest.raises(syrinx_amd.SxqError) as e:

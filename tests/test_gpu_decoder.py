@@ -28,16 +28,30 @@ pytestmark = pytest.mark.gpu
 GLUE_RTOL = 4e-6        # |gpu - oracle| <= GLUE_RTOL * (|oracle| + max |oracle|) for f32 glue ops
 LOGIT_RTOL = 1e-5       # max |gpu - oracle| / max |oracle| of a step's logits, no Q8 flip
 LOGIT_RTOL_FLIP = 5e-2  # the same bound for any step (one activation one Q8 step apart)
-TIGHT_FRACTION = 0.6    # share of steps that must meet LOGIT_RTOL
+TIGHT_FRACTION = 0.6    # share of a test's steps that must meet LOGIT_RTOL (one flip always allowed)
 KV_ATOL = 2e-5          # post-RoPE key rows (unit-RMS values), absolute
 
-_regimes = {"tight": 0, "flip": 0}
+class _Tally:
+    """Steps of one test in the tight (no Q8 flip) and flip regimes; each test checks its
+    own tally, so the check does not depend on which tests ran before."""
+
+    def __init__(self):
+        self.tight = 0
+        self.flip = 0
+
+    def mostly_tight(self):
+        n = self.tight + self.flip
+        assert n > 0 and self.flip <= max(1, int((1.0 - TIGHT_FRACTION) * n)), (self.tight, self.flip)
 
 
-def _check(got, orc, want, what):
+def _check(got, orc, want, what, tally=None):
     err = _rel(got, want)
     tight = err <= LOGIT_RTOL
-    _regimes["tight" if tight else "flip"] += 1
+    if tally is not None:
+        if tight:
+            tally.tight += 1
+        else:
+            tally.flip += 1
     print(f"{what}: rel err {err:.2e} (smallest quantization margin {orc.margin:.1e})")
     assert err <= LOGIT_RTOL_FLIP, (what, err, orc.margin)
 
@@ -86,6 +100,65 @@ def _build(cfg, cuda, seed, n_streams):
             vec(nkv * hd, ("bk", l), D.BK, l, 0.0, 0.02)
             vec(nkv * hd, ("bv", l), D.BV, l, 0.0, 0.02)
             W[("bqkv", l)] = np.concatenate([W.pop(("bq", l)), W.pop(("bk", l)), W.pop(("bv", l))])
+        else:
+            lin(qkv_n, cfg.dim, ("wqkv", l), D.WQKV, l)
+        lin(cfg.dim, nh * hd, ("wo", l), D.WO, l)
+        lin(cfg.intermediate, cfg.dim, ("w1", l), D.W1, l)
+        lin(cfg.intermediate, cfg.dim, ("w3", l), D.W3, l)
+        lin(cfg.dim, cfg.intermediate, ("w2", l), D.W2, l)
+        vec(cfg.dim, ("attn_norm", l), D.ATTN_NORM, l, 1.0, 0.1)
+        vec(cfg.dim, ("ffn_norm", l), D.FFN_NORM, l, 1.0, 0.1)
+        if cfg.qk_norm:
+            vec(hd, ("q_norm", l), D.Q_NORM, l, 1.0, 0.1)
+            vec(hd, ("k_norm", l), D.K_NORM, l, 1.0, 0.1)
+    lin(cfg.vocab, cfg.dim, "head", D.HEAD, -1)
+    vec(cfg.dim, "final_norm", D.FINAL_NORM, -1, 1.0, 0.1)
+    if cfg.head_bias:
+        vec(cfg.vocab, "head_bias", D.HEAD_BIAS, -1, 0.0, 0.02)
+    if not cfg.tied_embedding:
+        rows = cfg.embed_rows or cfg.vocab
+        vec(rows * cfg.dim, "embed", D.EMBED, -1, 0.0, 0.5)
+        W["embed"] = W["embed"].reshape(rows, cfg.dim)
+    if cfg.n_codebooks:
+        vec(cfg.n_codebooks * cfg.codebook_size * cfg.dim, "codebook", D.CODEBOOK_EMBED, -1, 0.0, 0.5)
+        W["codebook"] = W["codebook"].reshape(-1, cfg.dim)
+    return lm, W
+
+
+def _build_dev(cfg, cuda, seed):
+    """Like _build, with the projection weights drawn on the GPU (full-size models):
+    N(0, 0.02) from a seeded torch generator, quantized by QTensor.quantize, the same
+    canonical blocks handed to the engine and to the oracle."""
+    dt = GgmlDType(cfg.weight_dtype)
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=cuda).manual_seed(seed)
+    lm = D.DecoderLM(cfg, device=cuda)
+    W = {}
+    hd, nh, nkv = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    qkv_n = (nh + 2 * nkv) * hd
+
+    def lin(n, k, key, slot, layer):
+        w = torch.randn(n, k, device=cuda, generator=gen) * 0.02
+        qt = QTensor.quantize(w, dt)
+        del w
+        lm.set_linear(layer, slot, QMatMul.from_qtensor(qt))
+        W[key] = qt.data().cpu().numpy().reshape(n, -1)
+
+    def vec(n, key, slot, layer, mean, std):
+        v = (mean + rng.standard_normal(n) * std).astype(np.float32)
+        lm.set_vector(layer, slot, torch.from_numpy(v))
+        W[key] = v
+
+    for l in range(cfg.n_layers):
+        if cfg.qkv_bias:
+            lin(nh * hd, cfg.dim, ("wq", l), D.WQ, l)
+            lin(nkv * hd, cfg.dim, ("wk", l), D.WK, l)
+            lin(nkv * hd, cfg.dim, ("wv", l), D.WV, l)
+            W[("wqkv", l)] = np.concatenate([W.pop(("wq", l)), W.pop(("wk", l)), W.pop(("wv", l))])
+            b = [(rng.standard_normal(r) * 0.02).astype(np.float32) for r in (nh * hd, nkv * hd, nkv * hd)]
+            for slot, v in zip((D.BQ, D.BK, D.BV), b):
+                lm.set_vector(l, slot, torch.from_numpy(v))
+            W[("bqkv", l)] = np.concatenate(b)
         else:
             lin(qkv_n, cfg.dim, ("wqkv", l), D.WQKV, l)
         lin(cfg.dim, nh * hd, ("wo", l), D.WO, l)
@@ -254,6 +327,7 @@ def test_every_op_of_a_step_matches_oracle(cuda, ora, kind, monkeypatch):
 
 
 def test_fish_slow_ar_step_matches_oracle(cuda, model_oracle):
+    tally = _Tally()
     cfg = _fish_small()
     lm, W = _build(cfg, cuda, 1, 1)
     orc = model_oracle.OracleDecoder(cfg, W, 1)
@@ -264,7 +338,7 @@ def test_fish_slow_ar_step_matches_oracle(cuda, model_oracle):
         logits, nxt = lm.step(ids=torch.from_numpy(fr))
         got = logits.cpu().numpy()[0]
         want = orc.step_one(0, frame=fr[0])
-        _check(got, orc, want, f"fish step {step}")
+        _check(got, orc, want, f"fish step {step}", tally)
         assert int(nxt[0]) == int(np.argmax(got))
         # the rows this step appended (post QK-RMSNorm + RoPE keys, raw values); after a
         # Q8 flip they carry its effect, so they are compared on flip-free steps only
@@ -277,10 +351,12 @@ def test_fish_slow_ar_step_matches_oracle(cuda, model_oracle):
                 np.testing.assert_allclose(k.cpu().numpy()[0], orc.k[0][l][g][pos], rtol=0, atol=KV_ATOL)
                 np.testing.assert_allclose(v.cpu().numpy()[0], orc.v[0][l][g][pos], rtol=0, atol=KV_ATOL)
     assert lm.lengths(1) == [44]
+    tally.mostly_tight()
 
 
 @pytest.mark.parametrize("dtype", [GgmlDType.Q8_0, GgmlDType.Q4_0])
 def test_cosyvoice2_lm_step_matches_oracle(cuda, model_oracle, dtype):
+    tally = _Tally()
     cfg = D.cosyvoice2_lm_config(n_layers=2, max_seq=64, dtype=dtype)
     lm, W = _build(cfg, cuda, 4, 1)
     orc = model_oracle.OracleDecoder(cfg, W, 1)
@@ -291,16 +367,18 @@ def test_cosyvoice2_lm_step_matches_oracle(cuda, model_oracle, dtype):
         logits, _ = lm.step(embeds=torch.from_numpy(emb))
         got = logits.cpu().numpy()[0]
         want = orc.step_one(0, embed=emb[0])
-        _check(got, orc, want, f"cv2 {dtype.name} step {step}")
+        _check(got, orc, want, f"cv2 {dtype.name} step {step}", tally)
     # token-id path through the dense speech-embedding table
     tok = np.array([[1234]], np.int32)
     logits, _ = lm.step(ids=torch.from_numpy(tok))
-    _check(logits.cpu().numpy()[0], orc, orc.step_one(0, frame=tok[0]), f"cv2 {dtype.name} token step")
+    _check(logits.cpu().numpy()[0], orc, orc.step_one(0, frame=tok[0]), f"cv2 {dtype.name} token step", tally)
+    tally.mostly_tight()
 
 
 # 4 streams: the task-split GEMV; 7 streams: Q4_K projections on the matrix-core GEMV
 @pytest.mark.parametrize("lengths", [[5, 70, 17, 0], [5, 70, 17, 0, 33, 1, 48]])
 def test_ragged_batch_matches_per_stream_oracle(cuda, model_oracle, lengths):
+    tally = _Tally()
     B = len(lengths)
     cfg = _fish_small(n_layers=1, max_batch=B)
     lm, W = _build(cfg, cuda, 7, B)
@@ -313,8 +391,9 @@ def test_ragged_batch_matches_per_stream_oracle(cuda, model_oracle, lengths):
         got = logits.cpu().numpy()
         for s in range(B):
             want = orc.step_one(s, frame=fr[s])
-            _check(got[s], orc, want, f"ragged step {step} stream {s} (len {lengths[s] + step})")
+            _check(got[s], orc, want, f"ragged step {step} stream {s} (len {lengths[s] + step})", tally)
     assert lm.lengths(B) == [L + 2 for L in lengths]
+    tally.mostly_tight()
 
 
 def test_graph_replay_equals_eager_and_feeds_back_argmax(cuda):
@@ -375,9 +454,114 @@ def test_full_cache_is_an_error(cuda):
     assert "full" in str(e.value)
 
 
-def test_most_steps_in_the_tight_regime():
-    # runs after the parity tests above (file order): flips must stay the exception
-    n = _regimes["tight"] + _regimes["flip"]
-    if n == 0:
-        pytest.skip("no parity steps ran")
-    assert n >= 15 and _regimes["tight"] >= TIGHT_FRACTION * n, _regimes
+def _replay_all(ora, lm, cfg, W, lengths, step, frames, logits, hidden, what):
+    """Op-by-op replay of one traced step of every stream (projections bit-exact, glue to
+    GLUE_RTOL), the step's logits and hidden against it, and the greedy argmax."""
+    tr = lm.trace(len(lengths))
+    got = logits.cpu().numpy()
+    for s_ in range(len(lengths)):
+        want = _replay_step(ora, lm, cfg, W, tr, s_, lengths[s_] + step, frame=frames[s_])
+        _bits_equal(got[s_], want, f"{what} stream {s_} head projection")
+        _bits_equal(hidden.cpu().numpy()[s_], tr["final_hn"][s_], f"{what} stream {s_} hidden")
+
+
+def test_sixteen_streams_ragged_kv_256_to_2048(cuda, ora, model_oracle):
+    """The skinny-batch configuration: 16 streams at the Qwen3-4B width (two layers, a
+    4096-row head), KV lengths drawn uniformly from 256..2048: 16-row matrix-core GEMVs,
+    16-stream fused attention with many splits per stream, the 16-stream argmax.  Two
+    consecutive steps, each replayed op by op for every stream (projections bit-exact,
+    the appended K/V rows checked, so the second step also verifies what the first
+    wrote), and each compared end to end with the per-stream oracle model.  At this
+    width nearly every step has an activation within 1e-5 of a Q8 rounding tie, so the
+    end-to-end comparison is held to the flip bound only; the replay is the exact check."""
+    import random
+    r = random.Random(5)
+    lengths = [r.randint(256, 2048) for _ in range(16)]
+    cfg = D.fish_s2_slow_ar_config(n_layers=2, max_seq=2048 + 8, max_batch=16, vocab=4096, n_codebooks=10,
+                                   codebook_size=64, semantic_begin=3000, semantic_end=4095)
+    lm, W = _build_dev(cfg, cuda, 31)
+    orc = model_oracle.OracleDecoder(cfg, W, 16)
+    _prefill(lm, orc, cfg, lengths, seed=32)
+    lm.enable_trace()
+    rng = np.random.default_rng(33)
+    for step in range(2):
+        fr = _frames(rng, 16, cfg)
+        logits, nxt, hidden = lm.step(ids=torch.from_numpy(fr), graph=True, want_hidden=True)
+        _replay_all(ora, lm, cfg, W, lengths, step, list(fr), logits, hidden, f"16 streams step {step}")
+        got = logits.cpu().numpy()
+        assert (nxt.cpu().numpy() == got.argmax(1)).all()
+        for s_ in range(16):
+            _check(got[s_], orc, orc.step_one(s_, frame=fr[s_]), f"16 streams step {step} stream {s_} "
+                                                                   f"(len {lengths[s_] + step})")
+    assert lm.lengths(16) == [L + 2 for L in lengths]
+
+
+def test_cosyvoice2_q8_0_24_layers_at_kv_512(cuda, ora, model_oracle):
+    """CosyVoice2 LM at its configuration: 24 layers, Q8_0, KV prefilled to 512
+    positions (eight 64-position attention splits at head_dim 64).  Two steps (an
+    embedding input, then a token id through the speech-embedding table), each
+    replayed op by op and compared end to end with the oracle model (flip bound)."""
+    cfg = D.cosyvoice2_lm_config(n_layers=24, max_seq=520, dtype=GgmlDType.Q8_0)
+    lm, W = _build_dev(cfg, cuda, 34)
+    orc = model_oracle.OracleDecoder(cfg, W, 1)
+    _prefill(lm, orc, cfg, [512], seed=35)
+    lm.enable_trace()
+    rng = np.random.default_rng(36)
+    emb = rng.standard_normal((1, cfg.dim)).astype(np.float32)
+    logits, _, hidden = lm.step(embeds=torch.from_numpy(emb), graph=True, want_hidden=True)
+    _replay_all(ora, lm, cfg, W, [512], 0, [None], logits, hidden, "cv2 kv512 step 0")
+    _check(logits.cpu().numpy()[0], orc, orc.step_one(0, embed=emb[0]), "cv2 kv512 step 0")
+    tok = np.array([[4321]], np.int32)
+    logits, _, hidden = lm.step(ids=torch.from_numpy(tok), graph=True, want_hidden=True)
+    _replay_all(ora, lm, cfg, W, [512], 1, list(tok), logits, hidden, "cv2 kv512 step 1")
+    _check(logits.cpu().numpy()[0], orc, orc.step_one(0, frame=tok[0]), "cv2 kv512 step 1")
+    assert lm.lengths(1) == [514]
+
+
+def test_full_36_layer_q4k_step_at_kv_1024(cuda, ora, model_oracle):
+    """The headline model at full size: 36 layers, Q4_K, the full 155776-row tied head,
+    KV 1024.  One step replayed op by op over all 36 layers (every projection and the
+    head bit-exact).  End to end, Q8 rounding-tie flips compound over 36 layers, so the
+    bound is the oracle's own sensitivity: the same oracle step on an embedding
+    perturbed by 2^-21 relative (about the size of the glue ops' float differences)
+    moves the logits by d_ref, and the GPU must stay within LOGIT_RTOL_FLIP + 2 d_ref."""
+    cfg = D.fish_s2_slow_ar_config(n_layers=36, max_seq=1032, max_batch=1)
+    lm, W = _build_dev(cfg, cuda, 37)
+    orc = model_oracle.OracleDecoder(cfg, W, 1)
+    _prefill(lm, orc, cfg, [1024], seed=38)
+    lm.enable_trace()
+    fr = _frames(np.random.default_rng(39), 1, cfg)
+    logits, nxt, hidden = lm.step(ids=torch.from_numpy(fr), graph=True, want_hidden=True)
+    _replay_all(ora, lm, cfg, W, [1024], 0, list(fr), logits, hidden, "qwen3-4b 36 layers")
+    got = logits.cpu().numpy()[0]
+    assert int(nxt[0]) == int(np.argmax(got))
+    import copy
+    refs = []
+    for sign in (1.0, -1.0):
+        o2 = copy.deepcopy(orc)
+        emb = o2.embed(fr[0]) * np.float32(1.0 + sign * 2.0 ** -21)
+        refs.append(o2.step_one(0, embed=emb.astype(np.float32)))
+    want = orc.step_one(0, frame=fr[0])
+    d_ref = max(_rel(r_, want) for r_ in refs)
+    err = _rel(got, want)
+    print(f"qwen3-4b 36 layers: rel err {err:.2e}, oracle under a 2^-21 input perturbation {d_ref:.2e}")
+    assert err <= LOGIT_RTOL_FLIP + 2.0 * d_ref, (err, d_ref)
+
+def test_slow_step_returns_logits_and_hidden(cuda, ora):
+    """SlowAr.slow_step returns (semantic_logits, hidden) as SlowAr::slow_step does
+    (crates/syrinx-fish/src/s2/slow_ar.rs:259-271): hidden is the post-final-RMSNorm
+    state [1, 1, dim] the head multiplies (slow_ar.rs:207-246)."""
+    cfg = _fish_small()
+    lm = D.SlowAr(cfg, device=cuda)
+    lm.init_random(seed=44, std=0.02)
+    lm.kv_fill_random([20], seed=45)
+    lm.enable_trace()
+    fr = _frames(np.random.default_rng(46), 1, cfg)[0]
+    logits, hidden = lm.slow_step(fr, pos=20)
+    assert logits.shape == (cfg.vocab,) and hidden.shape == (1, 1, cfg.dim)
+    tr = lm.trace(1)
+    _bits_equal(hidden.cpu().numpy()[0, 0], tr["final_hn"][0], "hidden == final RMSNorm output")
+    h_last = tr["layers"][-1]["h_out"][0]
+    _glue_close(hidden.cpu().numpy()[0, 0], ora.rms_norm(h_last, np.ones(cfg.dim, np.float32), cfg.norm_eps),
+                "hidden vs oracle RMSNorm of the last residual")
+    assert int(lm.last_argmax()[0]) == int(np.argmax(logits.cpu().numpy()))

@@ -313,9 +313,9 @@ def test_prefill_gemm_within_f16_rounding_bound(cuda, ora, n, k, m):
 
 
 def test_forward_captured_in_a_graph(cuda, ora):
-    # QMatMul.forward captured into a HIP graph after one eager call of the same shape (the
-    # workspace cannot grow during capture): GEMV, matrix-core GEMV and the split-K
-    # prefill GEMM, each replayed several times with eager work between the replays
+    # QMatMul.forward captured into a HIP graph (it takes a workspace of its own from the
+    # graph's memory pool): GEMV, matrix-core GEMV and the split-K prefill GEMM, each
+    # replayed several times with eager work between the replays
     cases = [(G.Q4K, 2560, 2560, 1), (G.Q4K, 1003, 2560, 9), (G.Q8_0, 896, 896, 3), (G.Q4K, 2560, 4096, 128)]
     for dt, n, k, m in cases:
         w = _weights(n, k, 40 + m)
@@ -335,3 +335,115 @@ def test_forward_captured_in_a_graph(cuda, ora):
             graph.replay()
             torch.cuda.synchronize()
             np.testing.assert_array_equal(y.cpu().numpy(), want, err_msg=f"{dt} m={m} replay {rep}")
+
+
+def test_captured_forward_survives_a_larger_eager_call(cuda, ora):
+    """Capture a one-row forward, then run an eager 128-row prefill forward (which grows
+    the library's shared workspace), then replay: the graph's workspace is its own, so
+    the replay is untouched by the regrowth."""
+    n, k = 2560, 4096
+    w = _weights(n, k, 60)
+    blocks = ora.quantize(ora.Q4K, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    x1 = torch.from_numpy(_acts(1, k, 61)).to(cuda)
+    want1 = ora.matmul(ora.Q4K, x1.cpu().numpy(), blocks)
+    s = torch.cuda.Stream(device=cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        y1 = qmm.forward(x1)
+    torch.cuda.synchronize()
+    big = torch.from_numpy(_acts(128, k, 62)).to(cuda)
+    for rep in range(2):
+        y_big = qmm.forward(big)  # eager, larger workspace
+        y1.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        _eq_bits(y1.cpu().numpy(), want1)
+        _prefill_check(ora, big.cpu().numpy(), blocks, k, y_big.cpu().numpy().astype(np.float64))
+
+
+def test_replays_overlapping_eager_forwards_on_another_stream(cuda, ora):
+    """A captured forward replayed on one stream while eager forwards of the same
+    QMatMul run on another stream: both stay bit-exact (the replay's workspace is not
+    the one the eager calls share)."""
+    n, k = 6144, 2560
+    blocks = ora.quantize(ora.Q4K, _weights(n, k, 63))
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    xg = torch.from_numpy(_acts(1, k, 64)).to(cuda)
+    xe = torch.from_numpy(_acts(9, k, 65)).to(cuda)
+    want_g = ora.matmul(ora.Q4K, xg.cpu().numpy(), blocks)
+    want_e = ora.matmul(ora.Q4K, xe.cpu().numpy(), blocks)
+    sg, se = torch.cuda.Stream(device=cuda), torch.cuda.Stream(device=cuda)
+    sg.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=sg):
+        yg = qmm.forward(xg)
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(20):
+        with torch.cuda.stream(sg):
+            graph.replay()
+        with torch.cuda.stream(se):
+            outs.append(qmm.forward(xe))
+    torch.cuda.synchronize()
+    _eq_bits(yg.cpu().numpy(), want_g)
+    for y in outs:
+        _eq_bits(y.cpu().numpy(), want_e)
+
+
+def test_shared_workspace_forward_is_refused_under_capture(cuda, ora):
+    """The C-ABI forward that uses the library's shared workspace refuses a capturing
+    stream (a replay could overlap later eager calls); the error names the
+    caller-workspace entry point."""
+    import ctypes
+    from syrinx_amd import lib
+    n, k = 256, 256
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(ora.quantize(ora.Q4K, _weights(n, k, 66)), (n, k), G.Q4K,
+                                                   device=cuda))
+    x = torch.from_numpy(_acts(1, k, 67)).to(cuda)
+    y = torch.empty((1, n), device=cuda)
+    shape = (ctypes.c_int64 * 2)(1, k)
+    s = torch.cuda.Stream(device=cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        rc = lib().sxq_qmm_forward(ctypes.c_void_p(qmm.handle()), ctypes.c_void_p(x.data_ptr()), shape, 2, None,
+                                   ctypes.c_void_p(y.data_ptr()), None, 0, ctypes.c_void_p(s.cuda_stream))
+        msg = lib().sxq_last_error().decode()
+    assert rc == 1 and "sxq_qmm_forward_ws" in msg, (rc, msg)
+
+
+def test_prefill_gemm_stays_finite_beyond_f16_range(cuda, ora):
+    """Rows with values beyond f16's range (65504) are scaled by a power of two before
+    the f16 rounding and back after the f32 accumulation: every output stays finite and
+    within the f16 bound, with the subnormal floor raised by the row's 2^e; rows that
+    stay below 2^15 give the same bits as without such rows in the batch."""
+    n, k, m = 640, 2560, 64
+    blocks = ora.quantize(ora.Q4K, _weights(n, k, 70))
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    rng = np.random.default_rng(71)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[1] *= 1e5                                   # every value of the row large
+    x[2, 7] = 1e30                                # one huge outlier in a normal row
+    x[3, :] = 65504.0
+    x[3, 1::2] = -70000.0                         # beyond f16's largest finite value
+    x[4, 100] = 32768.0                           # exactly at the scaling threshold
+    x[5] *= 1e-3                                  # small values, unscaled
+    y = qmm.forward(torch.from_numpy(x).to(cuda)).cpu().numpy().astype(np.float64)
+    assert np.isfinite(y).all()
+    wd = ora.dequantize(ora.Q4K, blocks, k).reshape(n, k).astype(np.float64)
+    y64 = x.astype(np.float64) @ wd.T
+    amax = np.abs(x).max(1)
+    e = np.where(amax >= 32768.0, np.frexp(amax)[1] - 15, 0).astype(np.float64)
+    S = np.abs(x).astype(np.float64) @ np.abs(wd).T
+    tol = ((2.0 ** -10 + k * 2.0 ** -24) * S + 2.0 ** -24 * np.abs(x).sum(1, keepdims=True)
+           + 2.0 ** (e[:, None] - 24) * np.abs(wd).sum(1)[None, :] + 1e-30)
+    err = np.abs(y - y64)
+    assert (err <= tol).all(), f"{int((err > tol).sum())} beyond the bound; worst ratio {float((err / tol).max()):.3g}"
+    # rows below the threshold are unaffected by the scaled rows in the same batch
+    plain = x.copy()
+    plain[1:5] = 0.0
+    y_plain = qmm.forward(torch.from_numpy(plain).to(cuda)).cpu().numpy()
+    keep = [0] + list(range(5, m))
+    _eq_bits(y[keep].astype(np.float32), y_plain[keep])
