@@ -130,6 +130,20 @@ sxq_status sxq_qmm_forward_ws(const sxq_qmm *qmm, const float *x, const int64_t 
                               const int64_t *x_strides, float *y, const float *bias, unsigned flags,
                               void *workspace, size_t workspace_bytes, void *stream);
 
+/* QMatMul::forward as sxq_qmm_forward (same checks, kernels and bits) on device pointers
+ * for callers that cannot allocate device memory: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  No counterpart in the reference
+ * (Candle allocates inside forward).  Its workspace is a fixed 64 MiB scratch array in
+ * the library's device image, one per GPU, held until the process ends; a call whose
+ * workspace would exceed it fails with SXQ_ERR_INVALID before any GPU work (the decode
+ * GEMV fits at any usual row count, the prefill GEMM up to ~1024 rows at the Qwen3-4B
+ * shapes).  Every call on one GPU shares that scratch: calls that overlap on a GPU (on
+ * different streams, or replays of graphs holding such calls) race and must be ordered
+ * by the caller.  flags: SXQ_BIT_EXACT only. */
+sxq_status sxq_qmm_forward_noalloc(const sxq_qmm *qmm, const float *x, const int64_t *x_shape, int x_ndim,
+                                   const int64_t *x_strides, float *y, const float *bias, unsigned flags,
+                                   void *stream);
+
 /* QTensor::{dtype, shape, storage_size_in_bytes} (storage accounting: load.rs:103). */
 sxq_status sxq_qmm_info(const sxq_qmm *qmm, int *dtype, int64_t *n, int64_t *k, size_t *storage_bytes);
 

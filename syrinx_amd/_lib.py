@@ -53,6 +53,7 @@ _SIGS = {
     "sxq_qmm_forward": (_I, [_P, _P, _P, _I, _P, _P, _P, _U, _P]),
     "sxq_qmm_workspace_size": (_I, [_P, _I64, _U, _P]),
     "sxq_qmm_forward_ws": (_I, [_P, _P, _P, _I, _P, _P, _P, _U, _P, _SZ, _P]),
+    "sxq_qmm_forward_noalloc": (_I, [_P, _P, _P, _I, _P, _P, _P, _U, _P]),
     "sxq_qmm_info": (_I, [_P, _P, _P, _P, _P]),
     "sxq_qmm_dequantize": (_I, [_P, _P, _P]),
     "sxq_qmm_export": (_I, [_P, _P, _P]),
