@@ -24,12 +24,14 @@
  * sets no rustflags, Cargo.toml:1-60) selects.
  *
  * Each function below names the Candle function it follows.  How each one is pinned
- * (golden vectors, closed forms, brute force) is listed in tests/test_oracle_*.py.
- * Pinned: f16 conversion, Q8_0/Q4_0/Q8_K from_float, all to_float, all vec_dot and
- * matmul.  Parity unpinned: the exact bytes Q4_K from_float (make_qkx1_quants)
- * produces -- only its round-trip error bound and its packing are checked; the GPU
- * path is compared to it bit-for-bit, but nothing outside this file confirms that
- * Candle produces the same bytes.
+ * (golden vectors, closed forms, brute force, exact-arithmetic known answers) is listed
+ * in tests/test_oracle_*.py: f16 conversion (numpy's RNE), Q8_0/Q4_0/Q8_K from_float
+ * (closed-form known answers), Q4_K from_float and make_qkx1_quants (known answers
+ * derived in exact arithmetic, each catching a named slip that the tests plant into a
+ * copy of this file), all to_float (hand-packed blocks), all vec_dot and matmul (f64
+ * bilinear form, one-hot activations), the glue ops (the reference's fixtures, closed
+ * forms).  What stays open is Candle's exact float accumulation order of vec_dot in a
+ * SIMD build (the generic order is restated; the f64 bound covers either).
  */
 #ifndef SXQ_ORACLE_H
 #define SXQ_ORACLE_H
