@@ -1,46 +1,51 @@
-"""Decode benchmark of the quantized-linear hot path on one MI355X.
+"""Benchmark of the quantized-linear hot path on one MI355X, every configuration in one run.
 
-Workload (the headline metric's configuration): batch-1 greedy decode of a
-Qwen3-4B-shaped Fish s2-pro slow AR -- 36 layers, dim 2560, 32/8 heads x 128,
-SwiGLU 9728, tied 155776-row head, every projection Q4_K -- with an f32 KV cache
-prefilled to 1024 positions (N(0,1)), generating `--steps` tokens (default 256).
-Weights are random N(0, 0.02) quantized with Candle's from_float (synthetic data).
+Headline (the `value` of the JSON line): batch-1 greedy decode of a Qwen3-4B-shaped Fish
+s2-pro slow AR -- 36 layers, dim 2560, 32/8 heads x 128, SwiGLU 9728, tied 155776-row
+head, every projection Q4_K -- with an f32 KV cache prefilled to 1024 positions (N(0,1)),
+generating `--steps` tokens.  Weights are random N(0, 0.02) quantized with Candle's
+from_float (synthetic data).  A step is one decode token (embedding -> 36 layers -> head
+-> argmax fed back on the device), replayed as a captured HIP graph; `value` is tokens
+per second over the timed steps.
 
-A step is one decode token (embedding -> 36 layers -> head -> argmax fed back on the
-device), replayed as a captured HIP graph.  `value` is tokens per second over the
-timed steps.  `roofline` is the Q4_K GEMV family (every projection of a token,
-launched back to back over 2.27 GB of weights, captured as a HIP graph like the decode
-step and replayed; the eager-launch time is reported beside it) timed with HIP events
-on the stream the kernels run on: algorithmic bytes (weight blocks + activations + outputs) per
-launch over the average launch duration, against 8 TB/s.  `cpu_baseline` times the
-oracle (the CPU restatement of Candle's quantized matmul) on one layer's projections
-plus the head, on this host's cores, and scales it to one token's GEMV work.
+`roofline` is the headline's dominant kernel family, the Q4_K decode GEMV: every
+projection of a token launched back to back over 2.27 GB of weights, captured as a HIP
+graph like the decode step and replayed, timed with HIP events on the stream the kernels
+run on: algorithmic bytes (weight blocks + activation blocks + f32 outputs) per launch
+over the average launch duration, against 8 TB/s.  `roofline.traffic` is the HBM bytes
+per launch that rocprofv3's FETCH_SIZE / WRITE_SIZE report for the same pass (read from
+the committed summary under profiles/, which gives the commands and the copy-kernel
+scale factor).
 
-`roofline.traffic` is the HBM bytes per GEMV launch that rocprofv3's FETCH_SIZE and
-WRITE_SIZE counters report for the same GEMV pass (read from the committed summary
-under profiles/, whose header gives the commands and the copy-kernel scale factor).
+The other configurations are objects in the same line, each with its own roofline and
+CPU baseline:
+  gemv_q8_0     one Q8_0 GEMV [4864 x 896] (the Qwen2-0.5B MLP up-projection) per
+                QMatMul call, 64 weight copies rotated (296 MB > the 256 MB MALL);
+  cv2_decode    the CosyVoice2 LM (Qwen2-0.5B shape, 24 layers, Q8_0, KV 512) decode;
+  q8_0_decode   the headline model with Q8_0 projections;
+  prefill       one Qwen3-4B layer's four projections at a 512-token prompt through
+                QMatMul.forward (the f16 MFMA GEMM with its conversion of x and split-K
+                sums), graph-replayed, against the 2.5 PFLOP/s dense f16 peak;
+  skinny_batch  16 concurrent streams, ragged KV lengths uniform over 256..2048.
 
-`prefill` is a second line in the same object: one Qwen3-4B layer's four projections
-(wqkv, wo, w1|w3, w2; Q4_K) applied to a 512-token prompt through QMatMul.forward, i.e.
-the f16 MFMA GEMM including its conversion of x and split-K sums, captured as a HIP
-graph and replayed (the eager time is reported beside it), against the 2.5 PFLOP/s
-dense f16 MFMA peak.
+CPU baselines (`cpu_baseline`: all threads this GPU's share of the host allows, at most
+16; `cpu_baseline_1thread`): the oracle -- the CPU restatement of Candle 0.8's generic
+quantized matmul (per-row activation quantization, then a vec-dot per output on a pool
+of threads over output columns) -- on a bounded sample of each workload, median of 20
+timed iterations after 3 warm-ups, scaled to the workload's unit as each `sample` says.
 
-`skinny_batch` is a third line: 16 concurrent streams decoding at once with ragged
-KV lengths drawn uniformly from 256..2048 (the GEMVs run 16 activation rows, attention
-and the KV append run per stream), tokens per second over all streams.
-
-Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--dtype q4k|q8_0] [--no-cpu] [--no-prefill] [--skinny-batch 16|0]
-       python bench.py --model cv2 --dtype q8_0 --kv 512   (the CosyVoice2 Qwen2-0.5B LM decode step)
-       python bench.py --mode gemv [--gemv-iters N]   (GEMV pass only, for counter runs)
-       python bench.py --mode copy                     (plain 1 GiB device copy, the counter scale)
-       python bench.py --mode prefill                  (the prefill line alone)
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--no-cpu] [--only LINE,...]
+       python bench.py --mode gemv [--dtype q4k|q8_0] [--gemv-iters N] [--rows N]   (GEMV pass, counter runs)
+       python bench.py --mode copy        (plain 1 GiB device copy: the counter scale)
+       python bench.py --mode prefill     (the prefill line alone)
+       python bench.py --mode decode1     (only the headline decode, for kernel traces)
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -48,6 +53,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA, MI355X
+Q4K, Q8_0 = 12, 8
+LINES = ("gemv_q8_0", "cv2_decode", "q8_0_decode", "prefill", "skinny_batch")
 
 
 def parse():
@@ -55,76 +63,146 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--dtype", default="q4k", choices=["q4k", "q8_0"])
-    ap.add_argument("--model", default="fish", choices=["fish", "cv2"],
-                    help="fish: the Qwen3-4B-shaped slow AR (the headline); cv2: the CosyVoice2 Qwen2-0.5B LM "
-                         "(24 layers, dim 896; pass --dtype q8_0 --kv 512 for its configuration)")
+    ap.add_argument("--dtype", default="q4k", choices=["q4k", "q8_0"], help="--mode gemv only")
+    ap.add_argument("--rows", type=int, default=1, help="--mode gemv: activation rows (streams)")
     ap.add_argument("--kv", type=int, default=1024)
-    ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--gemv-iters", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--mode", default="decode", choices=["decode", "gemv", "copy", "prefill"],
-                    help="decode: the benchmark; gemv: only the per-token GEMV pass (for counter runs); "
-                         "copy: a plain device copy of known size (the counter scale); prefill: the "
-                         "512-token prefill GEMMs of one Qwen3-4B layer on MFMA")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-GEMM line of the decode bench")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--only", default=",".join(LINES), help="comma-separated extra lines to run")
+    ap.add_argument("--mode", default="decode", choices=["decode", "decode1", "gemv", "copy", "prefill"])
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--prefill-iters", type=int, default=20)
-    ap.add_argument("--skinny-batch", type=int, default=16,
-                    help="streams of the skinny-batch line (ragged KV lengths uniform over 256..2048); 0 skips it")
+    ap.add_argument("--skinny-batch", type=int, default=16)
     ap.add_argument("--skinny-steps", type=int, default=64)
     return ap.parse_args()
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv2_q4k_qwen3_4b_decode_traffic.txt")
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def measured_traffic():
-    """HBM bytes per GEMV launch from the committed counter summary (None if absent)."""
+# ------------------------------------------------------------------ CPU baseline helpers
+def cpu_threads():
+    """Threads for the all-cores CPU baseline: the cores this process may use, at most 16
+    (one GPU's share of the host)."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return None
+    return "unknown"
 
 
-def gemv_roofline(lm, torch, iters):
-    """Average duration of the GEMV launches of one token (all 36 layers + head)."""
-    dev = lm.device
-    from syrinx_amd._lib import check, lib
+def cpu_median(fn, iters=20, warm=3):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_entry(value, unit, threads, sample):
+    return {"value": round(value, 4), "unit": unit, "cores": threads, "kind": "port", "cpu_model": cpu_model(),
+            "host_logical_cores": os.cpu_count(), "sample": sample}
+
+
+def oracle_mod():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle  # the CPU oracle, timed as the CPU baseline
+    return oracle
+
+
+def quantized_blocks(torch, dev, n, k, dt, seed):
+    """Random N(0, 0.02) [n, k] weights quantized on the GPU, as host canonical blocks."""
+    from syrinx_amd import GgmlDType, QTensor
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = torch.randn(n, k, device=dev, generator=g) * 0.02
+    b = QTensor.quantize(w, GgmlDType(dt)).data().cpu().numpy().reshape(n, -1)
+    del w
+    return b
+
+
+def cpu_layer_token(torch, dev, cfg, dt, head_rows_div, label, rows=(1, 1)):
+    """tok/s of one step's GEMV work on the CPU: median time of one layer's projections
+    (as the reference calls them) x n_layers + the head (timed on 1/head_rows_div of its
+    rows, scaled up), at all threads (rows[0] activation rows) and at 1 thread (rows[1]);
+    tokens per second = rows / step time."""
+    import numpy as np
+    ora = oracle_mod()
+    hd, nh, nkv = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    if cfg.qkv_bias:  # Qwen2: q, k, v, o, gate, up, down as separate QMatMuls
+        shapes = [(nh * hd, cfg.dim), (nkv * hd, cfg.dim), (nkv * hd, cfg.dim), (cfg.dim, nh * hd),
+                  (cfg.intermediate, cfg.dim), (cfg.intermediate, cfg.dim), (cfg.dim, cfg.intermediate)]
+    else:            # Fish: fused wqkv, wo, w1, w3, w2
+        shapes = [((nh + 2 * nkv) * hd, cfg.dim), (cfg.dim, nh * hd), (cfg.intermediate, cfg.dim),
+                  (cfg.intermediate, cfg.dim), (cfg.dim, cfg.intermediate)]
+    mats = [(k, quantized_blocks(torch, dev, n, k, dt, 11 + i)) for i, (n, k) in enumerate(shapes)]
+    head_rows = cfg.vocab // head_rows_div
+    head = quantized_blocks(torch, dev, head_rows, cfg.dim, dt, 99)
+    rng = np.random.default_rng(0)
+    out = {}
+    for key, th, m in (("cpu_baseline", cpu_threads(), rows[0]), ("cpu_baseline_1thread", 1, rows[1])):
+        xs = {k: rng.standard_normal((m, k)).astype(np.float32) for k, _ in mats}
+        xh = rng.standard_normal((m, cfg.dim)).astype(np.float32)
+        t_layer = cpu_median(lambda: [ora.matmul(dt, xs[k], b, threads=th) for k, b in mats])
+        t_head = cpu_median(lambda: ora.matmul(dt, xh, head, threads=th)) * head_rows_div
+        tok = m / (cfg.n_layers * t_layer + t_head)
+        out[key] = cpu_entry(tok, "tok/s (GEMV share of a step)", th,
+                             f"{label}: one layer's {len(mats)} projections at {m} activation row{'s' if m > 1 else ''} "
+                             f"(median of 20 after 3 warm-ups: {t_layer * 1e3:.2f} ms) x {cfg.n_layers} layers + the "
+                             f"head timed on {head_rows} of its {cfg.vocab} rows and scaled ({t_head * 1e3:.2f} ms), "
+                             f"through the oracle's k_quants::matmul (generic vec-dot, {th} thread{'s' if th > 1 else ''})")
+    return out
+
+
+# ------------------------------------------------------------------ GPU measurements
+def gemv_roofline(lm, torch, iters, rows=1):
+    """Average duration of the GEMV launches of one step (every layer's four projections
+    + the head) at `rows` activation rows, graph-replayed, timed with HIP events."""
     import ctypes
-    s = torch.cuda.current_stream(dev)
-    n_launch = 4 * lm.cfg.n_layers + 1
-    layer_b, head_b = lm.weight_bytes()
-    # algorithmic bytes per token of GEMV: weight blocks + f32 outputs + activation blocks
+    from syrinx_amd._lib import check, lib
+    s = torch.cuda.current_stream(lm.device)
     c = lm.cfg
+    n_launch = 4 * c.n_layers + 1
+    layer_b, head_b = lm.weight_bytes()
     qkv_n = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
-    outs = 4 * (qkv_n + c.dim + 2 * c.intermediate + c.dim) * c.n_layers + 4 * c.vocab
-    act_blk = 292 if c.weight_dtype == 12 else 34
-    bs = 256 if c.weight_dtype == 12 else 32
-    acts = act_blk * ((2 * c.dim + c.n_heads * c.head_dim + c.intermediate) // bs * c.n_layers + c.dim // bs)
+    outs = rows * (4 * (qkv_n + c.dim + 2 * c.intermediate + c.dim) * c.n_layers + 4 * c.vocab)
+    act_blk = 292 if c.weight_dtype == Q4K else 34
+    bs = 256 if c.weight_dtype == Q4K else 32
+    acts = rows * act_blk * ((2 * c.dim + c.n_heads * c.head_dim + c.intermediate) // bs * c.n_layers + c.dim // bs)
     algo = layer_b + head_b + outs + acts
+
+    def one(stream):
+        check(lib().sxq_lm_gemv_pass(lm._h, rows, 1, ctypes.c_void_p(stream.cuda_stream)))
+
     for _ in range(2):
-        check(lib().sxq_lm_gemv_pass(lm._h, 1, 1, ctypes.c_void_p(s.cuda_stream)))
+        one(s)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # eager launches (reported alongside): each launch adds the host-queue dispatch cost
     e0.record(s)
     for _ in range(iters):
-        check(lib().sxq_lm_gemv_pass(lm._h, 1, 1, ctypes.c_void_p(s.cuda_stream)))
+        one(s)
     e1.record(s)
     torch.cuda.synchronize()
     eager_ms = e0.elapsed_time(e1) / iters
-    # the measured pass: the same launches captured once as a HIP graph and replayed, as
-    # the decode step runs them
     graph = torch.cuda.CUDAGraph()
-    cs = torch.cuda.Stream(dev)
+    cs = torch.cuda.Stream(lm.device)
     cs.wait_stream(s)
     with torch.cuda.graph(graph, stream=cs):
-        check(lib().sxq_lm_gemv_pass(lm._h, 1, 1, ctypes.c_void_p(cs.cuda_stream)))
+        one(cs)
     s.wait_stream(cs)
     for _ in range(2):
         graph.replay()
@@ -135,75 +213,113 @@ def gemv_roofline(lm, torch, iters):
     e1.record(s)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / iters
-    avg_us = ms * 1000.0 / n_launch
     achieved = algo / (ms * 1e-3) / 1e9
-    traffic = measured_traffic() if c.weight_dtype == 12 else None
+    kernel = ("k_gemv_mma_q4k" if rows > 4 else "k_gemv2_q4k") if c.weight_dtype == Q4K else "k_gemv2_q80"
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None if traffic is None else round(traffic),
-            "algorithmic_bytes_per_launch": round(algo / n_launch),
-            "kernel": "k_gemv2_q4k" if c.weight_dtype == 12 else "k_gemv2_q80",
-            "bytes_per_token": algo, "launches_per_token": n_launch, "avg_launch_us": round(avg_us, 3),
-            "gemv_us_per_token": round(ms * 1000.0, 2), "replay": "hip graph",
-            "eager_gemv_us_per_token": round(eager_ms * 1000.0, 2)}
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "algorithmic_bytes_per_launch": round(algo / n_launch), "kernel": kernel, "rows": rows,
+            "bytes_per_step": algo, "launches_per_step": n_launch, "avg_launch_us": round(ms * 1000.0 / n_launch, 3),
+            "gemv_us_per_step": round(ms * 1000.0, 2), "replay": "hip graph",
+            "eager_gemv_us_per_step": round(eager_ms * 1000.0, 2)}
 
 
-def cpu_threads():
-    """The host cores this process may use, capped at 16 (one GPU's share of the host)."""
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv2_q4k_qwen3_4b_decode_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per Q4_K decode GEMV launch from the committed counter summary."""
     try:
-        n = len(os.sched_getaffinity(0))
-    except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
-def cpu_baseline(lm, torch, budget_s=12.0):
-    """Oracle (CPU port of Candle's quantized matmul) on whole tokens' GEMV work.
+def timed_decode(lm, torch, frame, kv, steps, warmup, batch=1):
+    """Greedy decode from a KV cache holding `kv` positions: graph-replayed steps timed
+    with HIP events on the stream they run on.  Returns ms per step."""
+    lm.step(ids=frame, graph=True)  # captures the graph
+    for _ in range(warmup):
+        lm.step(n=batch, graph=True, want_logits=False)
+    lm.set_lengths([kv] * batch)
+    lm.step(ids=frame, graph=True, want_logits=False)
+    lm.set_lengths([kv] * batch)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream(lm.device)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        lm.step(n=batch, graph=True, want_logits=False)
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
-    One token = the four projections 36 times (layer 0's weights stand in for every
-    layer: 57 MB per layer, far beyond the host caches) + the head; tokens are run until
-    `budget_s` seconds have passed (at least one)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
-    import oracle  # the CPU oracle, timed as the CPU baseline
-    from syrinx_amd import GgmlDType, QTensor
-    c = lm.cfg
-    dt = GgmlDType(c.weight_dtype)
-    dev = lm.device
-    rng = np.random.default_rng(0)
-    qkv_n = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
-    shapes = [(qkv_n, c.dim), (c.dim, c.n_heads * c.head_dim), (2 * c.intermediate, c.dim), (c.dim, c.intermediate)]
-    blocks = []
-    g = torch.Generator(device=dev).manual_seed(1)
-    for n, k in shapes + [(c.vocab, c.dim)]:
+
+def fish_frame(lm, torch, n=1):
+    f = torch.zeros((n, lm.ids_per), dtype=torch.int32)
+    f[:, 0] = 151700
+    f[:, 1:] = (torch.arange(n, dtype=torch.int32)[:, None] * 11 + torch.arange(lm.ids_per - 1)) * 37 % 4096
+    return f
+
+
+def q8_0_gemv(torch, cpu, copies=64, reps=20):
+    """Config 1: one Q8_0 GEMV [4864 x 896] per QMatMul.forward (activation quantization
+    + GEMV), 64 weight copies rotated so the weights stream from HBM, not the MALL."""
+    from syrinx_amd import GgmlDType, QMatMul, QTensor
+    dev = torch.device("cuda:0")
+    n, k = 4864, 896
+    g = torch.Generator(device=dev).manual_seed(0)
+    mats = []
+    for _ in range(copies):
         w = torch.randn(n, k, device=dev, generator=g) * 0.02
-        blocks.append((k, QTensor.quantize(w, dt).data().cpu().numpy().reshape(n, -1)))
-        del w
-    xs = {k: rng.standard_normal((1, k)).astype(np.float32) for k, _ in blocks}
-    threads = cpu_threads()
-    tokens = 0
-    t0 = time.perf_counter()
-    while tokens == 0 or time.perf_counter() - t0 < budget_s:
-        for _ in range(c.n_layers):
-            for k, b in blocks[:4]:
-                oracle.matmul(int(dt), xs[k], b, threads=threads)
-        k, b = blocks[4]
-        oracle.matmul(int(dt), xs[k], b, threads=threads)
-        tokens += 1
-    total = time.perf_counter() - t0
-    return {"value": round(tokens / total, 3), "unit": "tok/s (GEMV share of a token)", "cores": threads,
-            "kind": "port",
-            "sample": f"{tokens} tokens of GEMV work ({c.n_layers} x layer-0's four projections + the head, "
-                      f"batch 1) through the oracle's k_quants::matmul (generic vec-dot, {threads} threads) "
-                      f"in {total:.1f} s"}
+        mats.append(QMatMul.from_qtensor(QTensor.quantize(w, GgmlDType.Q8_0)))
+    x = torch.randn(1, k, device=dev, generator=g)
+    ys = [q.forward(x) for q in mats]  # eager warm-up
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.current_stream(dev)
+    cs = torch.cuda.Stream(dev)
+    cs.wait_stream(s)
+    with torch.cuda.graph(graph, stream=cs):
+        ys = [q.forward(x) for q in mats]
+    s.wait_stream(cs)
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * copies)
+    algo = n * (k // 32) * 34 + 4 * k + 4 * n  # weight blocks + f32 x + f32 y (4,653,568 B)
+    gbs = algo / (us * 1e-6) / 1e9
+    out = {"workload": f"one Q8_0 GEMV [{n} x {k}] (Qwen2-0.5B MLP up-projection) per QMatMul.forward, x [1 x {k}] "
+                       f"N(0,1), weights N(0,0.02), {copies} weight copies rotated ({copies * n * (k // 32) * 34 / 1e6:.0f} MB)"
+                       ", graph-replayed",
+           "value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(us, 3), "bytes_per_call": algo,
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "kernel": "k_gemv2_q80 (+ the activation quantizer, per call)"}}
+    if cpu:
+        import numpy as np
+        ora = oracle_mod()
+        blocks = mats[0].export_blocks().cpu().numpy().reshape(n, -1)
+        xh = x.cpu().numpy()
+        for key, th in (("cpu_baseline", cpu_threads()), ("cpu_baseline_1thread", 1)):
+            t = cpu_median(lambda: ora.matmul(Q8_0, xh, blocks, threads=th))
+            out[key] = cpu_entry(algo / t / 1e9, "GB/s", th,
+                                 f"the same GEMV through the oracle's k_quants::matmul ({th} thread"
+                                 f"{'s' if th > 1 else ''}), median of 20 after 3 warm-ups: {t * 1e6:.1f} us per call")
+    return out
 
 
-MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA, MI355X
-
-
-def prefill_gemms(torch, tokens, iters):
-    """One Qwen3-4B layer's projections at a `tokens`-row prompt through QMatMul.forward
-    (Q4_K weights, the f16 MFMA prefill GEMM incl. its f16 conversion of x)."""
+def prefill_gemms(torch, tokens, iters, cpu=False):
+    """Config 4: one Qwen3-4B layer's projections at a `tokens`-row prompt through
+    QMatMul.forward (Q4_K weights, the f16 MFMA prefill GEMM incl. its f16 conversion)."""
     from syrinx_amd import GgmlDType, QMatMul, QTensor
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(3)
@@ -228,8 +344,6 @@ def prefill_gemms(torch, tokens, iters):
     e1.record(s)
     torch.cuda.synchronize()
     eager_ms = e0.elapsed_time(e1) / iters
-    # the measured layer: the same four forwards captured once as a HIP graph and
-    # replayed, as the decode step runs (the eager time is reported beside it)
     graph = torch.cuda.CUDAGraph()
     cs = torch.cuda.Stream(dev)
     cs.wait_stream(s)
@@ -247,28 +361,46 @@ def prefill_gemms(torch, tokens, iters):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / iters
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"workload": f"Qwen3-4B layer projections (wqkv, wo, w1|w3, w2) at M={tokens}, Q4_K weights, "
-                        "f16 MFMA with f32 accumulation",
-            "us_per_layer": round(ms * 1000.0, 2), "flops_per_layer": flops, "achieved": round(tflops, 1),
-            "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-            "replay": "hip graph", "eager_us_per_layer": round(eager_ms * 1000.0, 2),
-            "ms_36_layers": round(36 * ms, 3)}
+    out = {"workload": f"Qwen3-4B layer projections (wqkv, wo, w1|w3, w2) at M={tokens}, Q4_K weights, "
+                       "f16 MFMA with f32 accumulation",
+           "us_per_layer": round(ms * 1000.0, 2), "flops_per_layer": flops, "value": round(tflops, 1),
+           "unit": "TFLOP/s", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+           "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+           "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                        "kernel": "k_gemm_q4k (+ k_x_to_f16_perm, k_gemm_splitk_sum)"},
+           "replay": "hip graph", "eager_us_per_layer": round(eager_ms * 1000.0, 2),
+           "ms_36_layers": round(36 * ms, 3)}
+    if cpu:
+        import numpy as np
+        ora = oracle_mod()
+        blocks = [(k, m.export_blocks().cpu().numpy().reshape(n, -1)) for (n, k), m in zip(shapes, mats)]
+        rng = np.random.default_rng(1)
+        for key, th, rows in (("cpu_baseline", cpu_threads(), 16), ("cpu_baseline_1thread", 1, 2)):
+            xr = {k: rng.standard_normal((rows, k)).astype(np.float32) for k, _ in blocks}
+            t = cpu_median(lambda: [ora.matmul(Q4K, xr[k], b, threads=th) for k, b in blocks])
+            t_layer = t * tokens / rows  # the CPU path's cost is linear in the rows
+            out[key] = cpu_entry(flops / t_layer / 1e12, "TFLOP/s", th,
+                                 f"one layer's four projections at {rows} prompt rows through the oracle's "
+                                 f"k_quants::matmul ({th} thread{'s' if th > 1 else ''}; per-row activation "
+                                 f"quantization + a vec-dot per output, cost linear in the rows), median of 20 after "
+                                 f"3 warm-ups ({t * 1e3:.1f} ms), scaled to {tokens} rows: "
+                                 f"{t_layer * 1e3:.0f} ms per layer")
+    return out
 
 
 SKINNY_KV = (256, 2048)
 
 
-def skinny_batch(lm, torch, n, steps, warmup):
-    """Greedy decode of n concurrent streams whose KV caches hold ragged lengths drawn
-    uniformly from 256..2048 (seeded): the GEMVs see n activation rows, attention and the
-    KV append run per stream at its own position."""
+def skinny_batch(lm, torch, n, steps, warmup, iters, cpu):
+    """Config 5: greedy decode of n concurrent streams whose KV caches hold ragged lengths
+    drawn uniformly from 256..2048 (seeded): the GEMVs see n activation rows, attention
+    and the KV append run per stream at its own position."""
     import random
     rng = random.Random(5)
     lengths = [rng.randint(*SKINNY_KV) for _ in range(n)]
     lm.kv_fill_random([SKINNY_KV[1]] * n, seed=2)
-    frame = torch.zeros((n, 1 + lm.cfg.n_codebooks), dtype=torch.int32)
-    frame[:, 0] = 151700
-    frame[:, 1:] = (torch.arange(n, dtype=torch.int32)[:, None] * 11 + torch.arange(lm.cfg.n_codebooks)) * 37 % 4096
+    frame = fish_frame(lm, torch, n)
     lm.set_lengths(lengths)
     lm.step(ids=frame, graph=True, want_logits=False)  # captures the n-stream graph
     for _ in range(warmup):
@@ -284,10 +416,17 @@ def skinny_batch(lm, torch, n, steps, warmup):
     e1.record(s)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1)
-    return {"workload": f"{n} concurrent streams, Qwen3-4B shape, Q4_K, ragged KV lengths uniform over "
-                        f"{SKINNY_KV[0]}..{SKINNY_KV[1]} (seed 5), {steps} steps",
-            "value": round(n * steps / (ms / 1000.0), 2), "unit": "tok/s (all streams)",
-            "ms_per_step": round(ms / steps, 4), "kv_lengths": lengths}
+    kv_bytes = 294912 * sum(L + steps // 2 for L in lengths)  # f32 K and V read per step, mid-run lengths
+    out = {"workload": f"{n} concurrent streams, Qwen3-4B shape, Q4_K, ragged KV lengths uniform over "
+                       f"{SKINNY_KV[0]}..{SKINNY_KV[1]} (seed 5), {steps} steps",
+           "value": round(n * steps / (ms / 1000.0), 2), "unit": "tok/s (all streams)",
+           "ms_per_step": round(ms / steps, 4), "kv_lengths": lengths, "kv_bytes_per_step": kv_bytes,
+           "roofline": gemv_roofline(lm, torch, iters, rows=n)}
+    if cpu:
+        # all threads at the full 16 rows; one thread at 2 rows (the CPU path's cost is
+        # linear in the rows: every row runs its own vec-dots over all the weights)
+        out.update(cpu_layer_token(torch, lm.device, lm.cfg, Q4K, 16, f"{n} streams", rows=(n, 2)))
+    return out
 
 
 def copy_calibration(torch, iters=8):
@@ -299,6 +438,38 @@ def copy_calibration(torch, iters=8):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"mode": "copy", "bytes_read_per_copy": n, "bytes_written_per_copy": n, "copies": iters}))
+
+
+def build_model(D, torch, kind, dtype, max_seq, max_batch):
+    dev = torch.device("cuda:0")
+    if kind == "cv2":
+        lm = D.Qwen2Lm(D.cosyvoice2_lm_config(n_layers=24, max_seq=max_seq, max_batch=max_batch, dtype=dtype),
+                       device=dev)
+    else:
+        lm = D.SlowAr(D.fish_s2_slow_ar_config(n_layers=36, max_seq=max_seq, max_batch=max_batch, dtype=dtype),
+                      device=dev)
+    lm.init_random(seed=0, std=0.02)
+    return lm
+
+
+def decode_line(D, torch, kind, dtype, kv, args, cpu, label):
+    t0 = time.time()
+    lm = build_model(D, torch, kind, dtype, kv + args.steps + args.warmup + 8, 1)
+    lm.kv_fill_random([kv], seed=1)
+    frame = fish_frame(lm, torch) if kind == "fish" else torch.tensor([[100]], dtype=torch.int32)
+    ms = timed_decode(lm, torch, frame, kv, args.steps, args.warmup)
+    roof = gemv_roofline(lm, torch, args.gemv_iters)
+    c = lm.cfg
+    out = {"workload": label, "value": round(1000.0 / ms, 2), "unit": "tok/s", "ms_per_step": round(ms, 4),
+           "config": {"n_layers": c.n_layers, "dim": c.dim, "heads": f"{c.n_heads}/{c.n_kv_heads}x{c.head_dim}",
+                      "intermediate": c.intermediate, "vocab": c.vocab, "kv_len": kv, "batch": 1, "graph": True},
+           "roofline": roof}
+    log(f"{label}: {out['value']} tok/s, GEMV {roof['gemv_us_per_step']} us ({roof['frac']:.3f}) "
+        f"[{time.time() - t0:.1f}s]")
+    if cpu:
+        out.update(cpu_layer_token(torch, lm.device, c, dtype, 16 if kind == "fish" else 1, label))
+    del lm
+    return out
 
 
 def main():
@@ -314,87 +485,76 @@ def main():
     if args.mode == "prefill":
         print(json.dumps({"mode": "prefill", "prefill": prefill_gemms(torch, args.prefill_tokens, args.prefill_iters)}))
         return
-    from syrinx_amd import GgmlDType
     from syrinx_amd import decoder as D
-
-    dev = torch.device("cuda:0")
-    dt = GgmlDType.Q4K if args.dtype == "q4k" else GgmlDType.Q8_0
-    skinny = args.skinny_batch if args.mode == "decode" and args.model == "fish" else 0
-    max_seq = max(args.kv, SKINNY_KV[1] if skinny else 0) + max(args.steps, args.skinny_steps) + args.warmup + 8
-    t0 = time.time()
-    if args.model == "cv2":
-        cfg = D.cosyvoice2_lm_config(n_layers=24, max_seq=max_seq, max_batch=args.batch, dtype=dt)
-        lm = D.Qwen2Lm(cfg, device=dev)
-    else:
-        cfg = D.fish_s2_slow_ar_config(n_layers=36, max_seq=max_seq, max_batch=max(args.batch, skinny), dtype=dt)
-        lm = D.SlowAr(cfg, device=dev)
-    lm.init_random(seed=0, std=0.02)
-    lm.kv_fill_random([args.kv] * args.batch, seed=1)
-    print(f"[bench] model ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    cpu = not args.no_cpu
     if args.mode == "gemv":
-        roof = gemv_roofline(lm, torch, args.gemv_iters)
+        dt = Q4K if args.dtype == "q4k" else Q8_0
+        lm = build_model(D, torch, "fish", dt, args.kv + 16, max(1, args.rows))
+        lm.kv_fill_random([args.kv] * args.rows, seed=1)
+        lm.step(ids=fish_frame(lm, torch, args.rows), graph=False, want_logits=False)  # fills the activation blocks
+        roof = gemv_roofline(lm, torch, args.gemv_iters, rows=args.rows)
         print(json.dumps({"mode": "gemv", "passes": 2 * (args.gemv_iters + 2), "roofline": roof}))
         return
-    rng_frame = torch.zeros((args.batch, lm.ids_per), dtype=torch.int32)
-    rng_frame[:, 0] = 151700 if args.model == "fish" else 100
-    rng_frame[:, 1:] = torch.arange(lm.ids_per - 1, dtype=torch.int32) * 37 % 4096
-    lm.step(ids=rng_frame, graph=True)  # captures the graph
-    for _ in range(args.warmup):
-        lm.step(n=args.batch, graph=True, want_logits=False)
-    torch.cuda.synchronize()
-    lm.set_lengths([args.kv] * args.batch)
-    lm.step(ids=rng_frame, graph=True, want_logits=False)
-    lm.set_lengths([args.kv] * args.batch)
-    torch.cuda.synchronize()
-    s = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_host0 = time.perf_counter()
-    e0.record(s)
-    for _ in range(args.steps):
-        lm.step(n=args.batch, graph=True, want_logits=False)
-    e1.record(s)
-    torch.cuda.synchronize()
-    t_host = time.perf_counter() - t_host0
-    ms = e0.elapsed_time(e1)
-    ms_per_step = ms / args.steps
-    tok_s = args.batch * args.steps / (ms / 1000.0)
-    print(f"[bench] {args.steps} steps in {ms:.1f} ms ({ms_per_step * 1000:.1f} us/token, host {t_host * 1000:.1f} ms)",
-          file=sys.stderr, flush=True)
+    only = set(x for x in args.only.split(",") if x) if args.mode == "decode" else set()
+    skinny = args.skinny_batch if "skinny_batch" in only else 0
+
+    # headline: Qwen3-4B shape, Q4_K, batch 1, KV 1024
+    t0 = time.time()
+    max_seq = max(args.kv, SKINNY_KV[1] if skinny else 0) + max(args.steps, args.skinny_steps) + args.warmup + 8
+    lm = build_model(D, torch, "fish", Q4K, max_seq, max(1, skinny))
+    lm.kv_fill_random([args.kv], seed=1)
+    log(f"model ready in {time.time() - t0:.1f}s")
+    ms = timed_decode(lm, torch, fish_frame(lm, torch), args.kv, args.steps, args.warmup)
+    log(f"{args.steps} steps: {ms * 1000:.1f} us/token")
+    if args.mode == "decode1":
+        print(json.dumps({"mode": "decode1", "ms_per_step": ms}))
+        return
     roof = gemv_roofline(lm, torch, args.gemv_iters)
-    print(f"[bench] GEMV: {roof['gemv_us_per_token']} us/token, {roof['achieved']} GB/s", file=sys.stderr, flush=True)
-    skinny_line = skinny_batch(lm, torch, skinny, args.skinny_steps, args.warmup) if skinny else None
-    cpu = None if args.no_cpu else cpu_baseline(lm, torch)
-    prefill = None
-    if not args.no_prefill and args.model == "fish":
-        prefill = prefill_gemms(torch, args.prefill_tokens, args.prefill_iters)
-        print(f"[bench] prefill: {prefill['us_per_layer']} us/layer, {prefill['achieved']} TFLOP/s", file=sys.stderr,
-              flush=True)
+    traffic = measured_traffic()
+    roof["traffic"] = None if traffic is None else round(traffic)
+    log(f"GEMV: {roof['gemv_us_per_step']} us/token, {roof['achieved']} GB/s")
+    lines = {}
+    if skinny:
+        lines["skinny_batch"] = skinny_batch(lm, torch, skinny, args.skinny_steps, args.warmup, args.gemv_iters, cpu)
+        log(f"skinny batch: {lines['skinny_batch']['value']} tok/s")
+    cpu_head = cpu_layer_token(torch, lm.device, lm.cfg, Q4K, 16, "Qwen3-4B shape, Q4_K") if cpu else {}
+    del lm
+    if "q8_0_decode" in only:
+        lines["q8_0_decode"] = decode_line(D, torch, "fish", Q8_0, args.kv, args, cpu,
+                                           f"Fish s2-pro slow AR (Qwen3-4B shape) greedy decode, Q8_0 projections, "
+                                           f"batch 1, f32 KV prefilled to {args.kv}, {args.steps} tokens")
+    if "cv2_decode" in only:
+        lines["cv2_decode"] = decode_line(D, torch, "cv2", Q8_0, 512, args, cpu,
+                                          f"CosyVoice2 LM (Qwen2-0.5B shape, 24 layers) greedy decode, Q8_0 "
+                                          f"projections, batch 1, f32 KV prefilled to 512, {args.steps} tokens")
+    if "gemv_q8_0" in only:
+        lines["gemv_q8_0"] = q8_0_gemv(torch, cpu)
+        log(f"Q8_0 GEMV: {lines['gemv_q8_0']['value']} GB/s")
+    if "prefill" in only:
+        lines["prefill"] = prefill_gemms(torch, args.prefill_tokens, args.prefill_iters, cpu)
+        log(f"prefill: {lines['prefill']['us_per_layer']} us/layer, {lines['prefill']['value']} TFLOP/s")
     out = {
         "metric": "decode tok/s Qwen3-4B-shape Q4_K bs=1; quant-GEMV HBM GB/s as % of peak",
-        "value": round(tok_s, 2),
+        "value": round(1000.0 / ms, 2),
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("q4k-weight x q8k-activation int dot, f32" if dt == GgmlDType.Q4K
-                  else "q8_0-weight x q8_0-activation int dot, f32"),
+        "dtype": "q4k-weight x q8k-activation int dot, f32",
         "data": "synthetic (random N(0,0.02) weights quantized by from_float; KV N(0,1))",
-        "config": {"workload": (f"Fish s2-pro slow AR (Qwen3-4B shape) greedy decode" if args.model == "fish" else
-                                f"CosyVoice2 LM (Qwen2-0.5B shape) greedy decode") +
-                               f", {args.dtype.upper()} projections, batch {args.batch}, f32 KV prefilled to "
-                               f"{args.kv}, {args.steps} tokens",
-                   "n_layers": cfg.n_layers, "dim": cfg.dim,
-                   "heads": f"{cfg.n_heads}/{cfg.n_kv_heads}x{cfg.head_dim}", "intermediate": cfg.intermediate,
-                   "vocab": cfg.vocab, "kv_len": args.kv, "batch": args.batch, "graph": True},
+        "config": {"workload": f"Fish s2-pro slow AR (Qwen3-4B shape) greedy decode, Q4_K projections, batch 1, "
+                               f"f32 KV prefilled to {args.kv}, {args.steps} tokens",
+                   "n_layers": 36, "dim": 2560, "heads": "32/8x128", "intermediate": 9728, "vocab": 155776,
+                   "kv_len": args.kv, "batch": 1, "graph": True},
         "roofline": roof,
-        "cpu_baseline": cpu,
-        "prefill": prefill,
-        "skinny_batch": skinny_line,
+        "cpu_baseline": cpu_head.get("cpu_baseline"),
+        "cpu_baseline_1thread": cpu_head.get("cpu_baseline_1thread"),
     }
+    out.update({k: lines.get(k) for k in LINES})
     print(json.dumps(out))
 
 
