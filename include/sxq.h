@@ -110,9 +110,10 @@ sxq_status sxq_qmm_create(int device, int dtype, int64_t n, int64_t k, const voi
  * tensor ... incompatible with ..."), x_ndim >= 2 ("input tensor has only one
  * dimension"), contiguous (x_strides NULL or row-major; else NOT_CONTIGUOUS);
  * y f32 [prod(x_shape[:-1]), n].  Outputs equal Candle's CPU vec-dot bit for bit for
- * every row count of Q8_0 / Q4_0 weights, and of Q4_K weights below 64 rows (decode
- * GEMV, rows 16 at a time) or with SXQ_BIT_EXACT; Q4_K with 64 or more rows runs the
- * f16 MFMA prefill GEMM (error bound at SXQ_BIT_EXACT above). */
+ * every row count of Q8_0 / Q4_0 weights (the decode GEMV up to 127 rows, 16 at a time;
+ * from 128 rows a GEMM on the int8 matrix cores that keeps Candle's per-block float
+ * order), and of Q4_K weights below 64 rows or with SXQ_BIT_EXACT; Q4_K with 64 or more
+ * rows runs the f16 MFMA prefill GEMM (error bound at SXQ_BIT_EXACT above). */
 sxq_status sxq_qmm_forward(const sxq_qmm *qmm, const float *x, const int64_t *x_shape, int x_ndim,
                            const int64_t *x_strides, float *y, const float *bias, unsigned flags, void *stream);
 

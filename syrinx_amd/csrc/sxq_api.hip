@@ -319,24 +319,28 @@ sxq_status plan_forward(const sxq_qmm* q, const int64_t* shape, int ndim, const 
     p->m = m;
     p->vdt = vec_dot_type(q->w.dtype);
     p->nbv = q->w.k / block_size(p->vdt);
-    // Many rows of a Q4_K weight: the f16 MFMA GEMM (operands rounded to f16, error below
-    // 2^-10 * sum |w x| per output) unless SXQ_BIT_EXACT asks for Candle's integer vec-dot.
-    p->gemm = q->w.dtype == kQ4K && m >= kGemmMinRows && !(flags & SXQ_BIT_EXACT);
+    // Many rows: a GEMM, one pass over the weights.  Q8_0 / Q4_0 run the int8 matrix-core
+    // GEMM, bit-identical to Candle's vec-dot.  Q4_K runs the f16 MFMA GEMM (operands
+    // rounded to f16, error below 2^-10 * sum |w x| per output) unless SXQ_BIT_EXACT asks
+    // for Candle's integer vec-dot (the GEMV, 16 rows at a time).
+    const bool q80 = q->w.dtype == kQ8_0 || q->w.dtype == kQ4_0;
+    p->gemm = q80 ? m >= kGemmQ80MinRows : (m >= kGemmMinRows && !(flags & SXQ_BIT_EXACT));
     p->ws = m == 0 ? 0
-                   : up256(p->gemm ? gemm_q4k_workspace(q->w.n, (int)m, q->w.k)
-                                   : (size_t)m * (size_t)p->nbv * act_block_bytes(p->vdt));
+                   : up256(p->gemm && !q80 ? gemm_q4k_workspace(q->w.n, (int)m, q->w.k)
+                                           : (size_t)m * (size_t)p->nbv * act_block_bytes(p->vdt));
     return SXQ_OK;
 }
 
 hipError_t run_forward(const sxq_qmm* q, const FwdPlan& p, const float* x, float* y, const float* bias, uint8_t* ws,
                        hipStream_t s) {
     const int64_t k = q->w.k, n = q->w.n, m = p.m;
-    if (p.gemm) {
+    if (p.gemm && q->w.dtype == kQ4K) {
         hipError_t e = launch_gemm_q4k_prep(x, k, (int)m, n, (int)k, ws, s);
         if (e == hipSuccess) e = launch_gemm_q4k(q->w, ws, (int)m, y, n, bias, nullptr, 0, s);
         return e;
     }
     hipError_t e = launch_quantize_act(p.vdt, false, x, k, (int)m, (int)k, ws, s);
+    if (p.gemm) return e == hipSuccess ? launch_gemm_q80(q->w, ws, (int)m, y, n, bias, nullptr, 0, s) : e;
     for (int64_t r0 = 0; r0 < m && e == hipSuccess; r0 += 16) {
         const int mm = (int)(m - r0 < 16 ? m - r0 : 16);
         e = launch_gemv(q->w, ws + (size_t)r0 * p.nbv * act_block_bytes(p.vdt), mm, y + r0 * n, n, bias, nullptr, 0, s);

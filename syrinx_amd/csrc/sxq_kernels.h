@@ -60,10 +60,17 @@ hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const
 // operands (+ bias, + res).  The workspace (gemm_q4k_workspace bytes) holds x rounded to
 // f16 in the GEMM's K order and, when K is split across workgroups, the partial tiles
 // and their counters; launch_gemm_q4k_prep fills it from x, then launch_gemm_q4k runs.
-constexpr int kGemmMinRows = 64;  // QMatMul::forward uses the GEMM from this many rows on
+constexpr int kGemmMinRows = 64;  // QMatMul::forward uses the Q4_K GEMM from this many rows on
+constexpr int kGemmQ80MinRows = 128;  // ... and the Q8_0 / Q4_0 GEMM (below: the GEMV, 16 rows at a time)
 size_t gemm_q4k_workspace(int64_t n, int m, int64_t k);
 hipError_t launch_gemm_q4k_prep(const float* x, int64_t ldx, int m, int64_t n, int k, void* ws, hipStream_t s);
 hipError_t launch_gemm_q4k(const QWeight& w, const void* ws, int m, float* y, int64_t ldy, const float* bias,
+                           const float* res, int64_t ldr, hipStream_t s);
+
+// Prefill GEMM for Q8_0 / Q4_0 weights (sxq_gemm_q80.hip): the same outputs as the GEMV
+// (Candle's vec-dot, bit for bit) from one pass over the weights on the int8 matrix
+// cores.  act: the Q8_0 activation blocks [m][nb] of launch_quantize_act (device layout).
+hipError_t launch_gemm_q80(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                            const float* res, int64_t ldr, hipStream_t s);
 
 }  // namespace sxq

@@ -256,6 +256,32 @@ PREFILL = [
 ]
 
 
+# Q8_0 / Q4_0 prompts: the int8 matrix-core GEMM, bit-identical to the oracle at every row
+# count (dtype, weight rows n, k, prompt rows m, with bias)
+PREFILL_Q80 = [
+    (G.Q8_0, 4864, 896, 512, False),   # CosyVoice2 gate/up at a 512-token prompt
+    (G.Q8_0, 896, 4864, 130, True),    # down projection, rows not a multiple of the 64-row tile
+    (G.Q4_0, 896, 896, 128, True),     # the dtype the reference ships, exactly two row tiles
+    (G.Q4_0, 1003, 896, 200, False),   # weight rows not a multiple of the 128-row tile
+    (G.Q8_0, 6144, 2560, 160, False),  # Qwen3-4B wqkv, Q8_0
+    (G.Q4_0, 6564, 896, 129, True),    # CosyVoice2 head shape, one row into the third tile
+]
+
+
+@pytest.mark.parametrize("dt,n,k,m,with_bias", PREFILL_Q80)
+def test_prefill_gemm_q8_0_q4_0_bit_exact(cuda, ora, dt, n, k, m, with_bias):
+    w = _weights(n, k, 80 + m)
+    x = _acts(m, k, 81 + m)
+    blocks = ora.quantize(int(dt), w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), dt, device=cuda))
+    b = (np.random.default_rng(82).standard_normal(n) * 0.02).astype(np.float32) if with_bias else None
+    y = qmm.forward(torch.from_numpy(x).to(cuda), bias=None if b is None else torch.from_numpy(b).to(cuda))
+    want = ora.matmul(int(dt), x, blocks)
+    if b is not None:
+        want = (want + b[None, :]).astype(np.float32)
+    _eq_bits(y.cpu().numpy(), want)
+
+
 def _prefill_check(ora, x, blocks, k, y, b=None):
     wd = ora.dequantize(ora.Q4K, blocks, k).reshape(-1, k).astype(np.float64)  # Candle's to_float, exact
     y64 = x.astype(np.float64) @ wd.T + (0.0 if b is None else b.astype(np.float64))
