@@ -265,6 +265,34 @@ sxq_status sxq_lm_get_lengths(const sxq_lm *lm, int32_t *lengths, int n_streams)
  * Each stream's token is placed at its current length, which then advances by one. */
 sxq_status sxq_lm_step(sxq_lm *lm, int n_streams, const int32_t *ids, const float *embeds, float *logits,
                        float *hidden, int32_t *next_ids, unsigned flags, void *stream);
+/* sxq_lm_prefill flags */
+#define SXQ_LM_EXACT 2u      /* Q4_K projections through Candle's integer vec-dot (bit-identical) rather than the
+                                f16 MFMA GEMM; Q8_0 / Q4_0 are bit-identical either way */
+#define SXQ_LM_ALL_LOGITS 4u /* logits (and hidden) for every prompt token, as Qwen2Lm::forward_logits_cached
+                                returns them; otherwise only each stream's last prompt token (SlowAr::prefill) */
+
+/* Prompt prefill of streams 0..n_streams-1 (device pointers, enqueued on `stream`):
+ *   SlowAr::prefill / prefill_batch (crates/syrinx-fish/src/s2/slow_ar.rs:250-256, 404-454),
+ *   Qwen2Lm::forward_logits_cached with t_new > 1 (crates/syrinx-lm/src/cv2/mod.rs:261-286).
+ * counts  host int32 [n_streams], tokens per stream (>= 1 each; ragged, no padding);
+ * ids     int32 [sum counts, 1 + n_codebooks] stream-major token frames, or NULL;
+ * embeds  f32 [sum counts, dim] input embeddings instead of ids, or NULL;
+ * Stream s's tokens take positions len[s] .. len[s] + counts[s] - 1 (each query attends its
+ * own stream's cache up to its own position), their keys and values are written to the
+ * cache, and len[s] advances by counts[s].  Outputs (each may be NULL): logits f32
+ * [n_streams, vocab] and hidden f32 [n_streams, dim] (post-final-RMSNorm) of each stream's
+ * last token, or with SXQ_LM_ALL_LOGITS [sum counts, vocab] / [sum counts, dim];
+ * next_ids int32 [n_streams] the greedy argmax of each stream's last logits.  Every
+ * projection runs on all sum(counts) rows at once (the prefill GEMMs).
+ * trace (test instrumentation, NULL for none): the f32 intermediates as for
+ * sxq_lm_set_trace with n = sum(counts) rows per segment (the final hidden: one row per
+ * stream, or per token with SXQ_LM_ALL_LOGITS); sxq_lm_prefill_trace_floats gives its size.
+ * head_dim must be 64 or 128. */
+sxq_status sxq_lm_prefill(sxq_lm *lm, int n_streams, const int32_t *counts, const int32_t *ids,
+                          const float *embeds, float *logits, float *hidden, int32_t *next_ids, unsigned flags,
+                          float *trace, size_t trace_capacity_floats, void *stream);
+sxq_status sxq_lm_prefill_trace_floats(const sxq_lm *lm, int64_t tokens, size_t *floats);
+
 /* Enqueue only the projection GEMVs of one step (every layer's fused QKV, O, gate|up
  * and down, plus the head if with_head) on the step's current activations: the
  * GEMV share of a token, for bandwidth measurement.  No reference counterpart. */

@@ -68,6 +68,8 @@ _SIGS = {
     "sxq_lm_get_lengths": (_I, [_P, _P, _I]),
     "sxq_lm_step": (_I, [_P, _I, _P, _P, _P, _P, _P, _U, _P]),
     "sxq_lm_read_kv": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "sxq_lm_prefill": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U, _P, _SZ, _P]),
+    "sxq_lm_prefill_trace_floats": (_I, [_P, _I64, _P]),
     "sxq_lm_gemv_pass": (_I, [_P, _I, _I, _P]),
     "sxq_lm_read_state": (_I, [_P, _I, _I, _P, _P]),
     "sxq_lm_trace_floats": (_I, [_P, _I, _P]),

@@ -49,6 +49,32 @@ hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int id
                          float* pval, int* pidx, unsigned* counter, hipStream_t s);
 hipError_t launch_fill_value(float* y, int64_t n, float v, hipStream_t s);
 
+// ---- prompt prefill (sxq_prefill.hip) -------------------------------------------------
+// Per-token QK-RMSNorm + RoPE + KV write: tok[2 t] = stream, tok[2 t + 1] = position of
+// prompt token t; queries -> qout [T][nh * hd].  hd in {64, 128}.
+hipError_t launch_prefill_rope_kv(const float* qkv, int T, int qkv_n, int nh, int nkv, int hd, const float* qn,
+                                  const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
+                                  const int* tok, float* qout, float* kc, float* vc, int64_t kv_stream_stride,
+                                  int max_seq, hipStream_t s);
+// Causal GQA attention of the prompt's queries over each stream's cache; tiles[4 i ..]
+// = {stream, first token row, token count (<= prefill_tile_tokens), first position}.
+bool prefill_attn_supported(int nh, int nkv, int hd);
+int prefill_tile_tokens(int nh, int nkv);
+hipError_t launch_prefill_attn(const float* q, const float* kc, const float* vc, const int* tiles, int n_tiles, int nh,
+                               int nkv, int hd, int max_seq, int64_t kv_stream_stride, float* ctx, hipStream_t s);
+// The token and tile tables of one prefill, built on the device from the per-stream
+// token counts and cache lengths (streams 0 .. n-1, tokens stream-major): tok (2 ints per
+// token), tiles (4 ints per tile, at most T + n tiles), last[s] = row of stream s's last
+// token (-1 without tokens); lengths[s] += counts[s] when `advance` (after the layers).
+struct PrefillMeta {
+    int n, tile_tokens;
+    int counts[16], lens[16];
+};
+hipError_t launch_prefill_tables(const PrefillMeta& pm, int T, int* tok, int* tiles, int* last, hipStream_t s);
+hipError_t launch_prefill_advance(const PrefillMeta& pm, int* len, hipStream_t s);
+// dst[i] = src[idx[i]] for n rows of `cols` floats.
+hipError_t launch_gather_rows(const float* src, const int* idx, int n, int cols, float* dst, hipStream_t s);
+
 // Arguments of the fused decode attention over one step of B streams.
 struct AttnArgs {
     const float* qkv;  // [B][qkv_n]: q (nh*hd) | k (nkv*hd) | v (nkv*hd)

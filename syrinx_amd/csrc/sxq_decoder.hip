@@ -187,40 +187,6 @@ SXQ_DEV float merge_elem(const float* part_s, int h, int hh, int d, int nsp, int
     return acc / lsum[hh];
 }
 
-// Copy rows [0, n) of a K and a V tile (row stride hd floats in global memory, hd + 4 in
-// LDS) with every thread's loads of a batch in flight together -- the LDS stores wait
-// for the whole batch rather than for each load in turn.  256 threads.
-SXQ_DEV void load_kv_tile(float* kt, float* vt, const float* kb, const float* vb, int n, int hd) {
-    constexpr int kBatch = 8;  // float4 of K and of V per thread per batch
-    const int hd4 = hd / 4, n4 = n * hd4, hdp = hd + 4;
-    for (int base = 0; base < n4; base += 256 * kBatch) {
-        float4 kv[kBatch], vv[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const int i = min(base + j * 256 + (int)threadIdx.x, n4 - 1);  // clamped: in bounds
-            const int p = i / hd4, d4 = i - p * hd4;
-            kv[j] = *(const float4*)(kb + (int64_t)p * hd + 4 * d4);
-            vv[j] = *(const float4*)(vb + (int64_t)p * hd + 4 * d4);
-        }
-        // An empty asm reading every loaded register: the loads cannot be sunk to their
-        // stores (each would then wait for its own load); they are all issued first and
-        // the stores below wait once for the batch.  It emits no instruction.
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j)
-            asm volatile("" ::"v"(kv[j].x), "v"(kv[j].y), "v"(kv[j].z), "v"(kv[j].w), "v"(vv[j].x), "v"(vv[j].y),
-                         "v"(vv[j].z), "v"(vv[j].w));
-        // clamped like the loads (unconditional, so no branch pulls a load down to its
-        // store): out-of-range threads rewrite the last row element with its own value
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const int i = min(base + j * 256 + (int)threadIdx.x, n4 - 1);
-            const int p = i / hd4, d4 = i - p * hd4;
-            *(float4*)(kt + p * hdp + 4 * d4) = kv[j];
-            *(float4*)(vt + p * hdp + 4 * d4) = vv[j];
-        }
-    }
-}
-
 // ------------------------------------------------------------- split-K decode attention
 // One workgroup takes P consecutive cached positions of one KV head for all G = nh/nkv
 // query heads sharing it (GQA without materialising repeat_kv) and writes per-head

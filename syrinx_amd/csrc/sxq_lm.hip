@@ -77,6 +77,8 @@ struct sxq_lm {
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
     hipStream_t cap = nullptr;
     std::map<GraphKey, hipGraphExec_t> graphs;
+    void* pf = nullptr;  // prefill workspace, grown to the largest prompt batch so far
+    size_t pf_size = 0;
     std::vector<void*> allocs;
     std::mutex mu;
 };
@@ -235,6 +237,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
 
 void destroy_lm(sxq_lm* lm) {
     for (auto& kv : lm->graphs) (void)hipGraphExecDestroy(kv.second);
+    if (lm->pf) (void)hipFree(lm->pf);
     if (lm->cap) (void)hipStreamDestroy(lm->cap);
     for (void* p : lm->allocs) (void)hipFree(p);
     delete lm;
@@ -261,6 +264,172 @@ sxq_status check_config(const sxq_lm_config* c) {
     if (c->n_codebooks < 0 || (c->n_codebooks > 0 && (c->codebook_size <= 0 || !c->tied_embedding)))
         return fail(SXQ_ERR_INVALID, "lm_create: codebooks need codebook_size > 0 and a tied embedding");
     return SXQ_OK;
+}
+
+// ---- prompt prefill -----------------------------------------------------------------
+
+// One projection of T prompt rows: x_f32 [T][k] (f32 rows) and act (the same rows as
+// device activation blocks) -> y [T][n] (+ bias, then res + that).  Q4_K: the f16 MFMA GEMM
+// from kGemmMinRows rows unless `exact`; Q8_0 / Q4_0: the int8 matrix-core GEMM from
+// kGemmQ80MinRows rows; otherwise the GEMV, 16 rows at a time (Candle's bits).
+hipError_t pf_proj(const sxq_lm* lm, const QWeight& w, const float* x, const uint8_t* act, int T, float* y,
+                   const float* bias, const float* res, bool exact, void* gemm_ws, hipStream_t s) {
+    const int64_t n = w.n;
+    if (w.dtype == kQ4K && !exact && T >= kGemmMinRows) {
+        hipError_t e = launch_gemm_q4k_prep(x, w.k, T, n, (int)w.k, gemm_ws, s);
+        return e == hipSuccess ? launch_gemm_q4k(w, gemm_ws, T, y, n, bias, res, n, s) : e;
+    }
+    if (w.dtype != kQ4K && T >= kGemmQ80MinRows) return launch_gemm_q80(w, act, T, y, n, bias, res, n, s);
+    const size_t rowb = (size_t)(w.k / block_size(lm->vdt)) * act_block_bytes(lm->vdt);
+    for (int r0 = 0; r0 < T; r0 += 16) {
+        const int mm = T - r0 < 16 ? T - r0 : 16;
+        hipError_t e = launch_gemv(w, act + (size_t)r0 * rowb, mm, y + (int64_t)r0 * n, n, bias,
+                                   res ? res + (int64_t)r0 * n : nullptr, n, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// Device buffers of one prefill of T tokens over n streams (offsets into lm->pf).
+struct PfLayout {
+    size_t h, hn, qkv, q, cx, gu, af, act, gemm, tok, tiles, last, total;
+};
+
+PfLayout pf_layout(const sxq_lm* lm, int T, int n) {
+    const sxq_lm_config& c = lm->c;
+    auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const size_t bs = block_size(lm->vdt), ab = act_block_bytes(lm->vdt);
+    int64_t kmax = c.dim > lm->ctx ? c.dim : lm->ctx;
+    if (c.intermediate > kmax) kmax = c.intermediate;
+    size_t gemm = 0;
+    if (c.weight_dtype == kQ4K) {
+        const LmLayer& L = lm->layers[0];
+        for (const QWeight* w : {&L.wqkv.w, &L.wo.w, &L.w13.w, &L.w2.w}) {
+            const size_t g = gemm_q4k_workspace(w->n, T, w->k);
+            if (g > gemm) gemm = g;
+        }
+        const size_t g = gemm_q4k_workspace(lm->head.w.n, T, lm->head.w.k);
+        if (g > gemm) gemm = g;
+    }
+    PfLayout p{};
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o += up(bytes);
+        return at;
+    };
+    p.h = take(sizeof(float) * (size_t)T * c.dim);
+    p.hn = take(sizeof(float) * (size_t)T * c.dim);
+    p.qkv = take(sizeof(float) * (size_t)T * lm->qkv_n);
+    p.q = take(sizeof(float) * (size_t)T * lm->ctx);
+    p.cx = take(sizeof(float) * (size_t)T * lm->ctx);
+    p.gu = take(sizeof(float) * (size_t)T * 2 * c.intermediate);
+    p.af = take(sizeof(float) * (size_t)T * c.intermediate);
+    p.act = take((size_t)T * (size_t)(kmax / (int64_t)bs) * ab);
+    p.gemm = take(gemm);
+    p.tok = take(sizeof(int) * 2 * (size_t)T);
+    p.tiles = take(sizeof(int) * 4 * (size_t)(T + n));
+    p.last = take(sizeof(int) * (size_t)n);
+    p.total = o;
+    return p;
+}
+
+size_t pf_trace_floats(const sxq_lm* lm, int T) { return trace_floats(lm, T); }
+
+hipError_t enqueue_prefill(sxq_lm* lm, const PrefillMeta& pm, int T, const int* ids, const float* embeds,
+                           float* logits_all, float* hidden_all, bool exact, float* tr, hipStream_t s) {
+    const sxq_lm_config& c = lm->c;
+    const PfLayout P = pf_layout(lm, T, pm.n);
+    uint8_t* base = (uint8_t*)lm->pf;
+    float* h = (float*)(base + P.h);
+    float* hn = (float*)(base + P.hn);
+    float* qkv = (float*)(base + P.qkv);
+    float* q = (float*)(base + P.q);
+    float* cx = (float*)(base + P.cx);
+    float* gu = (float*)(base + P.gu);
+    float* af = (float*)(base + P.af);
+    uint8_t* act = base + P.act;
+    void* gws = base + P.gemm;
+    int* tok = (int*)(base + P.tok);
+    int* tiles = (int*)(base + P.tiles);
+    int* last = (int*)(base + P.last);
+    const int I = c.intermediate, n = pm.n;
+    const size_t Td = (size_t)T * c.dim;
+    hipError_t e = hipSuccess;
+#define PF(x)                          \
+    do {                               \
+        e = (x);                       \
+        if (e != hipSuccess) return e; \
+    } while (0)
+    auto record = [&](const float* src, size_t floats) -> hipError_t {
+        if (!tr) return hipSuccess;
+        hipError_t r = hipMemcpyAsync(tr, src, floats * sizeof(float), hipMemcpyDeviceToDevice, s);
+        tr += floats;
+        return r;
+    };
+    int n_tiles = 0;
+    for (int i = 0; i < n; ++i) n_tiles += (pm.counts[i] + pm.tile_tokens - 1) / pm.tile_tokens;
+    PF(launch_prefill_tables(pm, T, tok, tiles, last, s));
+    if (embeds) {
+        PF(hipMemcpyAsync(h, embeds, sizeof(float) * Td, hipMemcpyDeviceToDevice, s));
+    } else if (c.tied_embedding) {
+        PF(launch_embed_quant_table(ids, lm->ids_per, T, lm->head.w, c.dim, lm->cb_embed, c.n_codebooks,
+                                    c.codebook_size, c.semantic_begin, c.semantic_end, h, s));
+    } else {
+        PF(launch_embed_dense(ids, lm->ids_per, T, lm->embed, c.embed_rows > 0 ? c.embed_rows : c.vocab, c.dim, h, s));
+    }
+    PF(record(h, Td));
+    for (int l = 0; l < c.n_layers; ++l) {
+        LmLayer& L = lm->layers[l];
+        float* kc = lm->kc + (int64_t)l * lm->kv_layer_stride;
+        float* vc = lm->vc + (int64_t)l * lm->kv_layer_stride;
+        PF(launch_rmsnorm_quant(lm->vdt, h, T, c.dim, L.attn_norm, c.norm_eps, act, hn, s));
+        PF(record(hn, Td));
+        PF(pf_proj(lm, L.wqkv.w, hn, act, T, qkv, L.bqkv, nullptr, exact, gws, s));
+        PF(record(qkv, (size_t)T * lm->qkv_n));
+        PF(launch_prefill_rope_kv(qkv, T, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim,
+                                  c.qk_norm ? L.q_norm : nullptr, c.qk_norm ? L.k_norm : nullptr, c.norm_eps,
+                                  c.rope_interleaved, lm->rope_cos, lm->rope_sin, tok, q, kc, vc,
+                                  lm->kv_stream_stride, c.max_seq, s));
+        PF(record(q, (size_t)T * lm->ctx));
+        PF(launch_prefill_attn(q, kc, vc, tiles, n_tiles, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq,
+                               lm->kv_stream_stride, cx, s));
+        PF(record(cx, (size_t)T * lm->ctx));
+        PF(launch_quantize_act(lm->vdt, false, cx, lm->ctx, T, lm->ctx, act, s));
+        PF(pf_proj(lm, L.wo.w, cx, act, T, h, nullptr, h, exact, gws, s));
+        PF(record(h, Td));
+        PF(launch_rmsnorm_quant(lm->vdt, h, T, c.dim, L.ffn_norm, c.norm_eps, act, hn, s));
+        PF(record(hn, Td));
+        PF(pf_proj(lm, L.w13.w, hn, act, T, gu, nullptr, nullptr, exact, gws, s));
+        PF(record(gu, (size_t)T * 2 * I));
+        PF(launch_silu_mul_quant(lm->vdt, gu, T, I, act, af, s));
+        PF(record(af, (size_t)T * I));
+        PF(pf_proj(lm, L.w2.w, af, act, T, h, nullptr, h, exact, gws, s));
+        PF(record(h, Td));
+    }
+    const float* hb = c.head_bias ? lm->head_bias : nullptr;
+    if (logits_all) {  // the head over every prompt row (Qwen2Lm::forward_logits_cached)
+        PF(launch_rmsnorm_quant(lm->vdt, h, T, c.dim, lm->final_norm, c.norm_eps, act, hn, s));
+        PF(pf_proj(lm, lm->head.w, hn, act, T, logits_all, hb, nullptr, exact, gws, s));
+        if (hidden_all) PF(hipMemcpyAsync(hidden_all, hn, sizeof(float) * Td, hipMemcpyDeviceToDevice, s));
+        PF(record(hn, Td));
+        PF(launch_gather_rows(hn, last, n, c.dim, lm->hn, s));
+        PF(launch_gather_rows(logits_all, last, n, c.vocab, lm->logits, s));
+    } else {  // the head on each stream's last row (SlowAr::head), as the decode step runs it
+        PF(launch_gather_rows(h, last, n, c.dim, lm->h, s));
+        NormIn ni;
+        ni.x = lm->h;
+        ni.w = lm->final_norm;
+        ni.eps = c.norm_eps;
+        ni.normed = lm->hn;
+        PF(launch_gemv_rmsnorm(lm->head.w, ni, n, lm->act_a, lm->logits, c.vocab, hb, nullptr, 0, s));
+        PF(record(lm->hn, (size_t)n * c.dim));
+    }
+    PF(launch_argmax(lm->logits, n, c.vocab, lm->d_ids, lm->ids_per, lm->d_next, nullptr, lm->am_val, lm->am_idx,
+                     lm->am_count, s));
+    PF(launch_prefill_advance(pm, lm->d_len, s));
+#undef PF
+    return hipSuccess;
 }
 
 }  // namespace
@@ -588,6 +757,74 @@ sxq_status sxq_lm_step(sxq_lm* lm, int n, const int32_t* ids, const float* embed
     if (hidden)
         HIP_TRY(hipMemcpyAsync(hidden, lm->hn, sizeof(float) * n * lm->c.dim, hipMemcpyDeviceToDevice, st), "lm_step: hidden");
     if (next_ids) HIP_TRY(hipMemcpyAsync(next_ids, lm->d_next, sizeof(int) * n, hipMemcpyDeviceToDevice, st), "lm_step: next ids");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_prefill_trace_floats(const sxq_lm* lm, int64_t tokens, size_t* floats) {
+    if (!lm || !floats) return fail(SXQ_ERR_INVALID, "lm_prefill_trace_floats: null pointer");
+    if (tokens < 1 || tokens > 65535) return fail(SXQ_ERR_INVALID, "lm_prefill_trace_floats: bad token count");
+    *floats = pf_trace_floats(lm, (int)tokens);
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_prefill(sxq_lm* lm, int n, const int32_t* counts, const int32_t* ids, const float* embeds,
+                          float* logits, float* hidden, int32_t* next_ids, unsigned flags, float* trace,
+                          size_t trace_capacity, void* stream) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_prefill: null handle");
+    if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_prefill: %d streams (max %d)", n, lm->c.max_batch);
+    if (!counts) return fail(SXQ_ERR_INVALID, "lm_prefill: null token counts");
+    if (flags & ~(SXQ_LM_EXACT | SXQ_LM_ALL_LOGITS)) return fail(SXQ_ERR_INVALID, "lm_prefill: unknown flags 0x%x", flags);
+    if (!ids == !embeds) return fail(SXQ_ERR_INVALID, "lm_prefill: give exactly one of ids and embeds");
+    const sxq_lm_config& c = lm->c;
+    if (!prefill_attn_supported(c.n_heads, c.n_kv_heads, c.head_dim))
+        return fail(SXQ_ERR_SHAPE, "lm_prefill: head_dim %d (64 or 128) or %d query heads per KV head unsupported",
+                    c.head_dim, c.n_heads / c.n_kv_heads);
+    std::lock_guard<std::mutex> lock(lm->mu);
+    PrefillMeta pm{};
+    pm.n = n;
+    pm.tile_tokens = prefill_tile_tokens(c.n_heads, c.n_kv_heads);
+    int64_t T = 0;
+    for (int s = 0; s < n; ++s) {
+        if (counts[s] < 0) return fail(SXQ_ERR_INVALID, "lm_prefill: negative token count for stream %d", s);
+        if ((int64_t)lm->h_len[s] + counts[s] > c.max_seq)
+            return fail(SXQ_ERR_INVALID, "lm_prefill: stream %d: %d cached + %d new positions exceed %d", s,
+                        lm->h_len[s], counts[s], c.max_seq);
+        pm.counts[s] = counts[s];
+        pm.lens[s] = lm->h_len[s];
+        T += counts[s];
+    }
+    if (T == 0) return SXQ_OK;
+    if (T > 65535) return fail(SXQ_ERR_INVALID, "lm_prefill: %lld tokens exceed 65535", (long long)T);
+    for (int s = 0; s < n; ++s)
+        if (counts[s] == 0) return fail(SXQ_ERR_INVALID, "lm_prefill: stream %d has no tokens", s);
+    if (trace && trace_capacity < pf_trace_floats(lm, (int)T))
+        return fail(SXQ_ERR_SHAPE, "lm_prefill: trace of %zu floats, %zu needed", trace_capacity,
+                    pf_trace_floats(lm, (int)T));
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    hipStream_t st = (hipStream_t)stream;
+    const PfLayout P = pf_layout(lm, (int)T, n);
+    if (lm->pf_size < P.total) {
+        HIP_TRY(hipDeviceSynchronize(), "lm_prefill: sync before regrowing the workspace");
+        if (lm->pf) (void)hipFree(lm->pf);
+        lm->pf = nullptr;
+        lm->pf_size = 0;
+        HIP_TRY(hipMalloc(&lm->pf, P.total), "lm_prefill: workspace");
+        lm->pf_size = P.total;
+    }
+    const bool all = (flags & SXQ_LM_ALL_LOGITS) != 0;
+    if (all && !logits) return fail(SXQ_ERR_INVALID, "lm_prefill: SXQ_LM_ALL_LOGITS needs a logits buffer");
+    HIP_TRY(enqueue_prefill(lm, pm, (int)T, ids, embeds, all ? logits : nullptr, all ? hidden : nullptr,
+                            (flags & SXQ_LM_EXACT) != 0, trace, st),
+            "lm_prefill");
+    for (int s = 0; s < n; ++s) lm->h_len[s] += counts[s];
+    if (logits && !all)
+        HIP_TRY(hipMemcpyAsync(logits, lm->logits, sizeof(float) * n * c.vocab, hipMemcpyDeviceToDevice, st),
+                "lm_prefill: logits");
+    if (hidden && !all)
+        HIP_TRY(hipMemcpyAsync(hidden, lm->hn, sizeof(float) * n * c.dim, hipMemcpyDeviceToDevice, st),
+                "lm_prefill: hidden");
+    if (next_ids) HIP_TRY(hipMemcpyAsync(next_ids, lm->d_next, sizeof(int) * n, hipMemcpyDeviceToDevice, st), "lm_prefill: ids");
     return SXQ_OK;
 }
 

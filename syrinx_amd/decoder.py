@@ -21,6 +21,8 @@ from ._lib import check, lib
 from .quantized import GgmlDType, QMatMul
 
 LM_GRAPH = 1
+LM_EXACT = 2       # prefill: Q4_K projections through Candle's integer vec-dot (bit-identical)
+LM_ALL_LOGITS = 4  # prefill: logits / hidden for every prompt token
 WQKV, WQ, WK, WV, WO, W1, W3, W2, HEAD = range(9)
 ATTN_NORM, FFN_NORM, Q_NORM, K_NORM, BQ, BK, BV, FINAL_NORM, HEAD_BIAS, EMBED, CODEBOOK_EMBED = range(11)
 
@@ -177,6 +179,45 @@ class DecoderLM:
                                 torch.cuda.current_stream(self.device).cuda_stream))
         return (logits, nxt, hidden) if want_hidden else (logits, nxt)
 
+    def prefill(self, prompts=None, embeds=None, exact: bool = False, all_logits: bool = False, trace: bool = False):
+        """Prompt prefill of streams 0..n-1 (sxq_lm_prefill): prompts is a list (one entry
+        per stream) of int32 token frames [T_s, 1 + n_codebooks] (or [T_s]), or embeds a
+        list of f32 [T_s, dim].  Each stream's tokens go at its current length, which then
+        advances by T_s.  Returns (logits, next_ids, hidden): logits [n, vocab] and hidden
+        [n, dim] of each stream's last token, or [sum T_s, ...] with all_logits; with
+        trace=True a fourth item, the trace of every intermediate (as trace())."""
+        c = self.cfg
+        if (prompts is None) == (embeds is None):
+            raise ValueError("prefill: give prompts or embeds")
+        rows = prompts if prompts is not None else embeds
+        n = len(rows)
+        if prompts is not None:
+            mats = [torch.as_tensor(p, dtype=torch.int32).reshape(-1, self.ids_per) for p in prompts]
+        else:
+            mats = [torch.as_tensor(e, dtype=torch.float32).reshape(-1, c.dim) for e in embeds]
+        counts = [int(m.shape[0]) for m in mats]
+        T = sum(counts)
+        data = torch.cat(mats).to(self.device).contiguous()
+        out_rows = T if all_logits else n
+        logits = torch.empty((out_rows, c.vocab), dtype=torch.float32, device=self.device)
+        hidden = torch.empty((out_rows, c.dim), dtype=torch.float32, device=self.device)
+        nxt = torch.empty((n,), dtype=torch.int32, device=self.device)
+        tr = None
+        if trace:
+            sz = ctypes.c_size_t()
+            check(lib().sxq_lm_prefill_trace_floats(self._h, T, ctypes.byref(sz)))
+            tr = torch.zeros(int(sz.value), dtype=torch.float32, device=self.device)
+        P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+        cnt = (ctypes.c_int32 * n)(*counts)
+        flags = (LM_EXACT if exact else 0) | (LM_ALL_LOGITS if all_logits else 0)
+        check(lib().sxq_lm_prefill(self._h, n, cnt, P(data) if prompts is not None else None,
+                                   P(data) if embeds is not None else None, P(logits), P(hidden), P(nxt), flags,
+                                   P(tr), tr.numel() if tr is not None else 0,
+                                   torch.cuda.current_stream(self.device).cuda_stream))
+        if trace:
+            return logits, nxt, hidden, self._parse_trace(tr.cpu().numpy(), T, out_rows)
+        return logits, nxt, hidden
+
     TRACE_SEGMENTS = ("hn_attn", "qkv", "q", "ctx", "h_mid", "hn_ffn", "gu", "act", "h_out")
 
     def enable_trace(self, on: bool = True) -> None:
@@ -193,8 +234,10 @@ class DecoderLM:
     def trace(self, n: int) -> dict:
         """The last traced step of n streams: {'embed': [n, dim], 'final_hn': [n, dim],
         'layers': [{segment: [n, size]} per layer]} as numpy arrays."""
+        return self._parse_trace(self._trace.cpu().numpy(), n, n)
+
+    def _parse_trace(self, t, n: int, n_final: int) -> dict:
         c = self.cfg
-        t = self._trace.cpu().numpy()
         qkv_n = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
         ctx = c.n_heads * c.head_dim
         sizes = dict(hn_attn=c.dim, qkv=qkv_n, q=ctx, ctx=ctx, h_mid=c.dim, hn_ffn=c.dim, gu=2 * c.intermediate,
@@ -210,7 +253,7 @@ class DecoderLM:
         out = {"embed": take(c.dim), "layers": []}
         for _ in range(c.n_layers):
             out["layers"].append({seg: take(sizes[seg]) for seg in self.TRACE_SEGMENTS})
-        out["final_hn"] = take(c.dim)
+        out["final_hn"] = t[off: off + n_final * c.dim].reshape(n_final, c.dim)
         return out
 
     def read_state(self, which: int, n: int = 1) -> torch.Tensor:
@@ -255,6 +298,24 @@ class SlowAr(DecoderLM):
         self._last_argmax = nxt
         return logits, hidden.reshape(hidden.shape[0], 1, -1)
 
+    def prefill(self, prompt, graph: bool = False):
+        """SlowAr::prefill (slow_ar.rs:250-256): prompt [1 + num_codebooks, T] (rows =
+        semantic ids then codebooks) into the cache at its current length.  Returns
+        (semantic_logits [vocab], hidden [1, 1, dim]) of the last prompt position."""
+        p = torch.as_tensor(prompt, dtype=torch.int32).reshape(self.ids_per, -1).t().contiguous()
+        logits, nxt, hidden = super().prefill(prompts=[p])
+        self._last_argmax = nxt
+        return logits[0], hidden.reshape(1, 1, -1)
+
+    def prefill_batch(self, prompts):
+        """SlowAr::prefill_batch (slow_ar.rs:404-454): ragged prompts [1 + num_codebooks,
+        T_i], one per stream, without left padding.  Returns (logits [n, vocab], hidden
+        [n, 1, dim]) of every stream's last prompt position."""
+        ps = [torch.as_tensor(p, dtype=torch.int32).reshape(self.ids_per, -1).t().contiguous() for p in prompts]
+        logits, nxt, hidden = super().prefill(prompts=ps)
+        self._last_argmax = nxt
+        return logits, hidden.reshape(len(ps), 1, -1)
+
     def last_argmax(self) -> torch.Tensor:
         """Greedy argmax ids [n] of the last step's logits (device int32)."""
         return self._last_argmax
@@ -264,7 +325,12 @@ class Qwen2Lm(DecoderLM):
     """CosyVoice2 LM cached decode (crates/syrinx-lm/src/cv2/mod.rs:255-286)."""
 
     def forward_logits_cached(self, embeds: torch.Tensor, graph: bool = True):
-        """embeds [b, 1, 896] -> logits [b, 1, 6564] for one new position per stream."""
-        b = embeds.shape[0]
-        logits, _ = self.step(embeds=embeds.reshape(b, -1), graph=graph)
-        return logits.reshape(b, 1, -1)
+        """embeds [b, t_new, 896] -> logits [b, t_new, 6564] for the new positions of every
+        stream (cv2/mod.rs:283-286): one decode step for t_new = 1, the prompt prefill with
+        every position's logits otherwise."""
+        b, t = embeds.shape[0], embeds.shape[1] if embeds.dim() == 3 else 1
+        if t == 1:
+            logits, _ = self.step(embeds=embeds.reshape(b, -1), graph=graph)
+            return logits.reshape(b, 1, -1)
+        logits, _, _ = self.prefill(embeds=[embeds[i].reshape(t, -1) for i in range(b)], all_logits=True)
+        return logits.reshape(b, t, -1)

@@ -565,3 +565,216 @@ def test_slow_step_returns_logits_and_hidden(cuda, ora):
     _glue_close(hidden.cpu().numpy()[0, 0], ora.rms_norm(h_last, np.ones(cfg.dim, np.float32), cfg.norm_eps),
                 "hidden vs oracle RMSNorm of the last residual")
     assert int(lm.last_argmax()[0]) == int(np.argmax(logits.cpu().numpy()))
+
+
+# ----------------------------------------------------------------------------- prefill
+def _f16_bound_ok(got, x, blocks, dt, k, what, bias=None):
+    """A projection of the f16 MFMA prefill GEMM: within the f16 rounding bound of the
+    f64 product of the exactly dequantized weight (the QMatMul GEMM's contract)."""
+    import oracle as ora_mod
+    wd = ora_mod.dequantize(dt, blocks, k).reshape(-1, k).astype(np.float64)
+    y64 = x.astype(np.float64) @ wd.T + (0.0 if bias is None else bias.astype(np.float64))
+    S = np.abs(x).astype(np.float64) @ np.abs(wd).T
+    tol = (2.0 ** -10 + k * 2.0 ** -24) * S + 2.0 ** -24 * np.abs(x).sum(1, keepdims=True) + 2.0 ** -24 * np.abs(
+        wd).sum(1)[None, :] + 1e-30
+    err = np.abs(got.astype(np.float64) - y64)
+    assert (err <= tol).all(), f"{what}: {(err > tol).sum()} beyond the f16 bound"
+
+
+def _replay_prefill(ora, lm, cfg, W, tr, counts, lens0, frames, exact):
+    """Check every op of a traced prefill: token t of stream s sits at position
+    lens0[s] + i; projections bit-exact (exact / Q8_0 / Q4_0) or within the f16 bound (the
+    Q4_K GEMM at >= 64 rows), glue to GLUE_RTOL, attention re-run by the oracle over the
+    GPU's own cache (whose rows are checked against the traced keys and values)."""
+    dt = int(cfg.weight_dtype)
+    hd, nh, nkv = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    G = nh // nkv
+    T = sum(counts)
+    gemm_f16 = dt == int(GgmlDType.Q4K) and not exact and T >= 64
+    rows = [(s, lens0[s] + i) for s in range(len(counts)) for i in range(counts[s])]
+    maxpos = max(p for _, p in rows) + 1
+    cos, sin = (ora.rope_tables_interleaved(maxpos, hd, cfg.rope_theta) if cfg.rope_interleaved
+                else ora.rope_tables_half(maxpos, hd, cfg.rope_theta))
+    rope = ora.rope_interleaved if cfg.rope_interleaved else ora.rope_half
+    if frames is not None:
+        import model
+        orc = model.OracleDecoder(cfg, W, 1)
+        for t in range(T):
+            _bits_equal(tr["embed"][t], orc.embed(frames[t]), f"embedding row {t}")
+
+    def proj(x, key, what, bias=None, res=None):
+        blocks = W[key]
+        if gemm_f16:
+            y = None  # compared against the traced output below
+            return y
+        y = ora.matmul(dt, x, blocks)
+        if bias is not None:
+            y = (y + bias[None, :]).astype(np.float32)
+        if res is not None:
+            y = (res + y).astype(np.float32)
+        return y
+
+    caches = {}
+    for l, Tl in enumerate(tr["layers"]):
+        h_in = tr["embed"] if l == 0 else tr["layers"][l - 1]["h_out"]
+        tag = f"layer {l}"
+        for t in range(T):
+            _glue_close(Tl["hn_attn"][t], ora.rms_norm(h_in[t], W[("attn_norm", l)], cfg.norm_eps), f"{tag} row {t} RMSNorm")
+        bias = W[("bqkv", l)] if cfg.qkv_bias else None
+        if gemm_f16:
+            _f16_bound_ok(Tl["qkv"], Tl["hn_attn"], W[("wqkv", l)], dt, cfg.dim, f"{tag} qkv", bias)
+        else:
+            _bits_equal(Tl["qkv"], proj(Tl["hn_attn"], ("wqkv", l), "qkv", bias), f"{tag} qkv projection")
+        for t, (s, p) in enumerate(rows):
+            q = Tl["qkv"][t][: nh * hd].reshape(nh, hd)
+            k = Tl["qkv"][t][nh * hd:(nh + nkv) * hd].reshape(nkv, hd)
+            v = Tl["qkv"][t][(nh + nkv) * hd:].reshape(nkv, hd)
+            if cfg.qk_norm:
+                q = np.stack([ora.rms_norm(q[i], W[("q_norm", l)], cfg.norm_eps) for i in range(nh)])
+                k = np.stack([ora.rms_norm(k[i], W[("k_norm", l)], cfg.norm_eps) for i in range(nkv)])
+            _glue_close(Tl["q"][t], rope(q, cos[p], sin[p]).reshape(-1), f"{tag} row {t} QK-norm + RoPE (q)")
+            kr = rope(k, cos[p], sin[p])
+            ctx = np.zeros(nh * hd, np.float32)
+            for g in range(nkv):
+                if (l, s, g) not in caches:
+                    kc, vc = lm.read_kv(l, s, g, 0, lens0[s] + counts[s])
+                    caches[(l, s, g)] = (kc.cpu().numpy(), vc.cpu().numpy())
+                kc, vc = caches[(l, s, g)]
+                _glue_close(kc[p], kr[g], f"{tag} row {t} key (head {g})")
+                _bits_equal(vc[p], v[g], f"{tag} row {t} value (head {g})")
+                for i in range(g * G, (g + 1) * G):
+                    ctx[i * hd:(i + 1) * hd] = ora.attend_one(Tl["q"][t][i * hd:(i + 1) * hd], kc[:p + 1], vc[:p + 1])
+            _glue_close(Tl["ctx"][t], ctx, f"{tag} row {t} causal attention")
+        if gemm_f16:
+            _f16_bound_ok(Tl["h_mid"] - h_in, Tl["ctx"], W[("wo", l)], dt, nh * hd, f"{tag} O projection")
+        else:
+            _bits_equal(Tl["h_mid"], proj(Tl["ctx"], ("wo", l), "wo", res=h_in), f"{tag} O projection + residual")
+        for t in range(T):
+            _glue_close(Tl["hn_ffn"][t], ora.rms_norm(Tl["h_mid"][t], W[("ffn_norm", l)], cfg.norm_eps),
+                        f"{tag} row {t} FFN RMSNorm")
+        I = cfg.intermediate
+        if gemm_f16:
+            _f16_bound_ok(Tl["gu"][:, :I], Tl["hn_ffn"], W[("w1", l)], dt, cfg.dim, f"{tag} gate")
+            _f16_bound_ok(Tl["gu"][:, I:], Tl["hn_ffn"], W[("w3", l)], dt, cfg.dim, f"{tag} up")
+        else:
+            _bits_equal(Tl["gu"], np.concatenate([proj(Tl["hn_ffn"], ("w1", l), "w1"),
+                                                  proj(Tl["hn_ffn"], ("w3", l), "w3")], axis=1), f"{tag} gate|up")
+        for t in range(T):
+            _glue_close(Tl["act"][t], ora.silu_mul(Tl["gu"][t][:I], Tl["gu"][t][I:]), f"{tag} row {t} SiLU*mul")
+        if gemm_f16:
+            _f16_bound_ok(Tl["h_out"] - Tl["h_mid"], Tl["act"], W[("w2", l)], dt, I, f"{tag} down projection")
+        else:
+            _bits_equal(Tl["h_out"], proj(Tl["act"], ("w2", l), "w2", res=Tl["h_mid"]), f"{tag} down + residual")
+    return rows
+
+
+PREFILL_KINDS = {
+    # name: (config, per-stream (cached length before, prompt tokens), exact)
+    "fish_q4k_exact_1stream": (lambda: _fish_small(n_layers=2), [(0, 37)], True),
+    "fish_q4k_gemm_after_cache": (lambda: _fish_small(n_layers=1), [(20, 70)], False),
+    "fish_q8_0_ragged3": (lambda: _fish_small(n_layers=2, max_batch=3, dtype=GgmlDType.Q8_0), [(5, 17), (0, 1),
+                                                                                                (31, 40)], True),
+    "cv2_q8_0_embeds": (lambda: D.cosyvoice2_lm_config(n_layers=2, max_seq=96, dtype=GgmlDType.Q8_0), [(9, 30)], True),
+    "cv2_q4_0_gemm_rows": (lambda: D.cosyvoice2_lm_config(n_layers=1, max_seq=200, dtype=GgmlDType.Q4_0),
+                           [(0, 130)], True),
+}
+
+
+@pytest.mark.parametrize("kind", list(PREFILL_KINDS))
+def test_prefill_every_op_matches_oracle(cuda, ora, kind):
+    """sxq_lm_prefill (SlowAr::prefill / prefill_batch, the CosyVoice2 prompt forward)
+    replayed op by op over every prompt row, then the head on each stream's last row."""
+    make, plan, exact = PREFILL_KINDS[kind]
+    cfg = make()
+    n = len(plan)
+    lm, W = _build(cfg, cuda, 51, n)
+    lens0 = [p[0] for p in plan]
+    counts = [p[1] for p in plan]
+    lm.kv_fill_random(lens0, seed=52)
+    rng = np.random.default_rng(53)
+    if kind.startswith("cv2"):
+        embs = [rng.standard_normal((c, cfg.dim)).astype(np.float32) for c in counts]
+        logits, nxt, hidden, tr = lm.prefill(embeds=[torch.from_numpy(e) for e in embs], exact=exact, trace=True)
+        frames = None
+    else:
+        prompts = [_frames(rng, c, cfg) for c in counts]
+        logits, nxt, hidden, tr = lm.prefill(prompts=[torch.from_numpy(p) for p in prompts], exact=exact, trace=True)
+        frames = np.concatenate(prompts)
+    _replay_prefill(ora, lm, cfg, W, tr, counts, lens0, frames, exact)
+    last_h = tr["layers"][-1]["h_out"]
+    got = logits.cpu().numpy()
+    ends = np.cumsum(counts) - 1
+    dt = int(cfg.weight_dtype)
+    for s in range(n):
+        _glue_close(tr["final_hn"][s], ora.rms_norm(last_h[ends[s]], W["final_norm"], cfg.norm_eps),
+                    f"stream {s} final RMSNorm")
+        _bits_equal(hidden.cpu().numpy()[s], tr["final_hn"][s], f"stream {s} hidden")
+        want = ora.matmul(dt, tr["final_hn"][s][None], W["head"])[0]
+        if cfg.head_bias:
+            want = (want + W["head_bias"]).astype(np.float32)
+        _bits_equal(got[s], want, f"stream {s} head")
+        assert int(nxt[s]) == int(np.argmax(got[s]))
+    assert lm.lengths(n) == [a + b for a, b in plan]
+
+
+def test_prefill_then_decode_matches_oracle_model(cuda, model_oracle):
+    """Prefill two ragged prompts, then decode two steps: every step's logits against the
+    oracle model that ran the same tokens one at a time (flip bound end to end; the
+    op-level replay above is the exact check)."""
+    cfg = _fish_small(n_layers=2, max_batch=2)
+    lm, W = _build(cfg, cuda, 54, 2)
+    orc = model_oracle.OracleDecoder(cfg, W, 2)
+    rng = np.random.default_rng(55)
+    prompts = [_frames(rng, 23, cfg), _frames(rng, 9, cfg)]
+    logits, nxt, hidden = lm.prefill(prompts=[torch.from_numpy(p) for p in prompts], exact=True)
+    for s, p in enumerate(prompts):
+        for i in range(len(p)):
+            want = orc.step_one(s, frame=p[i])
+        _check(logits.cpu().numpy()[s], orc, want, f"prefill stream {s} last position")
+    for step in range(2):
+        fr = _frames(rng, 2, cfg)
+        lg, _ = lm.step(ids=torch.from_numpy(fr), graph=True)
+        for s in range(2):
+            _check(lg.cpu().numpy()[s], orc, orc.step_one(s, frame=fr[s]), f"decode after prefill {step} stream {s}")
+    assert lm.lengths(2) == [25, 11]
+
+
+def test_slow_ar_prefill_and_qwen2_all_logits_shapes(cuda, model_oracle):
+    """SlowAr.prefill(prompt [1 + num_codebooks, T]) -> (logits [vocab], hidden [1, 1, dim])
+    (slow_ar.rs:250-256); prefill_batch -> ([n, vocab], [n, 1, dim]); Qwen2Lm's
+    forward_logits_cached over t_new > 1 embeddings returns every position's logits
+    [b, t_new, vocab] (cv2/mod.rs:283-286), each against the oracle model."""
+    cfg = _fish_small(n_layers=1, max_batch=2)
+    lm = D.SlowAr(cfg, device=cuda)
+    lm.init_random(seed=56)
+    prompt = _frames(np.random.default_rng(57), 12, cfg).T  # [1 + num_codebooks, T]
+    logits, hidden = lm.prefill(prompt)
+    assert logits.shape == (cfg.vocab,) and hidden.shape == (1, 1, cfg.dim)
+    assert lm.lengths(1) == [12]
+    lm.reset()
+    lb, hb = lm.prefill_batch([prompt, prompt[:, :5]])
+    assert lb.shape == (2, cfg.vocab) and hb.shape == (2, 1, cfg.dim)
+    np.testing.assert_array_equal(lb.cpu().numpy()[0], logits.cpu().numpy())
+    assert lm.lengths(2) == [12, 5]
+
+    cv = D.cosyvoice2_lm_config(n_layers=2, max_seq=64, dtype=GgmlDType.Q8_0)
+    q2, W = _build(cv, cuda, 58, 1)
+    orc = model_oracle.OracleDecoder(cv, W, 1)
+    emb = np.random.default_rng(59).standard_normal((1, 6, cv.dim)).astype(np.float32)
+    out = D.Qwen2Lm.forward_logits_cached(q2, torch.from_numpy(emb))
+    assert out.shape == (1, 6, cv.vocab)
+    for i in range(6):
+        _check(out.cpu().numpy()[0, i], orc, orc.step_one(0, embed=emb[0, i]), f"cv2 prompt position {i}")
+
+
+def test_prefill_argument_errors(cuda):
+    cfg = _fish_small(n_layers=1, max_batch=2)
+    cfg.max_seq = 16
+    lm = D.DecoderLM(cfg, device=cuda)
+    lm.init_random(seed=60)
+    from syrinx_amd import SxqError
+    with pytest.raises(SxqError, match="exceed"):
+        lm.prefill(prompts=[np.zeros((17, 11), np.int32)])
+    with pytest.raises(SxqError, match="no tokens"):
+        lm.prefill(prompts=[np.zeros((3, 11), np.int32), np.zeros((0, 11), np.int32)])
+    assert lm.lengths(2) == [0, 0]
