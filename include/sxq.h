@@ -293,6 +293,52 @@ sxq_status sxq_lm_prefill(sxq_lm *lm, int n_streams, const int32_t *counts, cons
                           float *trace, size_t trace_capacity_floats, void *stream);
 sxq_status sxq_lm_prefill_trace_floats(const sxq_lm *lm, int64_t tokens, size_t *floats);
 
+/* ---- Samplers: the reference's seeded token draws on the device ---------------------
+ * A decode loop samples each step's logits on the GPU and writes the token straight into
+ * the next step's ids, so only token ids (not logit rows) ever cross to the host.  Each
+ * stream has its own SplitMix64 state (rng[s], device uint64, seeded by the caller with the
+ * reference's seed and advanced per draw exactly as the reference advances it).  On the
+ * device top_k must be 1..64 and RAS windows at most 64 ids.  out[s * out_stride] receives
+ * stream s's token (an ids frame's semantic slot, say). */
+typedef struct {
+    float temperature;        /* softmax temperature of the normal draw */
+    float top_p;              /* nucleus cutoff */
+    int32_t top_k;            /* candidate cap, 1..64 */
+    float repetition_penalty; /* codebook draws: divides positive / multiplies negative logits of `recent` ids; 1 = off */
+    int32_t ras_win_size;     /* semantic draws: RAS window (recent semantic ids), <= 64 */
+    float ras_high_temp;      /* RAS fallback draw */
+    float ras_high_top_p;
+    int32_t semantic_begin;   /* semantic draws may pick only [begin, end] and stop_id (begin > end: any id) */
+    int32_t semantic_end;
+    int32_t stop_id;
+} sxq_fish_sampling;
+
+/* Sampler::sample_semantic (crates/syrinx-fish/src/common/sampling.rs:150-163) for n
+ * streams: logits f32 [n][vocab] (row stride logits_stride floats, left unchanged), the
+ * semantic constraint, a normal and a high-temperature draw, the high one used when the
+ * normal token is a semantic id already in the stream's window.  window int32
+ * [n][ras_win_size] (oldest first) and window_len int32 [n] (device, may both be NULL): the
+ * driver's rolling window (common/dualar.rs:188-205), updated with the drawn token unless
+ * it is stop_id. */
+sxq_status sxq_sample_semantic(int device, const float *logits, int64_t logits_stride, int n, int vocab,
+                               const sxq_fish_sampling *params, uint64_t *rng, int32_t *window, int32_t *window_len,
+                               int32_t *out, int out_stride, void *stream);
+/* Sampler::sample_codebook (common/sampling.rs:139-145): the repetition penalty over recent
+ * [n][n_recent] ids (or NULL), then the temperature / top-p / top-k draw. */
+sxq_status sxq_sample_codebook(int device, const float *logits, int64_t logits_stride, int n, int vocab,
+                               const sxq_fish_sampling *params, uint64_t *rng, const int32_t *recent, int n_recent,
+                               int32_t *out, int out_stride, void *stream);
+/* CosyVoice ras_sampling after log_softmax_vec (crates/syrinx-lm/src/cv2/sampling.rs:13-22,
+ * 104-124; the generate loop at crates/syrinx-lm/src/cv2/generate.rs:150-161): logits f32
+ * [n][vocab] are overwritten with their log-probabilities (ids [eos_begin, eos_end) at -inf
+ * when ignore_eos), a nucleus draw (top_p, top_k), replaced by a draw from the full
+ * distribution when it repeats >= win * tau_r times among the stream's last `win` tokens.
+ * decoded int32 [n][win] (oldest first) and decoded_len [n] (device, may both be NULL): that
+ * history, extended by the drawn token unless it is a stop id. */
+sxq_status sxq_sample_ras(int device, float *logits, int64_t logits_stride, int n, int vocab, int ignore_eos,
+                          int eos_begin, int eos_end, float top_p, int top_k, int win, float tau_r, uint64_t *rng,
+                          int32_t *decoded, int32_t *decoded_len, int32_t *out, int out_stride, void *stream);
+
 /* Enqueue only the projection GEMVs of one step (every layer's fused QKV, O, gate|up
  * and down, plus the head if with_head) on the step's current activations: the
  * GEMV share of a token, for bandwidth measurement.  No reference counterpart. */

@@ -1,0 +1,496 @@
+// sxq_sample.hip -- the reference's seeded token samplers on the device, so a decode loop
+// hands only a token id (not a logit row) from one step to the next.
+//
+//   Fish dual-AR   crates/syrinx-fish/src/common/sampling.rs: SplitMix64 (:20-37),
+//                  sample_semantic (:150-163: semantic constraint + RAS),
+//                  sample_codebook (:139-145: repetition penalty + nucleus),
+//                  logits_to_probs (:186-240), multinomial1 (:249-263);
+//   CosyVoice2/3   crates/syrinx-lm/src/cv2/sampling.rs: log_softmax_vec (:13-22),
+//                  nucleus_sampling (:64-87), random_sampling (:91-95), ras_sampling
+//                  (:104-124); its callers push every non-stop token into the history
+//                  (crates/syrinx-lm/src/cv2/generate.rs:150-161) and the Fish driver
+//                  keeps the last ras_win_size semantic ids (common/dualar.rs:188-205).
+//
+// One 1024-thread workgroup per stream.  Both samplers only ever draw from the top_k
+// largest keys (Fish: logits; CosyVoice: probabilities), so the row is reduced on the
+// device to its top_k (key, id) pairs in the reference's order -- key descending, ties by
+// ascending id -- by a radix select over the ordered key bits (4 passes of 8-bit digit
+// histograms, then a compaction that takes ties at the cut in id order), and the
+// reference's per-candidate float steps then run on one lane in its order.  Sums over the
+// whole row (softmax normalisers, the full-distribution draw) are f64 as in the reference,
+// added in a fixed tree order here rather than left to right (a difference below 1e-15
+// relative, which moves a draw only when the uniform lands that close to a boundary).
+// An f32 exponential is exp in f64 rounded to f32 (the correctly rounded value).
+#include <math.h>
+
+#include "../../include/sxq.h"
+#include "sxq_abi.h"
+#include "sxq_kernels.h"
+
+using namespace sxq;
+using namespace sxq::abi;
+
+namespace {
+
+constexpr int kST = 1024;        // threads per workgroup (one stream)
+constexpr int kMaxTopK = 64;     // largest top_k the device samplers take
+constexpr int kMaxWindow = 64;   // largest RAS window
+
+SXQ_DEV uint64_t splitmix_next(uint64_t& state) {
+    state += 0x9E3779B97F4A7C15ull;
+    uint64_t z = state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+SXQ_DEV double splitmix_f64(uint64_t& state) { return (double)(splitmix_next(state) >> 11) * (1.0 / 9007199254740992.0); }
+
+// Ordered bits: larger float -> larger unsigned key (-inf lowest of the non-NaN values).
+SXQ_DEV uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+SXQ_DEV float exp_f32(float x) { return (float)exp((double)x); }
+
+// The ids a draw ranges over, in id order: [lo, hi) plus, if extra >= 0, the one id
+// `extra` (outside [lo, hi)); element e -> id.
+struct View {
+    int lo, hi, extra;
+    SXQ_DEV int count() const { return hi - lo + (extra >= 0 ? 1 : 0); }
+    SXQ_DEV int id(int e) const {
+        if (extra < 0) return lo + e;
+        if (extra < lo) return e == 0 ? extra : lo + e - 1;
+        return e < hi - lo ? lo + e : extra;
+    }
+};
+
+struct Shared {
+    unsigned hist[256];
+    float fred[kST / 64];
+    double dred[kST / 64];
+    unsigned cnt[kST];
+    float cand_key[kMaxTopK];
+    int cand_id[kMaxTopK];
+    float top_key[kMaxTopK];  // sorted: key descending, id ascending
+    int top_id[kMaxTopK];
+    unsigned ncand;
+    uint32_t kth;
+    int need, result;
+    double dval;
+    float fval;
+};
+
+SXQ_DEV float block_max(float v, Shared& sh) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float m = sh.fred[0];
+        for (int i = 1; i < kST / 64; ++i) m = fmaxf(m, sh.fred[i]);
+        sh.fval = m;
+    }
+    __syncthreads();
+    return sh.fval;
+}
+
+SXQ_DEV double block_sum(double v, Shared& sh) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) sh.dred[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double s = 0.0;
+        for (int i = 0; i < kST / 64; ++i) s += sh.dred[i];
+        sh.dval = s;
+    }
+    __syncthreads();
+    return sh.dval;
+}
+
+// The K largest keys of the view (key(e) a functor over element index), in the
+// reference's sort order, into sh.top_key / sh.top_id; returns K' = min(K, count).
+template <class KeyF>
+SXQ_DEV int top_k_select(const View& v, KeyF key, int K, Shared& sh) {
+    const int n = v.count(), tid = threadIdx.x;
+    K = min(K, n);
+    uint32_t prefix = 0, mask = 0;
+    int rem = K;
+    for (int d = 24; d >= 0; d -= 8) {
+        for (int b = tid; b < 256; b += kST) sh.hist[b] = 0;
+        __syncthreads();
+        for (int e = tid; e < n; e += kST) {
+            const uint32_t u = order_key(key(e));
+            if ((u & mask) == prefix) atomicAdd(&sh.hist[(u >> d) & 0xFF], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int above = 0, b = 255;
+            for (; b > 0; --b) {
+                if (above + (int)sh.hist[b] >= rem) break;
+                above += (int)sh.hist[b];
+            }
+            sh.need = rem - above;  // elements of digit b still needed
+            sh.kth = (uint32_t)b;
+        }
+        __syncthreads();
+        prefix |= sh.kth << d;
+        mask |= 0xFFu << d;
+        rem = sh.need;
+        __syncthreads();
+    }
+    // prefix = the K-th largest key; `rem` of the elements equal to it are taken, the
+    // ones with the smallest ids: thread t scans the contiguous elements [t*c, t*c + c).
+    const int chunk = (n + kST - 1) / kST, e0 = tid * chunk, e1 = min(n, e0 + chunk);
+    if (tid == 0) sh.ncand = 0;
+    unsigned ties = 0;
+    for (int e = e0; e < e1; ++e) ties += order_key(key(e)) == prefix;
+    sh.cnt[tid] = ties;
+    __syncthreads();
+    if (tid == 0) {  // exclusive scan of the tie counts in id order
+        unsigned acc = 0;
+        for (int t = 0; t < kST; ++t) {
+            const unsigned c = sh.cnt[t];
+            sh.cnt[t] = acc;
+            acc += c;
+        }
+    }
+    __syncthreads();
+    unsigned rank = sh.cnt[tid];
+    for (int e = e0; e < e1; ++e) {
+        const float k = key(e);
+        const uint32_t u = order_key(k);
+        bool take = u > prefix;
+        if (u == prefix) take = rank++ < (unsigned)rem;
+        if (take) {
+            const unsigned slot = atomicAdd(&sh.ncand, 1u);
+            if (slot < (unsigned)kMaxTopK) {
+                sh.cand_key[slot] = k;
+                sh.cand_id[slot] = v.id(e);
+            }
+        }
+    }
+    __syncthreads();
+    // rank sort of the K candidates: key descending, ties by ascending id
+    if (tid < K) {
+        const float k = sh.cand_key[tid];
+        const int id = sh.cand_id[tid];
+        const uint32_t u = order_key(k);
+        int r = 0;
+        for (int j = 0; j < K; ++j) {
+            const uint32_t uj = order_key(sh.cand_key[j]);
+            r += uj > u || (uj == u && sh.cand_id[j] < id);
+        }
+        sh.top_key[r] = k;
+        sh.top_id[r] = id;
+    }
+    __syncthreads();
+    return K;
+}
+
+// Fish logits_to_probs over the sorted candidates + multinomial1 (one lane): rank 0
+// always kept, then while cum <= top_p and rank < top_k (cum of exp(l - max) / total in
+// f64); temperature softmax over the kept in f64, probabilities rounded to f32 and
+// renormalised; the inverse-CDF draw walks the kept ids in id order.
+SXQ_DEV int fish_draw(const Shared& sh, int K, double total, float mx, float temperature, float top_p, int top_k,
+                      uint64_t& rng) {
+    int keep = 0;
+    double cum = 0.0;
+    for (int r = 0; r < K; ++r) {
+        if (!(r == 0 || (cum <= (double)top_p && r < top_k))) break;
+        ++keep;
+        cum += exp((double)(sh.top_key[r] - mx)) / total;
+    }
+    const float t = fmaxf(temperature, 1e-5f);
+    float kmax = -INFINITY;
+    for (int r = 0; r < keep; ++r) kmax = fmaxf(kmax, sh.top_key[r] / t);
+    // kept ids in id order
+    int ord[kMaxTopK];
+    for (int r = 0; r < keep; ++r) {
+        int pos = 0;
+        for (int j = 0; j < keep; ++j) pos += sh.top_id[j] < sh.top_id[r];
+        ord[pos] = r;
+    }
+    double e[kMaxTopK], psum = 0.0;
+    for (int i = 0; i < keep; ++i) {
+        e[i] = exp((double)(sh.top_key[ord[i]] / t - kmax));
+        psum += e[i];
+    }
+    float p[kMaxTopK];
+    double tot = 0.0;
+    for (int i = 0; i < keep; ++i) {
+        p[i] = (float)e[i];
+        if (psum > 0.0) p[i] = (float)((double)p[i] / psum);
+        tot += (double)p[i];
+    }
+    if (tot <= 0.0) return 0;
+    const double u = splitmix_f64(rng) * tot;
+    double acc = 0.0;
+    for (int i = 0; i < keep; ++i) {
+        acc += (double)p[i];
+        if (u < acc) return sh.top_id[ord[i]];
+    }
+    return -1;  // the reference's fall-through: the row's last id (the caller maps it)
+}
+
+struct FishArgs {
+    const float* logits;
+    int64_t stride;
+    int vocab;
+    sxq_fish_sampling p;
+    uint64_t* rng;
+    int32_t* window;
+    int32_t* window_len;
+    const int32_t* recent;
+    int n_recent;
+    int32_t* out;
+    int out_stride;
+};
+
+// mode 0: sample_semantic (constraint + RAS, window update); mode 1: sample_codebook.
+template <int MODE>
+__global__ __launch_bounds__(kST) void k_sample_fish(FishArgs A) {
+    __shared__ Shared sh;
+    const int s = blockIdx.x, tid = threadIdx.x;
+    const float* row = A.logits + (int64_t)s * A.stride;
+    const sxq_fish_sampling& P = A.p;
+    View v{0, A.vocab, -1};
+    if (MODE == 0 && P.semantic_begin <= P.semantic_end) {
+        v.lo = max(0, P.semantic_begin);
+        v.hi = min(A.vocab, P.semantic_end + 1);
+        v.extra = (P.stop_id >= 0 && P.stop_id < A.vocab && (P.stop_id < v.lo || P.stop_id >= v.hi)) ? P.stop_id : -1;
+    }
+    // the repetition penalty (codebook draws): applied per occurrence, in list order
+    __shared__ float pen_val[kMaxWindow];
+    __shared__ int pen_id[kMaxWindow];
+    __shared__ int n_pen;
+    if (tid == 0) {
+        n_pen = 0;
+        const bool on = MODE == 1 && A.recent && fabsf(P.repetition_penalty - 1.0f) >= 1.1920929e-07f;
+        for (int i = 0; on && i < A.n_recent && i < kMaxWindow; ++i) {
+            const int id = A.recent[(int64_t)s * A.n_recent + i];
+            if (id < 0 || id >= A.vocab) continue;
+            int j = 0;
+            while (j < n_pen && pen_id[j] != id) ++j;
+            float l = j < n_pen ? pen_val[j] : row[id];
+            l = l > 0.0f ? l / P.repetition_penalty : l * P.repetition_penalty;
+            pen_val[j] = l;
+            pen_id[j] = id;
+            if (j == n_pen) ++n_pen;
+        }
+    }
+    __syncthreads();
+    auto key = [&](int e) -> float {
+        const int id = v.id(e);
+        float l = row[id];
+        if (MODE == 1)
+            for (int j = 0; j < n_pen; ++j)
+                if (pen_id[j] == id) l = pen_val[j];
+        return l;
+    };
+    const int n = v.count();
+    float mx = -INFINITY;
+    for (int e = tid; e < n; e += kST) mx = fmaxf(mx, key(e));
+    mx = block_max(mx, sh);
+    double tot = 0.0;
+    for (int e = tid; e < n; e += kST) tot += exp((double)(key(e) - mx));
+    tot = block_sum(tot, sh);
+    const int K = top_k_select(v, key, P.top_k, sh);
+    if (tid != 0) return;
+    uint64_t rng = A.rng[s];
+    int tok = fish_draw(sh, K, tot, mx, P.temperature, P.top_p, P.top_k, rng);
+    if (tok < 0) tok = A.vocab - 1;
+    if (MODE == 0) {
+        int high = fish_draw(sh, K, tot, mx, P.ras_high_temp, P.ras_high_top_p, P.top_k, rng);
+        if (high < 0) high = A.vocab - 1;
+        int* win = A.window ? A.window + (int64_t)s * P.ras_win_size : nullptr;
+        int len = A.window_len ? A.window_len[s] : 0;
+        bool in_window = false;
+        for (int i = 0; win && i < len; ++i) in_window |= win[i] == tok;
+        const bool semantic = tok >= P.semantic_begin && tok <= P.semantic_end;
+        if (in_window && semantic) tok = high;
+        if (win && tok != P.stop_id && P.ras_win_size > 0) {  // the driver's window roll
+            if (len == P.ras_win_size) {
+                for (int i = 1; i < len; ++i) win[i - 1] = win[i];
+                --len;
+            }
+            win[len++] = tok;
+            A.window_len[s] = len;
+        }
+    }
+    A.rng[s] = rng;
+    A.out[(int64_t)s * A.out_stride] = tok;
+}
+
+struct RasArgs {
+    float* logits;
+    int64_t stride;
+    int vocab, ignore_eos, eos_begin, eos_end;
+    float top_p, tau_r;
+    int top_k, win;
+    uint64_t* rng;
+    int32_t* decoded;
+    int32_t* decoded_len;
+    int32_t* out;
+    int out_stride;
+};
+
+// ras_sampling over log_softmax(logits): the row is overwritten by its log-probabilities
+// (the stop ids -inf when ignore_eos), as log_softmax_vec + the mask produce them.
+__global__ __launch_bounds__(kST) void k_sample_ras(RasArgs A) {
+    __shared__ Shared sh;
+    __shared__ double chunk_sum[kST];
+    const int s = blockIdx.x, tid = threadIdx.x, n = A.vocab;
+    float* row = A.logits + (int64_t)s * A.stride;
+    float mx = -INFINITY;
+    for (int i = tid; i < n; i += kST) mx = fmaxf(mx, row[i]);
+    mx = block_max(mx, sh);
+    double tot = 0.0;
+    for (int i = tid; i < n; i += kST) tot += exp((double)(row[i] - mx));
+    tot = block_sum(tot, sh);
+    const double lse = (double)mx + log(tot);
+    for (int i = tid; i < n; i += kST) {
+        float lp = (float)((double)row[i] - lse);
+        if (A.ignore_eos && i >= A.eos_begin && i < A.eos_end) lp = -INFINITY;
+        row[i] = lp;
+    }
+    __syncthreads();
+    const View v{0, n, -1};
+    auto key = [&](int e) -> float { return exp_f32(row[e]); };
+    const int K = top_k_select(v, key, A.top_k, sh);
+    uint64_t rng = A.rng[s];
+    // nucleus: the leading candidates while cum (f32) < top_p and count < top_k, drawn
+    // in that (sorted) order
+    if (tid == 0) {
+        float cum = 0.0f;
+        int c = 0;
+        while (c < K && cum < A.top_p && c < A.top_k) cum += sh.top_key[c++];
+        double tsum = 0.0;
+        for (int i = 0; i < c; ++i) tsum += (double)sh.top_key[i];
+        const double u = splitmix_f64(rng) * tsum;
+        double acc = 0.0;
+        int pick = c - 1;
+        for (int i = 0; i < c; ++i) {
+            acc += (double)sh.top_key[i];
+            if (u < acc) {
+                pick = i;
+                break;
+            }
+        }
+        const int top = sh.top_id[pick < 0 ? 0 : pick];
+        int rep = 0;
+        const int len = A.decoded_len ? A.decoded_len[s] : 0;
+        const int* hist = A.decoded ? A.decoded + (int64_t)s * A.win : nullptr;
+        for (int i = 0; hist && i < len; ++i) rep += hist[i] == top;
+        sh.result = (float)rep >= (float)A.win * A.tau_r ? -1 : top;
+    }
+    __syncthreads();
+    if (sh.result < 0) {  // random_sampling over the full distribution, ids in order
+        const int chunk = (n + kST - 1) / kST, e0 = tid * chunk, e1 = min(n, e0 + chunk);
+        double cs = 0.0;
+        for (int i = e0; i < e1; ++i) cs += (double)exp_f32(row[i]);
+        chunk_sum[tid] = cs;
+        __syncthreads();
+        if (tid == 0) {
+            double total = 0.0;
+            for (int t = 0; t < kST; ++t) total += chunk_sum[t];
+            sh.dval = splitmix_f64(rng) * total;
+            double acc = 0.0;
+            int t = 0;
+            for (; t < kST - 1 && acc + chunk_sum[t] <= sh.dval; ++t) acc += chunk_sum[t];
+            sh.need = t;        // the chunk holding the crossing
+            sh.dred[0] = acc;   // the sum before that chunk
+            sh.result = n - 1;  // the reference's fall-through: the last id
+        }
+        __syncthreads();
+        if (tid == sh.need && e0 < e1) {
+            double acc = sh.dred[0];
+            int pick = e1 - 1;  // summed in another association than chunk_sum: stay in the chunk
+            for (int i = e0; i < e1; ++i) {
+                acc += (double)exp_f32(row[i]);
+                if (sh.dval < acc) {
+                    pick = i;
+                    break;
+                }
+            }
+            sh.result = pick;
+        }
+        __syncthreads();
+    }
+    if (tid != 0) return;
+    const int tok = sh.result;
+    if (A.decoded && (tok < A.eos_begin || tok >= A.eos_end) && A.win > 0) {  // the generate loop's history
+        int* hist = A.decoded + (int64_t)s * A.win;
+        int len = A.decoded_len[s];
+        if (len == A.win) {
+            for (int i = 1; i < len; ++i) hist[i - 1] = hist[i];
+            --len;
+        }
+        hist[len++] = tok;
+        A.decoded_len[s] = len;
+    }
+    A.rng[s] = rng;
+    A.out[(int64_t)s * A.out_stride] = tok;
+}
+
+sxq_status check_common(int n, int vocab, int top_k, const void* logits, const void* rng, const void* out) {
+    if (n < 1 || n > 65535 || vocab < 1) return fail(SXQ_ERR_INVALID, "sample: bad shape (%d streams, %d ids)", n, vocab);
+    if (top_k < 1 || top_k > kMaxTopK)
+        return fail(SXQ_ERR_INVALID, "sample: top_k %d outside 1..%d on the device", top_k, kMaxTopK);
+    if (!logits || !rng || !out) return fail(SXQ_ERR_INVALID, "sample: null pointer");
+    return SXQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+sxq_status sxq_sample_semantic(int device, const float* logits, int64_t logits_stride, int n, int vocab,
+                               const sxq_fish_sampling* p, uint64_t* rng, int32_t* window, int32_t* window_len,
+                               int32_t* out, int out_stride, void* stream) {
+    if (!p) return fail(SXQ_ERR_INVALID, "sample_semantic: null parameters");
+    sxq_status st = check_common(n, vocab, p->top_k, logits, rng, out);
+    if (st != SXQ_OK) return st;
+    if (p->ras_win_size < 0 || p->ras_win_size > kMaxWindow)
+        return fail(SXQ_ERR_INVALID, "sample_semantic: ras_win_size %d outside 0..%d", p->ras_win_size, kMaxWindow);
+    if (!window != !window_len) return fail(SXQ_ERR_INVALID, "sample_semantic: window and window_len go together");
+    DeviceGuard g(device);
+    HIP_TRY(g.err, "hipSetDevice");
+    FishArgs A{logits, logits_stride, vocab, *p, rng, window, window_len, nullptr, 0, out, out_stride};
+    hipLaunchKernelGGL(k_sample_fish<0>, dim3(n), dim3(kST), 0, (hipStream_t)stream, A);
+    HIP_TRY(hipGetLastError(), "sample_semantic");
+    return SXQ_OK;
+}
+
+sxq_status sxq_sample_codebook(int device, const float* logits, int64_t logits_stride, int n, int vocab,
+                               const sxq_fish_sampling* p, uint64_t* rng, const int32_t* recent, int n_recent,
+                               int32_t* out, int out_stride, void* stream) {
+    if (!p) return fail(SXQ_ERR_INVALID, "sample_codebook: null parameters");
+    sxq_status st = check_common(n, vocab, p->top_k, logits, rng, out);
+    if (st != SXQ_OK) return st;
+    if (n_recent < 0 || n_recent > kMaxWindow || (n_recent > 0 && !recent))
+        return fail(SXQ_ERR_INVALID, "sample_codebook: %d recent ids (at most %d)", n_recent, kMaxWindow);
+    DeviceGuard g(device);
+    HIP_TRY(g.err, "hipSetDevice");
+    FishArgs A{logits, logits_stride, vocab, *p, rng, nullptr, nullptr, recent, n_recent, out, out_stride};
+    hipLaunchKernelGGL(k_sample_fish<1>, dim3(n), dim3(kST), 0, (hipStream_t)stream, A);
+    HIP_TRY(hipGetLastError(), "sample_codebook");
+    return SXQ_OK;
+}
+
+sxq_status sxq_sample_ras(int device, float* logits, int64_t logits_stride, int n, int vocab, int ignore_eos,
+                          int eos_begin, int eos_end, float top_p, int top_k, int win, float tau_r, uint64_t* rng,
+                          int32_t* decoded, int32_t* decoded_len, int32_t* out, int out_stride, void* stream) {
+    sxq_status st = check_common(n, vocab, top_k, logits, rng, out);
+    if (st != SXQ_OK) return st;
+    if (win < 0 || win > kMaxWindow) return fail(SXQ_ERR_INVALID, "sample_ras: window %d outside 0..%d", win, kMaxWindow);
+    if (!decoded != !decoded_len) return fail(SXQ_ERR_INVALID, "sample_ras: decoded and decoded_len go together");
+    DeviceGuard g(device);
+    HIP_TRY(g.err, "hipSetDevice");
+    RasArgs A{logits, logits_stride, vocab, ignore_eos, eos_begin, eos_end, top_p, tau_r, top_k, win, rng, decoded,
+              decoded_len, out, out_stride};
+    hipLaunchKernelGGL(k_sample_ras, dim3(n), dim3(kST), 0, (hipStream_t)stream, A);
+    HIP_TRY(hipGetLastError(), "sample_ras");
+    return SXQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,119 @@
+"""The device samplers (libsxq sxq_sample_*) against the oracle restatement of the
+reference's samplers (oracle/sampling.py) on the same logits and seeds: every draw must
+pick the same id, and the SplitMix64 states must advance identically (checked through
+the ids of the following draws).  Plus the reference's distribution property (an
+unbiased categorical draw), measured on the device."""
+import numpy as np
+import pytest
+import torch
+
+import sampling as S
+from syrinx_amd.sampling import FishSampler, RasSampler, SamplingParams
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cuda():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    return torch.device("cuda:0")
+
+
+def _logits(rng, n, vocab, scale=3.0, ties=False):
+    x = (rng.standard_normal((n, vocab)) * scale).astype(np.float32)
+    if ties:  # blocks of equal values: the cut falls inside a tie, ordered by id
+        x[:, ::7] = x[:, :1]
+    return x
+
+
+@pytest.mark.parametrize("ties", [False, True])
+def test_semantic_draws_equal_oracle(cuda, ties):
+    """Slow-AR semantic draws at the Qwen3-4B vocabulary (155776) with the s2 semantic
+    range and stop id, RAS window on the device, 12 consecutive draws of 8 streams."""
+    n, vocab = 8, 155776
+    begin, end, stop = 151678, 155773, 151645
+    params = SamplingParams()
+    dev = FishSampler([42 + i for i in range(n)], params, (begin, end, stop), device=cuda)
+    refs = [S.FishSampler(42 + i) for i in range(n)]
+    windows = [[] for _ in range(n)]
+    rng = np.random.default_rng(1)
+    for step in range(12):
+        x = _logits(rng, n, vocab, 1.0, ties)
+        if step % 3 == 2:  # make repeats likely: peak a recent id so RAS triggers
+            for i in range(n):
+                if windows[i]:
+                    x[i, windows[i][-1]] += 6.0
+        got = dev.sample_semantic(torch.from_numpy(x).to(cuda)).cpu().numpy()
+        for i in range(n):
+            want = refs[i].sample_semantic(x[i], windows[i], begin, end, stop)
+            assert got[i] == want, (step, i, got[i], want)
+            if want != stop:
+                windows[i].append(want)
+                windows[i] = windows[i][-params.ras_win_size:]
+    w = dev.window.cpu().numpy()
+    L = dev.window_len.cpu().numpy()
+    for i in range(n):
+        assert list(w[i][:L[i]]) == windows[i]
+
+
+def test_codebook_draws_with_repetition_penalty_equal_oracle(cuda):
+    n, vocab = 16, 4096
+    params = SamplingParams(temperature=0.8, top_p=0.7, top_k=40, repetition_penalty=1.3)
+    dev = FishSampler([7 * i + 1 for i in range(n)], params, device=cuda)
+    refs = [S.FishSampler(7 * i + 1, temperature=0.8, top_p=0.7, top_k=40, repetition_penalty=1.3) for i in range(n)]
+    rng = np.random.default_rng(2)
+    for step in range(10):
+        x = _logits(rng, n, vocab, 2.0, ties=(step % 2 == 1))
+        recent = rng.integers(0, vocab, (n, 6)).astype(np.int32)
+        recent[:, 5] = recent[:, 4]  # a duplicate id is penalized twice
+        got = dev.sample_codebook(torch.from_numpy(x).to(cuda), torch.from_numpy(recent).to(cuda)).cpu().numpy()
+        for i in range(n):
+            assert got[i] == refs[i].sample_codebook(x[i], list(recent[i])), (step, i)
+
+
+@pytest.mark.parametrize("ignore_eos", [False, True])
+def test_cosyvoice_ras_draws_equal_oracle(cuda, ignore_eos):
+    """CosyVoice2 speech vocabulary (6564, stop ids 6561..6563): log_softmax, nucleus
+    (top_p 0.8, top_k 25), the repetition fallback to the full distribution."""
+    n, vocab = 12, 6564
+    dev = RasSampler([100 + i for i in range(n)], device=cuda)
+    refs = [S.SplitMix64(100 + i) for i in range(n)]
+    hist = [[] for _ in range(n)]
+    rng = np.random.default_rng(3)
+    for step in range(15):
+        x = _logits(rng, n, vocab, 2.0)
+        x[:, 6561:6564] += 4.0 * (step % 4 == 0)
+        if step % 2 == 1:
+            for i in range(n):
+                if hist[i]:
+                    x[i, hist[i][-1]] += 8.0  # repeats: the fallback draw follows
+        xt = torch.from_numpy(x).to(cuda)
+        got = dev.sample(xt, ignore_eos).cpu().numpy()
+        for i in range(n):
+            want = S.ras_sampling(x[i], hist[i], refs[i], ignore_eos, 6561, 6564)
+            assert got[i] == want, (step, i, got[i], want)
+            if not 6561 <= want < 6564:
+                hist[i] = (hist[i] + [want])[-10:]
+        # the row now holds log_softmax (stop ids -inf when ignored)
+        lp = xt.cpu().numpy()
+        want_lp = S.log_softmax_vec(x[0])
+        if ignore_eos:
+            want_lp[6561:6564] = -np.inf
+        np.testing.assert_allclose(lp[0], want_lp, rtol=0, atol=2e-6)
+
+
+def test_device_draws_are_an_unbiased_categorical(cuda):
+    """The reference's multinomial property (tests/real_cv3_multinomial.rs) on the device:
+    4096 streams with different seeds draw from the same 5-way row."""
+    n = 4096
+    probs = np.array([0.05, 0.10, 0.20, 0.50, 0.15], np.float32)
+    x = np.tile(np.log(probs)[None, :], (n, 1)).astype(np.float32)
+    params = SamplingParams(temperature=1.0, top_p=1.0, top_k=5, repetition_penalty=1.0)
+    counts = np.zeros(5)
+    dev = FishSampler(list(range(1, n + 1)), params, device=cuda)
+    for _ in range(10):
+        got = dev.sample_codebook(torch.from_numpy(x).to(cuda)).cpu().numpy()
+        counts += np.bincount(got, minlength=5)
+    f = counts / counts.sum()
+    assert np.abs(f - probs).max() < 1e-2, f
