@@ -251,6 +251,10 @@ sxq_status sxq_lm_kv_fill_random(sxq_lm *lm, const int32_t *lengths, int n_strea
  * (SlowAr::reset, slow_ar.rs:79-81). */
 sxq_status sxq_lm_set_lengths(sxq_lm *lm, const int32_t *lengths, int n_streams);
 sxq_status sxq_lm_get_lengths(const sxq_lm *lm, int32_t *lengths, int n_streams);
+/* Empty the caches of streams 0..n_streams-1, ordered on `stream` (no host wait): the
+ * per-frame reset of the Fish fast AR's local cache (crates/syrinx-fish/src/s2/fast_ar.rs:
+ * a new KvCache per expand), and SlowAr::reset.  Must not be recorded into a graph. */
+sxq_status sxq_lm_reset(sxq_lm *lm, int n_streams, void *stream);
 /* One decode step for streams 0..n_streams-1 (device pointers, enqueued on `stream`):
  *   ids      int32 [n_streams, 1 + n_codebooks] token ids (Fish frame: semantic id then
  *            codes), or NULL to reuse the previous step's argmax (codes kept);
@@ -319,15 +323,19 @@ typedef struct {
  * normal token is a semantic id already in the stream's window.  window int32
  * [n][ras_win_size] (oldest first) and window_len int32 [n] (device, may both be NULL): the
  * driver's rolling window (common/dualar.rs:188-205), updated with the drawn token unless
- * it is stop_id. */
+ * it is stop_id.  active int32 [n] (device, or NULL): drive_batch's per-stream "not
+ * finished" flag (common/dualar.rs:286-305): a stream whose flag is 0 draws nothing (its rng
+ * and window are kept, its token is written as 0, the inert pad), and a stream that draws
+ * stop_id has its flag cleared. */
 sxq_status sxq_sample_semantic(int device, const float *logits, int64_t logits_stride, int n, int vocab,
                                const sxq_fish_sampling *params, uint64_t *rng, int32_t *window, int32_t *window_len,
-                               int32_t *out, int out_stride, void *stream);
+                               int32_t *active, int32_t *out, int out_stride, void *stream);
 /* Sampler::sample_codebook (common/sampling.rs:139-145): the repetition penalty over recent
- * [n][n_recent] ids (or NULL), then the temperature / top-p / top-k draw. */
+ * [n][n_recent] ids (or NULL), then the temperature / top-p / top-k draw.  active as for
+ * sxq_sample_semantic, read only (FastAr::expand_batch's `active`, s2/fast_ar.rs:206-213). */
 sxq_status sxq_sample_codebook(int device, const float *logits, int64_t logits_stride, int n, int vocab,
                                const sxq_fish_sampling *params, uint64_t *rng, const int32_t *recent, int n_recent,
-                               int32_t *out, int out_stride, void *stream);
+                               const int32_t *active, int32_t *out, int out_stride, void *stream);
 /* CosyVoice ras_sampling after log_softmax_vec (crates/syrinx-lm/src/cv2/sampling.rs:13-22,
  * 104-124; the generate loop at crates/syrinx-lm/src/cv2/generate.rs:150-161): logits f32
  * [n][vocab] are overwritten with their log-probabilities (ids [eos_begin, eos_end) at -inf
@@ -338,6 +346,30 @@ sxq_status sxq_sample_codebook(int device, const float *logits, int64_t logits_s
 sxq_status sxq_sample_ras(int device, float *logits, int64_t logits_stride, int n, int vocab, int ignore_eos,
                           int eos_begin, int eos_end, float top_p, int top_k, int win, float tau_r, uint64_t *rng,
                           int32_t *decoded, int32_t *decoded_len, int32_t *out, int out_stride, void *stream);
+
+/* FastAr::expand / expand_batch (crates/syrinx-fish/src/s2/fast_ar.rs:116-224) on the
+ * device, over a fast-AR engine `fast` (sxq_lm with n_codebooks 0, a dense embedding table
+ * -- the shared fast_embeddings -- of >= vocab rows, vocab = the residual codebook size,
+ * max_seq >= n_codes), for streams 0..n_streams-1, enqueued on `stream`:
+ *   hidden   f32 [n_streams, dim] (device) the slow head's hidden (sxq_lm_step's `hidden`),
+ *            run at position 0 (the conditioning prefix; its logits are unused);
+ *   semantic int32, stream s at semantic[s * semantic_stride]: the sampled semantic ids;
+ *            codebook 0 is first_code = clamp(semantic - params->semantic_begin, 0, vocab - 1);
+ *   active   int32 [n_streams] or NULL: 0 marks a finished stream, which draws nothing (its
+ *            rng is kept and its codes are 0), as expand_batch's `active`;
+ *   codes    int32 output, codebook cb of stream s at codes[s * codes_stride + cb],
+ *            cb = 0..n_codes-1; codebook cb >= 1 is Sampler::sample_codebook (params, rng[s],
+ *            no repetition list: the reference passes an empty `recent`) of position cb's
+ *            logits, and position cb + 1 embeds it.
+ * The engine's caches are emptied first (a fresh KvCache per frame) and hold n_codes
+ * positions afterwards.  With SXQ_LM_GRAPH the whole expansion is one HIP graph, captured
+ * per distinct argument set (pointers, strides, sampling values) and replayed after.
+ * Fish's slow ids frame [semantic, code 0 .. code n_codes-1] is filled in place by passing
+ * semantic = frame, codes = frame + 1 and both strides = 1 + n_codes. */
+sxq_status sxq_fish_fast_expand(sxq_lm *fast, int n_streams, const float *hidden, const int32_t *semantic,
+                                int semantic_stride, const int32_t *active, const sxq_fish_sampling *params,
+                                uint64_t *rng, int n_codes, int32_t *codes, int codes_stride, unsigned flags,
+                                void *stream);
 
 /* Enqueue only the projection GEMVs of one step (every layer's fused QKV, O, gate|up
  * and down, plus the head if with_head) on the step's current activations: the

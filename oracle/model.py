@@ -48,6 +48,13 @@ class OracleDecoder:
         self.k[s][layer][g] = [np.asarray(r, np.float32) for r in k_rows]
         self.v[s][layer][g] = [np.asarray(r, np.float32) for r in v_rows]
 
+    def reset(self, s):
+        """An empty cache for stream s (the fast AR's fresh KvCache per frame)."""
+        for l in range(self.c.n_layers):
+            for g in range(self.c.n_kv_heads):
+                self.k[s][l][g] = []
+                self.v[s][l][g] = []
+
     def length(self, s):
         return len(self.k[s][0][0])
 
@@ -109,6 +116,7 @@ class OracleDecoder:
             h = (r + d).astype(np.float32)
             self.trace.update({"qkv": qkv, "q": q.reshape(-1), "gu": np.concatenate([g_, u_]), "h": h})
         hn = ora.rms_norm(h, self.W["final_norm"], c.norm_eps)
+        self.hidden = hn  # SlowAr::head's `hidden` (norm_fastlayer_input, no fast_project_in)
         logits = self._mm(hn, self.W["head"], "head")
         if c.head_bias:
             logits = (logits + self.W["head_bias"]).astype(np.float32)

@@ -66,13 +66,15 @@ _SIGS = {
     "sxq_lm_kv_fill_random": (_I, [_P, _P, _I, _U64]),
     "sxq_lm_set_lengths": (_I, [_P, _P, _I]),
     "sxq_lm_get_lengths": (_I, [_P, _P, _I]),
+    "sxq_lm_reset": (_I, [_P, _I, _P]),
     "sxq_lm_step": (_I, [_P, _I, _P, _P, _P, _P, _P, _U, _P]),
     "sxq_lm_read_kv": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "sxq_lm_prefill": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U, _P, _SZ, _P]),
     "sxq_lm_prefill_trace_floats": (_I, [_P, _I64, _P]),
     "sxq_lm_gemv_pass": (_I, [_P, _I, _I, _P]),
-    "sxq_sample_semantic": (_I, [_I, _P, _I64, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
-    "sxq_sample_codebook": (_I, [_I, _P, _I64, _I, _I, _P, _P, _P, _I, _P, _I, _P]),
+    "sxq_sample_semantic": (_I, [_I, _P, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "sxq_sample_codebook": (_I, [_I, _P, _I64, _I, _I, _P, _P, _P, _I, _P, _P, _I, _P]),
+    "sxq_fish_fast_expand": (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I, _I, _P]),
     "sxq_sample_ras": (_I, [_I, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I, _F, _P, _P, _P, _P, _I, _P]),
     "sxq_lm_read_state": (_I, [_P, _I, _I, _P, _P]),
     "sxq_lm_trace_floats": (_I, [_P, _I, _P]),

@@ -8,6 +8,15 @@
 namespace sxq {
 namespace abi {
 
+// Fish samplers shared with the fast-AR driver (sxq_sample.hip): the codebook draw into
+// out (and a copy into out2, may be null), and FastAr::first_code into ids (and codes).
+bool fish_sampling_fits(const sxq_fish_sampling& p);
+hipError_t launch_sample_codebook(const float* logits, int64_t stride, int n, int vocab, const sxq_fish_sampling& p,
+                                  uint64_t* rng, const int32_t* active, int32_t* out, int out_stride, int32_t* out2,
+                                  int out2_stride, hipStream_t s);
+hipError_t launch_first_codes(const int32_t* semantic, int sem_stride, int n, int begin, int residual,
+                              const int32_t* active, int32_t* ids, int32_t* codes, int codes_stride, hipStream_t s);
+
 // Record `fmt` as this thread's sxq_last_error() and return `code`.
 sxq_status fail(sxq_status code, const char* fmt, ...);
 // Map a HIP error to SXQ_ERR_OOM / SXQ_ERR_DEVICE with its text.

@@ -48,6 +48,8 @@ constexpr int kArgmaxSlices = 64;
 hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, int* len,
                          float* pval, int* pidx, unsigned* counter, hipStream_t s);
 hipError_t launch_fill_value(float* y, int64_t n, float v, hipStream_t s);
+// A fill kernel (not a memset node, so it may sit inside a captured graph).
+hipError_t launch_fill_int(int* y, int n, int v, hipStream_t s);
 
 // ---- prompt prefill (sxq_prefill.hip) -------------------------------------------------
 // Per-token QK-RMSNorm + RoPE + KV write: tok[2 t] = stream, tok[2 t + 1] = position of

@@ -486,6 +486,11 @@ __global__ void k_fill_value(float* __restrict__ y, int64_t n, float v) {
     if (i < n) y[i] = v;
 }
 
+__global__ void k_fill_int(int* __restrict__ y, int n, int v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = v;
+}
+
 // ------------------------------------------------------------------------ launchers
 hipError_t launch_rmsnorm_quant(int vdt, const float* h, int rows, int dim, const float* w, float eps, uint8_t* act,
                                 float* normed, hipStream_t s) {
@@ -618,6 +623,12 @@ hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int id
                          float* pval, int* pidx, unsigned* counter, hipStream_t s) {
     hipLaunchKernelGGL(k_argmax, dim3(B, kArgmaxSlices), dim3(256), 0, s, logits, vocab, ids, ids_per, out_ids, len,
                        pval, pidx, counter);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_int(int* y, int n, int v, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_int, dim3((n + 255) / 256), dim3(256), 0, s, y, n, v);
     return hipGetLastError();
 }
 

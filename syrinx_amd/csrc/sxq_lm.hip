@@ -13,6 +13,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "sxq_abi.h"
@@ -77,6 +78,7 @@ struct sxq_lm {
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
     hipStream_t cap = nullptr;
     std::map<GraphKey, hipGraphExec_t> graphs;
+    std::map<std::string, hipGraphExec_t> expand_graphs;  // keyed by the raw bytes of the arguments
     void* pf = nullptr;  // prefill workspace, grown to the largest prompt batch so far
     size_t pf_size = 0;
     std::vector<void*> allocs;
@@ -235,8 +237,68 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
     return hipSuccess;
 }
 
+// FastAr::expand_batch (crates/syrinx-fish/src/s2/fast_ar.rs:170-224) as one kernel
+// sequence over the engine's buffers: the cache emptied (a fresh KvCache), position 0 run
+// on the slow hidden (its logits unused), codebook 0 = first_code of the semantic id, then
+// positions 1..n_codes-1 each embed the previous code (the dense shared table) and draw the
+// next code from their logits on the device -- into the engine's ids (the next input) and
+// into codes[s * codes_stride + cb].
+constexpr size_t kMaxExpandGraphs = 16;  // captured expansions kept per engine
+
+struct ExpandArgs {
+    int n;
+    const float* hidden;
+    const int32_t* semantic;
+    int sem_stride;
+    const int32_t* active;
+    sxq_fish_sampling p;
+    uint64_t* rng;
+    int n_codes;
+    int32_t* codes;
+    int codes_stride;
+};
+
+hipError_t enqueue_expand(sxq_lm* lm, const ExpandArgs& a, hipStream_t s) {
+    const sxq_lm_config& c = lm->c;
+    hipError_t e = launch_fill_int(lm->d_len, a.n, 0, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(lm->h, a.hidden, sizeof(float) * (size_t)a.n * c.dim, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = enqueue_step(lm, a.n, true, s);
+    if (e == hipSuccess)
+        e = launch_first_codes(a.semantic, a.sem_stride, a.n, a.p.semantic_begin, c.vocab, a.active, lm->d_ids, a.codes,
+                               a.codes_stride, s);
+    for (int cb = 1; cb < a.n_codes && e == hipSuccess; ++cb) {
+        e = enqueue_step(lm, a.n, false, s);
+        if (e == hipSuccess)
+            e = launch_sample_codebook(lm->logits, c.vocab, a.n, c.vocab, a.p, a.rng, a.active, lm->d_ids, 1,
+                                       a.codes + cb, a.codes_stride, s);
+    }
+    return e;
+}
+
+std::string expand_key(const ExpandArgs& a) {
+    std::string k;
+    auto put = [&](const void* p, size_t b) { k.append((const char*)p, b); };
+    put(&a.n, sizeof a.n);
+    put(&a.hidden, sizeof a.hidden);
+    put(&a.semantic, sizeof a.semantic);
+    put(&a.sem_stride, sizeof a.sem_stride);
+    put(&a.active, sizeof a.active);
+    put(&a.p.temperature, sizeof(float));
+    put(&a.p.top_p, sizeof(float));
+    put(&a.p.top_k, sizeof(int32_t));
+    put(&a.p.repetition_penalty, sizeof(float));
+    put(&a.p.semantic_begin, sizeof(int32_t));
+    put(&a.rng, sizeof a.rng);
+    put(&a.n_codes, sizeof a.n_codes);
+    put(&a.codes, sizeof a.codes);
+    put(&a.codes_stride, sizeof a.codes_stride);
+    return k;
+}
+
 void destroy_lm(sxq_lm* lm) {
     for (auto& kv : lm->graphs) (void)hipGraphExecDestroy(kv.second);
+    for (auto& kv : lm->expand_graphs) (void)hipGraphExecDestroy(kv.second);
     if (lm->pf) (void)hipFree(lm->pf);
     if (lm->cap) (void)hipStreamDestroy(lm->cap);
     for (void* p : lm->allocs) (void)hipFree(p);
@@ -694,6 +756,17 @@ sxq_status sxq_lm_set_lengths(sxq_lm* lm, const int32_t* lengths, int n) {
     return SXQ_OK;
 }
 
+sxq_status sxq_lm_reset(sxq_lm* lm, int n, void* stream) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_reset: null handle");
+    if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_reset: %d streams (max %d)", n, lm->c.max_batch);
+    std::lock_guard<std::mutex> lock(lm->mu);
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    HIP_TRY(hipMemsetAsync(lm->d_len, 0, sizeof(int) * n, (hipStream_t)stream), "lm_reset");
+    for (int s = 0; s < n; ++s) lm->h_len[s] = 0;
+    return SXQ_OK;
+}
+
 sxq_status sxq_lm_get_lengths(const sxq_lm* lm, int32_t* lengths, int n) {
     if (!lm || !lengths) return fail(SXQ_ERR_INVALID, "lm_get_lengths: null pointer");
     if (n < 1 || n > lm->c.max_batch) return fail(SXQ_ERR_INVALID, "lm_get_lengths: bad stream count");
@@ -757,6 +830,57 @@ sxq_status sxq_lm_step(sxq_lm* lm, int n, const int32_t* ids, const float* embed
     if (hidden)
         HIP_TRY(hipMemcpyAsync(hidden, lm->hn, sizeof(float) * n * lm->c.dim, hipMemcpyDeviceToDevice, st), "lm_step: hidden");
     if (next_ids) HIP_TRY(hipMemcpyAsync(next_ids, lm->d_next, sizeof(int) * n, hipMemcpyDeviceToDevice, st), "lm_step: next ids");
+    return SXQ_OK;
+}
+
+sxq_status sxq_fish_fast_expand(sxq_lm* lm, int n, const float* hidden, const int32_t* semantic, int semantic_stride,
+                                const int32_t* active, const sxq_fish_sampling* params, uint64_t* rng, int n_codes,
+                                int32_t* codes, int codes_stride, unsigned flags, void* stream) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "fast_expand: null handle");
+    const sxq_lm_config& c = lm->c;
+    if (n < 1 || n > c.max_batch) return fail(SXQ_ERR_INVALID, "fast_expand: %d streams (max %d)", n, c.max_batch);
+    if (!hidden || !semantic || !params || !rng || !codes) return fail(SXQ_ERR_INVALID, "fast_expand: null pointer");
+    if (flags & ~SXQ_LM_GRAPH) return fail(SXQ_ERR_INVALID, "fast_expand: unknown flags 0x%x", flags);
+    if (c.n_codebooks != 0 || c.tied_embedding || (c.embed_rows > 0 && c.embed_rows < c.vocab))
+        return fail(SXQ_ERR_INVALID,
+                    "fast_expand: the engine must embed single code ids from a dense table of >= vocab rows "
+                    "(n_codebooks 0, tied_embedding 0)");
+    if (n_codes < 1 || n_codes > c.max_seq)
+        return fail(SXQ_ERR_INVALID, "fast_expand: %d codes per frame (the local cache holds %d)", n_codes, c.max_seq);
+    if (semantic_stride < 1 || codes_stride < 1) return fail(SXQ_ERR_INVALID, "fast_expand: strides must be >= 1");
+    if (!fish_sampling_fits(*params)) return fail(SXQ_ERR_INVALID, "fast_expand: top_k %d outside 1..64", params->top_k);
+    std::lock_guard<std::mutex> lock(lm->mu);
+    if (lm->trace) return fail(SXQ_ERR_INVALID, "fast_expand: clear the step trace first");
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    hipStream_t st = (hipStream_t)stream;
+    const ExpandArgs a{n, hidden, semantic, semantic_stride, active, *params, rng, n_codes, codes, codes_stride};
+    if (flags & SXQ_LM_GRAPH) {
+        const std::string key = expand_key(a);
+        auto it = lm->expand_graphs.find(key);
+        if (it == lm->expand_graphs.end()) {
+            if (lm->expand_graphs.size() >= kMaxExpandGraphs) {  // callers cycling buffers: start over
+                HIP_TRY(hipStreamSynchronize(st), "fast_expand: sync before dropping graphs");
+                for (auto& kv : lm->expand_graphs) (void)hipGraphExecDestroy(kv.second);
+                lm->expand_graphs.clear();
+            }
+            hipGraph_t graph = nullptr;
+            hipGraphExec_t exec = nullptr;
+            HIP_TRY(hipStreamSynchronize(st), "fast_expand: sync before capture");
+            HIP_TRY(hipStreamBeginCapture(lm->cap, hipStreamCaptureModeThreadLocal), "fast_expand: begin capture");
+            hipError_t e = enqueue_expand(lm, a, lm->cap);
+            hipError_t e2 = hipStreamEndCapture(lm->cap, &graph);
+            if (e == hipSuccess) e = e2;
+            if (e == hipSuccess) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            if (graph) (void)hipGraphDestroy(graph);
+            if (e != hipSuccess) return hip_fail(e, "fast_expand: graph capture");
+            it = lm->expand_graphs.emplace(key, exec).first;
+        }
+        HIP_TRY(hipGraphLaunch(it->second, st), "fast_expand: graph launch");
+    } else {
+        HIP_TRY(enqueue_expand(lm, a, st), "fast_expand");
+    }
+    for (int s = 0; s < n; ++s) lm->h_len[s] = n_codes;
     return SXQ_OK;
 }
 

@@ -244,6 +244,9 @@ struct FishArgs {
     int n_recent;
     int32_t* out;
     int out_stride;
+    int32_t* active;  // [n] or null: a zero entry draws nothing (rng kept, out 0); a stop draw clears it
+    int32_t* out2;    // a second copy of the token (null: none), out2[s * out2_stride]
+    int out2_stride;
 };
 
 // mode 0: sample_semantic (constraint + RAS, window update); mode 1: sample_codebook.
@@ -253,6 +256,13 @@ __global__ __launch_bounds__(kST) void k_sample_fish(FishArgs A) {
     const int s = blockIdx.x, tid = threadIdx.x;
     const float* row = A.logits + (int64_t)s * A.stride;
     const sxq_fish_sampling& P = A.p;
+    if (A.active && A.active[s] == 0) {  // a finished stream: an inert 0, no draw (drive_batch)
+        if (tid == 0) {
+            A.out[(int64_t)s * A.out_stride] = 0;
+            if (A.out2) A.out2[(int64_t)s * A.out2_stride] = 0;
+        }
+        return;
+    }
     View v{0, A.vocab, -1};
     if (MODE == 0 && P.semantic_begin <= P.semantic_end) {
         v.lo = max(0, P.semantic_begin);
@@ -316,9 +326,11 @@ __global__ __launch_bounds__(kST) void k_sample_fish(FishArgs A) {
             win[len++] = tok;
             A.window_len[s] = len;
         }
+        if (A.active && tok == P.stop_id) A.active[s] = 0;  // is_stop: frozen from here on
     }
     A.rng[s] = rng;
     A.out[(int64_t)s * A.out_stride] = tok;
+    if (A.out2) A.out2[(int64_t)s * A.out2_stride] = tok;
 }
 
 struct RasArgs {
@@ -432,6 +444,22 @@ __global__ __launch_bounds__(kST) void k_sample_ras(RasArgs A) {
     A.out[(int64_t)s * A.out_stride] = tok;
 }
 
+// FastAr::first_code (crates/syrinx-fish/src/s2/fast_ar.rs:105-110) per stream:
+// clamp(semantic - begin, 0, residual - 1), u32 saturating at 0; an inactive stream's
+// first code is the inert 0 (drive_batch's placeholder).
+__global__ void k_first_codes(const int32_t* __restrict__ semantic, int sem_stride, int n, int begin, int residual,
+                              const int32_t* __restrict__ active, int32_t* __restrict__ ids,
+                              int32_t* __restrict__ codes, int codes_stride) {
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= n) return;
+    const int64_t tok = (int64_t)(uint32_t)semantic[(int64_t)s * sem_stride];
+    int64_t c = tok - begin;
+    c = c < 0 ? 0 : (c > residual - 1 ? residual - 1 : c);
+    if (active && active[s] == 0) c = 0;
+    ids[s] = (int32_t)c;
+    if (codes) codes[(int64_t)s * codes_stride] = (int32_t)c;
+}
+
 sxq_status check_common(int n, int vocab, int top_k, const void* logits, const void* rng, const void* out) {
     if (n < 1 || n > 65535 || vocab < 1) return fail(SXQ_ERR_INVALID, "sample: bad shape (%d streams, %d ids)", n, vocab);
     if (top_k < 1 || top_k > kMaxTopK)
@@ -442,11 +470,35 @@ sxq_status check_common(int n, int vocab, int top_k, const void* logits, const v
 
 }  // namespace
 
+namespace sxq {
+namespace abi {
+
+bool fish_sampling_fits(const sxq_fish_sampling& p) { return p.top_k >= 1 && p.top_k <= kMaxTopK; }
+
+hipError_t launch_sample_codebook(const float* logits, int64_t stride, int n, int vocab, const sxq_fish_sampling& p,
+                                  uint64_t* rng, const int32_t* active, int32_t* out, int out_stride, int32_t* out2,
+                                  int out2_stride, hipStream_t s) {
+    FishArgs A{logits, stride, vocab, p, rng, nullptr, nullptr, nullptr, 0, out, out_stride,
+               const_cast<int32_t*>(active), out2, out2_stride};
+    hipLaunchKernelGGL(k_sample_fish<1>, dim3(n), dim3(kST), 0, s, A);
+    return hipGetLastError();
+}
+
+hipError_t launch_first_codes(const int32_t* semantic, int sem_stride, int n, int begin, int residual,
+                              const int32_t* active, int32_t* ids, int32_t* codes, int codes_stride, hipStream_t s) {
+    hipLaunchKernelGGL(k_first_codes, dim3((n + 63) / 64), dim3(64), 0, s, semantic, sem_stride, n, begin, residual,
+                       active, ids, codes, codes_stride);
+    return hipGetLastError();
+}
+
+}  // namespace abi
+}  // namespace sxq
+
 extern "C" {
 
 sxq_status sxq_sample_semantic(int device, const float* logits, int64_t logits_stride, int n, int vocab,
                                const sxq_fish_sampling* p, uint64_t* rng, int32_t* window, int32_t* window_len,
-                               int32_t* out, int out_stride, void* stream) {
+                               int32_t* active, int32_t* out, int out_stride, void* stream) {
     if (!p) return fail(SXQ_ERR_INVALID, "sample_semantic: null parameters");
     sxq_status st = check_common(n, vocab, p->top_k, logits, rng, out);
     if (st != SXQ_OK) return st;
@@ -455,7 +507,7 @@ sxq_status sxq_sample_semantic(int device, const float* logits, int64_t logits_s
     if (!window != !window_len) return fail(SXQ_ERR_INVALID, "sample_semantic: window and window_len go together");
     DeviceGuard g(device);
     HIP_TRY(g.err, "hipSetDevice");
-    FishArgs A{logits, logits_stride, vocab, *p, rng, window, window_len, nullptr, 0, out, out_stride};
+    FishArgs A{logits, logits_stride, vocab, *p, rng, window, window_len, nullptr, 0, out, out_stride, active, nullptr, 0};
     hipLaunchKernelGGL(k_sample_fish<0>, dim3(n), dim3(kST), 0, (hipStream_t)stream, A);
     HIP_TRY(hipGetLastError(), "sample_semantic");
     return SXQ_OK;
@@ -463,7 +515,7 @@ sxq_status sxq_sample_semantic(int device, const float* logits, int64_t logits_s
 
 sxq_status sxq_sample_codebook(int device, const float* logits, int64_t logits_stride, int n, int vocab,
                                const sxq_fish_sampling* p, uint64_t* rng, const int32_t* recent, int n_recent,
-                               int32_t* out, int out_stride, void* stream) {
+                               const int32_t* active, int32_t* out, int out_stride, void* stream) {
     if (!p) return fail(SXQ_ERR_INVALID, "sample_codebook: null parameters");
     sxq_status st = check_common(n, vocab, p->top_k, logits, rng, out);
     if (st != SXQ_OK) return st;
@@ -471,7 +523,8 @@ sxq_status sxq_sample_codebook(int device, const float* logits, int64_t logits_s
         return fail(SXQ_ERR_INVALID, "sample_codebook: %d recent ids (at most %d)", n_recent, kMaxWindow);
     DeviceGuard g(device);
     HIP_TRY(g.err, "hipSetDevice");
-    FishArgs A{logits, logits_stride, vocab, *p, rng, nullptr, nullptr, recent, n_recent, out, out_stride};
+    FishArgs A{logits, logits_stride, vocab, *p, rng, nullptr, nullptr, recent, n_recent, out, out_stride,
+               const_cast<int32_t*>(active), nullptr, 0};
     hipLaunchKernelGGL(k_sample_fish<1>, dim3(n), dim3(kST), 0, (hipStream_t)stream, A);
     HIP_TRY(hipGetLastError(), "sample_codebook");
     return SXQ_OK;

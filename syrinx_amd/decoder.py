@@ -99,6 +99,21 @@ def cosyvoice2_lm_config(n_layers=24, max_seq=1024, max_batch=1, dtype=GgmlDType
     return DecoderConfig(**base)
 
 
+def fish_s2_fast_ar_config(n_layers=4, num_codebooks=10, residual_size=4096, max_batch=1, dtype=GgmlDType.Q4K,
+                           **kw) -> DecoderConfig:
+    """The s2-pro fast AR (the audio decoder, crates/syrinx-fish/src/s2/fast_ar.rs:1-66):
+    4 layers of the slow block's geometry (dim 2560, 32/8 heads of 128, SwiGLU 9728, eps
+    1e-6) with no QK-norm and no qkv/o bias, interleaved RoPE (base 1e6) over the codebook
+    axis, a local cache of num_codebooks positions, the shared fast_embeddings table
+    [residual_size, 2560] as its input and fast_output [residual_size, 2560] as its head."""
+    base = dict(n_layers=n_layers, dim=2560, n_heads=32, n_kv_heads=8, head_dim=128, intermediate=9728,
+                vocab=residual_size, max_seq=num_codebooks, max_batch=max_batch, weight_dtype=int(dtype),
+                norm_eps=1e-6, rope_theta=1e6, rope_interleaved=1, qk_norm=0, qkv_bias=0, head_bias=0,
+                tied_embedding=0, embed_rows=residual_size)
+    base.update(kw)
+    return DecoderConfig(**base)
+
+
 class DecoderLM:
     """A decode-step engine (sxq_lm) on one GPU."""
 
@@ -149,8 +164,9 @@ class DecoderLM:
         return list(arr)
 
     def reset(self, n=None) -> None:
-        """SlowAr::reset (slow_ar.rs:79-81): empty caches."""
-        self.set_lengths([0] * (n or self.cfg.max_batch))
+        """SlowAr::reset (slow_ar.rs:79-81): empty the caches of streams 0..n-1, ordered on
+        the current stream."""
+        check(lib().sxq_lm_reset(self._h, n or self.cfg.max_batch, torch.cuda.current_stream(self.device).cuda_stream))
 
     def weight_bytes(self):
         lb, hb = ctypes.c_size_t(), ctypes.c_size_t()
@@ -159,10 +175,12 @@ class DecoderLM:
 
     # -- step ---------------------------------------------------------------------------
     def step(self, ids: torch.Tensor = None, embeds: torch.Tensor = None, n: int = None, graph: bool = False,
-             want_logits: bool = True, want_hidden: bool = False):
+             want_logits: bool = True, want_hidden: bool = False, out=None):
         """One token for n streams.  ids int32 [n, 1 + n_codebooks] (or [n]) or embeds
         f32 [n, dim]; None for both reuses the previous argmax.  Returns (logits, next_ids),
-        or (logits, next_ids, hidden) with want_hidden (the post-final-RMSNorm state)."""
+        or (logits, next_ids, hidden) with want_hidden (the post-final-RMSNorm state).
+        out = (logits, next_ids, hidden) writes into those device tensors instead (fixed
+        buffers for a loop whose later launches are captured on their addresses)."""
         if ids is not None:
             ids = ids.to(device=self.device, dtype=torch.int32).reshape(-1, self.ids_per).contiguous()
             n = ids.shape[0]
@@ -171,9 +189,16 @@ class DecoderLM:
             n = embeds.shape[0]
         if n is None:
             raise ValueError("step: give ids, embeds or n")
-        logits = torch.empty((n, self.cfg.vocab), dtype=torch.float32, device=self.device) if want_logits else None
-        nxt = torch.empty((n,), dtype=torch.int32, device=self.device)
-        hidden = torch.empty((n, self.cfg.dim), dtype=torch.float32, device=self.device) if want_hidden else None
+        if out is not None:
+            logits, nxt, hidden = out
+            for t, w in ((logits, self.cfg.vocab), (hidden, self.cfg.dim)):
+                if t is not None and (t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != n * w):
+                    raise ValueError("step: out buffers must be contiguous f32 of n rows")
+            want_hidden = True
+        else:
+            logits = torch.empty((n, self.cfg.vocab), dtype=torch.float32, device=self.device) if want_logits else None
+            nxt = torch.empty((n,), dtype=torch.int32, device=self.device)
+            hidden = torch.empty((n, self.cfg.dim), dtype=torch.float32, device=self.device) if want_hidden else None
         P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
         check(lib().sxq_lm_step(self._h, n, P(ids), P(embeds), P(logits), P(hidden), P(nxt), LM_GRAPH if graph else 0,
                                 torch.cuda.current_stream(self.device).cuda_stream))
@@ -291,12 +316,14 @@ class SlowAr(DecoderLM):
         self._last_argmax = nxt
         return logits[0], hidden.reshape(1, 1, -1)
 
-    def slow_step_batch(self, frames, graph: bool = True):
+    def slow_step_batch(self, frames, graph: bool = True, out=None):
         """frames: [n, 1 + num_codebooks]; ragged cache lengths need no left padding
-        (slow_ar.rs:456-499).  Returns (semantic_logits [n, vocab], hidden [n, 1, dim])."""
-        logits, nxt, hidden = self.step(ids=torch.as_tensor(frames, dtype=torch.int32), graph=graph, want_hidden=True)
+        (slow_ar.rs:456-499).  Returns (semantic_logits [n, vocab], hidden [n, 1, dim]);
+        out = (logits, next_ids, hidden) as for step()."""
+        logits, nxt, hidden = self.step(ids=torch.as_tensor(frames, dtype=torch.int32), graph=graph, want_hidden=True,
+                                        out=out)
         self._last_argmax = nxt
-        return logits, hidden.reshape(hidden.shape[0], 1, -1)
+        return logits, hidden.reshape(-1, 1, self.cfg.dim)
 
     def prefill(self, prompt, graph: bool = False):
         """SlowAr::prefill (slow_ar.rs:250-256): prompt [1 + num_codebooks, T] (rows =
@@ -334,3 +361,49 @@ class Qwen2Lm(DecoderLM):
             return logits.reshape(b, 1, -1)
         logits, _, _ = self.prefill(embeds=[embeds[i].reshape(t, -1) for i in range(b)], all_logits=True)
         return logits.reshape(b, t, -1)
+
+
+class FastAr(DecoderLM):
+    """Fish s2 fast AR (crates/syrinx-fish/src/s2/fast_ar.rs:28-224) over the decode engine:
+    the per-frame expansion of one slow hidden into num_codebooks codes runs on the device,
+    drawing each residual code with the driver's FishSampler (sxq_fish_fast_expand)."""
+
+    def first_code(self, semantic_token: int, semantic_begin: int) -> int:
+        """FastAr::first_code (fast_ar.rs:105-110): clamp(tok - begin, 0, residual - 1),
+        saturating at 0."""
+        return min(max(int(semantic_token) - int(semantic_begin), 0), self.cfg.vocab - 1)
+
+    def expand_batch(self, hidden: torch.Tensor, semantic: torch.Tensor, sampler, active: torch.Tensor = None,
+                     codes: torch.Tensor = None, graph: bool = True, n_codes: int = None):
+        """FastAr::expand_batch (fast_ar.rs:170-224).  hidden f32 [n, 1, dim] (device), the
+        sampled semantic ids (device int32: [n], or a column view such as frames[:, 0] of a
+        [n, 1 + n_codes] ids frame), `sampler` a FishSampler of n streams (its rng advances
+        by one draw per residual code of each active stream), `active` int32 [n] or None.
+        Writes and returns codes [n, n_codes] (or the given strided view, e.g. frames[:, 1:])
+        with codes[:, 0] = first_code(semantic)."""
+        n_codes = n_codes or self.cfg.max_seq
+        hidden = hidden.reshape(-1, self.cfg.dim)
+        n = hidden.shape[0]
+        if hidden.dtype != torch.float32 or not hidden.is_contiguous() or hidden.device != self.device:
+            raise ValueError("expand_batch: hidden must be contiguous f32 on the engine's device")
+        if semantic.dtype != torch.int32 or semantic.device != self.device or semantic.shape[0] != n:
+            raise ValueError("expand_batch: semantic must be int32 [n] on the engine's device")
+        if codes is None:
+            codes = torch.empty((n, n_codes), dtype=torch.int32, device=self.device)
+        if codes.dtype != torch.int32 or codes.shape[0] != n or codes.shape[-1] < n_codes or codes.stride(-1) != 1:
+            raise ValueError("expand_batch: codes must be int32 [n, >= n_codes] with unit column stride")
+        if sampler.n != n:
+            raise ValueError(f"expand_batch: the sampler holds {sampler.n} streams, not {n}")
+        c = sampler._c()
+        P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+        check(lib().sxq_fish_fast_expand(self._h, n, P(hidden), P(semantic), semantic.stride(0), P(active),
+                                         ctypes.byref(c), P(sampler.rng), n_codes, P(codes), codes.stride(0),
+                                         LM_GRAPH if graph else 0, torch.cuda.current_stream(self.device).cuda_stream))
+        return codes
+
+    def expand(self, hidden: torch.Tensor, first_code: int, sampler, graph: bool = True):
+        """FastAr::expand (fast_ar.rs:116-160) for one frame: returns the num_codebooks
+        codes (a host list, index 0 == first_code)."""
+        sem = torch.tensor([int(first_code) + sampler.semantic[0]], dtype=torch.int32, device=self.device)
+        return self.expand_batch(hidden, sem, sampler, graph=graph)[0].tolist()
+

@@ -76,28 +76,31 @@ class FishSampler:
         return FishSamplingParams(p.temperature, p.top_p, p.top_k, p.repetition_penalty, p.ras_win_size,
                                   p.ras_high_temp, p.ras_high_top_p, b, e, stop)
 
-    def sample_semantic(self, logits: torch.Tensor, out: torch.Tensor = None, out_stride: int = 1):
+    def sample_semantic(self, logits: torch.Tensor, out: torch.Tensor = None, out_stride: int = 1,
+                        active: torch.Tensor = None):
         """logits [n, vocab] f32 (device) -> ids [n] int32; with `out` the ids go to
-        out[i * out_stride] instead (e.g. column 0 of the next step's frames)."""
+        out[i * out_stride] instead (e.g. column 0 of the next step's frames).  `active`
+        int32 [n] (device): streams at 0 draw nothing; a stop draw sets a stream's flag to 0."""
         logits = logits.reshape(self.n, -1)
         if out is None:
             out = torch.empty(self.n, dtype=torch.int32, device=self.device)
         c = self._c()
         check(lib().sxq_sample_semantic(_dev(self.device), _p(logits), logits.stride(0), self.n, logits.shape[1],
-                                        ctypes.byref(c), _p(self.rng), _p(self.window), _p(self.window_len), _p(out),
-                                        out_stride, torch.cuda.current_stream(self.device).cuda_stream))
+                                        ctypes.byref(c), _p(self.rng), _p(self.window), _p(self.window_len),
+                                        _p(active), _p(out), out_stride,
+                                        torch.cuda.current_stream(self.device).cuda_stream))
         return out
 
     def sample_codebook(self, logits: torch.Tensor, recent: torch.Tensor = None, out: torch.Tensor = None,
-                        out_stride: int = 1):
+                        out_stride: int = 1, active: torch.Tensor = None):
         logits = logits.reshape(self.n, -1)
         if out is None:
             out = torch.empty(self.n, dtype=torch.int32, device=self.device)
         n_recent = 0 if recent is None else recent.shape[1]
         c = self._c()
         check(lib().sxq_sample_codebook(_dev(self.device), _p(logits), logits.stride(0), self.n, logits.shape[1],
-                                        ctypes.byref(c), _p(self.rng), _p(recent), n_recent, _p(out), out_stride,
-                                        torch.cuda.current_stream(self.device).cuda_stream))
+                                        ctypes.byref(c), _p(self.rng), _p(recent), n_recent, _p(active), _p(out),
+                                        out_stride, torch.cuda.current_stream(self.device).cuda_stream))
         return out
 
 

@@ -69,6 +69,13 @@ def test_workspace_entry_points_check_arguments_without_a_gpu():
     assert "null handle" in L.sxq_last_error().decode()
 
 
+def test_fast_expand_and_reset_check_arguments_without_a_gpu():
+    L = _lib.lib()
+    assert L.sxq_fish_fast_expand(None, 1, None, None, 1, None, None, None, 10, None, 1, 0, None) == _lib.ERR_INVALID
+    assert "null handle" in L.sxq_last_error().decode()
+    assert L.sxq_lm_reset(None, 1, None) == _lib.ERR_INVALID
+
+
 def test_python_mirror_rejects_misaligned_quantize():
     import torch
     with pytest.raises(syrinx_amd.SxqError) as e:

@@ -69,11 +69,11 @@ def model_oracle():
     return model
 
 
-def _build(cfg, cuda, seed, n_streams):
-    """Random weights -> GPU engine and the same blocks/vectors for the oracle."""
+def _build(cfg, cuda, seed, n_streams, cls=D.DecoderLM):
+    """Random weights -> GPU engine (of class cls) and the same blocks/vectors for the oracle."""
     rng = np.random.default_rng(seed)
     dt = GgmlDType(cfg.weight_dtype)
-    lm = D.DecoderLM(cfg, device=cuda)
+    lm = cls(cfg, device=cuda)
     W = {}
     hd, nh, nkv = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     qkv_n = (nh + 2 * nkv) * hd

@@ -117,3 +117,32 @@ def test_device_draws_are_an_unbiased_categorical(cuda):
         counts += np.bincount(got, minlength=5)
     f = counts / counts.sum()
     assert np.abs(f - probs).max() < 1e-2, f
+
+
+def test_active_flags_freeze_finished_streams(cuda):
+    """drive_batch's `finished` on the device: a stream whose flag is 0 draws nothing (rng
+    kept, token 0), a semantic draw of the stop id clears the stream's flag, and codebook
+    draws read the flags without changing them."""
+    n, vocab = 3, 300
+    begin, end, stop = 100, 199, 250
+    params = SamplingParams()
+    dev = FishSampler([7, 8, 9], params, (begin, end, stop), device=cuda)
+    x = np.full((n, vocab), -30.0, np.float32)
+    x[0, stop] = 20.0   # stream 0 draws the stop id
+    x[1, 120] = 20.0
+    x[2, 150] = 20.0
+    active = torch.tensor([1, 0, 1], dtype=torch.int32, device=cuda)
+    rng0 = dev.rng.clone()
+    got = dev.sample_semantic(torch.from_numpy(x).to(cuda), active=active).cpu().numpy()
+    assert got.tolist() == [stop, 0, 150]
+    assert active.cpu().tolist() == [0, 0, 1]
+    adv = (dev.rng - rng0).cpu().tolist()
+    assert adv[1] == 0 and adv[0] == adv[2] != 0  # two uniforms each for streams 0 and 2
+    assert dev.window_len.cpu().tolist() == [0, 0, 1]  # a stop is not pushed into the window
+    before = dev.rng.clone()
+    y = np.zeros((n, 64), np.float32)
+    y[:, 5] = 30.0
+    codes = dev.sample_codebook(torch.from_numpy(y).to(cuda), active=active).cpu().numpy()
+    assert codes.tolist() == [0, 0, 5]
+    assert active.cpu().tolist() == [0, 0, 1]
+    assert torch.equal(dev.rng[:2], before[:2]) and not torch.equal(dev.rng[2:], before[2:])
