@@ -162,6 +162,28 @@ sxq_status sxq_qmm_destroy(sxq_qmm *qmm);
 sxq_status sxq_fill_normal(int device, float *out, int64_t n, uint64_t seed, float mean, float std_dev,
                            void *stream);
 
+/* ---- Embedding tables: per-row int8 / int4 with dequant-on-gather -------------------
+ * quantize_embed (crates/syrinx-lm/src/cv2/quant.rs:38-89) and embed_rows
+ * (crates/syrinx-lm/src/cv2/generate.rs:22-67), the embedding policy of
+ * Qwen2Lm::load_quantized (cv2/load.rs:86-91).  Row r of an f32 table [rows, h] gets
+ * scale[r] = max|row| / qmax + 1e-12 and codes round(x / scale) in [-qmax, qmax]:
+ *   SXQ_EMBED_INT8: qmax 127, q [rows, h] bytes code + 128;
+ *   SXQ_EMBED_INT4: qmax 7, q [rows, h / 2] bytes, element 2j in the low nibble of byte j,
+ *                   2j + 1 in the high one, each code + 8 (h must be even).
+ * A gathered element is (float)code * scale[row], bit for bit the reference's. */
+enum { SXQ_EMBED_INT4 = 4, SXQ_EMBED_INT8 = 8 };
+/* The scheme a table of row width h is stored at: int4 falls back to int8 for odd h
+ * (quant.rs:41-46). */
+sxq_status sxq_embed_scheme(int requested, int64_t h, int *effective);
+/* Quantize a device f32 table into device q (rows * h or rows * h / 2 bytes) and scale
+ * (rows floats), enqueued on `stream`. */
+sxq_status sxq_embed_quantize(int device, int scheme, const float *table, int64_t rows, int64_t h, uint8_t *q,
+                              float *scale, void *stream);
+/* out f32 [n, h] = the dequantized rows ids[0..n) (device int32; an id outside the table
+ * gives a zero row), enqueued on `stream`. */
+sxq_status sxq_embed_gather(int device, int scheme, const uint8_t *q, const float *scale, int64_t rows, int64_t h,
+                            const int32_t *ids, int n, float *out, void *stream);
+
 /* ---- Decoder step: the callers of QMatMul in one autoregressive LM token ------------
  *
  * One decode step of a Qwen2/Qwen3-style LM for up to 16 independent streams, all on
@@ -240,6 +262,11 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config *cfg, sxq_lm **out);
 sxq_status sxq_lm_set_linear(sxq_lm *lm, int layer, int which, const sxq_qmm *w);
 /* Copy an f32 vector (norm weight, bias, embedding table) into a slot. */
 sxq_status sxq_lm_set_vector(sxq_lm *lm, int layer, int which, const float *data, int64_t n, int src_is_device);
+/* Hold the model's dense input table (SXQ_LM_EMBED, [embed_rows, dim]) as a per-row int8 /
+ * int4 table instead (sxq_embed_quantize's layout, device pointers copied in): every step
+ * and prefill then dequantizes the rows it gathers (Qwen2Lm::embed_rows of the quantized
+ * build, cv2/generate.rs:22-67).  Only for models with an untied input table. */
+sxq_status sxq_lm_set_embed_quantized(sxq_lm *lm, int scheme, const uint8_t *q, const float *scale);
 /* Synthetic weights: every projection N(0, std) quantized with from_float, norm weights
  * 1, biases / tables N(0, std).  For benchmarks; no reference counterpart. */
 sxq_status sxq_lm_init_random(sxq_lm *lm, uint64_t seed, float std_dev);

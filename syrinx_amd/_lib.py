@@ -67,6 +67,10 @@ _SIGS = {
     "sxq_lm_set_lengths": (_I, [_P, _P, _I]),
     "sxq_lm_get_lengths": (_I, [_P, _P, _I]),
     "sxq_lm_reset": (_I, [_P, _I, _P]),
+    "sxq_lm_set_embed_quantized": (_I, [_P, _I, _P, _P]),
+    "sxq_embed_scheme": (_I, [_I, _I64, _P]),
+    "sxq_embed_quantize": (_I, [_I, _I, _P, _I64, _I64, _P, _P, _P]),
+    "sxq_embed_gather": (_I, [_I, _I, _P, _P, _I64, _I64, _P, _I, _P, _P]),
     "sxq_lm_step": (_I, [_P, _I, _P, _P, _P, _P, _P, _U, _P]),
     "sxq_lm_read_kv": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "sxq_lm_prefill": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _U, _P, _SZ, _P]),

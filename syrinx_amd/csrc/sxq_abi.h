@@ -17,6 +17,12 @@ hipError_t launch_sample_codebook(const float* logits, int64_t stride, int n, in
 hipError_t launch_first_codes(const int32_t* semantic, int sem_stride, int n, int begin, int residual,
                               const int32_t* active, int32_t* ids, int32_t* codes, int codes_stride, hipStream_t s);
 
+// Per-row int8 / int4 embedding tables (sxq_embed.hip).
+int embed_effective_scheme(int scheme, int64_t h);
+size_t embed_code_bytes(int scheme, int64_t rows, int64_t h);
+hipError_t launch_embed_gather(int scheme, const uint8_t* q, const float* scale, int64_t rows, int h, const int32_t* ids,
+                               int ids_stride, int n, float* out, hipStream_t s);
+
 // Record `fmt` as this thread's sxq_last_error() and return `code`.
 sxq_status fail(sxq_status code, const char* fmt, ...);
 // Map a HIP error to SXQ_ERR_OOM / SXQ_ERR_DEVICE with its text.

@@ -60,6 +60,9 @@ struct sxq_lm {
     std::vector<LmLayer> layers;
     DevWeight head;
     float *head_bias = nullptr, *final_norm = nullptr, *embed = nullptr, *cb_embed = nullptr;
+    int embed_scheme = 0;            // SXQ_EMBED_INT8 / _INT4 when the input table is held quantized
+    uint8_t* embed_q = nullptr;      // its codes, and per-row scales
+    float* embed_scale = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
     float *kc = nullptr, *vc = nullptr;
     int* d_len = nullptr;
@@ -172,6 +175,9 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
         if (c.tied_embedding)
             STEP(launch_embed_quant_table(lm->d_ids, lm->ids_per, n, lm->head.w, c.dim, lm->cb_embed, c.n_codebooks,
                                           c.codebook_size, c.semantic_begin, c.semantic_end, lm->h, s));
+        else if (lm->embed_scheme)
+            STEP(launch_embed_gather(lm->embed_scheme, lm->embed_q, lm->embed_scale, c.embed_rows > 0 ? c.embed_rows : c.vocab,
+                                     c.dim, lm->d_ids, lm->ids_per, n, lm->h, s));
         else
             STEP(launch_embed_dense(lm->d_ids, lm->ids_per, n, lm->embed, c.embed_rows > 0 ? c.embed_rows : c.vocab, c.dim,
                                     lm->h, s));
@@ -438,7 +444,11 @@ hipError_t enqueue_prefill(sxq_lm* lm, const PrefillMeta& pm, int T, const int* 
         PF(launch_embed_quant_table(ids, lm->ids_per, T, lm->head.w, c.dim, lm->cb_embed, c.n_codebooks,
                                     c.codebook_size, c.semantic_begin, c.semantic_end, h, s));
     } else {
-        PF(launch_embed_dense(ids, lm->ids_per, T, lm->embed, c.embed_rows > 0 ? c.embed_rows : c.vocab, c.dim, h, s));
+        if (lm->embed_scheme)
+            PF(launch_embed_gather(lm->embed_scheme, lm->embed_q, lm->embed_scale, c.embed_rows > 0 ? c.embed_rows : c.vocab,
+                                   c.dim, ids, lm->ids_per, T, h, s));
+        else
+            PF(launch_embed_dense(ids, lm->ids_per, T, lm->embed, c.embed_rows > 0 ? c.embed_rows : c.vocab, c.dim, h, s));
     }
     PF(record(h, Td));
     for (int l = 0; l < c.n_layers; ++l) {
@@ -696,6 +706,36 @@ sxq_status sxq_lm_set_vector(sxq_lm* lm, int layer, int which, const float* data
     HIP_TRY(g.err, "hipSetDevice");
     HIP_TRY(hipMemcpy(dst, data, sizeof(float) * n, src_is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
             "lm_set_vector: copy");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_set_embed_quantized(sxq_lm* lm, int scheme, const uint8_t* q, const float* scale) {
+    if (!lm) return fail(SXQ_ERR_INVALID, "lm_set_embed_quantized: null handle");
+    const sxq_lm_config& c = lm->c;
+    if (c.tied_embedding || !lm->embed)
+        return fail(SXQ_ERR_INVALID, "lm_set_embed_quantized: this model has a tied embedding");
+    if (scheme != SXQ_EMBED_INT8 && scheme != SXQ_EMBED_INT4)
+        return fail(SXQ_ERR_INVALID, "lm_set_embed_quantized: unknown scheme %d", scheme);
+    if (embed_effective_scheme(scheme, c.dim) != scheme)
+        return fail(SXQ_ERR_INVALID, "lm_set_embed_quantized: int4 needs an even row width (dim %d)", c.dim);
+    if (!q || !scale) return fail(SXQ_ERR_INVALID, "lm_set_embed_quantized: null pointer");
+    std::lock_guard<std::mutex> lock(lm->mu);
+    DeviceGuard g(lm->device);
+    HIP_TRY(g.err, "hipSetDevice");
+    const int64_t rows = c.embed_rows > 0 ? c.embed_rows : c.vocab;
+    const size_t qb = embed_code_bytes(scheme, rows, c.dim);
+    if (!lm->embed_q) {  // sized for int8, the larger of the two
+        HIP_TRY(dalloc(lm, (void**)&lm->embed_q, embed_code_bytes(SXQ_EMBED_INT8, rows, c.dim)), "lm_set_embed_quantized");
+        HIP_TRY(dalloc(lm, (void**)&lm->embed_scale, sizeof(float) * rows), "lm_set_embed_quantized");
+    }
+    HIP_TRY(hipDeviceSynchronize(), "lm_set_embed_quantized: drain");
+    HIP_TRY(hipMemcpy(lm->embed_q, q, qb, hipMemcpyDefault), "lm_set_embed_quantized: codes");
+    HIP_TRY(hipMemcpy(lm->embed_scale, scale, sizeof(float) * rows, hipMemcpyDefault), "lm_set_embed_quantized: scales");
+    lm->embed_scheme = scheme;
+    for (auto& kv : lm->graphs) (void)hipGraphExecDestroy(kv.second);  // captured with the dense gather
+    lm->graphs.clear();
+    for (auto& kv : lm->expand_graphs) (void)hipGraphExecDestroy(kv.second);
+    lm->expand_graphs.clear();
     return SXQ_OK;
 }
 

@@ -146,6 +146,12 @@ class DecoderLM:
         torch.cuda.current_stream(self.device).synchronize()
         check(lib().sxq_lm_set_vector(self._h, layer, which, ctypes.c_void_p(t.data_ptr()), t.numel(), 1))
 
+    def set_embed_quantized(self, qe) -> None:
+        """Hold the input table (EMBED) as a QEmbed: steps and prefill gather-dequantize it."""
+        torch.cuda.current_stream(self.device).synchronize()
+        check(lib().sxq_lm_set_embed_quantized(self._h, qe.scheme, ctypes.c_void_p(qe.q.data_ptr()),
+                                                ctypes.c_void_p(qe.scale.data_ptr())))
+
     def init_random(self, seed: int = 0, std: float = 0.02) -> None:
         check(lib().sxq_lm_init_random(self._h, seed, std))
 

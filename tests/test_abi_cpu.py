@@ -76,6 +76,18 @@ def test_fast_expand_and_reset_check_arguments_without_a_gpu():
     assert L.sxq_lm_reset(None, 1, None) == _lib.ERR_INVALID
 
 
+def test_embed_entry_points_check_arguments_without_a_gpu():
+    L = _lib.lib()
+    eff = ctypes.c_int()
+    assert L.sxq_embed_scheme(4, 896, ctypes.byref(eff)) == _lib.OK and eff.value == 4
+    assert L.sxq_embed_scheme(4, 81, ctypes.byref(eff)) == _lib.OK and eff.value == 8  # odd width: int8
+    assert L.sxq_embed_scheme(5, 896, ctypes.byref(eff)) == _lib.ERR_INVALID
+    assert L.sxq_embed_quantize(0, 4, None, 10, 81, None, None, None) == _lib.ERR_INVALID
+    assert "odd" in L.sxq_last_error().decode()
+    assert L.sxq_embed_gather(0, 8, None, None, 10, 16, None, 0, None, None) == _lib.OK  # nothing to gather
+    assert L.sxq_lm_set_embed_quantized(None, 4, None, None) == _lib.ERR_INVALID
+
+
 def test_python_mirror_rejects_misaligned_quantize():
     import torch
     with pytest.raises(syrinx_amd.SxqError) as e:

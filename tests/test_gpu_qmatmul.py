@@ -282,6 +282,33 @@ def test_prefill_gemm_q8_0_q4_0_bit_exact(cuda, ora, dt, n, k, m, with_bias):
     _eq_bits(y.cpu().numpy(), want)
 
 
+# The CosyVoice3 flow's DiT linears (crates/syrinx-acoustic/src/cv3/dit.rs, Q4_0 from
+# crates/syrinx-acoustic/src/cv3/mod.rs:150-168, bias added after QMatMul::forward at
+# :200-211) at M = CFG batch 2 x 250 mel frames, and their batch-row users at M = 2.
+DIT = [
+    (1024, 1024, 500),   # to_q / to_k / to_v / to_out.0 (dit.rs:241-267)
+    (2048, 1024, 500),   # ff.0.0 (dit.rs:272)
+    (1024, 2048, 500),   # ff.2
+    (1024, 320, 500),    # input_embed.proj over [x, cond, mu, spks] (dit.rs:61-64)
+    (80, 1024, 500),     # proj_out (dit.rs:79)
+    (6144, 1024, 2),     # AdaLayerNormZero linear (dit.rs:196)
+    (1024, 256, 2),      # time_mlp.0 (dit.rs:93)
+]
+
+
+@pytest.mark.parametrize("n,k,m", DIT)
+def test_flow_dit_linears_bit_exact(cuda, ora, n, k, m):
+    w = _weights(n, k, 90 + n)
+    x = _acts(m, k, 91 + k)
+    blocks = ora.quantize(ora.Q4_0, w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4_0, device=cuda))
+    b = (np.random.default_rng(92).standard_normal(n) * 0.02).astype(np.float32)
+    y = qmm.forward(torch.from_numpy(x).to(cuda).reshape(2, m // 2, k), bias=torch.from_numpy(b).to(cuda))
+    assert tuple(y.shape) == (2, m // 2, n)
+    want = (ora.matmul(ora.Q4_0, x, blocks) + b[None, :]).astype(np.float32)
+    _eq_bits(y.reshape(m, n).cpu().numpy(), want)
+
+
 def _prefill_check(ora, x, blocks, k, y, b=None):
     wd = ora.dequantize(ora.Q4K, blocks, k).reshape(-1, k).astype(np.float64)  # Candle's to_float, exact
     y64 = x.astype(np.float64) @ wd.T + (0.0 if b is None else b.astype(np.float64))
