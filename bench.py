@@ -26,7 +26,9 @@ CPU baseline:
   prefill       one Qwen3-4B layer's four projections at a 512-token prompt through
                 QMatMul.forward (the f16 MFMA GEMM with its conversion of x and split-K
                 sums), graph-replayed, against the 2.5 PFLOP/s dense f16 peak;
-  skinny_batch  16 concurrent streams, ragged KV lengths uniform over 256..2048.
+  skinny_batch  16 concurrent streams, ragged KV lengths uniform over 256..2048;
+  fish_frame    Fish s2-pro dual-AR frames at batch 1: the slow step + the semantic draw +
+                the 4-layer fast AR's 10 codebook positions with nine device draws.
 
 CPU baselines (`cpu_baseline`: all threads this GPU's share of the host allows, at most
 16; `cpu_baseline_1thread`): the oracle -- the CPU restatement of Candle 0.8's generic
@@ -38,6 +40,7 @@ Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--no-cpu] [--only
        python bench.py --mode gemv [--dtype q4k|q8_0] [--gemv-iters N] [--rows N]   (GEMV pass, counter runs)
        python bench.py --mode copy        (plain 1 GiB device copy: the counter scale)
        python bench.py --mode prefill     (the prefill line alone)
+       python bench.py --mode frame [--frames N]   (the fish_frame line alone)
        python bench.py --mode decode1     (only the headline decode, for kernel traces)
 """
 from __future__ import annotations
@@ -55,7 +58,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA, MI355X
 Q4K, Q8_0 = 12, 8
-LINES = ("gemv_q8_0", "cv2_decode", "q8_0_decode", "prefill", "skinny_batch")
+LINES = ("gemv_q8_0", "cv2_decode", "q8_0_decode", "prefill", "skinny_batch", "fish_frame")
 
 
 def parse():
@@ -69,11 +72,12 @@ def parse():
     ap.add_argument("--gemv-iters", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--only", default=",".join(LINES), help="comma-separated extra lines to run")
-    ap.add_argument("--mode", default="decode", choices=["decode", "decode1", "gemv", "copy", "prefill"])
+    ap.add_argument("--mode", default="decode", choices=["decode", "decode1", "gemv", "copy", "prefill", "frame"])
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--prefill-iters", type=int, default=20)
     ap.add_argument("--skinny-batch", type=int, default=16)
     ap.add_argument("--skinny-steps", type=int, default=64)
+    ap.add_argument("--frames", type=int, default=64, help="fish_frame line: timed frames")
     return ap.parse_args()
 
 
@@ -429,6 +433,54 @@ def skinny_batch(lm, torch, n, steps, warmup, iters, cpu):
     return out
 
 
+def fish_frames(D, torch, kv, frames, warmup, cpu, n=1):
+    """Fish s2-pro dual-AR frames at batch n: per frame the slow AR step (36 layers, KV
+    `kv`), the semantic draw, and the 4-layer fast AR over the 10 codebook positions with
+    nine codebook draws, all on the device (syrinx_amd.dualar.generate_frames, the loop
+    drive / drive_batch run: one graph per slow step and one per expansion, the host
+    reading the streams' stop flags once per frame behind the next slow step).  Timed by
+    the host clock around the loop (it synchronises with the host every frame)."""
+    from syrinx_amd import dualar as DA
+    from syrinx_amd.sampling import FishSampler, SamplingParams
+    dev = torch.device("cuda:0")
+    slow = build_model(D, torch, "fish", Q4K, kv + frames + warmup + 8, n)
+    fast = D.FastAr(D.fish_s2_fast_ar_config(n_layers=4, max_batch=n), device=dev)
+    fast.init_random(seed=3, std=0.02)
+    slow.kv_fill_random([kv] * n, seed=1)
+    logits, _, hidden = slow.step(ids=fish_frame(slow, torch, n), graph=True, want_hidden=True)
+    smp = FishSampler([42 + i for i in range(n)], SamplingParams(), semantic=(151678, 155773, -1), device=dev)
+    frame = torch.zeros((n, 1 + slow.cfg.n_codebooks), dtype=torch.int32, device=dev)
+    active = torch.ones(n, dtype=torch.int32, device=dev)
+    DA.generate_frames(slow, fast, smp, logits, hidden.reshape(n, 1, -1), warmup, kv + 1, active, frame)  # captures
+    slow.set_lengths([kv + 1] * n)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out, _ = DA.generate_frames(slow, fast, smp, logits, hidden.reshape(n, 1, -1), frames, kv + 1, active, frame)
+    sec = time.perf_counter() - t0
+    assert len(out) == frames
+    sl, sh = slow.weight_bytes()
+    fl, fh = fast.weight_bytes()
+    per_frame = sl + sh + fast.cfg.max_seq * (fl + fh)  # weight bytes streamed per frame
+    achieved = per_frame * frames / sec / 1e9
+    res = {"workload": f"Fish s2-pro dual-AR frames: slow AR (Qwen3-4B shape, 36 layers, Q4_K, f32 KV {kv}) + "
+                       f"semantic draw + fast AR (4 layers of the same block, Q4_K, 10 codebook positions, nine "
+                       f"codebook draws), batch {n}, {frames} frames",
+           "value": round(n * frames / sec, 2), "unit": "frames/s", "ms_per_frame": round(sec * 1000.0 / frames, 4),
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                        "bytes_per_frame": per_frame, "kernel": "whole frame (weights streamed once per step)"}}
+    if cpu:
+        a = cpu_layer_token(torch, dev, slow.cfg, Q4K, 16, "slow AR")
+        b = cpu_layer_token(torch, dev, fast.cfg, Q4K, 1, "fast AR")
+        for key in ("cpu_baseline", "cpu_baseline_1thread"):
+            ts, tf = 1.0 / a[key]["value"], 1.0 / b[key]["value"]
+            res[key] = cpu_entry(1.0 / (ts + fast.cfg.max_seq * tf), "frames/s (GEMV share of a frame)",
+                                 a[key]["cores"], f"one slow-AR step + 10 fast-AR steps of GEMV work: "
+                                 f"{a[key]['sample']}; {b[key]['sample']}")
+    del slow, fast
+    return res
+
+
 def copy_calibration(torch, iters=8):
     """A plain device-to-device copy of 1 GiB: its counters give the FETCH/WRITE scale."""
     n = 1 << 30
@@ -487,6 +539,9 @@ def main():
         return
     from syrinx_amd import decoder as D
     cpu = not args.no_cpu
+    if args.mode == "frame":
+        print(json.dumps({"mode": "frame", "fish_frame": fish_frames(D, torch, args.kv, args.frames, 8, cpu)}))
+        return
     if args.mode == "gemv":
         dt = Q4K if args.dtype == "q4k" else Q8_0
         lm = build_model(D, torch, "fish", dt, args.kv + 16, max(1, args.rows))
@@ -530,6 +585,9 @@ def main():
     if "gemv_q8_0" in only:
         lines["gemv_q8_0"] = q8_0_gemv(torch, cpu)
         log(f"Q8_0 GEMV: {lines['gemv_q8_0']['value']} GB/s")
+    if "fish_frame" in only:
+        lines["fish_frame"] = fish_frames(D, torch, args.kv, args.frames, 8, cpu)
+        log(f"fish frames: {lines['fish_frame']['value']} frames/s")
     if "prefill" in only:
         lines["prefill"] = prefill_gemms(torch, args.prefill_tokens, args.prefill_iters, cpu)
         log(f"prefill: {lines['prefill']['us_per_layer']} us/layer, {lines['prefill']['value']} TFLOP/s")

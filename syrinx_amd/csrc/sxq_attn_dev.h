@@ -96,6 +96,26 @@ SXQ_DEV void rope_store(float2 y, int interleaved, float* dst, float* gdst, int 
     }
 }
 
+// The group's context slice (thread t < T holds elements 4t .. 4t + 3, zeros past T): the
+// optional f32 record, then the activation blocks of the O projection -- the quantizers'
+// lane layout, wave w quantizing chunk w of 256 elements.
+template <int VDT, int HD>
+SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, float4 v) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int dim = A.nh * HD;
+    if (tid < T && A.ctx_out) *(float4*)(A.ctx_out + (int64_t)s * dim + (int64_t)g * gd + 4 * tid) = v;
+    const int nbr = VDT == kQ8K ? dim / 256 : dim / 32;  // activation blocks per row
+    uint8_t* arow = A.act + (int64_t)s * nbr * act_block_bytes(VDT);
+    const int blk_first = VDT == kQ8K ? (g * gd) / 256 : (g * gd) / 32;  // the slice's first block
+    uint8_t* qdst = arow + (size_t)blk_first * act_block_bytes(VDT);
+    if (tid < ((T + 63) & ~63)) {
+        if (VDT == kQ8K)
+            wave_quantize_q8k<false>(v, lane, qdst + (size_t)wave * sizeof(ActQ8K));
+        else
+            wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < gd / 32, qdst + (size_t)wave * 8 * sizeof(ActQ8_0));
+    }
+}
+
 // Fused decode attention for split sp of KV head group g of stream s, NT threads:
 // P = NT/8 cached positions [sp*P, sp*P + P).  QK-norm + RoPE of the group's G queries
 // (from the qkv row), in the split holding position len also the new token's key/value
@@ -247,9 +267,13 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
         }
         const float l = wave_sum_rows(ls);
         if (lane == 0) {
-            float* pm = part_s + ((int64_t)(g * G + wave) * max_splits + sp) * PR;
-            store_agent(pm, m);
-            store_agent(pm + 1, l);
+            if (nsp == 1) {
+                knew[wave] = l;  // (the new key is in kr by now)
+            } else {
+                float* pm = part_s + ((int64_t)(g * G + wave) * max_splits + sp) * PR;
+                store_agent(pm, m);
+                store_agent(pm + 1, l);
+            }
         }
     }
     __syncthreads();
@@ -273,6 +297,25 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
         *(float4*)(red + qi * gd + h * HD + d) = a;
     }
     __syncthreads();
+    if (nsp == 1) {
+        // One split holds every position: its weights exp(m - m) are 1, so the merge
+        // below would give acc / l bit for bit -- without the hand-off.
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (tid < T) {
+            float4 a = *(const float4*)(red + 4 * tid);
+            for (int q = 1; q < nq; ++q) {
+                const float4 b = *(const float4*)(red + q * gd + 4 * tid);
+                a.x += b.x;
+                a.y += b.y;
+                a.z += b.z;
+                a.w += b.w;
+            }
+            const float ls = knew[(4 * tid) / HD];
+            v = make_float4(a.x / ls, a.y / ls, a.z / ls, a.w / ls);
+        }
+        attn_emit_context<VDT, HD>(A, s, g, gd, T, v);
+        return;
+    }
     if (tid < T) {
         float4 a = *(const float4*)(red + 4 * tid);
         for (int q = 1; q < nq; ++q) {
@@ -356,33 +399,21 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
     }
     if (mt) *(float4*)(red2 + qi * gd + h * HD + d) = a;
     __syncthreads();
-    // 8. context: thread t < T holds elements 4t .. 4t + 3 of the group's slice, which is
-    //    the quantizers' lane layout (wave w: chunk w of 256 elements).
-    const int dim = nh * HD;
-    const int nbr = VDT == kQ8K ? dim / 256 : dim / 32;  // activation blocks per row
-    uint8_t* arow = A.act + (int64_t)s * nbr * act_block_bytes(VDT);
-    const int blk_first = VDT == kQ8K ? (g * gd) / 256 : (g * gd) / 32;  // the slice's first block
-    uint8_t* qdst = arow + (size_t)blk_first * act_block_bytes(VDT);
-    if (tid < ((T + 63) & ~63)) {
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (tid < T) {
-            float4 c = *(const float4*)(red2 + 4 * tid);
-            for (int q = 1; q < nq; ++q) {
-                const float4 b = *(const float4*)(red2 + q * gd + 4 * tid);
-                c.x += b.x;
-                c.y += b.y;
-                c.z += b.z;
-                c.w += b.w;
-            }
-            const float ls = lsum[(4 * tid) / HD];
-            v = make_float4(c.x / ls, c.y / ls, c.z / ls, c.w / ls);
-            if (A.ctx_out) *(float4*)(A.ctx_out + (int64_t)s * dim + (int64_t)g * gd + 4 * tid) = v;
+    // 8. context: thread t < T holds elements 4t .. 4t + 3 of the group's slice
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (tid < T) {
+        float4 c = *(const float4*)(red2 + 4 * tid);
+        for (int q = 1; q < nq; ++q) {
+            const float4 b = *(const float4*)(red2 + q * gd + 4 * tid);
+            c.x += b.x;
+            c.y += b.y;
+            c.z += b.z;
+            c.w += b.w;
         }
-        if (VDT == kQ8K)
-            wave_quantize_q8k<false>(v, lane, qdst + (size_t)wave * sizeof(ActQ8K));
-        else
-            wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < gd / 32, qdst + (size_t)wave * 8 * sizeof(ActQ8_0));
+        const float ls = lsum[(4 * tid) / HD];
+        v = make_float4(c.x / ls, c.y / ls, c.z / ls, c.w / ls);
     }
+    attn_emit_context<VDT, HD>(A, s, g, gd, T, v);
     if (tid == 0) __hip_atomic_store(&A.counter[s * nkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -69,17 +69,42 @@ struct Shared {
     unsigned hist[256];
     float fred[kST / 64];
     double dred[kST / 64];
-    unsigned cnt[kST];
+    unsigned wsum[kST / 64];
     float cand_key[kMaxTopK];
     int cand_id[kMaxTopK];
     float top_key[kMaxTopK];  // sorted: key descending, id ascending
     int top_id[kMaxTopK];
+    double term[kMaxTopK];    // per-candidate f64 terms of a draw (by rank, then by id order)
+    float prob[kMaxTopK];
+    int ord[kMaxTopK];        // kept ranks in id order
     unsigned ncand;
     uint32_t kth;
     int need, result;
     double dval;
     float fval;
 };
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+SXQ_DEV unsigned wave_incl_scan(unsigned x) {
+    const int lane = threadIdx.x & 63;
+    for (int o = 1; o < 64; o <<= 1) {
+        const unsigned y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+
+// Exclusive prefix sum of one value per thread over the workgroup, in thread order.
+SXQ_DEV unsigned block_excl_scan(unsigned v, Shared& sh) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const unsigned incl = wave_incl_scan(v);
+    if (lane == 63) sh.wsum[wave] = incl;
+    __syncthreads();
+    unsigned base = 0;
+    for (int w = 0; w < wave; ++w) base += sh.wsum[w];
+    __syncthreads();
+    return base + incl - v;
+}
 
 SXQ_DEV float block_max(float v, Shared& sh) {
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -123,14 +148,24 @@ SXQ_DEV int top_k_select(const View& v, KeyF key, int K, Shared& sh) {
             if ((u & mask) == prefix) atomicAdd(&sh.hist[(u >> d) & 0xFF], 1u);
         }
         __syncthreads();
-        if (tid == 0) {
-            int above = 0, b = 255;
-            for (; b > 0; --b) {
-                if (above + (int)sh.hist[b] >= rem) break;
-                above += (int)sh.hist[b];
+        // the digit b where the count of keys from the top first reaches rem (b = 0 at
+        // the latest): lane l of wave 0 holds digits 255 - 4l .. 252 - 4l
+        if (tid < 64) {
+            const int top = 255 - 4 * tid;
+            const unsigned c0 = sh.hist[top], c1 = sh.hist[top - 1], c2 = sh.hist[top - 2], c3 = sh.hist[top - 3];
+            const unsigned incl = wave_incl_scan(c0 + c1 + c2 + c3);
+            const unsigned excl = incl - (c0 + c1 + c2 + c3);
+            if ((excl < (unsigned)rem && (unsigned)rem <= incl) || (tid == 63 && incl < (unsigned)rem)) {
+                unsigned above = excl;
+                const unsigned c[4] = {c0, c1, c2, c3};
+                int t = 0;
+                for (; t < 3; ++t) {
+                    if (above + c[t] >= (unsigned)rem) break;
+                    above += c[t];
+                }
+                sh.need = rem - (int)above;  // elements of digit b still needed
+                sh.kth = (uint32_t)(top - t);
             }
-            sh.need = rem - above;  // elements of digit b still needed
-            sh.kth = (uint32_t)b;
         }
         __syncthreads();
         prefix |= sh.kth << d;
@@ -144,18 +179,7 @@ SXQ_DEV int top_k_select(const View& v, KeyF key, int K, Shared& sh) {
     if (tid == 0) sh.ncand = 0;
     unsigned ties = 0;
     for (int e = e0; e < e1; ++e) ties += order_key(key(e)) == prefix;
-    sh.cnt[tid] = ties;
-    __syncthreads();
-    if (tid == 0) {  // exclusive scan of the tie counts in id order
-        unsigned acc = 0;
-        for (int t = 0; t < kST; ++t) {
-            const unsigned c = sh.cnt[t];
-            sh.cnt[t] = acc;
-            acc += c;
-        }
-    }
-    __syncthreads();
-    unsigned rank = sh.cnt[tid];
+    unsigned rank = block_excl_scan(ties, sh);  // ties before this thread's chunk, in id order
     for (int e = e0; e < e1; ++e) {
         const float k = key(e);
         const uint32_t u = order_key(k);
@@ -187,49 +211,68 @@ SXQ_DEV int top_k_select(const View& v, KeyF key, int K, Shared& sh) {
     return K;
 }
 
-// Fish logits_to_probs over the sorted candidates + multinomial1 (one lane): rank 0
-// always kept, then while cum <= top_p and rank < top_k (cum of exp(l - max) / total in
-// f64); temperature softmax over the kept in f64, probabilities rounded to f32 and
-// renormalised; the inverse-CDF draw walks the kept ids in id order.
-SXQ_DEV int fish_draw(const Shared& sh, int K, double total, float mx, float temperature, float top_p, int top_k,
+// Fish logits_to_probs over the sorted candidates + multinomial1, run by wave 0 (every
+// lane returns the token and advances its copy of rng alike).  The exponentials and
+// divisions are per candidate, one lane each; the sums keep the reference's order, added
+// by every lane over the shared terms: rank 0 always kept, then while cum <= top_p and
+// rank < top_k (cum of exp(l - max) / total in f64, rank order); temperature softmax
+// over the kept in f64 (the largest scaled key is rank 0's), probabilities rounded to f32
+// and renormalised in id order; the inverse-CDF draw walks the kept ids in id order.
+SXQ_DEV int fish_draw(Shared& sh, int K, double total, float mx, float temperature, float top_p, int top_k,
                       uint64_t& rng) {
+    const int lane = threadIdx.x & 63;
+    if (lane < K) sh.term[lane] = exp((double)(sh.top_key[lane] - mx)) / total;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     int keep = 0;
     double cum = 0.0;
     for (int r = 0; r < K; ++r) {
         if (!(r == 0 || (cum <= (double)top_p && r < top_k))) break;
         ++keep;
-        cum += exp((double)(sh.top_key[r] - mx)) / total;
+        cum += sh.term[r];
     }
     const float t = fmaxf(temperature, 1e-5f);
-    float kmax = -INFINITY;
-    for (int r = 0; r < keep; ++r) kmax = fmaxf(kmax, sh.top_key[r] / t);
-    // kept ids in id order
-    int ord[kMaxTopK];
-    for (int r = 0; r < keep; ++r) {
+    const float kmax = sh.top_key[0] / t;
+    __builtin_amdgcn_wave_barrier();
+    if (lane < keep) {
         int pos = 0;
-        for (int j = 0; j < keep; ++j) pos += sh.top_id[j] < sh.top_id[r];
-        ord[pos] = r;
+        for (int j = 0; j < keep; ++j) pos += sh.top_id[j] < sh.top_id[lane];
+        sh.ord[pos] = lane;
     }
-    double e[kMaxTopK], psum = 0.0;
-    for (int i = 0; i < keep; ++i) {
-        e[i] = exp((double)(sh.top_key[ord[i]] / t - kmax));
-        psum += e[i];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    double e_mine = 0.0;
+    if (lane < keep) {
+        e_mine = exp((double)(sh.top_key[sh.ord[lane]] / t - kmax));
+        sh.term[lane] = e_mine;  // id order
     }
-    float p[kMaxTopK];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    double psum = 0.0;
+    for (int i = 0; i < keep; ++i) psum += sh.term[i];
+    __builtin_amdgcn_wave_barrier();
+    if (lane < keep) {
+        float p = (float)e_mine;
+        if (psum > 0.0) p = (float)((double)p / psum);
+        sh.prob[lane] = p;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     double tot = 0.0;
-    for (int i = 0; i < keep; ++i) {
-        p[i] = (float)e[i];
-        if (psum > 0.0) p[i] = (float)((double)p[i] / psum);
-        tot += (double)p[i];
-    }
+    for (int i = 0; i < keep; ++i) tot += (double)sh.prob[i];
     if (tot <= 0.0) return 0;
     const double u = splitmix_f64(rng) * tot;
     double acc = 0.0;
+    int tok = -1;  // the reference's fall-through: the row's last id (the caller maps it)
     for (int i = 0; i < keep; ++i) {
-        acc += (double)p[i];
-        if (u < acc) return sh.top_id[ord[i]];
+        acc += (double)sh.prob[i];
+        if (u < acc) {
+            tok = sh.top_id[sh.ord[i]];
+            break;
+        }
     }
-    return -1;  // the reference's fall-through: the row's last id (the caller maps it)
+    __builtin_amdgcn_wave_barrier();
+    return tok;
 }
 
 struct FishArgs {
@@ -305,13 +348,17 @@ __global__ __launch_bounds__(kST) void k_sample_fish(FishArgs A) {
     for (int e = tid; e < n; e += kST) tot += exp((double)(key(e) - mx));
     tot = block_sum(tot, sh);
     const int K = top_k_select(v, key, P.top_k, sh);
-    if (tid != 0) return;
+    if (tid >= 64) return;
     uint64_t rng = A.rng[s];
     int tok = fish_draw(sh, K, tot, mx, P.temperature, P.top_p, P.top_k, rng);
     if (tok < 0) tok = A.vocab - 1;
+    int high = -1;
     if (MODE == 0) {
-        int high = fish_draw(sh, K, tot, mx, P.ras_high_temp, P.ras_high_top_p, P.top_k, rng);
+        high = fish_draw(sh, K, tot, mx, P.ras_high_temp, P.ras_high_top_p, P.top_k, rng);
         if (high < 0) high = A.vocab - 1;
+    }
+    if (tid != 0) return;
+    if (MODE == 0) {
         int* win = A.window ? A.window + (int64_t)s * P.ras_win_size : nullptr;
         int len = A.window_len ? A.window_len[s] : 0;
         bool in_window = false;

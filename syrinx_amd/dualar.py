@@ -59,17 +59,40 @@ def drive_batch(slow: SlowAr, fast: FastAr, prompts, stop_id: int, params: Drive
 
     slow.reset(n)
     logits0, hidden0 = slow.prefill_batch(prompts)
+    frames, flags = generate_frames(slow, fast, sampler, logits0, hidden0, params.max_new_frames, tmax)
+    f = torch.stack(frames)      # [T, n, 1 + n_cb]
+    a = torch.stack(flags)       # [T, n]: the frame of step t counts for stream i when still active
+    out = []
+    for i in range(n):
+        keep = a[:, i] != 0
+        out.append(f[keep, i, 1:].t().contiguous())
+    return out
+
+
+def generate_frames(slow: SlowAr, fast: FastAr, sampler: FishSampler, logits0, hidden0, max_new_frames: int,
+                    pos: int, active: torch.Tensor = None, frame: torch.Tensor = None):
+    """The frame loop of drive_batch (dualar.rs:286-346) from a prefilled slow cache whose
+    last step gave logits0 [n, vocab] and hidden0 [n, 1, dim]; pos is the longest stream's
+    cache length.  Returns the frames [n, 1 + n_cb] of every pass and the streams' active
+    flags after each pass's semantic draw (device tensors; the host has synchronised).
+    `active` / `frame` may be passed to keep their buffers (and the captured expansion)
+    across calls."""
+    c = slow.cfg
+    n_cb = c.n_codebooks
+    n = logits0.shape[0]
+    dev = slow.device
     # fixed buffers: the expansion graph is captured on their addresses
     logits = logits0.contiguous()
     hidden = hidden0.reshape(n, c.dim).contiguous()
     nxt = torch.empty(n, dtype=torch.int32, device=dev)
-    pos = tmax
-    frame = torch.zeros((n, 1 + n_cb), dtype=torch.int32, device=dev)
-    active = torch.ones(n, dtype=torch.int32, device=dev)
+    if frame is None:
+        frame = torch.zeros((n, 1 + n_cb), dtype=torch.int32, device=dev)
+    if active is None:
+        active = torch.ones(n, dtype=torch.int32, device=dev)
     frames, flags = [], []
     flag_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
     done = torch.cuda.Event()
-    for _ in range(params.max_new_frames):
+    for _ in range(max_new_frames):
         # 1. each active stream's semantic draw (a stop freezes the stream); 2. the frame
         sampler.sample_semantic(logits, out=frame[:, 0], out_stride=1 + n_cb, active=active)
         fast.expand_batch(hidden, frame[:, 0], sampler, active=active, codes=frame[:, 1:], n_codes=n_cb)
@@ -77,7 +100,7 @@ def drive_batch(slow: SlowAr, fast: FastAr, prompts, stop_id: int, params: Drive
         flags.append(active.clone())
         flag_host.copy_(active, non_blocking=True)
         done.record()
-        if len(frames) >= params.max_new_frames or pos + 1 >= c.max_seq:
+        if len(frames) >= max_new_frames or pos + 1 >= c.max_seq:
             break
         # 4. feed the frame back (enqueued before the host looks at the flags)
         slow.slow_step_batch(frame, out=(logits, nxt, hidden))
@@ -86,10 +109,4 @@ def drive_batch(slow: SlowAr, fast: FastAr, prompts, stop_id: int, params: Drive
         if not bool(flag_host.any()):
             break
     torch.cuda.current_stream(dev).synchronize()
-    f = torch.stack(frames)      # [T, n, 1 + n_cb]
-    a = torch.stack(flags)       # [T, n]: the frame of step t counts for stream i when still active
-    out = []
-    for i in range(n):
-        keep = a[:, i] != 0
-        out.append(f[keep, i, 1:].t().contiguous())
-    return out
+    return frames, flags

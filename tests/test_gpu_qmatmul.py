@@ -500,3 +500,37 @@ def test_prefill_gemm_stays_finite_beyond_f16_range(cuda, ora):
     y_plain = qmm.forward(torch.from_numpy(plain).to(cuda)).cpu().numpy()
     keep = [0] + list(range(5, m))
     _eq_bits(y[keep].astype(np.float32), y_plain[keep])
+
+
+@pytest.mark.parametrize("mode", ["f32", "f16", "dequantize_all", "dequantize_all_f16"])
+def test_dense_qmatmul_variants(cuda, ora, monkeypatch, mode):
+    """Candle's dense QMatMul variants (QMatMul::from_arc): an F32 / F16 QTensor, or a
+    quantized one under CANDLE_DEQUANTIZE_ALL (f32 weight = to_float) or
+    CANDLE_DEQUANTIZE_ALL_F16 (f16 weight, the input cast to f16 and the product cast
+    back).  The weight must be Candle's exactly; the product is a dense GEMM, within the
+    rounding bound of its precision (cv2/load.rs:107-110 keeps unaligned 2-D weights f16)."""
+    n, k, m = 300, 512, 7
+    w = _weights(n, k, 95)
+    x = _acts(m, k, 96)
+    if mode == "f32":
+        qt, wd, eps = QTensor.quantize(torch.from_numpy(w), G.F32, device=cuda), w.astype(np.float64), 2.0 ** -15
+    elif mode == "f16":
+        qt = QTensor.quantize(torch.from_numpy(w), G.F16, device=cuda)
+        wd, eps = w.astype(np.float16).astype(np.float64), 2.0 ** -15
+    else:
+        blocks = ora.quantize(ora.Q4K, w)
+        qt = QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda)
+        wd = ora.dequantize(ora.Q4K, blocks, k).reshape(n, k).astype(np.float64)
+        eps = 2.0 ** -15  # f32 accumulation over k = 512 terms: below k * 2^-24 of sum |x w|
+        monkeypatch.setenv("CANDLE_DEQUANTIZE_ALL" if mode == "dequantize_all" else "CANDLE_DEQUANTIZE_ALL_F16", "1")
+        if mode == "dequantize_all_f16":
+            wd, eps = wd.astype(np.float16).astype(np.float64), 2.0 ** -10  # plus the f16 output rounding
+    qmm = QMatMul.from_qtensor(qt)
+    assert qmm.handle() == 0  # a dense weight: no sxq_qmm behind it
+    wt = qmm._dense.to(torch.float64).cpu().numpy()
+    np.testing.assert_array_equal(wt, wd)
+    y = qmm.forward(torch.from_numpy(x).to(cuda)).cpu().numpy().astype(np.float64)
+    xr = x.astype(np.float16).astype(np.float64) if mode == "dequantize_all_f16" else x.astype(np.float64)
+    ref = xr @ wd.T
+    bound = eps * (np.abs(xr) @ np.abs(wd).T) + 1e-30
+    assert (np.abs(y - ref) <= bound).all(), float((np.abs(y - ref) / bound).max())
