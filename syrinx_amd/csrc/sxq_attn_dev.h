@@ -192,7 +192,7 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
         const float* src = has_new && vr == slot ? vrow_new + col : vb + (int64_t)vr * HD + col;
         vr4[r] = ld_global((const v4f*)src);
     }
-    __builtin_amdgcn_sched_barrier(0);
+    issue_point();
     // 3. norm + RoPE in registers while the tile is in flight; stored once it has landed
     const float2 y = rope_pair<HD>(rin, inw != nullptr, A.eps, A.inv_hd, lane);
     float2 y2 = make_float2(0.0f, 0.0f);

@@ -127,8 +127,12 @@ SXQ_HD float f16_bits_to_f32(uint16_t h) {
     return __builtin_bit_cast(float, sign | ((exp + 112u) << 23) | (man << 13));
 }
 
-// Rust `v as i8` for an already-rounded value (saturating; NaN -> 0).
-SXQ_HD int sat_i8(float v) { return v != v ? 0 : (v >= 127.0f ? 127 : (v <= -128.0f ? -128 : (int)v)); }
+// Rust `v as i8` for an already-rounded value (saturating; NaN -> 0).  Written as a
+// clamp and a select so the device code has no branches.
+SXQ_HD int sat_i8(float v) {
+    const int c = (int)fminf(fmaxf(v, -128.0f), 127.0f);
+    return v != v ? 0 : c;
+}
 
 // ---------------------------------------------------------------------------------
 // Cross-lane helpers (wave64).  DPP controls: quad_perm xor1 = 0xB1, xor2 = 0x4E,

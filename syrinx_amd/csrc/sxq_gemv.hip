@@ -227,8 +227,8 @@ template <int NT, int MMAX, int KP = Stage<NT, MMAX>::kPer>
 SXQ_DEV void act_fetch(uint4 (&v)[KP], const uint8_t* __restrict__ act, int total_u4) {
 #pragma unroll
     for (int k = 0; k < KP; ++k)
-        v[k] = ((const uint4*)act)[min(k * NT + (int)threadIdx.x, total_u4 - 1)];
-    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
+        v[k] = ld_global((const uint4*)opaque_ptr(act) + min(k * NT + (int)threadIdx.x, total_u4 - 1));
+    issue_point();  // keep these loads ahead of the weight loads
 }
 template <int NT, int MMAX, int KP = Stage<NT, MMAX>::kPer>
 SXQ_DEV void act_store(const uint4 (&v)[KP], uint4* lds, const uint8_t* __restrict__ act, int total_u4) {
@@ -350,12 +350,14 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restric
         const int c = wave + 16 * j, cc = min(c, nb - 1);
         valid[j] = c < nb;
         out[j] = la + cc;
-        v[j] = *(const float4*)(x + cc * 256 + 4 * lane);
+        v[j] = ld_global((const float4*)(opaque_ptr(x) + cc * 256 + 4 * lane));
     }
-    __builtin_amdgcn_sched_barrier(0);
+    issue_point();
     uint4 q[TM], h[TM];
     q4k_tile_load<NT, TM>(hdr, qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
-    if (wave < nb) wave_quantize_q8k_n<J, false>(v, lane, out, valid);  // uniform per wave
+    // Called by every wave (a wave past the last chunk writes nothing): under a branch the
+    // compiler would sink the loads above into it, behind the weight loads.
+    wave_quantize_q8k_n<J, false>(v, lane, out, valid);
     lds_barrier();
     q4k_tile_products<1, NT, TM>(q, h, la, nb, 1, rows, R, pr);
     __syncthreads();

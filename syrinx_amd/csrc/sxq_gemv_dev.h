@@ -59,14 +59,17 @@ SXQ_DEV void q4k_tile_load(const uint4* __restrict__ hdr, const uint4* __restric
                            uint4 (&q)[TM], uint4 (&h)[TM]) {
     constexpr int SLOTS = NT / 8;
     const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
-    const char* qbase = (const char*)qs + (l << 4);
-    const char* hbase = (const char*)hdr;
+    const char* qbase = (const char*)opaque_ptr(qs) + (l << 4);
+    const char* hbase = (const char*)opaque_ptr(hdr);
 #pragma unroll
     for (int u = 0; u < TM; ++u) {
         const uint32_t blk = blk0 + (uint32_t)min(u * SLOTS + grp, tasks - 1);
         q[u] = ld_global((const uint4*)(qbase + (blk << 7)));
         h[u] = ld_global((const uint4*)(hbase + (blk << 4)));
     }
+    // The weight loads are all issued here: a prologue's arithmetic on its own (earlier)
+    // loads would otherwise make them wait, or they would sink behind it.
+    issue_point();
 }
 
 // The same for a tile of two row segments: tasks [0, seg) are blocks blkA + t, tasks
@@ -77,8 +80,8 @@ SXQ_DEV void q4k_tile_load2(const uint4* __restrict__ hdr, const uint4* __restri
                             int seg, int tasks, uint4 (&q)[TM], uint4 (&h)[TM]) {
     constexpr int SLOTS = NT / 8;
     const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
-    const char* qbase = (const char*)qs + (l << 4);
-    const char* hbase = (const char*)hdr;
+    const char* qbase = (const char*)opaque_ptr(qs) + (l << 4);
+    const char* hbase = (const char*)opaque_ptr(hdr);
 #pragma unroll
     for (int u = 0; u < TM; ++u) {
         const int t = min(u * SLOTS + grp, tasks - 1);
@@ -86,6 +89,7 @@ SXQ_DEV void q4k_tile_load2(const uint4* __restrict__ hdr, const uint4* __restri
         q[u] = ld_global((const uint4*)(qbase + (blk << 7)));
         h[u] = ld_global((const uint4*)(hbase + (blk << 4)));
     }
+    issue_point();  // as in q4k_tile_load
 }
 
 // Layout of the per-block float products: one chain per (activation row rr, tile row
@@ -216,9 +220,9 @@ SXQ_DEV float q4k_tile_fold(const float* pr, int nb, int RC, int rr, int rows) {
 // produce the same bits.
 SXQ_DEV void norm_fetch(float4& xv, float4& wv, const NormIn& ni, int dim) {
     const int i = min((int)threadIdx.x, dim / 4 - 1);  // clamped: every load in bounds
-    xv = ((const float4*)ni.x)[i];
-    wv = ((const float4*)ni.w)[i];
-    __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the weight loads
+    xv = ld_global((const float4*)opaque_ptr(ni.x) + i);
+    wv = ld_global((const float4*)opaque_ptr(ni.w) + i);
+    issue_point();  // keep these loads ahead of the weight loads
 }
 template <int VDT>
 SXQ_DEV void norm_quant_store(const float4& xv, const float4& wv, const NormIn& ni, int dim, uint8_t* lds_act,

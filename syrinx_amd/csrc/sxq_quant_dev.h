@@ -76,98 +76,91 @@ SXQ_DEV float rmsnorm_sumsq_1024(float ss, float* red) {
     return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
 }
 
+// Round half away from zero (Rust's f32::round) of a finite or NaN value.
+SXQ_DEV float round_away(float t) { return roundf(t); }
+
 // Quantize J chunks of 256 consecutive activations at once (lane i holds elements
 // 4i..4i+3 of chunk j in v[j]) to Q8_K blocks: k_quants.rs BlockQ8K::from_float.  The
-// chunks' reductions are interleaved so their cross-lane latencies overlap; chunk j is
+// chunks' steps are interleaved so their cross-lane latencies overlap; chunk j is
 // written only if `valid[j]` (wave-uniform).  Writes the device layout (ActQ8K,
 // class-major qs) or the canonical BlockQ8K.
+//
+// Candle's loop keeps the first element of largest magnitude (`amax < |x|`, so NaN is
+// never taken and ties go to the lower index): here the magnitude maximum is a max
+// over lanes (NaN-ignoring maxNum starting from 0, as amax starts at 0), and the first
+// element reaching it is found by a ballot over lanes and an in-lane scan.  The
+// quantized value is min(round(iscale * x), 127) (f32::min: NaN -> 127), which lies in
+// [-128, 127] (|iscale * x| <= 128 up to rounding) and so converts without saturation.
 template <int J, bool CANON>
 SXQ_DEV void wave_quantize_q8k_n(const float4 (&v)[J], int lane, void* const (&out)[J], const bool (&valid)[J]) {
-    float am[J], x[J][4];
-    int ix[J];
+    float x[J][4], am[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         x[j][0] = v[j].x; x[j][1] = v[j].y; x[j][2] = v[j].z; x[j][3] = v[j].w;
-        // first element of largest magnitude (Candle keeps the first on ties: `amax < |x|`)
-        am[j] = fabsf(x[j][0]);
-        ix[j] = 0;
-#pragma unroll
-        for (int r = 1; r < 4; ++r)
-            if (am[j] < fabsf(x[j][r])) { am[j] = fabsf(x[j][r]); ix[j] = r; }
+        am[j] = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(x[j][0])), fabsf(x[j][1])), fabsf(x[j][2])), fabsf(x[j][3]));
     }
-    float wmax[J];
+    // wave maximum of |x|: DPP inside 16-lane rows, then the four row maxima as scalars
+    // (non-negative floats order like their bit patterns)
+    float wm[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(am[j], dpp_f32<0xB1>(am[j]));
+    for (int j = 0; j < J; ++j) wm[j] = fmaxf(am[j], dpp_f32<0xB1>(am[j]));
 #pragma unroll
-    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], dpp_f32<0x4E>(wmax[j]));
+    for (int j = 0; j < J; ++j) wm[j] = fmaxf(wm[j], dpp_f32<0x4E>(wm[j]));
 #pragma unroll
-    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], dpp_f32<0x141>(wmax[j]));
+    for (int j = 0; j < J; ++j) wm[j] = fmaxf(wm[j], dpp_f32<0x141>(wm[j]));
 #pragma unroll
-    for (int j = 0; j < J; ++j) wmax[j] = fmaxf(wmax[j], dpp_f32<0x140>(wmax[j]));
-    // the four 16-lane row maxima, read as scalars (max is exact in any order)
+    for (int j = 0; j < J; ++j) wm[j] = fmaxf(wm[j], dpp_f32<0x140>(wm[j]));
+    uint32_t wmax[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j)
-        wmax[j] = fmaxf(fmaxf(row_total(wmax[j], 0), row_total(wmax[j], 1)),
-                        fmaxf(row_total(wmax[j], 2), row_total(wmax[j], 3)));
-    int first[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) first[j] = am[j] == wmax[j] ? 4 * lane + ix[j] : 256;
-#pragma unroll
-    for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0xB1>(first[j]));
-#pragma unroll
-    for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0x4E>(first[j]));
-#pragma unroll
-    for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0x141>(first[j]));
-#pragma unroll
-    for (int j = 0; j < J; ++j) first[j] = min(first[j], dpp_i32<0x140>(first[j]));
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-        first[j] = min(min(__builtin_amdgcn_readlane(first[j], 0), __builtin_amdgcn_readlane(first[j], 16)),
-                       min(__builtin_amdgcn_readlane(first[j], 32), __builtin_amdgcn_readlane(first[j], 48)));
-    int q[J][4], s8[J], s4[J];
+    for (int j = 0; j < J; ++j) {
+        const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, wm[j]), 0);
+        const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, wm[j]), 16);
+        const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, wm[j]), 32);
+        const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, wm[j]), 48);
+        wmax[j] = max(max(r0, r1), max(r2, r3));
+    }
+    int q[J][4];
     float d[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        // the max element itself (signed): its component, read from its lane
-        const int f = __builtin_amdgcn_readfirstlane(first[j]);
-        const int src = f >> 2, comp = f & 3;
-        const float mine = comp == 0 ? x[j][0] : comp == 1 ? x[j][1] : comp == 2 ? x[j][2] : x[j][3];
-        const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), src & 63));
+        const float w = __builtin_bit_cast(float, wmax[j]);
+        // the first element with |x| == w: the lowest lane holding one, then its first
+        const float a0 = fabsf(x[j][0]), a1 = fabsf(x[j][1]), a2 = fabsf(x[j][2]);
+        const float mine = a0 == w ? x[j][0] : (a1 == w ? x[j][1] : (a2 == w ? x[j][2] : x[j][3]));
+        const uint64_t hit = __ballot(am[j] == w);
+        const int src = hit ? __builtin_ctzll(hit) : 0;
+        const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), src));
         q[j][0] = q[j][1] = q[j][2] = q[j][3] = 0;
         d[j] = 0.0f;
-        if (wmax[j] != 0.0f) {
+        if (w != 0.0f) {  // uniform
             const float iscale = -128.0f / mx;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float t = roundf(iscale * x[j][r]);
-                t = (t != t || t > 127.0f) ? 127.0f : t;  // f32::min(t, 127.0) ignores NaN
-                q[j][r] = sat_i8(t);
-            }
+            for (int r = 0; r < 4; ++r) q[j][r] = (int)fminf(round_away(iscale * x[j][r]), 127.0f);
             d[j] = 1.0f / iscale;
         }
-        // bsums: 16 elements = 4 lanes (a quad); bs2: 32 elements = 8 lanes.
-        s4[j] = q[j][0] + q[j][1] + q[j][2] + q[j][3];
-        s4[j] += dpp_i32<0xB1>(s4[j]);
-        s4[j] += dpp_i32<0x4E>(s4[j]);
-        s8[j] = s4[j] + dpp_i32<0x141>(s4[j]);
     }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         if (!valid[j]) continue;
+        const uint32_t packed = (uint32_t)(q[j][0] & 0xFF) | ((uint32_t)(q[j][1] & 0xFF) << 8) |
+                                ((uint32_t)(q[j][2] & 0xFF) << 16) | ((uint32_t)(q[j][3] & 0xFF) << 24);
+        // bsums: 16 elements = 4 lanes (a quad); bs2: 32 elements = 8 lanes
+        int s4 = __builtin_amdgcn_sdot4((int)packed, 0x01010101, 0, false);
+        s4 += dpp_i32<0xB1>(s4);
+        s4 += dpp_i32<0x4E>(s4);
         if (CANON) {
             BlockQ8K* b = (BlockQ8K*)out[j];
-            const uint32_t packed = (uint32_t)(q[j][0] & 0xFF) | ((uint32_t)(q[j][1] & 0xFF) << 8) |
-                                    ((uint32_t)(q[j][2] & 0xFF) << 16) | ((uint32_t)(q[j][3] & 0xFF) << 24);
             ((uint32_t*)b->qs)[lane] = packed;
-            if ((lane & 3) == 0) b->bsums[lane >> 2] = (int16_t)s4[j];
+            if ((lane & 3) == 0) b->bsums[lane >> 2] = (int16_t)s4;
             if (lane == 0) b->d = d[j];
         } else {
+            const int s8 = s4 + dpp_i32<0x141>(s4);
             ActQ8K* b = (ActQ8K*)out[j];
             // element e = 4*lane + r: sub-block jj = lane/8, class l = 4*(lane%2) + r, t = (lane%8)/2
             const int jj = lane >> 3, t = (lane & 7) >> 1, l0 = 4 * (lane & 1);
 #pragma unroll
             for (int r = 0; r < 4; ++r) b->qs[4 * (8 * (l0 + r) + jj) + t] = (int8_t)q[j][r];
-            if ((lane & 7) == 0) b->bs2[jj] = s8[j];
+            if ((lane & 7) == 0) b->bs2[jj] = s8;
             if (lane == 0) b->d = d[j];
         }
     }

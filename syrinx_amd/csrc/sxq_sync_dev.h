@@ -69,6 +69,24 @@ SXQ_DEV T ld_global(const T* p) {
     return __builtin_bit_cast(T, v);
 }
 
+// The loads issued above this point stay issued above it: neither the optimizer (which
+// would sink a load to its first use, e.g. behind a prologue's arithmetic on other
+// loads) nor the instruction scheduler moves a memory access or an instruction across
+// it.  It waits for nothing.
+SXQ_DEV void issue_point() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The same (wave-uniform) pointer with its provenance hidden from the optimizer: loads
+// through it are ordinary memory reads, which issue_point keeps on their side, where
+// loads through a const __restrict__ kernel argument count as invariant and move freely.
+template <typename T>
+SXQ_DEV T* opaque_ptr(T* p) {
+    asm volatile("" : "+s"(p));
+    return p;
+}
+
 // Workgroup barrier without __syncthreads()'s memory fence: loads in flight stay in
 // flight (the fence would wait for all of them).
 SXQ_DEV void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
