@@ -306,7 +306,46 @@ def _fish_layers(w: dict, base: str) -> int:
 
 
 def _q(w: dict, name: str, dtype: GgmlDType) -> QMatMul:
-    return QMatMul.from_qtensor(QTensor.quantize(w[name].contiguous(), dtype))
+    t = w[name]
+    if isinstance(t, QTensor):  # already quantized (a GGUF checkpoint)
+        if t.dtype() != dtype:
+            raise ValueError(f"{name} is {t.dtype().name}, the engine runs {GgmlDType(dtype).name}")
+        return QMatMul.from_qtensor(t)
+    return QMatMul.from_qtensor(QTensor.quantize(t.contiguous(), dtype))
+
+
+# The Fish weights fish_engines runs as QMatMul projections; every other tensor is a
+# vector or a dense table.
+_FISH_LINEAR = re.compile(r"^(layers|fast_layers)\.\d+\.(attention\.(wqkv|wo)|feed_forward\.(w1|w2|w3))\.weight$")
+
+
+def is_fish_projection(name: str) -> bool:
+    return bool(_FISH_LINEAR.match(name)) or name in ("embeddings.weight", "fast_output.weight")
+
+
+def save_fish_gguf(w: dict, path: str, dtype: GgmlDType = GgmlDType.Q4K) -> None:
+    """Quantize a load_fish_lm bag once and store it as GGUF: the projections (and the tied
+    slow head / fast output tables) as `dtype` blocks made by Candle's from_float, the
+    norms and embedding tables f32.  load_fish_gguf reads it back for fish_engines."""
+    from . import gguf
+    tensors = []
+    for name in sorted(w):
+        t = w[name]
+        if is_fish_projection(name) and not isinstance(t, QTensor):
+            t = QTensor.quantize(t.contiguous(), dtype)
+        tensors.append((name, t))
+    gguf.save(path, [("general.architecture", "fish-s2"), ("general.quantization", GgmlDType(dtype).name)], tensors)
+
+
+def load_fish_gguf(path: str, device="cuda:0") -> dict:
+    """A GGUF checkpoint as a fish_engines bag: quantized tensors as QTensors on `device`
+    (no re-quantization), f32/f16 tensors as f32 torch tensors."""
+    from . import gguf
+    c = gguf.Content.read(path)
+    out = {}
+    for name, ti in c.tensor_infos.items():
+        out[name] = c.dense(name, device) if ti.ggml_dtype in (0, 1) else c.tensor(name, device)
+    return out
 
 
 def _wire_fish(lm, w: dict, base: str, L: int, dtype: GgmlDType, qk_norm: bool) -> None:
@@ -373,5 +412,6 @@ def fish_engines(w: dict, n_codebooks: int = 10, semantic_begin: int = 151678, s
     return slow, fast
 
 
-__all__ = ["DecoderConfig", "load_cv2_quantized", "cv2_engine", "load_fish_lm", "fish_engines", "remap_qwen3_key",
+__all__ = ["DecoderConfig", "load_cv2_quantized", "cv2_engine", "load_fish_lm", "fish_engines", "save_fish_gguf",
+           "load_fish_gguf", "is_fish_projection", "remap_qwen3_key",
            "resolve_shards", "fuse_qkv", "cv2_policy", "Footprint", "Cv2Weights"]

@@ -244,3 +244,34 @@ def test_fish_engines_from_sharded_checkpoint_match_oracle(cuda, tmp_path, ora, 
                 lg, _ = eng.step(ids=torch.tensor([code], dtype=torch.int32))
                 _check(lg[0].cpu().numpy(), orc, orc.step_one(0, frame=[code]), f"fast code {code}", tally)
     tally.mostly_tight()
+
+
+def test_fish_engines_from_gguf_equal_engines_from_checkpoint(cuda, tmp_path, ora):
+    """A checkpoint quantized once into GGUF (save_fish_gguf) and loaded back
+    (load_fish_gguf: the stored blocks become QMatMuls without re-quantization) gives
+    the engines of the safetensors load: the stored blocks are the oracle's from_float of
+    the same weights, and the logits of both engines are bit-identical."""
+    src = _fish_checkpoint(tmp_path)
+    w = I.load_fish_lm(str(tmp_path), device=cuda)
+    path = str(tmp_path / "fish.gguf")
+    I.save_fish_gguf(w, path, GgmlDType.Q4K)
+    from syrinx_amd import gguf as G
+    c = G.Content.read(path)
+    assert c.metadata["general.quantization"].to_string() == "Q4K"
+    name = "layers.1.feed_forward.w2.weight"
+    assert c.tensor_infos[name].ggml_dtype == int(GgmlDType.Q4K) and c.tensor_infos[name].shape == (FD, FI)
+    assert bytes(c.tensor_bytes(name)) == ora.quantize(ora.Q4K, _f32(src[f"text_model.model.{name}"])).tobytes()
+    assert c.tensor_infos["norm.weight"].ggml_dtype == 0
+    g = I.load_fish_gguf(path, device=cuda)
+    kw = dict(n_codebooks=NCB, semantic_begin=BEGIN, semantic_end=BEGIN + R - 1, max_seq=16, max_batch=1,
+              dtype=GgmlDType.Q4K, device=cuda)
+    a_slow, a_fast = I.fish_engines(w, **kw)
+    b_slow, b_fast = I.fish_engines(g, **kw)
+    for frame in ([BEGIN + 3, 1, 2, 3, 4, 5, 6], [17, 0, 0, 0, 0, 0, 0]):
+        la, _, ha = a_slow.step(ids=torch.tensor([frame], dtype=torch.int32), want_hidden=True)
+        lb, _, hb = b_slow.step(ids=torch.tensor([frame], dtype=torch.int32), want_hidden=True)
+        assert torch.equal(la, lb) and torch.equal(ha, hb)
+    h0 = torch.from_numpy(np.random.default_rng(5).standard_normal(FD).astype(np.float32))[None]
+    assert torch.equal(a_fast.step(embeds=h0)[0], b_fast.step(embeds=h0)[0])
+    with pytest.raises(ValueError, match="Q4K"):
+        I.fish_engines(g, **dict(kw, dtype=GgmlDType.Q8_0))
