@@ -129,6 +129,10 @@ CASES = [
     (G.Q8_0, 896, 4864, 7),    # Q8_0 in chunks: 4 + 3
     (G.Q4K, 7, 256, 12),       # matrix-core GEMV: fewer weight rows than a tile, one block
     (G.Q4K, 40, 1536, 16),     # matrix-core GEMV: 6 blocks = a full and a partial chunk
+    # matrix-core GEMV with two 16-row tiles per workgroup (16384 rows and more)
+    (G.Q4K, 19456, 2560, 16),  # Qwen3-4B fused w1|w3 at the 16-stream batch
+    (G.Q4K, 16400, 512, 7),    # last workgroup: one live tile, the other clamped
+    (G.Q4K, 16389, 1024, 5),   # last workgroup: five live rows
 ]
 
 
