@@ -100,43 +100,60 @@ SXQ_DEV void wave_quantize_q8k_n(const float4 (&v)[J], int lane, void* const (&o
         am[j] = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(x[j][0])), fabsf(x[j][1])), fabsf(x[j][2])), fabsf(x[j][3]));
     }
     // wave maximum of |x|: DPP inside 16-lane rows, then the four row maxima as scalars
-    // (non-negative floats order like their bit patterns)
-    float wm[J];
+    // (am is a non-negative float, never NaN, so it orders like its bit pattern and the
+    // steps are integer maxima, one DPP instruction each)
+    uint32_t wm[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) wm[j] = fmaxf(am[j], dpp_f32<0xB1>(am[j]));
+    for (int j = 0; j < J; ++j) wm[j] = __builtin_bit_cast(uint32_t, am[j]);
 #pragma unroll
-    for (int j = 0; j < J; ++j) wm[j] = fmaxf(wm[j], dpp_f32<0x4E>(wm[j]));
+    for (int j = 0; j < J; ++j) wm[j] = max(wm[j], (uint32_t)dpp_i32<0xB1>((int)wm[j]));
 #pragma unroll
-    for (int j = 0; j < J; ++j) wm[j] = fmaxf(wm[j], dpp_f32<0x141>(wm[j]));
+    for (int j = 0; j < J; ++j) wm[j] = max(wm[j], (uint32_t)dpp_i32<0x4E>((int)wm[j]));
 #pragma unroll
-    for (int j = 0; j < J; ++j) wm[j] = fmaxf(wm[j], dpp_f32<0x140>(wm[j]));
+    for (int j = 0; j < J; ++j) wm[j] = max(wm[j], (uint32_t)dpp_i32<0x141>((int)wm[j]));
+#pragma unroll
+    for (int j = 0; j < J; ++j) wm[j] = max(wm[j], (uint32_t)dpp_i32<0x140>((int)wm[j]));
     uint32_t wmax[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, wm[j]), 0);
-        const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, wm[j]), 16);
-        const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, wm[j]), 32);
-        const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane(__builtin_bit_cast(int, wm[j]), 48);
+        const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)wm[j], 0);
+        const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)wm[j], 16);
+        const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)wm[j], 32);
+        const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)wm[j], 48);
         wmax[j] = max(max(r0, r1), max(r2, r3));
     }
+    // the signed maximum element of each chunk: the first element with |x| == w, i.e. the
+    // lowest lane holding one, then its first (selects from the last element back, no branch)
+    float mx[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const float w = __builtin_bit_cast(float, wmax[j]);
+        float mine = x[j][3];
+        mine = fabsf(x[j][2]) == w ? x[j][2] : mine;
+        mine = fabsf(x[j][1]) == w ? x[j][1] : mine;
+        mine = fabsf(x[j][0]) == w ? x[j][0] : mine;
+        const uint64_t hit = __ballot(am[j] == w);
+        const int src = hit ? __builtin_ctzll(hit) : 0;
+        mx[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), src));
+    }
+    // iscale = -128 / max and d = 1 / iscale of the J chunks in one pair of divisions: chunk
+    // j's max in lane j (the other lanes divide a copy, never read)
+    float mxv = mx[0];
+#pragma unroll
+    for (int j = 1; j < J; ++j) mxv = lane == j ? mx[j] : mxv;
+    const float isv = -128.0f / mxv;
+    const float dv = 1.0f / isv;
     int q[J][4];
     float d[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const float w = __builtin_bit_cast(float, wmax[j]);
-        // the first element with |x| == w: the lowest lane holding one, then its first
-        const float a0 = fabsf(x[j][0]), a1 = fabsf(x[j][1]), a2 = fabsf(x[j][2]);
-        const float mine = a0 == w ? x[j][0] : (a1 == w ? x[j][1] : (a2 == w ? x[j][2] : x[j][3]));
-        const uint64_t hit = __ballot(am[j] == w);
-        const int src = hit ? __builtin_ctzll(hit) : 0;
-        const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), src));
         q[j][0] = q[j][1] = q[j][2] = q[j][3] = 0;
         d[j] = 0.0f;
-        if (w != 0.0f) {  // uniform
-            const float iscale = -128.0f / mx;
+        if (wmax[j] != 0u) {  // uniform
+            const float iscale = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, isv), j));
 #pragma unroll
             for (int r = 0; r < 4; ++r) q[j][r] = (int)fminf(round_away(iscale * x[j][r]), 127.0f);
-            d[j] = 1.0f / iscale;
+            d[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dv), j));
         }
     }
 #pragma unroll
