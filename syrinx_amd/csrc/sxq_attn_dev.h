@@ -116,41 +116,75 @@ SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, f
     }
 }
 
-// Fused decode attention for split sp of KV head group g of stream s, NT threads:
-// P = NT/8 cached positions [sp*P, sp*P + P).  QK-norm + RoPE of the group's G queries
-// (from the qkv row), in the split holding position len also the new token's key/value
-// (norm + RoPE of k, appended to the cache), then the split's partials
-// {m, l, 0, 0, acc[hd]} per head
+typedef float attn_v4f __attribute__((ext_vector_type(4)));  // (HIP's float4 array would go to scratch)
+
+// The key tile of split sp (P = NT/8 positions) into registers: 8 lanes per position,
+// 16-byte pieces 32 floats apart, so every load instruction reads whole 128-byte rows;
+// rows past the stream's last position (L - 1) clamped to it (loaded, never used).
+template <int HD, int NT>
+SXQ_DEV void attn_load_k(float4 (&kr)[HD / 32], const AttnArgs& A, int64_t head_off, int sp, int L) {
+    constexpr int P = NT / 8;
+    const int tid = threadIdx.x, p0 = sp * P, slot = min(P, L - p0) - 1;
+    const int kp = tid >> 3, kcol = 4 * (tid & 7);
+    const float* krow = A.kc + head_off + (int64_t)(p0 + min(kp, slot)) * HD + kcol;
+#pragma unroll
+    for (int j = 0; j < HD / 32; ++j) kr[j] = ld_global((const float4*)(krow + 32 * j));
+}
+// The value tile of split sp, coalesced: round r holds floats [r*4NT, r*4NT + 4NT) of the
+// tile, 4 per thread.  In the split holding position L - 1 (the last of the nsp) that row
+// is the new value, read from the qkv row.  (Register loads, not direct-to-LDS ones: with
+// a direct-to-LDS load in flight the compiler waits for every load before the first use
+// of any.)
+template <int HD, int NT>
+SXQ_DEV void attn_load_v(attn_v4f (&vr4)[HD / 32], const AttnArgs& A, int64_t head_off, const float* vrow_new, int sp,
+                         int L, int nsp) {
+    constexpr int P = NT / 8, VR = P * HD / (4 * NT);
+    static_assert(VR == HD / 32, "NT = 8 P");
+    const int tid = threadIdx.x, p0 = sp * P, slot = min(P, L - p0) - 1;
+    const bool has_new = sp == nsp - 1;
+    const float* vb = A.vc + head_off + (int64_t)p0 * HD;
+#pragma unroll
+    for (int r = 0; r < VR; ++r) {
+        const int e = r * 4 * NT + 4 * tid;
+        const int vr = min(e / HD, slot), col = e - (e / HD) * HD;
+        const float* src = has_new && vr == slot ? vrow_new + col : vb + (int64_t)vr * HD + col;
+        vr4[r] = ld_global((const attn_v4f*)src);
+    }
+}
+
+// The partials of one split of the fused decode attention, NT threads: split sp of KV
+// head group g of stream s, P = NT/8 cached positions [sp*P, sp*P + P) (the stream holds
+// pos + 1 positions in nsp splits), leaving the split's partials {m, l, 0, 0, acc[hd]}
+// per head
 //   m = max_j s_j, l = sum_j exp(s_j - m), acc = sum_j exp(s_j - m) v_j,  s_j = (q . k_j) * scale
-// and, in the last split of the group to finish (a per-(stream, group) arrival counter,
-// reset after use), the merge of the group's heads and the quantization of that G*hd
-// slice of the context for the O projection.
+// in part_s -- or, when one split holds every position, the group's context itself.
+// QK-norm + RoPE of the group's G queries (from the qkv row) and, in the split holding
+// position pos, of the new token's key, appended to the cache with its value.  Returns
+// true when the caller is to publish the partials (nsp > 1).
 //
-// Latency layout (a launch holds ~B * n_kv * L / P workgroups, about one per CU, so
-// every phase is a chain of dependent steps rather than a throughput problem):
+// Latency layout (a launch holds ~B * n_kv * L / P workgroups, about one per CU at batch
+// 1, so every phase is a chain of dependent steps rather than a throughput problem):
 //   * the loads of each wave's norm + RoPE item (wave h: query head h; wave G: the new
-//     key) go first, then the key tile into registers (8 lanes per position, 16-byte
-//     pieces 32 floats apart: every load instruction reads whole 128-byte rows) and the
-//     value tile, so the norm + RoPE runs while the tile is in flight;
+//     key) go first, then the key tile and the value tile, so the norm + RoPE runs while
+//     the tiles are in flight;
 //   * scores: each lane dots its key elements with the same elements of every query
-//     (LDS broadcast), reduced over its 8 lanes with DPP;
+//     (LDS broadcast), reduced over its 8 lanes with DPP; the value tile goes to LDS
+//     after them (it is first read by the weighted values);
 //   * softmax: a wave per head, positions lane + 64 i, DPP reductions;
 //   * weighted values: nq = NT / (G*HD/4) position sets, a thread per (set, head, 4
-//     columns), the sets summed in order through LDS;
-//   * merge: the same (set, head, 4 columns) threads read their splits' partials with
-//     16-byte coherent loads issued together, the split weights formed meanwhile.
-// Requires HD in {64, 128}, G <= 8 and G*HD a whole number of activation blocks.
-template <int VDT, int HD, int NT>
-SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* smem, bool* last) {
-    constexpr int P = NT / 8, KJ = HD / 32, PR = HD + 4, NW = NT / 64;
-    typedef float v4f __attribute__((ext_vector_type(4)));  // (HIP's float4 array would go to scratch)
+//     columns), the sets summed in order through LDS.
+// The barriers are LDS-only (lds_barrier): no global access inside the split is read
+// back by another thread of the workgroup (the partials are published after it).
+template <int VDT, int HD, int NT, int GC>
+SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int nsp, float* smem, float* part_s,
+                        __amdgpu_buffer_rsrc_t prs) {
+    constexpr int P = NT / 8, KJ = HD / 32, PR = HD + 4, NW = NT / 64, VR = HD / 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = A.len[s], L = pos + 1, p0 = sp * P;
-    if (p0 >= L) return;
+    const int L = pos + 1, p0 = sp * P;
     const int nh = A.nh, nkv = A.nkv, max_splits = A.max_splits;
-    const int np = min(P, L - p0), nsp = (L + P - 1) / P;
-    const int G = nh / nkv, gd = G * HD, T = gd / 4, nq = NT / T;
-    const bool has_new = pos < p0 + np;  // position pos is then row np - 1 of the tile
+    const int np = min(P, L - p0);
+    const int G = GC > 0 ? GC : nh / nkv, gd = G * HD, T = gd / 4, nq = NT / T;
+    const bool has_new = sp == nsp - 1;  // position pos is then row np - 1 of the tile
     const int slot = np - 1;
     float* vt = smem;         // [P][HD]   value tile
     float* qs = vt + P * HD;  // [G][HD]   queries after QK-norm + RoPE
@@ -161,64 +195,42 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
     const float* cos_row = A.cos_t + (int64_t)pos * (HD / 2);
     const float* sin_row = A.sin_t + (int64_t)pos * (HD / 2);
     const int64_t head_off = (int64_t)s * A.kv_stream_stride + (int64_t)g * A.max_seq * HD;
-    const float* kb = A.kc + head_off + (int64_t)p0 * HD;
-    const float* vb = A.vc + head_off + (int64_t)p0 * HD;
     const float* vrow_new = row + (int64_t)(nh + nkv + g) * HD;
+    const int kp = tid >> 3, kcol = 4 * (tid & 7);
 
-    // 1. this wave's norm + RoPE item (every wave loads one; idle waves repeat the last)
+    // 1. this wave's norm + RoPE item (every wave loads one; idle waves repeat the last),
+    //    then the key and value tiles
     const int nitem = G + (has_new ? 1 : 0);
     const int item = min(wave, nitem - 1);
     const bool isq = item < G;
-    const float* isrc = row + (int64_t)(isq ? g * G + item : nh + g) * HD;
     const float* inw = isq ? A.qn : A.kn;
-    const RopeIn rin = rope_load<HD>(isrc, inw, A.interleaved, cos_row, sin_row, lane);
-    // 2. the key tile into registers (rows past np clamped to a cached row: loaded, never used)
-    const int kp = tid >> 3, kcol = 4 * (tid & 7);
-    const float* krow = kb + (int64_t)min(kp, slot) * HD + kcol;
+    const RopeIn rin =
+        rope_load<HD>(row + (int64_t)(isq ? g * G + item : nh + g) * HD, inw, A.interleaved, cos_row, sin_row, lane);
     float4 kr[KJ];
-#pragma unroll
-    for (int j = 0; j < KJ; ++j) kr[j] = ld_global((const float4*)(krow + 32 * j));
-    // ... and the value tile, coalesced: round r holds floats [r*4NT, r*4NT + 4NT) of the
-    // tile, 4 per thread.  Row `slot` of the split holding the new token is the new value,
-    // read from the qkv row in that lane.  (Register loads, not direct-to-LDS ones: with a
-    // direct-to-LDS load in flight the compiler waits for every load before the first use
-    // of any, which would serialise the norm + RoPE below behind the tile.)
-    constexpr int VR = P * HD / (4 * NT);
-    v4f vr4[VR];
-#pragma unroll
-    for (int r = 0; r < VR; ++r) {
-        const int e = r * 4 * NT + 4 * tid;
-        const int vr = min(e / HD, slot), col = e - (e / HD) * HD;
-        const float* src = has_new && vr == slot ? vrow_new + col : vb + (int64_t)vr * HD + col;
-        vr4[r] = ld_global((const v4f*)src);
-    }
+    attn_v4f vr4[VR];
+    attn_load_k<HD, NT>(kr, A, head_off, sp, L);
+    attn_load_v<HD, NT>(vr4, A, head_off, vrow_new, sp, L, nsp);
     issue_point();
-    // 3. norm + RoPE in registers while the tile is in flight; stored once it has landed
-    const float2 y = rope_pair<HD>(rin, inw != nullptr, A.eps, A.inv_hd, lane);
-    float2 y2 = make_float2(0.0f, 0.0f);
-    if (wave + NW < nitem) {  // G == NW: the new key is a second item of wave 0
-        const RopeIn r2 = rope_load<HD>(row + (int64_t)(nh + g) * HD, A.kn, A.interleaved, cos_row, sin_row, lane);
-        y2 = rope_pair<HD>(r2, A.kn != nullptr, A.eps, A.inv_hd, lane);
+    // 2. norm + RoPE in registers while the tiles are in flight
+    {
+        float2 y = rope_pair<HD>(rin, inw != nullptr, A.eps, A.inv_hd, lane);
+        float2 y2 = make_float2(0.0f, 0.0f);
+        if (wave + NW < nitem) {  // G == NW: the new key is a second item of wave 0
+            const RopeIn r2 = rope_load<HD>(row + (int64_t)(nh + g) * HD, A.kn, A.interleaved, cos_row, sin_row, lane);
+            y2 = rope_pair<HD>(r2, A.kn != nullptr, A.eps, A.inv_hd, lane);
+        }
+        float* kapp = A.kc + head_off + (int64_t)pos * HD;  // the new key's cache row
+        if (wave < nitem)
+            rope_store<HD>(y, A.interleaved, isq ? qs + item * HD : knew,
+                           isq ? (A.q_out && sp == 0 ? A.q_out + ((int64_t)s * nh + g * G + item) * HD : nullptr) : kapp,
+                           lane);
+        if (wave + NW < nitem) rope_store<HD>(y2, A.interleaved, knew, kapp, lane);
+        lds_barrier();
     }
+    if (has_new && kp == slot)
 #pragma unroll
-    for (int r = 0; r < VR; ++r) *(v4f*)(vt + r * 4 * NT + 4 * tid) = vr4[r];
-    float* kapp = A.kc + head_off + (int64_t)pos * HD;  // the new key's cache row
-    if (wave < nitem)
-        rope_store<HD>(y, A.interleaved, isq ? qs + item * HD : knew,
-                       isq ? (A.q_out && sp == 0 ? A.q_out + ((int64_t)s * nh + g * G + item) * HD : nullptr) : kapp,
-                       lane);
-    if (wave + NW < nitem) rope_store<HD>(y2, A.interleaved, knew, kapp, lane);
-    __syncthreads();
-    if (has_new) {
-        if (kp == slot)
-#pragma unroll
-            for (int j = 0; j < KJ; ++j) kr[j] = *(const float4*)(knew + kcol + 32 * j);
-        if (wave == NW - 1)  // append the new value to the cache
-#pragma unroll
-            for (int t = 0; t < HD / 64; ++t)
-                A.vc[head_off + (int64_t)pos * HD + lane + 64 * t] = vt[slot * HD + lane + 64 * t];
-    }
-    // 4. scores: partial dots over this lane's key elements, summed over the 8 lanes of the
+        for (int j = 0; j < KJ; ++j) kr[j] = *(const float4*)(knew + kcol + 32 * j);
+    // 3. scores: partial dots over this lane's key elements, summed over the 8 lanes of the
     //    position; lane c of the 8 writes head c's score
     float sv[8];
 #pragma unroll
@@ -245,10 +257,15 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
     for (int h = 1; h < 8; ++h)
         if (c8 == h) mine = sv[h];
     if (c8 < G) sc[c8 * P + kp] = mine * A.scale + 0.0f;
-    __syncthreads();
-    // 5. softmax of head `wave` over the tile's positions (lane + 64 i)
-    float* part_s = A.part + (int64_t)s * nh * max_splits * PR;
-    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(part_s, (uint32_t)nh * (uint32_t)max_splits * PR * 4);
+    // the value tile into LDS (it is first read by the weighted values)
+#pragma unroll
+    for (int r = 0; r < VR; ++r) *(attn_v4f*)(vt + r * 4 * NT + 4 * tid) = vr4[r];
+    lds_barrier();
+    if (has_new && wave == NW - 1)  // append the new value to the cache
+#pragma unroll
+        for (int t = 0; t < HD / 64; ++t)
+            A.vc[head_off + (int64_t)pos * HD + lane + 64 * t] = vt[slot * HD + lane + 64 * t];
+    // 4. softmax of head `wave` over the tile's positions (lane + 64 i)
     if (wave < G) {
         constexpr int PL = P / 64;
         float x[PL], mx = -INFINITY;
@@ -276,12 +293,11 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
             }
         }
     }
-    __syncthreads();
-    // 6. weighted values: thread (set qi, head h, columns d..d+3) over the set's positions
+    lds_barrier();
+    // 5. weighted values: thread (set qi, head h, columns d..d+3) over the set's positions
     const int pps = (P + nq - 1) / nq;
     const int qi = tid / T, rr = tid - qi * T, h = rr / (HD / 4), d = 4 * (rr - h * (HD / 4));
-    const bool mt = qi < nq;
-    if (mt) {
+    if (qi < nq) {
         const int pa = qi * pps, pb = min(pa + pps, np);
         const float* e = sc + h * P;
         float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -296,10 +312,10 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
         }
         *(float4*)(red + qi * gd + h * HD + d) = a;
     }
-    __syncthreads();
+    lds_barrier();
     if (nsp == 1) {
         // One split holds every position: its weights exp(m - m) are 1, so the merge
-        // below would give acc / l bit for bit -- without the hand-off.
+        // would give acc / l bit for bit -- without the hand-off.
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (tid < T) {
             float4 a = *(const float4*)(red + 4 * tid);
@@ -314,7 +330,7 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
             v = make_float4(a.x / ls, a.y / ls, a.z / ls, a.w / ls);
         }
         attn_emit_context<VDT, HD>(A, s, g, gd, T, v);
-        return;
+        return false;
     }
     if (tid < T) {
         float4 a = *(const float4*)(red + 4 * tid);
@@ -327,11 +343,37 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
         }
         store16_coherent(prs, (uint32_t)(((g * G + h) * max_splits + sp) * PR + 4 + d) * 4, a);
     }
+    return true;
+}
+
+// Fused decode attention for split sp of KV head group g of stream s (attn_split),
+// then, in the last split of the group to finish (a per-(stream, group) arrival
+// counter, reset after use), the merge of the group's heads and the quantization of that
+// G*hd slice of the context for the O projection.
+//   merge: the same (set, head, 4 columns) threads as the weighted values read their
+//   splits' partials with 16-byte coherent loads issued together, the split weights
+//   formed meanwhile.
+// Requires HD in {64, 128}, G <= 8 and G*HD a whole number of activation blocks; GC is
+// G as a compile-time constant (the Qwen3-4B and Qwen2-0.5B groups), or 0 to read it
+// from A at run time.
+template <int VDT, int HD, int NT, int GC>
+SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* smem, bool* last) {
+    constexpr int P = NT / 8, PR = HD + 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = A.len[s], nsp = (pos + P) / P;
+    if (sp >= nsp) return;
+    const int nh = A.nh, nkv = A.nkv, max_splits = A.max_splits;
+    const int G = GC > 0 ? GC : nh / nkv, gd = G * HD, T = gd / 4, nq = NT / T;
+    float* part_s = A.part + (int64_t)s * nh * max_splits * PR;
+    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(part_s, (uint32_t)nh * (uint32_t)max_splits * PR * 4);
+    if (!attn_split<VDT, HD, NT, GC>(A, s, g, sp, pos, nsp, smem, part_s, prs)) return;
     // the last split of the group to arrive merges the group's heads
     if (!publish_and_count(&A.counter[s * nkv + g], (unsigned)nsp, last)) return;
 
-    // 7. merge: ctx = sum_z exp(m_z - M) acc_z / sum_z exp(m_z - M) l_z, M = max_z m_z.
-    //    The tile LDS is free now: wts [G][nsp] | lsum [G] | red2 [nq][gd].
+    // merge: ctx = sum_z exp(m_z - M) acc_z / sum_z exp(m_z - M) l_z, M = max_z m_z.
+    // The tile LDS is free now: wts [G][nsp] | lsum [G] | red2 [nq][gd].
+    const int qi = tid / T, rr = tid - qi * T, h = rr / (HD / 4), d = 4 * (rr - h * (HD / 4));
+    const bool mt = qi < nq;
     float* wts = smem;
     float* lsum = wts + G * nsp;
     float* red2 = smem + ((G * nsp + G + 3) & ~3);

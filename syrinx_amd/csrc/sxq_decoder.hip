@@ -291,12 +291,15 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ 
 }
 
 // The per-launch kernel: grid (B, n_kv, ceil(max_seq / kAttnSplitFused)), kAttnThreads threads.
-template <int VDT, int HD>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs A) {
+// At least six waves per SIMD (at most 80 VGPRs): three workgroups per CU, as the LDS
+// allows.  GC: the query heads per KV head as a compile-time constant, or 0 (read at
+// run time).
+template <int VDT, int HD, int GC>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_attn_decode(AttnArgs A) {
     static_assert(kAttnThreads / 8 == kAttnSplitFused, "a split is one position per 8 lanes");
     extern __shared__ float4 smem4[];  // float4: 16-byte aligned after any static LDS
     __shared__ bool last;
-    attn_decode_body<VDT, HD, kAttnThreads>(A, blockIdx.x, blockIdx.y, blockIdx.z, (float*)smem4, &last);
+    attn_decode_body<VDT, HD, kAttnThreads, GC>(A, blockIdx.x, blockIdx.y, blockIdx.z, (float*)smem4, &last);
 }
 
 // grid (B, ceil(nh*hd/256)), 256 threads: merge the splits of the heads covering
@@ -547,18 +550,25 @@ bool attn_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits) {
            attn_decode_lds(nh, nkv, hd, max_splits) <= 160 * 1024;
 }
 
-template <int VDT, int HD>
+// The instance for a head group: G = 4 at head_dim 128 (Qwen3-4B, 32/8 heads) and G = 7
+// at head_dim 64 (Qwen2-0.5B, 14/2 heads) compiled for their G, any other group size
+// through the run-time instance.
+template <int VDT, int HD, int GC>
 static const void* attn_decode_fn() {
-    return (const void*)k_attn_decode<VDT, HD>;
+    return (const void*)k_attn_decode<VDT, HD, GC>;
 }
-static const void* attn_decode_kernel(int vdt, int hd) {
-    if (vdt == kQ8K) return hd == 64 ? attn_decode_fn<kQ8K, 64>() : attn_decode_fn<kQ8K, 128>();
-    return hd == 64 ? attn_decode_fn<kQ8_0, 64>() : attn_decode_fn<kQ8_0, 128>();
+template <int VDT>
+static const void* attn_decode_kernel_vdt(int hd, int G) {
+    if (hd == 128) return G == 4 ? attn_decode_fn<VDT, 128, 4>() : attn_decode_fn<VDT, 128, 0>();
+    return G == 7 ? attn_decode_fn<VDT, 64, 7>() : attn_decode_fn<VDT, 64, 0>();
+}
+static const void* attn_decode_kernel(int vdt, int hd, int G) {
+    return vdt == kQ8K ? attn_decode_kernel_vdt<kQ8K>(hd, G) : attn_decode_kernel_vdt<kQ8_0>(hd, G);
 }
 
 hipError_t attn_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits) {
     const int lds = (int)attn_decode_lds(nh, nkv, hd, max_splits);
-    return hipFuncSetAttribute(attn_decode_kernel(vdt, hd), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    return hipFuncSetAttribute(attn_decode_kernel(vdt, hd, nh / nkv), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 }
 
 hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, int nh, int nkv, int hd, const float* qn,
@@ -595,7 +605,7 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
     const dim3 grid(B, nkv, (max_seq + kAttnSplitFused - 1) / kAttnSplitFused);  // partial records: max_splits per head
     const size_t lds = attn_decode_lds(nh, nkv, hd, max_splits);
     void* args[] = {&A};
-    return hipLaunchKernel(attn_decode_kernel(vdt, hd), grid, dim3(kAttnThreads), args, lds, s);
+    return hipLaunchKernel(attn_decode_kernel(vdt, hd, nh / nkv), grid, dim3(kAttnThreads), args, lds, s);
 }
 
 hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s) {
