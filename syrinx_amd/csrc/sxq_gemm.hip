@@ -334,7 +334,13 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(const _Float16* __restrict__ x
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 h = hnext;
         load_group(grp_of(li + 1), 1);
+        // The wait before the next barrier leaves exactly one load in flight, which must
+        // be this header load: the scheduler may not move either register load above the
+        // stage's LDS loads (were an LDS load issued last, the barrier could pass with its
+        // 1 KB of the stage still unwritten).
+        __builtin_amdgcn_sched_barrier(0);
         w1 = load_w(grp_of(li + 1));
+        __builtin_amdgcn_sched_barrier(0);
         hnext = load_h(min(b0 + li / 2 + 1, b1 - 1));
         __builtin_amdgcn_sched_barrier(0);
         compute(std::integral_constant<int, 0>(), w0, &h);
