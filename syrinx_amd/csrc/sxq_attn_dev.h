@@ -99,8 +99,13 @@ SXQ_DEV void rope_store(float2 y, int interleaved, float* dst, float* gdst, int 
 // The group's context slice (thread t < T holds elements 4t .. 4t + 3, zeros past T): the
 // optional f32 record, then the activation blocks of the O projection -- the quantizers'
 // lane layout, wave w quantizing chunk w of 256 elements.
-template <int VDT, int HD>
-SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, float4 v) {
+// PUB (Q8_K): the slice is read by other workgroups of the same launch (the O projection
+// of k_attn_wo_decode), so it is quantized into LDS at smem + A.pub_off bytes, copied out
+// by wave 0 with agent-coherent 16-byte stores and, once those have completed, counted
+// in A.ready.
+template <int VDT, int HD, bool PUB = false>
+SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, float4 v, float* smem) {
+    static_assert(!PUB || VDT == kQ8K, "published slices are Q8_K blocks");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int dim = A.nh * HD;
     if (tid < T && A.ctx_out) *(float4*)(A.ctx_out + (int64_t)s * dim + (int64_t)g * gd + 4 * tid) = v;
@@ -108,6 +113,19 @@ SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, f
     uint8_t* arow = A.act + (int64_t)s * nbr * act_block_bytes(VDT);
     const int blk_first = VDT == kQ8K ? (g * gd) / 256 : (g * gd) / 32;  // the slice's first block
     uint8_t* qdst = arow + (size_t)blk_first * act_block_bytes(VDT);
+    if constexpr (PUB) {
+        uint8_t* ql = (uint8_t*)smem + A.pub_off;
+        if (tid < ((T + 63) & ~63)) wave_quantize_q8k<false>(v, lane, ql + (size_t)wave * sizeof(ActQ8K));
+        lds_barrier();
+        if (wave == 0) {
+            const int nu4 = (gd / 256) * (int)(sizeof(ActQ8K) / 16);
+            const __amdgpu_buffer_rsrc_t r = coherent_rsrc(qdst, (uint32_t)nu4 * 16);
+            for (int i = lane; i < nu4; i += 64) store16_coherent(r, (uint32_t)i * 16, ((const float4*)ql)[i]);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice has reached the coherent level
+            if (lane == 0) __hip_atomic_fetch_add(A.ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
     if (tid < ((T + 63) & ~63)) {
         if (VDT == kQ8K)
             wave_quantize_q8k<false>(v, lane, qdst + (size_t)wave * sizeof(ActQ8K));
@@ -175,7 +193,7 @@ SXQ_DEV void attn_load_v(attn_v4f (&vr4)[HD / 32], const AttnArgs& A, int64_t he
 //     columns), the sets summed in order through LDS.
 // The barriers are LDS-only (lds_barrier): no global access inside the split is read
 // back by another thread of the workgroup (the partials are published after it).
-template <int VDT, int HD, int NT, int GC>
+template <int VDT, int HD, int NT, int GC, bool PUB = false>
 SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int nsp, float* smem, float* part_s,
                         __amdgpu_buffer_rsrc_t prs) {
     constexpr int P = NT / 8, KJ = HD / 32, PR = HD + 4, NW = NT / 64, VR = HD / 32;
@@ -329,7 +347,7 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
             const float ls = knew[(4 * tid) / HD];
             v = make_float4(a.x / ls, a.y / ls, a.z / ls, a.w / ls);
         }
-        attn_emit_context<VDT, HD>(A, s, g, gd, T, v);
+        attn_emit_context<VDT, HD, PUB>(A, s, g, gd, T, v, smem);
         return false;
     }
     if (tid < T) {
@@ -356,7 +374,7 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
 // Requires HD in {64, 128}, G <= 8 and G*HD a whole number of activation blocks; GC is
 // G as a compile-time constant (the Qwen3-4B and Qwen2-0.5B groups), or 0 to read it
 // from A at run time.
-template <int VDT, int HD, int NT, int GC>
+template <int VDT, int HD, int NT, int GC, bool PUB = false>
 SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* smem, bool* last) {
     constexpr int P = NT / 8, PR = HD + 4;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -366,7 +384,7 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
     const int G = GC > 0 ? GC : nh / nkv, gd = G * HD, T = gd / 4, nq = NT / T;
     float* part_s = A.part + (int64_t)s * nh * max_splits * PR;
     const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(part_s, (uint32_t)nh * (uint32_t)max_splits * PR * 4);
-    if (!attn_split<VDT, HD, NT, GC>(A, s, g, sp, pos, nsp, smem, part_s, prs)) return;
+    if (!attn_split<VDT, HD, NT, GC, PUB>(A, s, g, sp, pos, nsp, smem, part_s, prs)) return;
     // the last split of the group to arrive merges the group's heads
     if (!publish_and_count(&A.counter[s * nkv + g], (unsigned)nsp, last)) return;
 
@@ -455,7 +473,7 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
         const float ls = lsum[(4 * tid) / HD];
         v = make_float4(c.x / ls, c.y / ls, c.z / ls, c.w / ls);
     }
-    attn_emit_context<VDT, HD>(A, s, g, gd, T, v);
+    attn_emit_context<VDT, HD, PUB>(A, s, g, gd, T, v, smem);
     if (tid == 0) __hip_atomic_store(&A.counter[s * nkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -94,6 +94,22 @@ struct AttnArgs {
     unsigned* counter;       // [B][nkv] arrival counters, zero between launches
     uint8_t* act;            // [B] quantized context rows (the O projection's input)
     float *ctx_out, *q_out;  // optional f32 copies of the context and the roped queries
+    unsigned* ready;         // k_attn_wo_decode: context slices published so far
+    uint32_t pub_off;        // k_attn_wo_decode: LDS byte offset of the slice staging
 };
+
+// Batch-1 decode attention and the O projection (Q4_K, y += ctx . Wo^T in place) as one
+// launch: the projection's workgroups follow the attention's and wait for the n_kv
+// context slices.  ready: this launch's counter, zero at the launch; ready_next: a counter
+// that no launch in flight uses, zeroed by this one (the counters of consecutive layers
+// chain this way: layer l's launch zeroes layer l + 1's).
+bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo, int dim);
+hipError_t attn_wo_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo);
+hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int nh, int nkv, int hd, const float* qn,
+                                      const float* kn, float eps, int interleaved, const float* cos_t,
+                                      const float* sin_t, const int* len, float* kc, float* vc, int max_seq,
+                                      int max_splits, float* part, unsigned* counter, uint8_t* act, const QWeight& wo,
+                                      float* y, unsigned* ready, unsigned* ready_next, float* ctx_out, float* q_out,
+                                      hipStream_t s);
 
 }  // namespace sxq

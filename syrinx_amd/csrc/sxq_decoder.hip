@@ -16,6 +16,7 @@
 // compute from the same f32 input (the wave quantizers of sxq_quant_dev.h).
 #include "sxq_attn_dev.h"
 #include "sxq_decoder.h"
+#include "sxq_gemv_dev.h"
 #include "sxq_sync_dev.h"
 #include "sxq_quant_dev.h"
 
@@ -602,10 +603,173 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
     A.act = act;
     A.ctx_out = ctx_out;
     A.q_out = q_out;
+    A.ready = nullptr;
+    A.pub_off = 0;
     const dim3 grid(B, nkv, (max_seq + kAttnSplitFused - 1) / kAttnSplitFused);  // partial records: max_splits per head
     const size_t lds = attn_decode_lds(nh, nkv, hd, max_splits);
     void* args[] = {&A};
     return hipLaunchKernel(attn_decode_kernel(vdt, hd, nh / nkv), grid, dim3(kAttnThreads), args, lds, s);
+}
+
+// ---- batch-1 decode attention + O projection as one launch ---------------------------
+// Workgroups [0, n_attn) are k_attn_decode's (split sp = id / n_kv of head group
+// g = id % n_kv), publishing their quantized context slices (attn_emit_context, PUB); the
+// rest each own R rows of the Q4_K O projection (k_gemv2_q4k's tile, 512 threads): they
+// issue their weight loads and the residual load at once, then one thread waits for the
+// n_kv slices (a bounded poll of the ready counter), the context row is staged into LDS
+// with agent-coherent loads, and the tile's products and in-order fold follow -- the same
+// arithmetic as the separate launches, bit for bit.  The wait cannot block the attention:
+// the workgroups of a launch are dispatched in id order, so every attention workgroup
+// holds its CU before the first projection workgroup does, and it never waits for one.
+// Should the poll run out anyway (about a second), the tile's outputs are NaN rather
+// than stale.
+struct WoArgs {
+    const uint4* hdr;  // Q4_K block headers, 16 B per block, [n][nb]
+    const uint4* qs;   // Q4_K quants, 128 B per block, [n][nb]
+    int n, nb, R;      // output rows, blocks per row, rows per workgroup
+    int n_attn;        // attention workgroups ahead of the projection's
+    float* y;          // the residual stream row [n], updated in place: y = y + ctx . W^T
+    unsigned* ready_next;
+    unsigned need;  // slices in the context row (n_kv)
+};
+constexpr int kWoTm = 2;  // task rounds of a projection tile: R * nb <= kWoTm * 64
+constexpr int kWoPollCap = 1 << 22;
+
+template <int HD, int GC>
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_attn_wo_decode(AttnArgs A,
+                                                                                                          WoArgs W) {
+    constexpr int NT = kAttnThreads, TM = kWoTm;
+    extern __shared__ float4 smem4[];
+    __shared__ bool flag;
+    const int id = blockIdx.x;
+    if (id < W.n_attn) {
+        attn_decode_body<kQ8K, HD, NT, GC, true>(A, 0, id % A.nkv, id / A.nkv, (float*)smem4, &flag);
+        return;
+    }
+    uint4* lds = (uint4*)smem4;
+    const int tid = threadIdx.x, t = id - W.n_attn;
+    const int nb = W.nb, row0 = t * W.R, rows = min(W.R, W.n - row0), tasks = rows * nb;
+    uint4 q[TM], h[TM];
+    q4k_tile_load<NT, TM>(W.hdr, W.qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
+    const int r = tid >> 3, l = tid & 7;
+    const float res = W.y[row0 + min(r, rows - 1)];  // clamped, unconditional; used by lane class 0 of rows < rows
+    issue_point();
+    if (tid == 0 && t == 0) __hip_atomic_store(W.ready_next, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int act_u4 = nb * (int)(sizeof(ActQ8K) / 16);
+    const __amdgpu_buffer_rsrc_t ar = coherent_rsrc(A.act, (uint32_t)act_u4 * 16);
+    float* pr = (float*)(lds + act_u4);  // product chains [R + 1][9][CS]
+    bool ok = true;
+    float v = 0.0f;
+    // Two passes over the same code: the first, on whatever the LDS holds, runs while the
+    // attention does and leaves the products' and the fold's instructions in the
+    // instruction cache (their first fetch would otherwise sit on the critical path);
+    // the second waits for the context and computes the result.
+#pragma nounroll
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) {
+            if (tid == 0) {
+                int it = 0;
+                while (__hip_atomic_load(A.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < W.need &&
+                       it < kWoPollCap) {
+                    __builtin_amdgcn_s_sleep(1);
+                    ++it;
+                }
+                flag = it < kWoPollCap;
+            }
+            lds_barrier();  // (also: every thread's first-pass fold has read the chains)
+            ok = flag;
+            // the context row into LDS, read at the coherent level (this XCD's L2 may
+            // hold an earlier layer's row)
+            for (int i = tid; i < act_u4; i += NT) {
+                const float4 x = load16_coherent(ar, (uint32_t)i * 16);
+                lds[i] = make_uint4(__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w));
+            }
+            lds_barrier();
+        }
+        q4k_tile_products<1, NT, TM>(q, h, (const ActQ8K*)lds, nb, 1, rows, W.R, pr);
+        __syncthreads();
+        v = q4k_tile_fold(pr, nb, W.R, 0, rows);
+    }
+    if (r < rows && l == 0) W.y[row0 + r] = ok ? res + v : __builtin_nanf("");
+}
+
+static int wo_rows(int nb) { return max(1, min(kAttnThreads / 8, kWoTm * (kAttnThreads / 8) / nb)); }
+static size_t wo_pub_off(int nh, int nkv, int hd, int max_splits) {
+    return (attn_decode_lds(nh, nkv, hd, max_splits) + 15) & ~(size_t)15;
+}
+static size_t attn_wo_lds(int nh, int nkv, int hd, int max_splits, int nb) {
+    const size_t G = nh / nkv;
+    const size_t attn = wo_pub_off(nh, nkv, hd, max_splits) + (G * hd / 256) * sizeof(ActQ8K);
+    const size_t R = wo_rows(nb);
+    const size_t wo = (size_t)nb * sizeof(ActQ8K) + (R + 1) * 9 * q4k_chain_stride(nb) * sizeof(float);
+    return attn > wo ? attn : wo;
+}
+static const void* attn_wo_kernel(int hd, int G) {
+    if (hd == 128) return G == 4 ? (const void*)k_attn_wo_decode<128, 4> : (const void*)k_attn_wo_decode<128, 0>;
+    return (const void*)k_attn_wo_decode<64, 0>;
+}
+
+bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo, int dim) {
+    return vdt == kQ8K && wo.dtype == kQ4K && attn_decode_fits(vdt, nh, nkv, hd, max_splits) && wo.k == (int64_t)nh * hd &&
+           wo.n == dim && wo.nb >= 1 && wo.nb <= kWoTm * (kAttnThreads / 8) &&
+           attn_wo_lds(nh, nkv, hd, max_splits, (int)wo.nb) <= 160 * 1024;
+}
+
+hipError_t attn_wo_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo) {
+    (void)vdt;
+    const int lds = (int)attn_wo_lds(nh, nkv, hd, max_splits, (int)wo.nb);
+    return hipFuncSetAttribute(attn_wo_kernel(hd, nh / nkv), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+}
+
+hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int nh, int nkv, int hd, const float* qn,
+                                      const float* kn, float eps, int interleaved, const float* cos_t,
+                                      const float* sin_t, const int* len, float* kc, float* vc, int max_seq,
+                                      int max_splits, float* part, unsigned* counter, uint8_t* act, const QWeight& wo,
+                                      float* y, unsigned* ready, unsigned* ready_next, float* ctx_out, float* q_out,
+                                      hipStream_t s) {
+    if (!attn_wo_decode_fits(vdt, nh, nkv, hd, max_splits, wo, (int)wo.n) ||
+        max_seq > kMaxSplitsFused * kAttnSplitFused || ready == ready_next)
+        return hipErrorInvalidValue;
+    AttnArgs A;
+    A.qkv = qkv;
+    A.qkv_n = qkv_n;
+    A.nh = nh;
+    A.nkv = nkv;
+    A.qn = qn;
+    A.kn = kn;
+    A.eps = eps;
+    A.inv_hd = (float)(1.0 / (double)hd);
+    A.scale = (float)(1.0 / sqrt((double)hd));
+    A.interleaved = interleaved;
+    A.cos_t = cos_t;
+    A.sin_t = sin_t;
+    A.len = len;
+    A.kc = kc;
+    A.vc = vc;
+    A.kv_stream_stride = (int64_t)nkv * max_seq * hd;  // one stream: unused
+    A.max_seq = max_seq;
+    A.part = part;
+    A.max_splits = max_splits;
+    A.counter = counter;
+    A.act = act;
+    A.ctx_out = ctx_out;
+    A.q_out = q_out;
+    A.ready = ready;
+    A.pub_off = (uint32_t)wo_pub_off(nh, nkv, hd, max_splits);
+    WoArgs W;
+    W.hdr = (const uint4*)wo.hdr;
+    W.qs = (const uint4*)wo.qs;
+    W.n = (int)wo.n;
+    W.nb = (int)wo.nb;
+    W.R = wo_rows(W.nb);
+    W.n_attn = nkv * ((max_seq + kAttnSplitFused - 1) / kAttnSplitFused);
+    W.y = y;
+    W.ready_next = ready_next;
+    W.need = (unsigned)nkv;
+    const int n_wo = (W.n + W.R - 1) / W.R;
+    const size_t lds = attn_wo_lds(nh, nkv, hd, max_splits, W.nb);
+    void* args[] = {&A, &W};
+    return hipLaunchKernel(attn_wo_kernel(hd, nh / nkv), dim3(W.n_attn + n_wo), dim3(kAttnThreads), args, lds, s);
 }
 
 hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s) {

@@ -76,6 +76,11 @@ struct sxq_lm {
     unsigned* am_count = nullptr;   // per-stream arrival counters (zero between steps)
     unsigned* attn_count = nullptr; // per-(stream, KV head) arrival counters of the fused attention
     bool attn_fused = false;
+    // one decode row: attention and the O projection as one launch, which waits on
+    // per-layer counters (layer l's launch zeroes layer l + 1's); wo_dirty: a step was
+    // enqueued only in part, so the counters are zeroed before the next one
+    bool wo_fused = false, wo_dirty = false;
+    unsigned* wo_ready = nullptr;  // [n_layers]
     bool swiglu = false;        // one decode row: gate|up GEMV with SwiGLU epilogue + quantizing down GEMV
     float* act_f32 = nullptr;   // SwiGLU output row of that pair [max_batch][intermediate]
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
@@ -183,6 +188,12 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                                     lm->h, s));
     }
     if (tr) STEP(record(lm->h, (size_t)n * c.dim));
+    const bool wo_fused = lm->wo_fused && n == 1;
+    if (lm->wo_dirty) {
+        STEP(launch_fill_int((int*)lm->wo_ready, c.n_layers, 0, s));
+        lm->wo_dirty = false;
+    }
+    lm->wo_dirty = wo_fused;  // until the whole step is enqueued
     const int I = c.intermediate;
     const size_t nd = (size_t)n * c.dim;
     auto norm_in = [&](const float* x, const float* w, float* normed) {
@@ -205,10 +216,17 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
         if (lm->attn_fused) {
             float* q_slot = tr ? slot((size_t)n * lm->ctx) : nullptr;
             float* ctx_slot = tr ? slot((size_t)n * lm->ctx) : nullptr;
-            STEP(launch_attention_decode(lm->vdt, lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn, kn,
-                                         c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len, kc, vc,
-                                         lm->kv_stream_stride, c.max_seq, lm->max_splits, lm->part, lm->attn_count,
-                                         lm->act_o, ctx_slot, q_slot, s));
+            if (wo_fused)
+                STEP(launch_attention_wo_decode(lm->vdt, lm->qkv, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn, kn,
+                                                c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len,
+                                                kc, vc, c.max_seq, lm->max_splits, lm->part, lm->attn_count, lm->act_o,
+                                                L.wo.w, lm->h, lm->wo_ready + l, lm->wo_ready + (l + 1) % c.n_layers,
+                                                ctx_slot, q_slot, s));
+            else
+                STEP(launch_attention_decode(lm->vdt, lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn,
+                                             kn, c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len,
+                                             kc, vc, lm->kv_stream_stride, c.max_seq, lm->max_splits, lm->part,
+                                             lm->attn_count, lm->act_o, ctx_slot, q_slot, s));
         } else {
             STEP(launch_qk_rope_append(lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn, kn, c.norm_eps,
                                        c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len, lm->qbuf, kc, vc,
@@ -218,7 +236,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                                   c.max_seq, lm->kv_stream_stride, kAttnSplit, lm->max_splits, lm->part, lm->act_o,
                                   tr ? slot((size_t)n * lm->ctx) : nullptr, s));
         }
-        STEP(launch_gemv(L.wo.w, lm->act_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+        if (!wo_fused) STEP(launch_gemv(L.wo.w, lm->act_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
         if (tr) STEP(record(lm->h, nd));
         if (lm->swiglu && n == 1) {
             STEP(launch_swiglu_pair(L.w13.w, L.w2.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), lm->gu,
@@ -240,6 +258,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
     STEP(launch_argmax(lm->logits, n, c.vocab, lm->d_ids, lm->ids_per, lm->d_next, lm->d_len, lm->am_val, lm->am_idx,
                        lm->am_count, s));
 #undef STEP
+    lm->wo_dirty = false;
     return hipSuccess;
 }
 
@@ -572,6 +591,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->am_idx, sizeof(int) * MB * kArgmaxSlices);
     A((void**)&lm->am_count, sizeof(unsigned) * MB);
     A((void**)&lm->attn_count, sizeof(unsigned) * MB * c.n_kv_heads);
+    A((void**)&lm->wo_ready, sizeof(unsigned) * c.n_layers);
     if (e != hipSuccess) {
         destroy_lm(lm);
         return hip_fail(e, "lm_create: allocation");
@@ -606,12 +626,20 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     if (e == hipSuccess) e = hipMemset(lm->d_ids, 0, sizeof(int) * MB * lm->ids_per);
     if (e == hipSuccess) e = hipMemset(lm->am_count, 0, sizeof(unsigned) * MB);
     if (e == hipSuccess) e = hipMemset(lm->attn_count, 0, sizeof(unsigned) * MB * c.n_kv_heads);
+    if (e == hipSuccess) e = hipMemset(lm->wo_ready, 0, sizeof(unsigned) * c.n_layers);
     lm->attn_fused = getenv("SXQ_ATTN_UNFUSED") == nullptr && attn_decode_fits(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits);
     lm->swiglu = getenv("SXQ_SWIGLU_UNFUSED") == nullptr && swiglu_pair_fits(lm->layers[0].w13.w, lm->layers[0].w2.w);
     if (e == hipSuccess && lm->attn_fused &&
         attn_decode_prepare(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits) != hipSuccess) {
         (void)hipGetLastError();  // clear it: the three-kernel path needs no opt-in
         lm->attn_fused = false;
+    }
+    lm->wo_fused = lm->attn_fused && c.n_layers >= 2 && getenv("SXQ_ATTN_WO_UNFUSED") == nullptr &&
+                   attn_wo_decode_fits(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits, lm->layers[0].wo.w, c.dim);
+    if (e == hipSuccess && lm->wo_fused &&
+        attn_wo_decode_prepare(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits, lm->layers[0].wo.w) != hipSuccess) {
+        (void)hipGetLastError();
+        lm->wo_fused = false;
     }
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&lm->cap, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipDeviceSynchronize();

@@ -441,6 +441,37 @@ def test_swiglu_pair_equals_three_launches(cuda, monkeypatch, graph):
         np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("graph", [False, True])
+@pytest.mark.parametrize("kv", [33, 200])
+def test_attention_and_o_projection_in_one_launch_equals_two(cuda, monkeypatch, graph, kv):
+    """One decode row: attention with the O projection's workgroups in the same launch
+    (waiting on per-layer ready counters, which consecutive layers zero for each other)
+    gives the bits of the attention launch followed by the O-projection GEMV -- with one
+    attention split (kv 33) and with a merge of four (kv 200), over three layers and five
+    steps, so every counter is used, zeroed and reused."""
+    cfg = _fish_small(n_layers=3)
+    cfg.max_seq = 256
+    res = {}
+    for mode in ("one", "two"):
+        if mode == "two":
+            monkeypatch.setenv("SXQ_ATTN_WO_UNFUSED", "1")  # read when the engine is created
+        lm = D.DecoderLM(cfg, device=cuda)
+        lm.init_random(seed=51, std=0.02)
+        lm.kv_fill_random([kv], seed=52)
+        fr = _frames(np.random.default_rng(53), 1, cfg)
+        logits, _ = lm.step(ids=torch.from_numpy(fr), graph=graph)
+        outs = [logits.cpu().numpy()]
+        for _ in range(4):
+            _ = torch.zeros(1000, device=cuda).sum().item()  # eager work between replays
+            logits, _ = lm.step(n=1, graph=graph)
+            outs.append(logits.cpu().numpy())
+        assert lm.lengths(1) == [kv + 5]
+        res[mode] = outs
+    for a, b in zip(res["one"], res["two"]):
+        assert np.isfinite(a).all()
+        np.testing.assert_array_equal(a, b)
+
+
 def test_full_cache_is_an_error(cuda):
     cfg = _fish_small(n_layers=1)
     cfg.max_seq = 8
