@@ -204,11 +204,12 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
     const int G = GC > 0 ? GC : nh / nkv, gd = G * HD, T = gd / 4, nq = NT / T;
     const bool has_new = sp == nsp - 1;  // position pos is then row np - 1 of the tile
     const int slot = np - 1;
-    float* vt = smem;         // [P][HD]   value tile
-    float* qs = vt + P * HD;  // [G][HD]   queries after QK-norm + RoPE
-    float* knew = qs + gd;    // [HD]      the new key after QK-norm + RoPE
-    float* sc = knew + HD;    // [G][P]    scores, then exp(s - m)
-    float* red = sc + G * P;  // [nq][gd]  per-position-set weighted sums
+    float* vt = smem;            // [P][HD]   value tile
+    float* knew = vt + P * HD;   // [HD]      the new key after QK-norm + RoPE
+    float* sc = knew + HD;       // [G][P]    scores, then exp(s - m)
+    float* qs = sc + G * P;      // [G][HD]   queries after QK-norm + RoPE (read by the scores)
+    float* red = qs;             // [nq-1][gd] weighted sums of position sets 1.. (written after
+                                 //            the scores; set 0's stay in its threads' registers)
     const float* row = A.qkv + (int64_t)s * A.qkv_n;
     const float* cos_row = A.cos_t + (int64_t)pos * (HD / 2);
     const float* sin_row = A.sin_t + (int64_t)pos * (HD / 2);
@@ -315,6 +316,7 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
     // 5. weighted values: thread (set qi, head h, columns d..d+3) over the set's positions
     const int pps = (P + nq - 1) / nq;
     const int qi = tid / T, rr = tid - qi * T, h = rr / (HD / 4), d = 4 * (rr - h * (HD / 4));
+    float4 own = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // set 0: thread tid < T holds elements 4 tid..
     if (qi < nq) {
         const int pa = qi * pps, pb = min(pa + pps, np);
         const float* e = sc + h * P;
@@ -328,7 +330,8 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
             a.z += w * v.z;
             a.w += w * v.w;
         }
-        *(float4*)(red + qi * gd + h * HD + d) = a;
+        if (qi == 0) own = a;
+        else *(float4*)(red + (qi - 1) * gd + h * HD + d) = a;
     }
     lds_barrier();
     if (nsp == 1) {
@@ -336,9 +339,9 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
         // would give acc / l bit for bit -- without the hand-off.
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (tid < T) {
-            float4 a = *(const float4*)(red + 4 * tid);
+            float4 a = own;
             for (int q = 1; q < nq; ++q) {
-                const float4 b = *(const float4*)(red + q * gd + 4 * tid);
+                const float4 b = *(const float4*)(red + (q - 1) * gd + 4 * tid);
                 a.x += b.x;
                 a.y += b.y;
                 a.z += b.z;
@@ -351,9 +354,9 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
         return false;
     }
     if (tid < T) {
-        float4 a = *(const float4*)(red + 4 * tid);
+        float4 a = own;
         for (int q = 1; q < nq; ++q) {
-            const float4 b = *(const float4*)(red + q * gd + 4 * tid);
+            const float4 b = *(const float4*)(red + (q - 1) * gd + 4 * tid);
             a.x += b.x;
             a.y += b.y;
             a.z += b.z;

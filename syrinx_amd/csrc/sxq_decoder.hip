@@ -540,7 +540,7 @@ hipError_t launch_attention(int vdt, const float* q, const float* kc, const floa
 static size_t attn_decode_lds(int nh, int nkv, int hd, int max_splits) {
     const size_t G = nh / nkv, gd = G * hd, nq = kAttnThreads / (gd / 4), P = kAttnThreads / 8;
     const size_t nspf = (size_t)max_splits < (size_t)kMaxSplitsFused ? max_splits : kMaxSplitsFused;
-    const size_t partial = P * hd + gd + hd + G * P + nq * gd;
+    const size_t partial = P * hd + hd + G * P + (nq > 1 ? nq - 1 : 1) * gd;  // the queries share the sums' space
     const size_t merge = ((G * nspf + G + 3) & ~(size_t)3) + nq * gd;
     return sizeof(float) * (partial > merge ? partial : merge);
 }
