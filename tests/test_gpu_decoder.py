@@ -472,6 +472,28 @@ def test_attention_and_o_projection_in_one_launch_equals_two(cuda, monkeypatch, 
         np.testing.assert_array_equal(a, b)
 
 
+def test_graph_replayed_at_shorter_lengths_than_captured(cuda):
+    """A step captured at a long length and replayed after the lengths were cut (the
+    attention grid and every length-dependent choice were fixed at capture; the splits
+    past the new length now idle) gives the bits of an eager step at the new lengths."""
+    cfg = _fish_small(n_layers=2)
+    cfg.max_seq = 256
+    fr = _frames(np.random.default_rng(73), 1, cfg)
+    outs = []
+    for graph in (True, False):
+        lm = D.DecoderLM(cfg, device=cuda)
+        lm.init_random(seed=71, std=0.02)
+        lm.kv_fill_random([200], seed=72)
+        if graph:
+            lm.step(ids=torch.from_numpy(fr), graph=True)  # captured with four splits per head group
+        lm.set_lengths([40])
+        logits, _ = lm.step(ids=torch.from_numpy(fr), graph=graph)
+        outs.append(logits.cpu().numpy())
+        assert lm.lengths(1) == [41]
+    assert np.isfinite(outs[0]).all()
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
 def test_full_cache_is_an_error(cuda):
     cfg = _fish_small(n_layers=1)
     cfg.max_seq = 8
