@@ -318,7 +318,51 @@ def q8_0_gemv(torch, cpu, copies=64, reps=20):
             out[key] = cpu_entry(algo / t / 1e9, "GB/s", th,
                                  f"the same GEMV through the oracle's k_quants::matmul ({th} thread"
                                  f"{'s' if th > 1 else ''}), median of 20 after 3 warm-ups: {t * 1e6:.1f} us per call")
+    out["host_ptr_drop_in"] = host_ptr_drop_in(torch)
     return out
+
+
+def host_ptr_drop_in(torch, reps=20):
+    """The per-projection drop-in with host buffers (SXQ_HOST_PTRS: x and y copied through
+    pageable host memory, one synchronisation per call), PCIe-inclusive: the 169 QMatMul
+    calls of one CosyVoice2 (Qwen2-0.5B, 24 layers, Q8_0) decode token -- q, k, v, o,
+    gate, up, down per layer and the head -- from numpy buffers, median of `reps` tokens.
+    Only the projections: the glue stays on the caller's CPU in this integration."""
+    import numpy as np
+    from syrinx_amd import GgmlDType, QMatMul, QTensor
+    from syrinx_amd.quantized import qmatmul_host
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    dim, kvd, inter, vocab = 896, 128, 4864, 6564
+    shapes = [(dim, dim), (kvd, dim), (kvd, dim), (dim, dim), (inter, dim), (inter, dim), (dim, inter)]
+    layers = []
+    for _ in range(24):
+        layers.append([QMatMul.from_qtensor(QTensor.quantize(torch.randn(n, k, device=dev, generator=g) * 0.02,
+                                                             GgmlDType.Q8_0)) for n, k in shapes])
+    head = QMatMul.from_qtensor(QTensor.quantize(torch.randn(vocab, dim, device=dev, generator=g) * 0.02,
+                                                 GgmlDType.Q8_0))
+    rng = np.random.default_rng(5)
+    xs = {k: rng.standard_normal((1, k)).astype(np.float32) for k in (dim, inter)}
+
+    def token():
+        for mats in layers:
+            for q, (n, k) in zip(mats, shapes):
+                qmatmul_host(q, xs[k])
+        qmatmul_host(head, xs[dim])
+
+    for _ in range(3):
+        token()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        token()
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    calls = 24 * len(shapes) + 1
+    return {"workload": f"{calls} QMatMul.forward calls of one CosyVoice2 Q8_0 decode token (24 layers x q,k,v,o,"
+                        "gate,up,down + head) with host (numpy) x and y via SXQ_HOST_PTRS, median of "
+                        f"{reps} tokens", "us_per_token": round(t * 1e6, 1), "us_per_call": round(t * 1e6 / calls, 2),
+            "tok_s_projection_share": round(1.0 / t, 1)}
 
 
 def prefill_gemms(torch, tokens, iters, cpu=False):
