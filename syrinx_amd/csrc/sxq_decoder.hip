@@ -632,7 +632,7 @@ struct WoArgs {
     unsigned* ready_next;
     unsigned need;  // slices in the context row (n_kv)
 };
-constexpr int kWoTm = 2;  // task rounds of a projection tile: R * nb <= kWoTm * 64
+constexpr int kWoTm = 1;  // task rounds of a projection tile: R * nb <= kWoTm * 128
 constexpr int kWoPollCap = 1 << 22;
 
 template <int HD, int GC>
@@ -649,7 +649,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6,
     uint4* lds = (uint4*)smem4;
     const int tid = threadIdx.x, t = id - W.n_attn;
     const int nb = W.nb, row0 = t * W.R, rows = min(W.R, W.n - row0), tasks = rows * nb;
-    uint4 q[TM], h[TM];
+    uint4 q[TM][kQ4kCpl], h[TM];
     q4k_tile_load<NT, TM>(W.hdr, W.qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
     const int r = tid >> 3, l = tid & 7;
     const float res = W.y[row0 + min(r, rows - 1)];  // clamped, unconditional; used by lane class 0 of rows < rows
@@ -693,7 +693,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6,
     if (r < rows && l == 0) W.y[row0 + r] = ok ? res + v : __builtin_nanf("");
 }
 
-static int wo_rows(int nb) { return max(1, min(kAttnThreads / 8, kWoTm * (kAttnThreads / 8) / nb)); }
+static int wo_rows(int nb) { return max(1, min(kAttnThreads / 8, kWoTm * (kAttnThreads / kQ4kLanes) / nb)); }
 static size_t wo_pub_off(int nh, int nkv, int hd, int max_splits) {
     return (attn_decode_lds(nh, nkv, hd, max_splits) + 15) & ~(size_t)15;
 }
@@ -711,7 +711,7 @@ static const void* attn_wo_kernel(int hd, int G) {
 
 bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo, int dim) {
     return vdt == kQ8K && wo.dtype == kQ4K && attn_decode_fits(vdt, nh, nkv, hd, max_splits) && wo.k == (int64_t)nh * hd &&
-           wo.n == dim && wo.nb >= 1 && wo.nb <= kWoTm * (kAttnThreads / 8) &&
+           wo.n == dim && wo.nb >= 1 && wo.nb <= kWoTm * (kAttnThreads / kQ4kLanes) &&
            attn_wo_lds(nh, nkv, hd, max_splits, (int)wo.nb) <= 160 * 1024;
 }
 

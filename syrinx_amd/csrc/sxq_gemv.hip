@@ -202,7 +202,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_q80(const uint16_t* __restr
 
 // ---------------------------------------------------------------------------------
 // Task-split GEMV (m = 1..4).  A 256-thread workgroup owns R consecutive rows; their
-// R*nb (row, block) tasks are dealt round-robin to 32 eight-lane groups (Q4_K), 128
+// R*nb (row, block) tasks are dealt round-robin to 256/kQ4kLanes lane groups (Q4_K), 128
 // lane pairs (Q8_0) or 256 lanes (Q4_0), at most TMAX tasks each.  Every group first
 // issues the weight loads of all its tasks (clamped, unconditional), then the
 // activation loads into LDS, so a wave has up to 2*TMAX 16-byte loads in flight and
@@ -238,7 +238,7 @@ SXQ_DEV void act_store(const uint4 (&v)[KP], uint4* lds, const uint8_t* __restri
     for (int i = KP * NT + threadIdx.x; i < total_u4; i += NT) lds[i] = ((const uint4*)act)[i];
 }
 
-// Q4_K task-split GEMV, NT threads (256 or 1024) per workgroup: NT/8 eight-lane groups,
+// Q4_K task-split GEMV, NT threads (256 or 1024) per workgroup: NT/kQ4kLanes lane groups,
 // TM rounds of tasks (the launch's tiles need no more; a round that held no task would
 // still issue its loads, and the epilogue would wait for them before reusing their
 // registers).
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
                                                   int64_t ldy, const float* __restrict__ bias, const float* res,
                                                   int64_t ldr, NormIn ni) {
     static_assert(!NORM || (NT == 1024 && MMAX == 1), "the fused RMSNorm prologue is for one row, 1024 threads");
-    constexpr int SLOTS = NT / 8;  // eight-lane groups = tasks per round
+    constexpr int SLOTS = NT / kQ4kLanes;  // lane groups = tasks per round
     extern __shared__ uint4 lds[];
     const ActQ8K* la = (const ActQ8K*)lds;
     const int row0 = blockIdx.x * R;
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q4k(const uint4* __restrict__ hdr,
     float4 xv, wv;
     if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 256);
     else act_fetch<NT, MMAX>(av, act, act_u4);
-    uint4 q[TM], h[TM];
+    uint4 q[TM][kQ4kCpl], h[TM];
     q4k_tile_load<NT, TM>(hdr, qs, blk0, tasks, q, h);
     if constexpr (NORM) {
         __shared__ float red[16];
@@ -301,7 +301,7 @@ template <int TM>
 __global__ __launch_bounds__(1024) void k_gemv2_q4k_swiglu(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
                                                            int I, int nb, int B, NormIn ni, float* __restrict__ gu,
                                                            float* __restrict__ act_f32) {
-    constexpr int NT = 1024, SLOTS = NT / 8;
+    constexpr int NT = 1024;
     extern __shared__ uint4 lds[];
     __shared__ float sw[NT / 8];  // the tile's row results: gate [0, Bt), up [Bt, 2Bt)
     __shared__ float red[16];
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_swiglu(const uint4* __restri
     float* pr = (float*)(lds + (size_t)nb * (sizeof(ActQ8K) / 16));  // product chains [2B + 1][9][CS]
     float4 xv, wv;
     norm_fetch(xv, wv, ni, nb * 256);
-    uint4 q[TM], h[TM];
+    uint4 q[TM][kQ4kCpl], h[TM];
     q4k_tile_load2<NT, TM>(hdr, qs, (uint32_t)g0 * (uint32_t)nb, (uint32_t)(I + g0) * (uint32_t)nb, seg, tasks, q, h);
     norm_quant_store<kQ8K>(xv, wv, ni, nb * 256, (uint8_t*)lds, red);
     lds_barrier();
@@ -334,7 +334,7 @@ template <int TM>
 __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
                                                           int n, int nb, int R, const float* __restrict__ x,
                                                           float* y, const float* res) {
-    constexpr int NT = 1024, SLOTS = NT / 8, J = 3;
+    constexpr int NT = 1024, J = 3;
     extern __shared__ uint4 lds[];
     ActQ8K* la = (ActQ8K*)lds;
     const int row0 = blockIdx.x * R, rows = min(R, n - row0), tasks = rows * nb;
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restric
         v[j] = ld_global((const float4*)(opaque_ptr(x) + cc * 256 + 4 * lane));
     }
     issue_point();
-    uint4 q[TM], h[TM];
+    uint4 q[TM][kQ4kCpl], h[TM];
     q4k_tile_load<NT, TM>(hdr, qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
     // Called by every wave (a wave past the last chunk writes nothing): under a branch the
     // compiler would sink the loads above into it, behind the weight loads.
@@ -467,7 +467,11 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
 // every lane group holds at most kTmax tasks, the epilogue has a thread per (row, lane
 // class), and LDS fits the workgroup's share of a CU's 160 KB: 60 KB for 256 threads,
 // 144 KB for 1024 (one workgroup per CU).
-static int tasks_per_round(int dtype, int nt) { return dtype == kQ4K ? nt / 8 : (dtype == kQ8_0 ? nt / 2 : nt); }
+static int tasks_per_round(int dtype, int nt) { return dtype == kQ4K ? nt / kQ4kLanes : (dtype == kQ8_0 ? nt / 2 : nt); }
+// Q4_K rounds of a 1024-thread workgroup: at most 7 (eight rounds of 12 weight registers
+// would not fit the 128 VGPRs of 1024 threads); kTmax elsewhere.
+constexpr int kTmaxQ4k1024 = 7;
+static int round_cap(int dtype, int nt) { return dtype == kQ4K && nt == 1024 ? kTmaxQ4k1024 : kTmax; }
 
 size_t gemv2_lds(int nb, int m, int R, int dtype, int nt) {
     const size_t ab = act_block_bytes(vec_dot_type(dtype));
@@ -487,7 +491,7 @@ int gemv2_rows(int n, int nb, int m, int dtype, int nt) {
     const int target_wg = env_wg > 0 ? env_wg : (nt == 1024 ? 256 : 1024);
     int R = (n + target_wg - 1) / target_wg;
     R = min(R, nt / 8);
-    R = min(R, max(1, tasks_per_round(dtype, nt) * kTmax / nb));
+    R = min(R, max(1, tasks_per_round(dtype, nt) * round_cap(dtype, nt) / nb));
     while (R > 1 && gemv2_lds(nb, m, R, dtype, nt) > gemv2_lds_cap(nt)) --R;
     return max(R, 1);
 }
@@ -497,7 +501,8 @@ int gemv2_rows(int n, int nb, int m, int dtype, int nt) {
 // no more workgroups than the one-per-CU target (otherwise the 256-thread kernel is the
 // better fit; with more rows the larger LDS share wins at any workgroup count).
 bool gemv2_fits(int n, int nb, int m, int dtype, int nt) {
-    if (nb > tasks_per_round(dtype, nt) * kTmax || gemv2_lds(nb, m, 1, dtype, nt) > gemv2_lds_cap(nt)) return false;
+    if (nb > tasks_per_round(dtype, nt) * round_cap(dtype, nt) || gemv2_lds(nb, m, 1, dtype, nt) > gemv2_lds_cap(nt))
+        return false;
     if (nt == 256 || m > 1) return true;
     const int R = gemv2_rows(n, nb, m, dtype, nt);
     return (n + R - 1) / R <= 256;
@@ -560,8 +565,13 @@ static hipError_t gemv2_launch(const QWeight& w, const void* act, int m, float* 
     const hipError_t e = with_rounds(rounds, [&](auto tmc) -> hipError_t {
         constexpr int TM = decltype(tmc)::value;
         if (w.dtype == kQ4K) {
-            if (const hipError_t e_ = allow_lds<k_gemv2_q4k<MMAX, NORM, NT, TM>>(lds); e_ != hipSuccess) return e_;
-            hipLaunchKernelGGL((k_gemv2_q4k<MMAX, NORM, NT, TM>), grid, block, lds, s, (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+            if constexpr (NT == 1024 && TM > kTmaxQ4k1024) {
+                return hipErrorInvalidValue;  // (gemv2_rows never asks for it)
+            } else {
+                if (const hipError_t e_ = allow_lds<k_gemv2_q4k<MMAX, NORM, NT, TM>>(lds); e_ != hipSuccess) return e_;
+                hipLaunchKernelGGL((k_gemv2_q4k<MMAX, NORM, NT, TM>), grid, block, lds, s, (const uint4*)w.hdr,
+                                   (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+            }
         } else if (w.dtype == kQ8_0) {
             if (const hipError_t e_ = allow_lds<k_gemv2_q80<MMAX, false, NORM, NT, TM>>(lds); e_ != hipSuccess) return e_;
             hipLaunchKernelGGL((k_gemv2_q80<MMAX, false, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
@@ -876,11 +886,11 @@ hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64
 }
 
 // SwiGLU pair sizing: B gate rows per tile so that the tiles spread over one
-// workgroup per CU, within the tile limits (2B rows <= NT/8, 2B*nb tasks <= kTmax rounds).
+// workgroup per CU, within the tile limits (2B rows <= NT/8, 2B*nb tasks <= kTmaxQ4k1024 rounds).
 static int swiglu_rows(int I, int nb) {
     int B = (I + 255) / 256;
     B = min(B, 1024 / 16);
-    B = min(B, max(1, (1024 / 8) * kTmax / (2 * nb)));
+    B = min(B, max(1, (1024 / kQ4kLanes) * kTmaxQ4k1024 / (2 * nb)));
     return max(B, 1);
 }
 
@@ -889,7 +899,7 @@ bool swiglu_pair_fits(const QWeight& gate_up, const QWeight& down) {
     return gate_up.dtype == kQ4K && down.dtype == kQ4K && gate_up.n == 2 * (int64_t)I && down.k == I &&
            gate_up.k <= kNormMaxDim && I % 256 == 0 && I / 256 <= 48 &&
            gemv2_fits((int)down.n, (int)down.nb, 1, kQ4K, 1024) &&
-           2 * swiglu_rows(I, nb) * nb <= (1024 / 8) * kTmax;
+           2 * swiglu_rows(I, nb) * nb <= (1024 / kQ4kLanes) * kTmaxQ4k1024;
 }
 
 hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const NormIn& ni, float* gu, float* act_f32,
@@ -898,20 +908,31 @@ hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const
     const int I = (int)(gate_up.n / 2), nb = (int)gate_up.nb;
     const int B = swiglu_rows(I, nb);
     const size_t lds1 = gemv2_lds(nb, 1, 2 * B, kQ4K, 1024);
-    hipError_t e = with_rounds((2 * B * nb + 127) / 128, [&](auto tmc) -> hipError_t {
-        hipLaunchKernelGGL(k_gemv2_q4k_swiglu<decltype(tmc)::value>, dim3((I + B - 1) / B), dim3(1024), lds1, s,
-                           (const uint4*)gate_up.hdr, (const uint4*)gate_up.qs, I, nb, B, ni, gu, act_f32);
-        return hipSuccess;
+    const int tpr = tasks_per_round(kQ4K, 1024);
+    hipError_t e = with_rounds((2 * B * nb + tpr - 1) / tpr, [&](auto tmc) -> hipError_t {
+        constexpr int TM = decltype(tmc)::value;
+        if constexpr (TM > kTmaxQ4k1024) {
+            return hipErrorInvalidValue;  // (swiglu_rows never asks for it)
+        } else {
+            hipLaunchKernelGGL(k_gemv2_q4k_swiglu<TM>, dim3((I + B - 1) / B), dim3(1024), lds1, s,
+                               (const uint4*)gate_up.hdr, (const uint4*)gate_up.qs, I, nb, B, ni, gu, act_f32);
+            return hipSuccess;
+        }
     });
     if (e == hipSuccess) e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int n = (int)down.n, nb2 = (int)down.nb;
     const int R = gemv2_rows(n, nb2, 1, kQ4K, 1024);
     const size_t lds2 = gemv2_lds(nb2, 1, R, kQ4K, 1024);
-    e = with_rounds((R * nb2 + 127) / 128, [&](auto tmc) -> hipError_t {
-        hipLaunchKernelGGL(k_gemv2_q4k_quant<decltype(tmc)::value>, dim3((n + R - 1) / R), dim3(1024), lds2, s,
-                           (const uint4*)down.hdr, (const uint4*)down.qs, n, nb2, R, act_f32, y, res);
-        return hipSuccess;
+    e = with_rounds((R * nb2 + tpr - 1) / tpr, [&](auto tmc) -> hipError_t {
+        constexpr int TM = decltype(tmc)::value;
+        if constexpr (TM > kTmaxQ4k1024) {
+            return hipErrorInvalidValue;  // (gemv2_rows never asks for it)
+        } else {
+            hipLaunchKernelGGL(k_gemv2_q4k_quant<TM>, dim3((n + R - 1) / R), dim3(1024), lds2, s,
+                               (const uint4*)down.hdr, (const uint4*)down.qs, n, nb2, R, act_f32, y, res);
+            return hipSuccess;
+        }
     });
     if (e != hipSuccess) return e;
     return hipGetLastError();

@@ -3,10 +3,11 @@
 // The results are Candle's vec-dot bit for bit.
 //
 // A tile is `rows` consecutive weight rows starting at block index blk0 (row-major,
-// nb blocks per row); its rows*nb (row, block) tasks are dealt round-robin to the NT/8
-// eight-lane groups of the workgroup, at most kTmax tasks each.  Lane l of a group
-// loads the 16 bytes holding class l (elements = l mod 8) of a block's four 32-byte
-// chunks (the device layout of sxq_common.h) and produces Candle's aux32[l] directly.
+// nb blocks per row); its rows*nb (row, block) tasks are dealt round-robin to the
+// NT/kQ4kLanes lane groups of the workgroup, at most kTmax tasks each.  Lane c of a group
+// loads the 16 kQ4kCpl bytes holding classes kQ4kCpl c .. (elements = l mod 8) of a
+// block's four 32-byte chunks (the device layout of sxq_common.h: class l's 16 bytes at
+// 16 l) and produces Candle's aux32[l] for them directly.
 #pragma once
 #include "sxq_kernels.h"
 #include "sxq_quant_dev.h"
@@ -15,7 +16,9 @@
 namespace sxq {
 
 constexpr int kTmax = 8;
-
+constexpr int kQ4kLanes = 4;            // lanes per (row, block) task
+constexpr int kQ4kCpl = 8 / kQ4kLanes;  // classes per lane
+static_assert(kQ4kLanes == 2 || kQ4kLanes == 4 || kQ4kLanes == 8, "a task's lanes share a DPP row");
 SXQ_DEV float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
 
 // The integer part of a Q4_K task, aux32[l] = sum_j sc_j * dot_j over the eight
@@ -56,15 +59,16 @@ SXQ_DEV int q4k_aux(const int (&w)[8], const int (&a)[8], int slo, int shi) {
 // must have at most TM * NT/8 tasks).
 template <int NT, int TM = kTmax>
 SXQ_DEV void q4k_tile_load(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, uint32_t blk0, int tasks,
-                           uint4 (&q)[TM], uint4 (&h)[TM]) {
-    constexpr int SLOTS = NT / 8;
-    const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
-    const char* qbase = (const char*)opaque_ptr(qs) + (l << 4);
+                           uint4 (&q)[TM][kQ4kCpl], uint4 (&h)[TM]) {
+    constexpr int SLOTS = NT / kQ4kLanes;
+    const int c = threadIdx.x % kQ4kLanes, grp = threadIdx.x / kQ4kLanes;
+    const char* qbase = (const char*)opaque_ptr(qs) + c * 16 * kQ4kCpl;
     const char* hbase = (const char*)opaque_ptr(hdr);
 #pragma unroll
     for (int u = 0; u < TM; ++u) {
         const uint32_t blk = blk0 + (uint32_t)min(u * SLOTS + grp, tasks - 1);
-        q[u] = ld_global((const uint4*)(qbase + (blk << 7)));
+#pragma unroll
+        for (int k = 0; k < kQ4kCpl; ++k) q[u][k] = ld_global((const uint4*)(qbase + (blk << 7) + 16 * k));
         h[u] = ld_global((const uint4*)(hbase + (blk << 4)));
     }
     // The weight loads are all issued here: a prologue's arithmetic on its own (earlier)
@@ -77,16 +81,17 @@ SXQ_DEV void q4k_tile_load(const uint4* __restrict__ hdr, const uint4* __restric
 // so a task's block index within its row is still t mod nb).
 template <int NT, int TM = kTmax>
 SXQ_DEV void q4k_tile_load2(const uint4* __restrict__ hdr, const uint4* __restrict__ qs, uint32_t blkA, uint32_t blkB,
-                            int seg, int tasks, uint4 (&q)[TM], uint4 (&h)[TM]) {
-    constexpr int SLOTS = NT / 8;
-    const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
-    const char* qbase = (const char*)opaque_ptr(qs) + (l << 4);
+                            int seg, int tasks, uint4 (&q)[TM][kQ4kCpl], uint4 (&h)[TM]) {
+    constexpr int SLOTS = NT / kQ4kLanes;
+    const int c = threadIdx.x % kQ4kLanes, grp = threadIdx.x / kQ4kLanes;
+    const char* qbase = (const char*)opaque_ptr(qs) + c * 16 * kQ4kCpl;
     const char* hbase = (const char*)opaque_ptr(hdr);
 #pragma unroll
     for (int u = 0; u < TM; ++u) {
         const int t = min(u * SLOTS + grp, tasks - 1);
         const uint32_t blk = t < seg ? blkA + (uint32_t)t : blkB + (uint32_t)(t - seg);
-        q[u] = ld_global((const uint4*)(qbase + (blk << 7)));
+#pragma unroll
+        for (int k = 0; k < kQ4kCpl; ++k) q[u][k] = ld_global((const uint4*)(qbase + (blk << 7) + 16 * k));
         h[u] = ld_global((const uint4*)(hbase + (blk << 4)));
     }
     issue_point();  // as in q4k_tile_load
@@ -104,15 +109,17 @@ SXQ_HD int q4k_chain_stride(int nb) {
     return 4 * (q | 1);
 }
 
-// Per-task float products into the chains: the eight lane terms (d_w*d_a)*(f32)aux32[l]
-// and the min term (dmin_w*d_a)*(f32)sumi of Candle's Q4_K vec-dot, against the LDS
-// activation blocks la [m][nb].  Task t is tile row t / nb, block t % nb; tasks past the
-// end (last round) compute on clamped loads and write into the spare row.
+// Per-task float products into the chains: the eight class terms (d_w*d_a)*(f32)aux32[l]
+// (lane c: classes CPL c .. CPL c + CPL - 1) and the min term (dmin_w*d_a)*(f32)sumi of
+// Candle's Q4_K vec-dot, against the LDS activation blocks la [m][nb].  sumi = sum_j
+// m_j * bsum_j over the eight sub-blocks is an integer (exact in any order): lane c adds
+// sub-blocks CPL c .. CPL c + CPL - 1, the task's lanes' parts meet by DPP.  Task t is tile row t / nb, block t % nb;
+// tasks past the end (last round) compute on clamped loads and write into the spare row.
 template <int MMAX, int NT, int TM = kTmax>
-SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const ActQ8K* la, int nb, int m,
+SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM][kQ4kCpl], const uint4 (&h)[TM], const ActQ8K* la, int nb, int m,
                                int rows, int RC, float* pr) {
-    constexpr int SLOTS = NT / 8;
-    const int l = threadIdx.x & 7, grp = threadIdx.x >> 3;
+    constexpr int SLOTS = NT / kQ4kLanes, CPL = kQ4kCpl;
+    const int c = threadIdx.x % kQ4kLanes, grp = threadIdx.x / kQ4kLanes;
     const int CS = q4k_chain_stride(nb), tasks = rows * nb;
     // Tile row and block of task u*SLOTS + grp, stepped by SLOTS each round.
     const uint32_t bstep = (uint32_t)SLOTS % (uint32_t)nb, rstep = (uint32_t)SLOTS / (uint32_t)nb;
@@ -124,11 +131,26 @@ SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const
         const uint32_t sc_hi = (h[u].w & 0x0F0F0F0Fu) | (((h[u].y >> 6) & 0x03030303u) << 4);
         const uint32_t mn_lo = h[u].z & 0x3F3F3F3Fu;
         const uint32_t mn_hi = ((h[u].w >> 4) & 0x0F0F0F0Fu) | (((h[u].z >> 6) & 0x03030303u) << 4);
-        const int ml = (int)(((l < 4 ? mn_lo : mn_hi) >> (8 * (l & 3))) & 0xFF);
-        const int w4[8] = {(int)(q[u].x & 0x0F0F0F0Fu), (int)((q[u].x >> 4) & 0x0F0F0F0Fu),
-                           (int)(q[u].y & 0x0F0F0F0Fu), (int)((q[u].y >> 4) & 0x0F0F0F0Fu),
-                           (int)(q[u].z & 0x0F0F0F0Fu), (int)((q[u].z >> 4) & 0x0F0F0F0Fu),
-                           (int)(q[u].w & 0x0F0F0F0Fu), (int)((q[u].w >> 4) & 0x0F0F0F0Fu)};
+        // the mins of this lane's sub-blocks j = CPL c + k: byte j of mn_lo (j < 4), j - 4 of mn_hi
+        int mk[CPL];
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const int j = CPL * c + k;
+            mk[k] = (int)(((j < 4 ? mn_lo : mn_hi) >> (8 * (j & 3))) & 0xFF);
+        }
+        int w4[CPL][8];
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const uint4 qq = q[u][k];
+            w4[k][0] = (int)(qq.x & 0x0F0F0F0Fu);
+            w4[k][1] = (int)((qq.x >> 4) & 0x0F0F0F0Fu);
+            w4[k][2] = (int)(qq.y & 0x0F0F0F0Fu);
+            w4[k][3] = (int)((qq.y >> 4) & 0x0F0F0F0Fu);
+            w4[k][4] = (int)(qq.z & 0x0F0F0F0Fu);
+            w4[k][5] = (int)((qq.z >> 4) & 0x0F0F0F0Fu);
+            w4[k][6] = (int)(qq.w & 0x0F0F0F0Fu);
+            w4[k][7] = (int)((qq.w >> 4) & 0x0F0F0F0Fu);
+        }
         const int slo = (int)sc_lo, shi = (int)sc_hi;  // scale of sub-block j: byte j of slo, j - 4 of shi
         const float dw = h2f(h[u].x & 0xFFFF), dminw = h2f(h[u].x >> 16);
         const bool live = row < (uint32_t)rows;
@@ -136,17 +158,27 @@ SXQ_DEV void q4k_tile_products(const uint4 (&q)[TM], const uint4 (&h)[TM], const
         for (int r = 0; r < MMAX; ++r) {
             if (r < m) {
                 const ActQ8K& a = la[r * nb + (int)b];
-                const uint4 A0 = ((const uint4*)a.qs)[2 * l];
-                const uint4 A1 = ((const uint4*)a.qs)[2 * l + 1];
-                const int Aj[8] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w,
-                                   (int)A1.x, (int)A1.y, (int)A1.z, (int)A1.w};
-                const int aux = q4k_aux(w4, Aj, slo, shi);
-                const int sumi = sum8_i32(__mul24(ml, a.bs2[l]));
-                const float ad = a.d;
                 // a task past the end writes into the spare row RC (never folded)
                 float* p = pr + ((r * (RC + 1) + (live ? (int)row : RC)) * 9) * CS + (int)b;
-                p[l * CS] = (dw * ad) * (float)aux;
-                if (l == 0) p[8 * CS] = (dminw * ad) * (float)sumi;  // the same in all eight lanes
+                const float ad = a.d;
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) {
+                    const int l = CPL * c + k;
+                    const uint4 A0 = ((const uint4*)a.qs)[2 * l];
+                    const uint4 A1 = ((const uint4*)a.qs)[2 * l + 1];
+                    const int Aj[8] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w,
+                                       (int)A1.x, (int)A1.y, (int)A1.z, (int)A1.w};
+                    const int aux = q4k_aux(w4[k], Aj, slo, shi);
+                    p[l * CS] = (dw * ad) * (float)aux;
+                }
+                int sumi = 0;
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) sumi += __mul24(mk[k], a.bs2[CPL * c + k]);
+                // the task's lanes (adjacent, within one DPP row)
+                if constexpr (kQ4kLanes >= 2) sumi += dpp_i32<0xB1>(sumi);
+                if constexpr (kQ4kLanes >= 4) sumi += dpp_i32<0x4E>(sumi);
+                if constexpr (kQ4kLanes >= 8) sumi += dpp_i32<0x141>(sumi);
+                if (c == 0) p[8 * CS] = (dminw * ad) * (float)sumi;
             }
         }
         b += bstep;
