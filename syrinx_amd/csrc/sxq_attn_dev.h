@@ -128,7 +128,8 @@ SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, f
     }
     if (tid < ((T + 63) & ~63)) {
         if (VDT == kQ8K)
-            wave_quantize_q8k<false>(v, lane, qdst + (size_t)wave * sizeof(ActQ8K));
+            wave_quantize_q8k<false>(v, lane, qdst + (size_t)wave * sizeof(ActQ8K), A.rec ? A.rec + blk_first + wave : nullptr,
+                                     s);
         else
             wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < gd / 32, qdst + (size_t)wave * 8 * sizeof(ActQ8_0));
     }

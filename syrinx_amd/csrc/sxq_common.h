@@ -83,6 +83,21 @@ static_assert(sizeof(ActQ8_0) == 48, "ActQ8_0 is 48 bytes");
 
 SXQ_HD size_t act_block_bytes(int vdt) { return vdt == kQ8K ? sizeof(ActQ8K) : sizeof(ActQ8_0); }
 
+// The same Q8_K activations of up to 16 rows, one record per 256-element block column,
+// laid out as the operands of the Q4_K matrix-core GEMV (v_mfma_f32_16x16x32_f16, the
+// activation rows as its 16 rows), written by the quantizers next to the ActQ8K rows:
+//   q  : q[l][r][g][s] = the f16 value of the q8 at qs[32 l + 8 g + {0,2,1,3,4,6,5,7}[s]]
+//        of row r (class l, lane group g: the eight k-slots lane (r, g) feeds)
+//   d  : d[r], the rows' scales
+//   bs : bs[h][r][g] = (float) bs2[g + 4 h] of row r
+// Rows a step does not have are never written and never read into a stored result.
+struct MmaRec {
+    _Float16 q[8][16][4][8];
+    float d[16];
+    float bs[2][16][4];
+};
+static_assert(sizeof(MmaRec) == 8768, "MmaRec is 8768 bytes");
+
 // Weight device layouts (repacked once at QMatMul creation; same total bytes as the
 // canonical blocks):
 //   Q4_K: hdr[n*nb] 16 B (d, dmin, scales[12], unchanged) + qs[n*nb] 128 B where

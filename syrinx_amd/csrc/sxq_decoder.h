@@ -4,8 +4,9 @@
 
 namespace sxq {
 
+// rec (optional, Q8_K, rows <= 16): also fill the rows' MmaRec records [dim / 256].
 hipError_t launch_rmsnorm_quant(int vdt, const float* h, int rows, int dim, const float* w, float eps, uint8_t* act,
-                                float* normed, hipStream_t s);
+                                float* normed, hipStream_t s, MmaRec* rec = nullptr);
 hipError_t launch_qk_rope_append(const float* qkv, int B, int qkv_n, int nh, int nkv, int hd, const float* qn,
                                  const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
                                  const int* len, float* qout, float* kc, float* vc, int64_t kv_stream_stride,
@@ -35,8 +36,9 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
                                    const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
                                    const int* len, float* kc, float* vc, int64_t kv_stream_stride, int max_seq,
                                    int max_splits, float* part, unsigned* counter, uint8_t* act, float* ctx_out,
-                                   float* q_out, hipStream_t s);
-hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s);
+                                   float* q_out, hipStream_t s, MmaRec* rec = nullptr);
+hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s,
+                                 MmaRec* rec = nullptr);
 hipError_t launch_embed_quant_table(const int* ids, int ids_per, int B, const QWeight& w, int dim, const float* cb,
                                     int n_cb, int cb_size, int sem_begin, int sem_end, float* h, hipStream_t s);
 hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
@@ -96,6 +98,7 @@ struct AttnArgs {
     float *ctx_out, *q_out;  // optional f32 copies of the context and the roped queries
     unsigned* ready;         // k_attn_wo_decode: context slices published so far
     uint32_t pub_off;        // k_attn_wo_decode: LDS byte offset of the slice staging
+    MmaRec* rec;             // optional (Q8_K, B <= 16): the context rows' MmaRec records too
 };
 
 // Batch-1 decode attention and the O projection (Q4_K, y += ctx . Wo^T in place) as one

@@ -52,7 +52,7 @@ SXQ_DEV void quantize_chunk(const float* vals, int c, int dim, int lane, uint8_t
 template <int VDT>
 __global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float* __restrict__ h, int dim, const float* __restrict__ w,
                                                         float inv_n, float eps, uint8_t* __restrict__ act,
-                                                        float* __restrict__ normed) {
+                                                        float* __restrict__ normed, MmaRec* __restrict__ rec) {
     __shared__ float red[16];
     const int row = blockIdx.x, c = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float* x = h + (int64_t)row * dim;
@@ -80,7 +80,7 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_quant(const float* __restrict_
     }
     const int nb = VDT == kQ8K ? dim / 256 : dim / 32;
     uint8_t* arow = act + (int64_t)row * nb * act_block_bytes(VDT);
-    if (VDT == kQ8K) wave_quantize_q8k<false>(v, lane, arow + (size_t)c * sizeof(ActQ8K));
+    if (VDT == kQ8K) wave_quantize_q8k<false>(v, lane, arow + (size_t)c * sizeof(ActQ8K), rec ? rec + c : nullptr, row);
     else wave_quantize_q8_0<false>(v, lane, c * 8 + (lane >> 3) < nb, arow + (size_t)c * 8 * sizeof(ActQ8_0));
 }
 
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(256) void k_attn_combine_quant(const float* __restr
 // gu row = [gate (I) | up (I)]; a = silu(g) * u with silu(g) = g / (1 + exp(-g)).
 template <int VDT>
 __global__ __launch_bounds__(64) void k_silu_mul_quant(const float* __restrict__ gu, int I, uint8_t* __restrict__ act,
-                                                       float* __restrict__ act_f32) {
+                                                       float* __restrict__ act_f32, MmaRec* __restrict__ rec) {
     const int s = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
     const float* g = gu + (int64_t)s * 2 * I;
     const float* u = g + I;
@@ -358,7 +358,7 @@ __global__ __launch_bounds__(64) void k_silu_mul_quant(const float* __restrict__
     const float4 v = make_float4(a[0], a[1], a[2], a[3]);
     const int nb = VDT == kQ8K ? I / 256 : I / 32;
     uint8_t* arow = act + (int64_t)s * nb * act_block_bytes(VDT);
-    if (VDT == kQ8K) wave_quantize_q8k<false>(v, lane, arow + (size_t)c * sizeof(ActQ8K));
+    if (VDT == kQ8K) wave_quantize_q8k<false>(v, lane, arow + (size_t)c * sizeof(ActQ8K), rec ? rec + c : nullptr, s);
     else wave_quantize_q8_0<false>(v, lane, c * 8 + (lane >> 3) < nb, arow + (size_t)c * 8 * sizeof(ActQ8_0));
 }
 
@@ -497,11 +497,14 @@ __global__ void k_fill_int(int* __restrict__ y, int n, int v) {
 
 // ------------------------------------------------------------------------ launchers
 hipError_t launch_rmsnorm_quant(int vdt, const float* h, int rows, int dim, const float* w, float eps, uint8_t* act,
-                                float* normed, hipStream_t s) {
+                                float* normed, hipStream_t s, MmaRec* rec) {
+    if (rec && (vdt != kQ8K || rows > 16)) return hipErrorInvalidValue;
     const float inv_n = (float)(1.0 / (double)dim);
     const dim3 grid(rows, (dim + 255) / 256);
-    if (vdt == kQ8K) hipLaunchKernelGGL((k_rmsnorm_quant<kQ8K>), grid, dim3(1024), 0, s, h, dim, w, inv_n, eps, act, normed);
-    else hipLaunchKernelGGL((k_rmsnorm_quant<kQ8_0>), grid, dim3(1024), 0, s, h, dim, w, inv_n, eps, act, normed);
+    if (vdt == kQ8K)
+        hipLaunchKernelGGL((k_rmsnorm_quant<kQ8K>), grid, dim3(1024), 0, s, h, dim, w, inv_n, eps, act, normed, rec);
+    else
+        hipLaunchKernelGGL((k_rmsnorm_quant<kQ8_0>), grid, dim3(1024), 0, s, h, dim, w, inv_n, eps, act, normed, rec);
     return hipGetLastError();
 }
 
@@ -576,9 +579,10 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
                                    const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
                                    const int* len, float* kc, float* vc, int64_t kv_stream_stride, int max_seq,
                                    int max_splits, float* part, unsigned* counter, uint8_t* act, float* ctx_out,
-                                   float* q_out, hipStream_t s) {
+                                   float* q_out, hipStream_t s, MmaRec* rec) {
     if (!attn_decode_fits(vdt, nh, nkv, hd, max_splits) || max_seq > kMaxSplitsFused * kAttnSplitFused)
         return hipErrorInvalidValue;
+    if (rec && (vdt != kQ8K || B > 16)) return hipErrorInvalidValue;
     AttnArgs A;
     A.qkv = qkv;
     A.qkv_n = qkv_n;
@@ -605,6 +609,7 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
     A.q_out = q_out;
     A.ready = nullptr;
     A.pub_off = 0;
+    A.rec = rec;
     const dim3 grid(B, nkv, (max_seq + kAttnSplitFused - 1) / kAttnSplitFused);  // partial records: max_splits per head
     const size_t lds = attn_decode_lds(nh, nkv, hd, max_splits);
     void* args[] = {&A};
@@ -756,6 +761,7 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
     A.q_out = q_out;
     A.ready = ready;
     A.pub_off = (uint32_t)wo_pub_off(nh, nkv, hd, max_splits);
+    A.rec = nullptr;
     WoArgs W;
     W.hdr = (const uint4*)wo.hdr;
     W.qs = (const uint4*)wo.qs;
@@ -772,10 +778,12 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
     return hipLaunchKernel(attn_wo_kernel(hd, nh / nkv), dim3(W.n_attn + n_wo), dim3(kAttnThreads), args, lds, s);
 }
 
-hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s) {
+hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s,
+                                 MmaRec* rec) {
+    if (rec && (vdt != kQ8K || B > 16)) return hipErrorInvalidValue;
     const dim3 grid(B, (I + 255) / 256);
-    if (vdt == kQ8K) hipLaunchKernelGGL((k_silu_mul_quant<kQ8K>), grid, dim3(64), 0, s, gu, I, act, act_f32);
-    else hipLaunchKernelGGL((k_silu_mul_quant<kQ8_0>), grid, dim3(64), 0, s, gu, I, act, act_f32);
+    if (vdt == kQ8K) hipLaunchKernelGGL((k_silu_mul_quant<kQ8K>), grid, dim3(64), 0, s, gu, I, act, act_f32, rec);
+    else hipLaunchKernelGGL((k_silu_mul_quant<kQ8_0>), grid, dim3(64), 0, s, gu, I, act, act_f32, rec);
     return hipGetLastError();
 }
 

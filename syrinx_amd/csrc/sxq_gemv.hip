@@ -15,7 +15,10 @@
 // Q4_0 lane l takes block b0 + l and the group folds the eight block terms in order.
 // Activations are copied from their quantized device layout into LDS once per
 // workgroup (in K chunks when m * K does not fit).
+#include <stddef.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 #include <type_traits>
 
@@ -832,6 +835,199 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
     }
 }
 
+// The same product with the activation operands read from the quantizers' MmaRec
+// records (f16 values already in operand order) instead of staged through LDS and
+// converted by every workgroup: per block a wave loads its class's 16 bytes per lane
+// from L2, a chunk ahead, into registers.  LDS holds the weights, the decoded headers
+// and the records' d and bs of a chunk (double-buffered, 37 KB).  The high nibbles
+// stay in place in the W' FMA ((1024 + 16 q) * (sc / 16) - 64 sc = q * sc, exact), and
+// full chunks run as straight-line code with the min term in wave 0 only, so the
+// scheduler overlaps the blocks.  Same float steps, same bits.
+constexpr int kRecBuf = 16 * kMmaWRow + kMmaHdr + kMmaChunk * 128 + kMmaChunk * 16;  // dwords per chunk buffer
+constexpr size_t kRecLds = 2 * (size_t)kRecBuf * 4;
+static_assert(kRecBuf >= 9 * 256, "the final class sums reuse a chunk buffer");
+
+SXQ_DEV half8_t mma_weight8_hi(uint32_t v, half2_t sc0, half2_t ns0, half2_t sc1, half2_t ns1) {
+    const uint32_t u = v >> 8;
+    const half2_t x0 = __builtin_elementwise_fma(mma_magic(v & 0x000F000Fu), sc0, ns0);
+    const half2_t x1 = __builtin_elementwise_fma(mma_magic(u & 0x000F000Fu), sc0, ns0);
+    const half2_t x2 = __builtin_elementwise_fma(mma_magic(v & 0x00F000F0u), sc1, ns1);
+    const half2_t x3 = __builtin_elementwise_fma(mma_magic(u & 0x00F000F0u), sc1, ns1);
+    return half8_t{x0.x, x0.y, x1.x, x1.y, x2.x, x2.y, x3.x, x3.y};
+}
+
+__global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
+                                                          int n, int nb, const MmaRec* __restrict__ rec, int m, float* y,
+                                                          int64_t ldy, const float* __restrict__ bias, const float* res,
+                                                          int64_t ldr) {
+    extern __shared__ uint4 lds[];
+    uint32_t* l32 = (uint32_t*)lds;  // [2][kRecBuf]: weights [16][kMmaWRow], headers [2][256] uint4, bs [4][128], d [4][16]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, nl = lane & 15;
+    const int row0 = blockIdx.x * kMmaRows;
+    const int nc = (nb + kMmaChunk - 1) / kMmaChunk;
+    const uint8_t* rb = (const uint8_t*)rec;
+
+    // chunk copy (clamped, so every load is in bounds): weight piece tid (row tid >> 5,
+    // 16-byte piece tid & 31); tid < 256: the header of (row tid & 15, block (tid >> 6) & 3);
+    // tid 256..383: the records' bs (32 pieces per block); tid 384..399: their d
+    uint4 swq0, sx;
+    auto stage_load = [&](int c) {
+        const int cc = min(c, nc - 1);
+        {
+            const int r = min(row0 + (tid >> 5), n - 1), p = tid & 31;
+            const int b = min(cc * kMmaChunk + (p >> 3), nb - 1);
+            swq0 = qs[((size_t)r * nb + b) * 8 + (p & 7)];
+        }
+        if (tid < 256) {
+            const int r = min(row0 + (tid & 15), n - 1), b = min(cc * kMmaChunk + ((tid >> 6) & 3), nb - 1);
+            sx = hdr[(size_t)r * nb + b];
+        } else if (tid < 384) {
+            const int u = tid - 256, b = min(cc * kMmaChunk + (u >> 5), nb - 1);
+            sx = ((const uint4*)(rb + (size_t)b * sizeof(MmaRec) + offsetof(MmaRec, bs)))[u & 31];
+        } else if (tid < 400) {
+            const int u = tid - 384, b = min(cc * kMmaChunk + (u >> 2), nb - 1);
+            sx = ((const uint4*)(rb + (size_t)b * sizeof(MmaRec) + offsetof(MmaRec, d)))[u & 3];
+        }
+    };
+    auto stage_store = [&](int c) {
+        uint32_t* bw = l32 + (c & 1) * kRecBuf;
+        *(uint4*)(bw + (tid >> 5) * kMmaWRow + (tid & 31) * 4) = swq0;
+        if (tid < 256) {  // one decode per (block, g, row): scales 2g and 2g + 1 (the latter / 16), d, dmin, mins
+            const uint4 sh = sx;
+            const int gg = (tid >> 4) & 3;
+            const uint32_t sc_lo = sh.y & 0x3F3F3F3Fu;
+            const uint32_t sc_hi = (sh.w & 0x0F0F0F0Fu) | (((sh.y >> 6) & 0x03030303u) << 4);
+            const uint32_t mn_lo = sh.z & 0x3F3F3F3Fu;
+            const uint32_t mn_hi = ((sh.w >> 4) & 0x0F0F0F0Fu) | (((sh.z >> 6) & 0x03030303u) << 4);
+            const uint32_t scw = (gg < 2 ? sc_lo : sc_hi) >> (16 * (gg & 1));
+            const float f0 = (float)(scw & 0xFF), f1 = (float)((scw >> 8) & 0xFF);
+            const half2_t sc0 = {(_Float16)f0, (_Float16)f0};
+            const half2_t sc1 = {(_Float16)(f1 * 0.0625f), (_Float16)(f1 * 0.0625f)};  // exact: f1 < 64
+            const half2_t ns0 = {(_Float16)(-1024.0f * f0), (_Float16)(-1024.0f * f0)};
+            const half2_t ns1 = {(_Float16)(-64.0f * f1), (_Float16)(-64.0f * f1)};
+            uint4* hd = (uint4*)(bw + 16 * kMmaWRow);
+            hd[tid] = make_uint4(__builtin_bit_cast(uint32_t, sc0), __builtin_bit_cast(uint32_t, ns0),
+                                 __builtin_bit_cast(uint32_t, sc1), __builtin_bit_cast(uint32_t, ns1));
+            hd[256 + tid] = make_uint4(__builtin_bit_cast(uint32_t, h2f(sh.x & 0xFFFF)),
+                                       __builtin_bit_cast(uint32_t, h2f(sh.x >> 16)),
+                                       __builtin_bit_cast(uint32_t, (float)((mn_lo >> (8 * gg)) & 0xFF)),
+                                       __builtin_bit_cast(uint32_t, (float)((mn_hi >> (8 * gg)) & 0xFF)));
+        } else if (tid < 400) {
+            ((uint4*)(bw + 16 * kMmaWRow + kMmaHdr))[tid - 256] = sx;  // bs [4][128] floats, then d [4][16]
+        }
+    };
+    // this wave's activation operands of chunk c: block j, class w, row nl, slots 8g .. 8g + 7
+    auto load_a = [&](int c, half8_t (&A)[kMmaChunk]) {
+        const int cc = min(c, nc - 1);
+#pragma unroll
+        for (int j = 0; j < kMmaChunk; ++j) {
+            const int b = min(cc * kMmaChunk + j, nb - 1);
+            A[j] = __builtin_bit_cast(half8_t, ld_global((const uint4*)&rec[b].q[w][nl][g][0]));
+        }
+    };
+    // chains of lane (nl, g), accumulator element e: activation row 4g + e, weight row nl
+    float s0c[4] = {0.f, 0.f, 0.f, 0.f}, sf[4] = {0.f, 0.f, 0.f, 0.f};
+    const bool wave0 = __builtin_amdgcn_readfirstlane(w) == 0;
+    auto body = [&](int c, const half8_t (&A)[kMmaChunk], int live, auto full, auto w0) {
+        const uint32_t* bw = l32 + (c & 1) * kRecBuf;
+        const uint4* bh = (const uint4*)(bw + 16 * kMmaWRow);
+        const float* bsv = (const float*)(bw + 16 * kMmaWRow + kMmaHdr);
+        const float* dv = bsv + kMmaChunk * 128;
+#pragma unroll
+        for (int j = 0; j < kMmaChunk; ++j) {
+            if (decltype(full)::value || j < live) {
+                const uint4 ha = bh[j * 64 + lane];
+                const half2_t sc0 = __builtin_bit_cast(half2_t, ha.x), ns0 = __builtin_bit_cast(half2_t, ha.y);
+                const half2_t sc1 = __builtin_bit_cast(half2_t, ha.z), ns1 = __builtin_bit_cast(half2_t, ha.w);
+                const uint32_t wq = bw[nl * kMmaWRow + j * 32 + 4 * w + g];  // class w dword g
+                const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+                const f32x4_t c0 =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(A[j], mma_weight8_hi(wq, sc0, ns0, sc1, ns1), z, 0, 0, 0);
+                const float4 ad = *(const float4*)(dv + j * 16 + 4 * g);  // d of activation rows 4g .. 4g + 3
+                const float adv[4] = {ad.x, ad.y, ad.z, ad.w};
+                if constexpr (decltype(w0)::value) {
+                    const uint4 hb = bh[256 + j * 64 + lane];
+                    const float dw = __builtin_bit_cast(float, hb.x);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float d = dw * adv[e];
+                        s0c[e] += d * c0[e];
+                    }
+                    // the min term: mins g and g + 4 against bs2 of activation row nl
+                    f32x4_t mi = z;
+                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32(bsv[j * 128 + nl * 4 + g], __builtin_bit_cast(float, hb.z), mi,
+                                                              0, 0, 0);
+                    mi = __builtin_amdgcn_mfma_f32_16x16x4f32(bsv[j * 128 + 64 + nl * 4 + g],
+                                                              __builtin_bit_cast(float, hb.w), mi, 0, 0, 0);
+                    const float dminw = __builtin_bit_cast(float, hb.y);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sf[e] -= (dminw * adv[e]) * mi[e];
+                } else {
+                    const float dw = ((const float*)(bh + 256 + j * 64 + lane))[0];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float d = dw * adv[e];
+                        s0c[e] += d * c0[e];
+                    }
+                }
+            }
+        }
+    };
+    using Yes = std::integral_constant<bool, true>;
+    using No = std::integral_constant<bool, false>;
+    auto compute = [&](int c, const half8_t (&A)[kMmaChunk]) {
+        const int live = min(kMmaChunk, nb - c * kMmaChunk);
+        if (live == kMmaChunk) {
+            if (wave0) body(c, A, live, Yes{}, Yes{});
+            else body(c, A, live, Yes{}, No{});
+        } else {
+            if (wave0) body(c, A, live, No{}, Yes{});
+            else body(c, A, live, No{}, No{});
+        }
+    };
+    // A0 / A1 alternate (the loop runs two chunks per trip, so both stay in registers):
+    // chunk c + 1's operands load while chunk c computes; the weights load two chunks ahead
+    half8_t A0[kMmaChunk], A1[kMmaChunk];
+    stage_load(0);
+    load_a(0, A0);
+    stage_store(0);
+    stage_load(1);
+    __syncthreads();
+    for (int c = 0; c < nc; c += 2) {
+        load_a(c + 1, A1);
+        compute(c, A0);
+        if (c + 1 < nc) stage_store(c + 1);
+        stage_load(c + 2);
+        __syncthreads();
+        if (c + 1 >= nc) break;
+        load_a(c + 2, A0);
+        compute(c + 1, A1);
+        if (c + 2 < nc) stage_store(c + 2);
+        stage_load(c + 3);
+        __syncthreads();
+    }
+    // the class sums meet in LDS (chunk buffer 0: every read of it is behind the last barrier)
+    float* xb = (float*)lds;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int i = (4 * g + e) * 16 + nl;
+        xb[w * 256 + i] = s0c[e];
+        if (w == 0) xb[8 * 256 + i] = sf[e];
+    }
+    __syncthreads();
+    const int mr = tid >> 4, row = row0 + (tid & 15);
+    if (tid < 256 && mr < m && row < n) {
+        float tot = -0.0f;
+#pragma unroll
+        for (int cl = 0; cl < 8; ++cl) tot += xb[cl * 256 + tid];
+        float v = xb[8 * 256 + tid] + tot;
+        if (bias) v = v + bias[row];
+        if (res) v = res[(int64_t)mr * ldr + row] + v;
+        y[(int64_t)mr * ldy + row] = v;
+    }
+}
+
 static hipError_t gemv_mma_launch(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                                   const float* res, int64_t ldr, hipStream_t s) {
     static const hipError_t attr =
@@ -843,22 +1039,45 @@ static hipError_t gemv_mma_launch(const QWeight& w, const void* act, int m, floa
     return hipGetLastError();
 }
 
+static bool gemv_v1() {
+    static const bool v1 = getenv("SXQ_GEMV_V1") != nullptr;
+    return v1;
+}
+static bool gemv_mma_on() {
+    static const bool mma = [] {
+        const char* e = getenv("SXQ_GEMV_MMA");
+        return !e || atoi(e) != 0;
+    }();
+    return mma;
+}
+
+bool gemv_rec_fits(const QWeight& w, int m) {
+    return !gemv_v1() && gemv_mma_on() && w.dtype == kQ4K && m > 4 && m <= 16 && w.n > 0;
+}
+
+hipError_t launch_gemv_rec(const QWeight& w, const void* act, const MmaRec* rec, int m, float* y, int64_t ldy,
+                           const float* bias, const float* res, int64_t ldr, hipStream_t s) {
+    if (!rec || !gemv_rec_fits(w, m)) return launch_gemv(w, act, m, y, ldy, bias, res, ldr, s);
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)k_gemv_mma_q4k_rec, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRecLds);
+    if (attr != hipSuccess) return attr;
+    const int n = (int)w.n, nb = (int)w.nb;
+    hipLaunchKernelGGL(k_gemv_mma_q4k_rec, dim3((unsigned)((n + kMmaRows - 1) / kMmaRows)), dim3(512), kRecLds, s,
+                       (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, rec, m, y, ldy, bias, res, ldr);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                        const float* res, int64_t ldr, hipStream_t s) {
     if (m <= 0 || w.n <= 0) return hipSuccess;
-    static const bool v1 = getenv("SXQ_GEMV_V1") != nullptr;
-    if (!v1) {
+    if (!gemv_v1()) {
         const int nb = (int)w.nb;
         const bool fits = gemv2_fits((int)w.n, nb, m, w.dtype, 256);
         if (fits && m == 1) return gemv2_dispatch<1>(w, act, m, y, ldy, bias, res, ldr, s);
         if (fits && m == 2) return gemv2_dispatch<2>(w, act, m, y, ldy, bias, res, ldr, s);
         if (fits && m <= 4) return gemv2_dispatch<4>(w, act, m, y, ldy, bias, res, ldr, s);
         // 5..16 rows of Q4_K: one pass over the weights on the matrix cores
-        static const bool mma = [] {
-            const char* e = getenv("SXQ_GEMV_MMA");
-            return !e || atoi(e) != 0;
-        }();
-        if (w.dtype == kQ4K && m <= 16 && mma) return gemv_mma_launch(w, act, m, y, ldy, bias, res, ldr, s);
+        if (w.dtype == kQ4K && m <= 16 && gemv_mma_on()) return gemv_mma_launch(w, act, m, y, ldy, bias, res, ldr, s);
         // 5..16 rows: the task-split kernel four activation rows at a time (each launch
         // streams the weights again; per row this is still well ahead of the
         // one-group-per-row kernel, whose few waves leave most of the GPU idle).
@@ -939,15 +1158,16 @@ hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const
 }
 
 hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,
-                               int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s) {
+                               int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s,
+                               MmaRec* rec) {
     if (m <= 0 || w.n <= 0) return hipSuccess;
-    static const bool v1 = getenv("SXQ_GEMV_V1") != nullptr;
     const int k = (int)w.k;
-    if (!v1 && m == 1 && k <= kNormMaxDim && gemv2_fits((int)w.n, (int)w.nb, 1, w.dtype, 1024))
+    if (!gemv_v1() && m == 1 && k <= kNormMaxDim && gemv2_fits((int)w.n, (int)w.nb, 1, w.dtype, 1024))
         return gemv2_launch<1, true, 1024>(w, nullptr, 1, y, ldy, bias, res, ldr, s, ni);
-    hipError_t e = launch_rmsnorm_quant(vec_dot_type(w.dtype), ni.x, m, k, ni.w, ni.eps, act_scratch, ni.normed, s);
+    if (!gemv_rec_fits(w, m)) rec = nullptr;
+    hipError_t e = launch_rmsnorm_quant(vec_dot_type(w.dtype), ni.x, m, k, ni.w, ni.eps, act_scratch, ni.normed, s, rec);
     if (e != hipSuccess) return e;
-    return launch_gemv(w, act_scratch, m, y, ldy, bias, res, ldr, s);
+    return launch_gemv_rec(w, act_scratch, rec, m, y, ldy, bias, res, ldr, s);
 }
 
 }  // namespace sxq

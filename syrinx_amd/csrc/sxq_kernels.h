@@ -31,6 +31,12 @@ struct QWeight {
 // ActQ8_0 otherwise).
 hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64_t ldy, const float* bias,
                        const float* res, int64_t ldr, hipStream_t s);
+// The same product, for the m (5..16) rows launch_gemv runs on the Q4_K matrix-core GEMV,
+// read from the MmaRec records [nb] the quantizers wrote beside `act` (the same values):
+// gemv_rec_fits tells when it applies; otherwise (or with rec null) this is launch_gemv.
+bool gemv_rec_fits(const QWeight& w, int m);
+hipError_t launch_gemv_rec(const QWeight& w, const void* act, const MmaRec* rec, int m, float* y, int64_t ldy,
+                           const float* bias, const float* res, int64_t ldr, hipStream_t s);
 
 // RMSNorm of f32 rows x [m, k] (crates/syrinx-fish/src/s2/nn.rs:100-106), the result
 // quantized and multiplied: y = quant(rmsnorm(x) * w_norm) . W^T (+ bias, + res).
@@ -44,8 +50,11 @@ struct NormIn {
     float eps = 0.0f;
     float* normed = nullptr;      // optional f32 copy of the normalised rows [m, k]
 };
+// rec (optional): MmaRec records [k / 256] for the 5..16-row Q4_K matrix-core GEMV, which
+// the RMSNorm kernel then also fills and the GEMV reads instead of act_scratch.
 hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,
-                               int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s);
+                               int64_t ldy, const float* bias, const float* res, int64_t ldr, hipStream_t s,
+                               MmaRec* rec = nullptr);
 
 // The feed-forward of one decode row (m = 1) around SwiGLU, Q4_K weights: the fused
 // RMSNorm GEMV of the gate|up weight [2I][k] (gate rows first) writes gu [2I] and

@@ -70,6 +70,8 @@ struct sxq_lm {
     float *h = nullptr, *qkv = nullptr, *qbuf = nullptr, *part = nullptr, *gu = nullptr, *logits = nullptr;
     float* hn = nullptr;  // post-final-RMSNorm hidden of the step [max_batch][dim] (SlowAr::head's `hidden`)
     uint8_t *act_a = nullptr, *act_o = nullptr, *act_d = nullptr;
+    // the same activations as matrix-core operand records (Q8_K models, 5..16 streams)
+    MmaRec *rec_a = nullptr, *rec_o = nullptr, *rec_d = nullptr;
     int *d_ids = nullptr, *d_next = nullptr;
     float* am_val = nullptr;        // argmax partials [max_batch * kArgmaxSlices]
     int* am_idx = nullptr;
@@ -204,12 +206,19 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
         ni.normed = normed;
         return ni;
     };
+    // 5..16 streams of a Q8_K model: the quantizers also write the matrix-core operand
+    // records, which the Q4_K GEMVs then read (each producer and its consumer get the same
+    // pointer; a GEMV that does not take records reads the Q8_K rows as before)
+    const bool rec_ok = n >= 5 && n <= 16 && lm->rec_a != nullptr;
+    MmaRec* rec_a = rec_ok ? lm->rec_a : nullptr;
+    MmaRec* rec_o = rec_ok && lm->attn_fused && !wo_fused ? lm->rec_o : nullptr;
+    MmaRec* rec_d = rec_ok ? lm->rec_d : nullptr;
     for (int l = 0; l < c.n_layers; ++l) {
         LmLayer& L = lm->layers[l];
         float* kc = lm->kc + (int64_t)l * lm->kv_layer_stride;
         float* vc = lm->vc + (int64_t)l * lm->kv_layer_stride;
         STEP(launch_gemv_rmsnorm(L.wqkv.w, norm_in(lm->h, L.attn_norm, tr ? slot(nd) : nullptr), n, lm->act_a, lm->qkv,
-                                 lm->qkv_n, L.bqkv, nullptr, 0, s));
+                                 lm->qkv_n, L.bqkv, nullptr, 0, s, rec_a));
         if (tr) STEP(record(lm->qkv, (size_t)n * lm->qkv_n));
         const float* qn = c.qk_norm ? L.q_norm : nullptr;
         const float* kn = c.qk_norm ? L.k_norm : nullptr;
@@ -226,7 +235,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                 STEP(launch_attention_decode(lm->vdt, lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn,
                                              kn, c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len,
                                              kc, vc, lm->kv_stream_stride, c.max_seq, lm->max_splits, lm->part,
-                                             lm->attn_count, lm->act_o, ctx_slot, q_slot, s));
+                                             lm->attn_count, lm->act_o, ctx_slot, q_slot, s, rec_o));
         } else {
             STEP(launch_qk_rope_append(lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn, kn, c.norm_eps,
                                        c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len, lm->qbuf, kc, vc,
@@ -236,7 +245,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                                   c.max_seq, lm->kv_stream_stride, kAttnSplit, lm->max_splits, lm->part, lm->act_o,
                                   tr ? slot((size_t)n * lm->ctx) : nullptr, s));
         }
-        if (!wo_fused) STEP(launch_gemv(L.wo.w, lm->act_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+        if (!wo_fused) STEP(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
         if (tr) STEP(record(lm->h, nd));
         if (lm->swiglu && n == 1) {
             STEP(launch_swiglu_pair(L.w13.w, L.w2.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), lm->gu,
@@ -245,15 +254,15 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
             if (tr) STEP(record(lm->act_f32, (size_t)I));
         } else {
             STEP(launch_gemv_rmsnorm(L.w13.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), n, lm->act_a,
-                                     lm->gu, 2 * I, nullptr, nullptr, 0, s));
+                                     lm->gu, 2 * I, nullptr, nullptr, 0, s, rec_a));
             if (tr) STEP(record(lm->gu, (size_t)n * 2 * I));
-            STEP(launch_silu_mul_quant(lm->vdt, lm->gu, n, I, lm->act_d, tr ? slot((size_t)n * I) : nullptr, s));
-            STEP(launch_gemv(L.w2.w, lm->act_d, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+            STEP(launch_silu_mul_quant(lm->vdt, lm->gu, n, I, lm->act_d, tr ? slot((size_t)n * I) : nullptr, s, rec_d));
+            STEP(launch_gemv_rec(L.w2.w, lm->act_d, rec_d, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
         }
         if (tr) STEP(record(lm->h, nd));
     }
     STEP(launch_gemv_rmsnorm(lm->head.w, norm_in(lm->h, lm->final_norm, lm->hn), n, lm->act_a, lm->logits, c.vocab,
-                             c.head_bias ? lm->head_bias : nullptr, nullptr, 0, s));
+                             c.head_bias ? lm->head_bias : nullptr, nullptr, 0, s, rec_a));
     if (tr) STEP(record(lm->hn, nd));
     STEP(launch_argmax(lm->logits, n, c.vocab, lm->d_ids, lm->ids_per, lm->d_next, lm->d_len, lm->am_val, lm->am_idx,
                        lm->am_count, s));
@@ -585,6 +594,11 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->act_a, ab * MB * (c.dim / bs));
     A((void**)&lm->act_o, ab * MB * (lm->ctx / bs));
     A((void**)&lm->act_d, ab * MB * (I / bs));
+    if (lm->vdt == kQ8K) {
+        A((void**)&lm->rec_a, sizeof(MmaRec) * (size_t)(c.dim / 256));
+        A((void**)&lm->rec_o, sizeof(MmaRec) * (size_t)(lm->ctx / 256));
+        A((void**)&lm->rec_d, sizeof(MmaRec) * (size_t)(I / 256));
+    }
     A((void**)&lm->d_ids, sizeof(int) * MB * lm->ids_per);
     A((void**)&lm->d_next, sizeof(int) * MB);
     A((void**)&lm->am_val, sizeof(float) * MB * kArgmaxSlices);
@@ -627,6 +641,9 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     if (e == hipSuccess) e = hipMemset(lm->am_count, 0, sizeof(unsigned) * MB);
     if (e == hipSuccess) e = hipMemset(lm->attn_count, 0, sizeof(unsigned) * MB * c.n_kv_heads);
     if (e == hipSuccess) e = hipMemset(lm->wo_ready, 0, sizeof(unsigned) * c.n_layers);
+    if (e == hipSuccess && lm->rec_a) e = hipMemset(lm->rec_a, 0, sizeof(MmaRec) * (size_t)(c.dim / 256));
+    if (e == hipSuccess && lm->rec_o) e = hipMemset(lm->rec_o, 0, sizeof(MmaRec) * (size_t)(lm->ctx / 256));
+    if (e == hipSuccess && lm->rec_d) e = hipMemset(lm->rec_d, 0, sizeof(MmaRec) * (size_t)(I / 256));
     lm->attn_fused = getenv("SXQ_ATTN_UNFUSED") == nullptr && attn_decode_fits(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits);
     lm->swiglu = getenv("SXQ_SWIGLU_UNFUSED") == nullptr && swiglu_pair_fits(lm->layers[0].w13.w, lm->layers[0].w2.w);
     if (e == hipSuccess && lm->attn_fused &&
@@ -1029,15 +1046,21 @@ sxq_status sxq_lm_gemv_pass(sxq_lm* lm, int n, int with_head, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     const sxq_lm_config& c = lm->c;
     const int I = c.intermediate;
+    // the step's GEMVs on whatever the buffers hold (records where the step reads them)
+    const bool rec_ok = n >= 5 && n <= 16 && lm->rec_a != nullptr;
+    const MmaRec* rec_a = rec_ok ? lm->rec_a : nullptr;
+    const MmaRec* rec_o = rec_ok && lm->attn_fused ? lm->rec_o : nullptr;
+    const MmaRec* rec_d = rec_ok ? lm->rec_d : nullptr;
     for (int l = 0; l < c.n_layers; ++l) {
         LmLayer& L = lm->layers[l];
-        HIP_TRY(launch_gemv(L.wqkv.w, lm->act_a, n, lm->qkv, lm->qkv_n, L.bqkv, nullptr, 0, s), "lm_gemv_pass");
-        HIP_TRY(launch_gemv(L.wo.w, lm->act_o, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
-        HIP_TRY(launch_gemv(L.w13.w, lm->act_a, n, lm->gu, 2 * I, nullptr, nullptr, 0, s), "lm_gemv_pass");
-        HIP_TRY(launch_gemv(L.w2.w, lm->act_d, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(L.wqkv.w, lm->act_a, rec_a, n, lm->qkv, lm->qkv_n, L.bqkv, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(L.w13.w, lm->act_a, rec_a, n, lm->gu, 2 * I, nullptr, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(L.w2.w, lm->act_d, rec_d, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
     }
     if (with_head)
-        HIP_TRY(launch_gemv(lm->head.w, lm->act_a, n, lm->logits, c.vocab, nullptr, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(lm->head.w, lm->act_a, rec_a, n, lm->logits, c.vocab, nullptr, nullptr, 0, s),
+                "lm_gemv_pass");
     return SXQ_OK;
 }
 

@@ -91,8 +91,12 @@ SXQ_DEV float round_away(float t) { return roundf(t); }
 // element reaching it is found by a ballot over lanes and an in-lane scan.  The
 // quantized value is min(round(iscale * x), 127) (f32::min: NaN -> 127), which lies in
 // [-128, 127] (|iscale * x| <= 128 up to rounding) and so converts without saturation.
+//
+// `rec` (optional, J pointers, each may be null): also write chunk j's values into row
+// `rec_row` of its matrix-core operand record.
 template <int J, bool CANON>
-SXQ_DEV void wave_quantize_q8k_n(const float4 (&v)[J], int lane, void* const (&out)[J], const bool (&valid)[J]) {
+SXQ_DEV void wave_quantize_q8k_n(const float4 (&v)[J], int lane, void* const (&out)[J], const bool (&valid)[J],
+                                 MmaRec* const* rec = nullptr, int rec_row = 0) {
     float x[J][4], am[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -179,17 +183,27 @@ SXQ_DEV void wave_quantize_q8k_n(const float4 (&v)[J], int lane, void* const (&o
             for (int r = 0; r < 4; ++r) b->qs[4 * (8 * (l0 + r) + jj) + t] = (int8_t)q[j][r];
             if ((lane & 7) == 0) b->bs2[jj] = s8;
             if (lane == 0) b->d = d[j];
+            if (rec && rec[j]) {
+                // element 4*lane + r: class l0 + r, lane group jj / 2, slot 4 (jj % 2) + {0,2,1,3}[t]
+                MmaRec* R = rec[j];
+                const int g = jj >> 1, slot = 4 * (jj & 1) + ((t & 1) << 1) + (t >> 1);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) R->q[l0 + r][rec_row][g][slot] = (_Float16)(float)q[j][r];
+                if ((lane & 7) == 0) R->bs[jj >> 2][rec_row][jj & 3] = (float)s8;
+                if (lane == 0) R->d[rec_row] = d[j];
+            }
         }
     }
 }
 
 // One chunk: see wave_quantize_q8k_n.
 template <bool CANON>
-SXQ_DEV void wave_quantize_q8k(float4 v, int lane, void* out) {
+SXQ_DEV void wave_quantize_q8k(float4 v, int lane, void* out, MmaRec* rec = nullptr, int rec_row = 0) {
     const float4 vv[1] = {v};
     void* const oo[1] = {out};
     const bool ok[1] = {true};
-    wave_quantize_q8k_n<1, CANON>(vv, lane, oo, ok);
+    MmaRec* const rr[1] = {rec};
+    wave_quantize_q8k_n<1, CANON>(vv, lane, oo, ok, rr, rec_row);
 }
 
 // Quantize 256 consecutive activations (8 Q8_0 blocks; lanes 8b..8b+7 own block b) to
