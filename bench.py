@@ -218,9 +218,14 @@ def gemv_roofline(lm, torch, iters, rows=1):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / iters
     achieved = algo / (ms * 1e-3) / 1e9
-    kernel = ("k_gemv_mma_q4k" if rows > 4 else "k_gemv2_q4k") if c.weight_dtype == Q4K else "k_gemv2_q80"
+    kernel = ("k_gemv_mma_q4k_rec" if rows > 4 else "k_gemv2_q4k") if c.weight_dtype == Q4K else "k_gemv2_q80"
+    # counters were collected for the 16-row Qwen3-4B-shape pass (the skinny-batch line)
+    traffic = None
+    if kernel == "k_gemv_mma_q4k_rec" and rows == 16 and c.dim == 2560 and c.n_layers == 36:
+        t = measured_traffic(SKINNY_TRAFFIC_FILE)
+        traffic = None if t is None else round(t)
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "algorithmic_bytes_per_launch": round(algo / n_launch), "kernel": kernel, "rows": rows,
             "bytes_per_step": algo, "launches_per_step": n_launch, "avg_launch_us": round(ms * 1000.0 / n_launch, 3),
             "gemv_us_per_step": round(ms * 1000.0, 2), "replay": "hip graph",
@@ -228,12 +233,13 @@ def gemv_roofline(lm, torch, iters, rows=1):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv2_q4k_qwen3_4b_decode_traffic.txt")
+SKINNY_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv_mma_q4k_rec_qwen3_4b_16stream_traffic.txt")
 
 
-def measured_traffic():
-    """HBM bytes per Q4_K decode GEMV launch from the committed counter summary."""
+def measured_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per GEMV launch from a committed counter summary."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return float(line.split(":", 1)[1])
