@@ -10,7 +10,12 @@ projection through the oracle's QMatMul restatement (Candle's generic CPU path):
                     crates/syrinx-lm/src/cv2/attention.rs:46-78 (q/k/v + bias ->
                     rotate-half RoPE -> append -> SDPA -> o_proj).
 The only weights it takes are the canonical GGML blocks and f32 vectors the GPU engine
-is given, so both sides multiply by identical quantized weights.
+is given, so both sides multiply by identical quantized weights.  With
+cfg.weight_dtype == F32 every projection is instead a dense f32 matrix [n, k] and
+x.W^T is accumulated in f64 and rounded once per output (Weights::linear's dense
+broadcast_matmul, crates/syrinx-fish/src/s2/nn.rs:61-74): the form in which the
+reference's toy-LM fixtures (tests/golden/parity/lm_*.json, PARITY.md sections 2-5)
+pin this step's composition.
 """
 from __future__ import annotations
 
@@ -23,8 +28,12 @@ class OracleDecoder:
     def __init__(self, cfg, weights: dict, n_streams: int):
         """cfg: an object with the DecoderConfig fields.  weights keys:
         ('wqkv', l), ('wo', l), ('w1', l), ('w3', l), ('w2', l), 'head'  -> uint8 blocks [n, row_bytes]
-        ('attn_norm', l), ('ffn_norm', l), ('q_norm', l), ('k_norm', l), ('bqkv', l),
-        'final_norm', 'head_bias', 'embed', 'codebook'                  -> f32 arrays."""
+                                                                            (f32 [n, k] when weight_dtype is F32)
+        ('attn_norm', l), ('ffn_norm', l), ('q_norm', l), ('k_norm', l), ('bqkv', l), ('bo', l),
+        'final_norm', 'head_bias', 'embed', 'codebook'                  -> f32 arrays.
+        'embed' is the dense input table [rows, dim] (Fish: embeddings.weight, also the
+        tied head's source); a tied model given no 'embed' embeds through the
+        dequantized head rows instead."""
         self.c = cfg
         self.W = weights
         self.dt = int(cfg.weight_dtype)
@@ -39,6 +48,10 @@ class OracleDecoder:
         self.v = [[[[] for _ in range(cfg.n_kv_heads)] for _ in range(cfg.n_layers)] for _ in range(n_streams)]
 
     def _mm(self, x, blocks, name=""):
+        if self.dt == ora.F32:
+            y = (np.asarray(blocks, np.float64) @ np.asarray(x, np.float64)).astype(np.float32)
+            self.margins.append((name, 1.0))
+            return y
         m = ora.quant_margin(ora.VEC_DOT[self.dt], x)
         self.margins.append((name, m))
         self.margin = min(self.margin, m)
@@ -59,10 +72,20 @@ class OracleDecoder:
         return len(self.k[s][0][0])
 
     def embed(self, frame):
+        """The step's input row: SlowAr::embed (crates/syrinx-fish/src/s2/slow_ar.rs:101-161)
+        -- the token's row of embeddings.weight (:117), plus on semantic positions the sum
+        of the offset codebook rows (:120-128, zeroed elsewhere :131-144) scaled by
+        1/sqrt(n_codebooks + 1) (:146-156); a plain gather without codebooks
+        (Qwen2Lm::embed, crates/syrinx-lm/src/cv2/generate.rs:22-67)."""
         c = self.c
         tok = int(frame[0])
-        if c.tied_embedding:
-            x = ora.dequantize(self.dt, self.W["head"][tok], c.dim)[0]
+        if c.tied_embedding or c.n_codebooks:
+            if "embed" in self.W:
+                x = np.asarray(self.W["embed"][tok], np.float32).copy()
+            elif self.dt == ora.F32:
+                x = np.asarray(self.W["head"][tok], np.float32).copy()
+            else:
+                x = ora.dequantize(self.dt, self.W["head"][tok], c.dim)[0]
             if c.n_codebooks:
                 vq = None
                 for i in range(c.n_codebooks):
@@ -106,7 +129,10 @@ class OracleDecoder:
                 g = i // G
                 ctx[i * hd:(i + 1) * hd] = ora.attend_one(q[i], np.stack(self.k[s][l][g]), np.stack(self.v[s][l][g]))
             o = self._mm(ctx, self.W[("wo", l)], f"o{l}")
+            if getattr(c, "o_bias", 0):
+                o = (o + self.W[("bo", l)]).astype(np.float32)
             h = (r + o).astype(np.float32)
+            attn_out = o
             r = h
             hn = ora.rms_norm(h, self.W[("ffn_norm", l)], c.norm_eps)
             g_ = self._mm(hn, self.W[("w1", l)], f"gate{l}")
@@ -115,6 +141,9 @@ class OracleDecoder:
             d = self._mm(a, self.W[("w2", l)], f"down{l}")
             h = (r + d).astype(np.float32)
             self.trace.update({"qkv": qkv, "q": q.reshape(-1), "gu": np.concatenate([g_, u_]), "h": h})
+            self.trace[("ctx", l)] = ctx
+            self.trace[("attn", l)] = attn_out
+            self.trace[("h", l)] = h
         hn = ora.rms_norm(h, self.W["final_norm"], c.norm_eps)
         self.hidden = hn  # SlowAr::head's `hidden` (norm_fastlayer_input, no fast_project_in)
         logits = self._mm(hn, self.W["head"], "head")
