@@ -220,11 +220,16 @@ typedef struct {
     int32_t qk_norm;          /* per-head RMSNorm of q and k before RoPE (Qwen3) */
     int32_t qkv_bias;         /* biases on q, k, v (Qwen2) */
     int32_t head_bias;        /* bias on the head (CosyVoice2 llm_decoder) */
-    int32_t tied_embedding;   /* token embedding = dequantized row of the head weight (Fish) */
+    int32_t tied_embedding;   /* the head is the quantized input table (Fish embeddings.weight): the token
+                                 embedding gathers the dense table once one is uploaded (SXQ_LM_EMBED, as
+                                 SlowAr::embed does, crates/syrinx-fish/src/s2/slow_ar.rs:117), else the
+                                 dequantized head row */
     int32_t n_codebooks;      /* Fish MCF: codebook rows summed on semantic positions; 0 = none */
     int32_t codebook_size;
     int32_t semantic_begin;   /* semantic token id range (inclusive) for the MCF scale */
     int32_t semantic_end;
+    int32_t o_bias;           /* bias on wo (Fish `attention.wo.bias`, detected from the checkpoint at
+                                 crates/syrinx-fish/src/s2/slow_ar.rs:91-93) */
 } sxq_lm_config;
 
 /* Projection slots for sxq_lm_set_linear (layer-local unless noted). */
@@ -251,7 +256,8 @@ enum {
     SXQ_LM_FINAL_NORM = 7,     /* model-level */
     SXQ_LM_HEAD_BIAS = 8,      /* model-level */
     SXQ_LM_EMBED = 9,          /* model-level dense table [embed_rows, dim] */
-    SXQ_LM_CODEBOOK_EMBED = 10 /* model-level [n_codebooks * codebook_size, dim] */
+    SXQ_LM_CODEBOOK_EMBED = 10, /* model-level [n_codebooks * codebook_size, dim] */
+    SXQ_LM_BO = 11              /* wo bias [dim] (o_bias models) */
 };
 
 /* sxq_lm_step flags */

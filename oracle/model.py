@@ -30,7 +30,8 @@ class OracleDecoder:
         ('wqkv', l), ('wo', l), ('w1', l), ('w3', l), ('w2', l), 'head'  -> uint8 blocks [n, row_bytes]
                                                                             (f32 [n, k] when weight_dtype is F32)
         ('attn_norm', l), ('ffn_norm', l), ('q_norm', l), ('k_norm', l), ('bqkv', l), ('bo', l),
-        'final_norm', 'head_bias', 'embed', 'codebook'                  -> f32 arrays.
+        'final_norm', 'head_bias', 'embed', 'codebook', 'project_in_bias' -> f32 arrays;
+        'project_in' (fast_project_in, optional)                         -> blocks like the projections.
         'embed' is the dense input table [rows, dim] (Fish: embeddings.weight, also the
         tied head's source); a tied model given no 'embed' embeds through the
         dequantized head rows instead."""
@@ -145,7 +146,13 @@ class OracleDecoder:
             self.trace[("attn", l)] = attn_out
             self.trace[("h", l)] = h
         hn = ora.rms_norm(h, self.W["final_norm"], c.norm_eps)
-        self.hidden = hn  # SlowAr::head's `hidden` (norm_fastlayer_input, no fast_project_in)
+        # SlowAr::head's `hidden` (slow_ar.rs:230-243): the post-norm state (norm_fastlayer_input),
+        # through fast_project_in when the checkpoint has one (a narrower fast AR)
+        self.hidden = hn
+        if "project_in" in self.W:
+            self.hidden = self._mm(hn, self.W["project_in"], "project_in")
+            if "project_in_bias" in self.W:
+                self.hidden = (self.hidden + self.W["project_in_bias"]).astype(np.float32)
         logits = self._mm(hn, self.W["head"], "head")
         if c.head_bias:
             logits = (logits + self.W["head_bias"]).astype(np.float32)

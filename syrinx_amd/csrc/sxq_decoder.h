@@ -39,8 +39,10 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
                                    float* q_out, hipStream_t s, MmaRec* rec = nullptr);
 hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s,
                                  MmaRec* rec = nullptr);
-hipError_t launch_embed_quant_table(const int* ids, int ids_per, int B, const QWeight& w, int dim, const float* cb,
-                                    int n_cb, int cb_size, int sem_begin, int sem_end, float* h, hipStream_t s);
+// table: the dense input table [table_rows][dim], or null to dequantize the rows of the tied head w
+hipError_t launch_embed_mcf(const int* ids, int ids_per, int B, const float* table, int64_t table_rows,
+                            const QWeight& w, int dim, const float* cb, int n_cb, int cb_size, int sem_begin,
+                            int sem_end, float* h, hipStream_t s);
 hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
                               hipStream_t s);
 // Greedy argmax per stream; with `len` also advances each stream's cached length.

@@ -395,23 +395,26 @@ SXQ_DEV float weight_elem(const QWeight& w, int64_t r, int e) {
     return (float)((i < 16 ? (byte & 0xF) : (byte >> 4)) - 8) * d;
 }
 
-// Fish MCF (slow_ar.rs:101-161) over the tied, quantized table:
+// Fish MCF (slow_ar.rs:101-161):
 //   x = (E[tok] + sum_i C[code_i + i*cb]) * 1/sqrt(n_cb + 1)   on semantic positions,
-//   x = E[tok] + 0 * (...)                                      otherwise.
-// Without codebooks (n_cb = 0) this is the plain gather E[tok].  Ids outside the table
-// (token >= rows, code >= cb_size, negatives) read nothing: their rows count as zero.
-__global__ __launch_bounds__(256) void k_embed_quant_table(const int* __restrict__ ids, int ids_per, QWeight w, int dim,
-                                                           const float* __restrict__ cb, int n_cb, int cb_size,
-                                                           int sem_begin, int sem_end, float inv_scale,
-                                                           float* __restrict__ h) {
+//   x = E[tok] + 0 * (...)                                      otherwise,
+// with E the dense embeddings.weight table when given (`table`, [rows][dim], the gather
+// of :117), else the dequantized rows of the tied head w (rows = w.n).  Without codebooks
+// (n_cb = 0) this is the plain gather E[tok].  Ids outside the table (token >= rows,
+// code >= cb_size, negatives) read nothing: their rows count as zero.
+__global__ __launch_bounds__(256) void k_embed_mcf(const int* __restrict__ ids, int ids_per,
+                                                   const float* __restrict__ table, int64_t rows, QWeight w, int dim,
+                                                   const float* __restrict__ cb, int n_cb, int cb_size,
+                                                   int sem_begin, int sem_end, float inv_scale,
+                                                   float* __restrict__ h) {
     const int s = blockIdx.x;
     const int* fr = ids + (int64_t)s * ids_per;
     const int tok = fr[0];
-    const bool tok_ok = tok >= 0 && (int64_t)tok < w.n;
+    const bool tok_ok = tok >= 0 && (int64_t)tok < rows;
     const bool sem = tok >= sem_begin && tok <= sem_end;
     const int e = blockIdx.y * 256 + threadIdx.x;  // grid (B, ceil(dim / 256))
     if (e < dim) {
-        float x = tok_ok ? weight_elem(w, tok, e) : 0.0f;
+        float x = !tok_ok ? 0.0f : table ? table[(int64_t)tok * dim + e] : weight_elem(w, tok, e);
         if (n_cb > 0) {
             float vq = 0.0f;
             for (int i = 0; i < n_cb; ++i) {
@@ -787,11 +790,13 @@ hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t
     return hipGetLastError();
 }
 
-hipError_t launch_embed_quant_table(const int* ids, int ids_per, int B, const QWeight& w, int dim, const float* cb,
-                                    int n_cb, int cb_size, int sem_begin, int sem_end, float* h, hipStream_t s) {
+hipError_t launch_embed_mcf(const int* ids, int ids_per, int B, const float* table, int64_t table_rows,
+                            const QWeight& w, int dim, const float* cb, int n_cb, int cb_size, int sem_begin,
+                            int sem_end, float* h, hipStream_t s) {
     const float inv_scale = 1.0f / sqrtf((float)n_cb + 1.0f);
-    hipLaunchKernelGGL(k_embed_quant_table, dim3(B, (dim + 255) / 256), dim3(256), 0, s, ids, ids_per, w, dim, cb, n_cb,
-                       cb_size, sem_begin, sem_end, inv_scale, h);
+    const int64_t rows = table ? table_rows : w.n;
+    hipLaunchKernelGGL(k_embed_mcf, dim3(B, (dim + 255) / 256), dim3(256), 0, s, ids, ids_per, table, rows, w, dim, cb,
+                       n_cb, cb_size, sem_begin, sem_end, inv_scale, h);
     return hipGetLastError();
 }
 

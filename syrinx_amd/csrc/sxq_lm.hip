@@ -34,6 +34,7 @@ struct DevWeight {
 struct LmLayer {
     DevWeight wqkv, wo, w13, w2;
     float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *bqkv = nullptr;
+    float* bo = nullptr;  // wo bias (models with o_bias)
 };
 
 // A captured step is specific to its stream count, its input (ids or embeddings) and the
@@ -59,6 +60,9 @@ struct sxq_lm {
     int64_t kv_stream_stride = 0, kv_layer_stride = 0;
     std::vector<LmLayer> layers;
     DevWeight head;
+    // embed: the dense input table; allocated at create for an untied model, on the first
+    // SXQ_LM_EMBED upload for a tied one (until then a tied model embeds through the
+    // dequantized head rows)
     float *head_bias = nullptr, *final_norm = nullptr, *embed = nullptr, *cb_embed = nullptr;
     int embed_scheme = 0;            // SXQ_EMBED_INT8 / _INT4 when the input table is held quantized
     uint8_t* embed_q = nullptr;      // its codes, and per-row scales
@@ -97,6 +101,9 @@ struct sxq_lm {
 
 namespace {
 
+// Rows of the dense input table (a tied model's is the head's source: vocab rows).
+int64_t embed_rows(const sxq_lm_config& c) { return c.embed_rows > 0 && !c.tied_embedding ? c.embed_rows : c.vocab; }
+
 hipError_t dalloc(sxq_lm* lm, void** p, size_t bytes) {
     hipError_t e = hipMalloc(p, bytes ? bytes : 1);
     if (e == hipSuccess) lm->allocs.push_back(*p);
@@ -130,14 +137,17 @@ hipError_t copy_rows(DevWeight& dst, const QWeight& src, int64_t r0, hipStream_t
                           hipMemcpyDeviceToDevice, s);
 }
 
-// Fill rows [r0, r0 + n) of dst with from_float(N(0, std)) in row chunks.
+// Fill rows [r0, r0 + n) of dst with from_float(N(0, std)) in row chunks; keep_f32 (or
+// null) receives the f32 rows before quantization ([n][k], row r0 first).
 hipError_t random_rows(DevWeight& dst, int64_t r0, int64_t n, uint64_t seed, float stdv, float* tmp_f32,
-                       uint8_t* tmp_blk, int64_t tmp_elems, hipStream_t s) {
+                       uint8_t* tmp_blk, int64_t tmp_elems, hipStream_t s, float* keep_f32 = nullptr) {
     const int64_t k = dst.w.k, nb = dst.w.nb;
     const int64_t chunk = tmp_elems / k;
     for (int64_t a = 0; a < n; a += chunk) {
         const int64_t rows = n - a < chunk ? n - a : chunk;
         hipError_t e = launch_fill_normal(tmp_f32, rows * k, seed * 1000003ull + (uint64_t)a, 0.0f, stdv, s);
+        if (e == hipSuccess && keep_f32)
+            e = hipMemcpyAsync(keep_f32 + a * k, tmp_f32, sizeof(float) * rows * k, hipMemcpyDeviceToDevice, s);
         if (e == hipSuccess) e = launch_from_float(dst.w.dtype, tmp_f32, rows * nb, tmp_blk, s);
         QWeight part = dst.w;
         const size_t hb = weight_hdr_bytes(dst.w.dtype), qb = weight_qs_bytes(dst.w.dtype);
@@ -147,6 +157,13 @@ hipError_t random_rows(DevWeight& dst, int64_t r0, int64_t n, uint64_t seed, flo
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+void drop_graphs(sxq_lm* lm) {
+    for (auto& kv : lm->graphs) (void)hipGraphExecDestroy(kv.second);
+    lm->graphs.clear();
+    for (auto& kv : lm->expand_graphs) (void)hipGraphExecDestroy(kv.second);
+    lm->expand_graphs.clear();
 }
 
 // Per-layer trace segments (each [n, size] f32): hn_attn, qkv, q, ctx, h_mid, hn_ffn,
@@ -179,14 +196,14 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
         return p;
     };
     if (!from_embeds) {
-        if (c.tied_embedding)
-            STEP(launch_embed_quant_table(lm->d_ids, lm->ids_per, n, lm->head.w, c.dim, lm->cb_embed, c.n_codebooks,
-                                          c.codebook_size, c.semantic_begin, c.semantic_end, lm->h, s));
+        if (c.n_codebooks > 0 || (c.tied_embedding && !lm->embed))
+            STEP(launch_embed_mcf(lm->d_ids, lm->ids_per, n, lm->embed, embed_rows(c), lm->head.w, c.dim, lm->cb_embed,
+                                  c.n_codebooks, c.codebook_size, c.semantic_begin, c.semantic_end, lm->h, s));
         else if (lm->embed_scheme)
-            STEP(launch_embed_gather(lm->embed_scheme, lm->embed_q, lm->embed_scale, c.embed_rows > 0 ? c.embed_rows : c.vocab,
+            STEP(launch_embed_gather(lm->embed_scheme, lm->embed_q, lm->embed_scale, embed_rows(c),
                                      c.dim, lm->d_ids, lm->ids_per, n, lm->h, s));
         else
-            STEP(launch_embed_dense(lm->d_ids, lm->ids_per, n, lm->embed, c.embed_rows > 0 ? c.embed_rows : c.vocab, c.dim,
+            STEP(launch_embed_dense(lm->d_ids, lm->ids_per, n, lm->embed, embed_rows(c), c.dim,
                                     lm->h, s));
     }
     if (tr) STEP(record(lm->h, (size_t)n * c.dim));
@@ -245,7 +262,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                                   c.max_seq, lm->kv_stream_stride, kAttnSplit, lm->max_splits, lm->part, lm->act_o,
                                   tr ? slot((size_t)n * lm->ctx) : nullptr, s));
         }
-        if (!wo_fused) STEP(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+        if (!wo_fused) STEP(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->h, c.dim, L.bo, lm->h, c.dim, s));
         if (tr) STEP(record(lm->h, nd));
         if (lm->swiglu && n == 1) {
             STEP(launch_swiglu_pair(L.w13.w, L.w2.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), lm->gu,
@@ -357,8 +374,8 @@ sxq_status check_config(const sxq_lm_config* c) {
         return fail(SXQ_ERR_BLOCK_ALIGN,
                     "lm_create: dim %d, n_heads*head_dim %d and intermediate %d must be multiples of the block size %d",
                     c->dim, c->n_heads * c->head_dim, c->intermediate, bs);
-    if (c->n_codebooks < 0 || (c->n_codebooks > 0 && (c->codebook_size <= 0 || !c->tied_embedding)))
-        return fail(SXQ_ERR_INVALID, "lm_create: codebooks need codebook_size > 0 and a tied embedding");
+    if (c->n_codebooks < 0 || (c->n_codebooks > 0 && c->codebook_size <= 0))
+        return fail(SXQ_ERR_INVALID, "lm_create: codebooks need codebook_size > 0");
     return SXQ_OK;
 }
 
@@ -468,15 +485,15 @@ hipError_t enqueue_prefill(sxq_lm* lm, const PrefillMeta& pm, int T, const int* 
     PF(launch_prefill_tables(pm, T, tok, tiles, last, s));
     if (embeds) {
         PF(hipMemcpyAsync(h, embeds, sizeof(float) * Td, hipMemcpyDeviceToDevice, s));
-    } else if (c.tied_embedding) {
-        PF(launch_embed_quant_table(ids, lm->ids_per, T, lm->head.w, c.dim, lm->cb_embed, c.n_codebooks,
-                                    c.codebook_size, c.semantic_begin, c.semantic_end, h, s));
+    } else if (c.n_codebooks > 0 || (c.tied_embedding && !lm->embed)) {
+        PF(launch_embed_mcf(ids, lm->ids_per, T, lm->embed, embed_rows(c), lm->head.w, c.dim, lm->cb_embed,
+                            c.n_codebooks, c.codebook_size, c.semantic_begin, c.semantic_end, h, s));
     } else {
         if (lm->embed_scheme)
-            PF(launch_embed_gather(lm->embed_scheme, lm->embed_q, lm->embed_scale, c.embed_rows > 0 ? c.embed_rows : c.vocab,
+            PF(launch_embed_gather(lm->embed_scheme, lm->embed_q, lm->embed_scale, embed_rows(c),
                                    c.dim, ids, lm->ids_per, T, h, s));
         else
-            PF(launch_embed_dense(ids, lm->ids_per, T, lm->embed, c.embed_rows > 0 ? c.embed_rows : c.vocab, c.dim, h, s));
+            PF(launch_embed_dense(ids, lm->ids_per, T, lm->embed, embed_rows(c), c.dim, h, s));
     }
     PF(record(h, Td));
     for (int l = 0; l < c.n_layers; ++l) {
@@ -496,7 +513,7 @@ hipError_t enqueue_prefill(sxq_lm* lm, const PrefillMeta& pm, int T, const int* 
                                lm->kv_stream_stride, cx, s));
         PF(record(cx, (size_t)T * lm->ctx));
         PF(launch_quantize_act(lm->vdt, false, cx, lm->ctx, T, lm->ctx, act, s));
-        PF(pf_proj(lm, L.wo.w, cx, act, T, h, nullptr, h, exact, gws, s));
+        PF(pf_proj(lm, L.wo.w, cx, act, T, h, L.bo, h, exact, gws, s));
         PF(record(h, Td));
         PF(launch_rmsnorm_quant(lm->vdt, h, T, c.dim, L.ffn_norm, c.norm_eps, act, hn, s));
         PF(record(hn, Td));
@@ -571,11 +588,12 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
         A((void**)&L.q_norm, sizeof(float) * hd);
         A((void**)&L.k_norm, sizeof(float) * hd);
         A((void**)&L.bqkv, sizeof(float) * lm->qkv_n);
+        if (c.o_bias) A((void**)&L.bo, sizeof(float) * c.dim);
     }
     if (e == hipSuccess) e = alloc_weight(lm, lm->head, dt, c.vocab, c.dim);
     A((void**)&lm->head_bias, sizeof(float) * c.vocab);
     A((void**)&lm->final_norm, sizeof(float) * c.dim);
-    if (!c.tied_embedding) A((void**)&lm->embed, sizeof(float) * (size_t)(c.embed_rows > 0 ? c.embed_rows : c.vocab) * c.dim);
+    if (!c.tied_embedding) A((void**)&lm->embed, sizeof(float) * (size_t)embed_rows(c) * c.dim);
     if (c.n_codebooks > 0) A((void**)&lm->cb_embed, sizeof(float) * (size_t)c.n_codebooks * c.codebook_size * c.dim);
     A((void**)&lm->rope_cos, sizeof(float) * (size_t)c.max_seq * (hd / 2));
     A((void**)&lm->rope_sin, sizeof(float) * (size_t)c.max_seq * (hd / 2));
@@ -633,6 +651,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
         if (e == hipSuccess) e = launch_fill_value(L.q_norm, hd, 1.0f, nullptr);
         if (e == hipSuccess) e = launch_fill_value(L.k_norm, hd, 1.0f, nullptr);
         if (e == hipSuccess) e = launch_fill_value(L.bqkv, lm->qkv_n, 0.0f, nullptr);
+        if (e == hipSuccess && L.bo) e = launch_fill_value(L.bo, c.dim, 0.0f, nullptr);
     }
     if (e == hipSuccess) e = launch_fill_value(lm->final_norm, c.dim, 1.0f, nullptr);
     if (e == hipSuccess) e = launch_fill_value(lm->head_bias, c.vocab, 0.0f, nullptr);
@@ -651,7 +670,8 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
         (void)hipGetLastError();  // clear it: the three-kernel path needs no opt-in
         lm->attn_fused = false;
     }
-    lm->wo_fused = lm->attn_fused && c.n_layers >= 2 && getenv("SXQ_ATTN_WO_UNFUSED") == nullptr &&
+    // (the fused launch's O projection has no bias epilogue: o_bias models run it as its own GEMV)
+    lm->wo_fused = lm->attn_fused && c.n_layers >= 2 && !c.o_bias && getenv("SXQ_ATTN_WO_UNFUSED") == nullptr &&
                    attn_wo_decode_fits(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits, lm->layers[0].wo.w, c.dim);
     if (e == hipSuccess && lm->wo_fused &&
         attn_wo_decode_prepare(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits, lm->layers[0].wo.w) != hipSuccess) {
@@ -718,7 +738,7 @@ sxq_status sxq_lm_set_linear(sxq_lm* lm, int layer, int which, const sxq_qmm* q)
 sxq_status sxq_lm_set_vector(sxq_lm* lm, int layer, int which, const float* data, int64_t n, int src_is_device) {
     if (!lm || !data) return fail(SXQ_ERR_INVALID, "lm_set_vector: null pointer");
     const sxq_lm_config& c = lm->c;
-    const bool per_layer = which <= SXQ_LM_BV;
+    const bool per_layer = which <= SXQ_LM_BV || which == SXQ_LM_BO;
     if (per_layer && (layer < 0 || layer >= c.n_layers)) return fail(SXQ_ERR_INVALID, "lm_set_vector: layer out of range");
     const int hd = c.head_dim;
     float* dst = nullptr;
@@ -731,12 +751,18 @@ sxq_status sxq_lm_set_vector(sxq_lm* lm, int layer, int which, const float* data
     case SXQ_LM_BQ: dst = lm->layers[layer].bqkv; want = lm->ctx; break;
     case SXQ_LM_BK: dst = lm->layers[layer].bqkv + lm->ctx; want = (int64_t)c.n_kv_heads * hd; break;
     case SXQ_LM_BV: dst = lm->layers[layer].bqkv + lm->ctx + (int64_t)c.n_kv_heads * hd; want = (int64_t)c.n_kv_heads * hd; break;
+    case SXQ_LM_BO:
+        if (!lm->layers[layer].bo) return fail(SXQ_ERR_INVALID, "lm_set_vector: this model has no wo bias (o_bias 0)");
+        dst = lm->layers[layer].bo;
+        want = c.dim;
+        break;
     case SXQ_LM_FINAL_NORM: dst = lm->final_norm; want = c.dim; break;
     case SXQ_LM_HEAD_BIAS: dst = lm->head_bias; want = c.vocab; break;
     case SXQ_LM_EMBED:
-        if (!lm->embed) return fail(SXQ_ERR_INVALID, "lm_set_vector: this model has a tied embedding");
+        // a tied model gets its dense table on the first upload (embeddings.weight, which the
+        // head quantizes: the embedding then gathers it, as SlowAr::embed does)
         dst = lm->embed;
-        want = (int64_t)(c.embed_rows > 0 ? c.embed_rows : c.vocab) * c.dim;
+        want = (int64_t)embed_rows(c) * c.dim;
         break;
     case SXQ_LM_CODEBOOK_EMBED:
         if (!lm->cb_embed) return fail(SXQ_ERR_INVALID, "lm_set_vector: this model has no codebooks");
@@ -749,6 +775,12 @@ sxq_status sxq_lm_set_vector(sxq_lm* lm, int layer, int which, const float* data
     std::lock_guard<std::mutex> lock(lm->mu);
     DeviceGuard g(lm->device);
     HIP_TRY(g.err, "hipSetDevice");
+    if (which == SXQ_LM_EMBED && !lm->embed) {
+        HIP_TRY(hipDeviceSynchronize(), "lm_set_vector: drain");
+        HIP_TRY(dalloc(lm, (void**)&lm->embed, sizeof(float) * (size_t)want), "lm_set_vector: dense input table");
+        drop_graphs(lm);  // captured with the head-row embedding
+        dst = lm->embed;
+    }
     HIP_TRY(hipMemcpy(dst, data, sizeof(float) * n, src_is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
             "lm_set_vector: copy");
     return SXQ_OK;
@@ -759,6 +791,8 @@ sxq_status sxq_lm_set_embed_quantized(sxq_lm* lm, int scheme, const uint8_t* q, 
     const sxq_lm_config& c = lm->c;
     if (c.tied_embedding || !lm->embed)
         return fail(SXQ_ERR_INVALID, "lm_set_embed_quantized: this model has a tied embedding");
+    if (c.n_codebooks > 0)
+        return fail(SXQ_ERR_INVALID, "lm_set_embed_quantized: the codebook (MCF) embedding gathers a dense table");
     if (scheme != SXQ_EMBED_INT8 && scheme != SXQ_EMBED_INT4)
         return fail(SXQ_ERR_INVALID, "lm_set_embed_quantized: unknown scheme %d", scheme);
     if (embed_effective_scheme(scheme, c.dim) != scheme)
@@ -767,7 +801,7 @@ sxq_status sxq_lm_set_embed_quantized(sxq_lm* lm, int scheme, const uint8_t* q, 
     std::lock_guard<std::mutex> lock(lm->mu);
     DeviceGuard g(lm->device);
     HIP_TRY(g.err, "hipSetDevice");
-    const int64_t rows = c.embed_rows > 0 ? c.embed_rows : c.vocab;
+    const int64_t rows = embed_rows(c);
     const size_t qb = embed_code_bytes(scheme, rows, c.dim);
     if (!lm->embed_q) {  // sized for int8, the larger of the two
         HIP_TRY(dalloc(lm, (void**)&lm->embed_q, embed_code_bytes(SXQ_EMBED_INT8, rows, c.dim)), "lm_set_embed_quantized");
@@ -777,10 +811,7 @@ sxq_status sxq_lm_set_embed_quantized(sxq_lm* lm, int scheme, const uint8_t* q, 
     HIP_TRY(hipMemcpy(lm->embed_q, q, qb, hipMemcpyDefault), "lm_set_embed_quantized: codes");
     HIP_TRY(hipMemcpy(lm->embed_scale, scale, sizeof(float) * rows, hipMemcpyDefault), "lm_set_embed_quantized: scales");
     lm->embed_scheme = scheme;
-    for (auto& kv : lm->graphs) (void)hipGraphExecDestroy(kv.second);  // captured with the dense gather
-    lm->graphs.clear();
-    for (auto& kv : lm->expand_graphs) (void)hipGraphExecDestroy(kv.second);
-    lm->expand_graphs.clear();
+    drop_graphs(lm);  // captured with the dense gather
     return SXQ_OK;
 }
 
@@ -813,11 +844,23 @@ sxq_status sxq_lm_init_random(sxq_lm* lm, uint64_t seed, float stdv) {
         V(L.q_norm, c.head_dim, 1.0f, 0.0f);
         V(L.k_norm, c.head_dim, 1.0f, 0.0f);
         V(L.bqkv, lm->qkv_n, 0.0f, c.qkv_bias ? stdv : 0.0f);
+        if (L.bo) V(L.bo, c.dim, 0.0f, stdv);
     }
-    W(lm->head, 0, c.vocab);
+    if (c.tied_embedding) {
+        // the tied head quantizes the dense table, which the embedding gathers: keep the
+        // f32 rows the head is made from as that table
+        if (!lm->embed && e == hipSuccess) {
+            e = hipDeviceSynchronize();
+            if (e == hipSuccess) e = dalloc(lm, (void**)&lm->embed, sizeof(float) * (size_t)c.vocab * c.dim);
+            drop_graphs(lm);
+        }
+        if (e == hipSuccess) e = random_rows(lm->head, 0, c.vocab, sd++, stdv, tmp, blk, tmp_elems, nullptr, lm->embed);
+    } else {
+        W(lm->head, 0, c.vocab);
+    }
     V(lm->final_norm, c.dim, 1.0f, 0.0f);
     V(lm->head_bias, c.vocab, 0.0f, c.head_bias ? stdv : 0.0f);
-    if (lm->embed) V(lm->embed, (int64_t)(c.embed_rows > 0 ? c.embed_rows : c.vocab) * c.dim, 0.0f, stdv);
+    if (lm->embed && !c.tied_embedding) V(lm->embed, (int64_t)embed_rows(c) * c.dim, 0.0f, stdv);
     if (lm->cb_embed) V(lm->cb_embed, (int64_t)c.n_codebooks * c.codebook_size * c.dim, 0.0f, stdv);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     (void)hipFree(tmp);
@@ -1054,7 +1097,7 @@ sxq_status sxq_lm_gemv_pass(sxq_lm* lm, int n, int with_head, void* stream) {
     for (int l = 0; l < c.n_layers; ++l) {
         LmLayer& L = lm->layers[l];
         HIP_TRY(launch_gemv_rec(L.wqkv.w, lm->act_a, rec_a, n, lm->qkv, lm->qkv_n, L.bqkv, nullptr, 0, s), "lm_gemv_pass");
-        HIP_TRY(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->gu, c.dim, L.bo, nullptr, 0, s), "lm_gemv_pass");
         HIP_TRY(launch_gemv_rec(L.w13.w, lm->act_a, rec_a, n, lm->gu, 2 * I, nullptr, nullptr, 0, s), "lm_gemv_pass");
         HIP_TRY(launch_gemv_rec(L.w2.w, lm->act_d, rec_d, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
     }

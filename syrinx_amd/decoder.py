@@ -24,7 +24,7 @@ LM_GRAPH = 1
 LM_EXACT = 2       # prefill: Q4_K projections through Candle's integer vec-dot (bit-identical)
 LM_ALL_LOGITS = 4  # prefill: logits / hidden for every prompt token
 WQKV, WQ, WK, WV, WO, W1, W3, W2, HEAD = range(9)
-ATTN_NORM, FFN_NORM, Q_NORM, K_NORM, BQ, BK, BV, FINAL_NORM, HEAD_BIAS, EMBED, CODEBOOK_EMBED = range(11)
+ATTN_NORM, FFN_NORM, Q_NORM, K_NORM, BQ, BK, BV, FINAL_NORM, HEAD_BIAS, EMBED, CODEBOOK_EMBED, BO = range(12)
 
 
 class LmConfig(ctypes.Structure):
@@ -36,7 +36,7 @@ class LmConfig(ctypes.Structure):
         ("rope_theta", ctypes.c_float), ("rope_interleaved", ctypes.c_int32), ("qk_norm", ctypes.c_int32),
         ("qkv_bias", ctypes.c_int32), ("head_bias", ctypes.c_int32), ("tied_embedding", ctypes.c_int32),
         ("n_codebooks", ctypes.c_int32), ("codebook_size", ctypes.c_int32), ("semantic_begin", ctypes.c_int32),
-        ("semantic_end", ctypes.c_int32),
+        ("semantic_end", ctypes.c_int32), ("o_bias", ctypes.c_int32),
     ]
 
 
@@ -64,6 +64,7 @@ class DecoderConfig:
     codebook_size: int = 0
     semantic_begin: int = 0
     semantic_end: int = -1
+    o_bias: int = 0
 
     def to_c(self) -> LmConfig:
         c = LmConfig()
@@ -310,6 +311,33 @@ class DecoderLM:
 class SlowAr(DecoderLM):
     """Fish s2 slow AR decode (crates/syrinx-fish/src/s2/slow_ar.rs)."""
 
+    project_in = None       # fast_project_in QMatMul [fast_dim, dim] (a narrower fast AR), or None
+    project_in_bias = None  # its bias (device f32 [fast_dim]), or None
+
+    def set_project_in(self, qmm: QMatMul, bias: torch.Tensor = None) -> None:
+        """A checkpoint's fast_project_in (slow_ar.rs:230-243): every hidden this engine
+        returns for the fast AR is then linear(normed, fast_project_in.weight[, .bias]),
+        a QMatMul forward on the device, instead of the post-norm hidden itself."""
+        if qmm.shape[1] != self.cfg.dim:
+            raise ValueError(f"fast_project_in takes {qmm.shape[1]} inputs, the slow AR's hidden has {self.cfg.dim}")
+        self.project_in = qmm
+        self.project_in_bias = None if bias is None else bias.detach().to(self.device, torch.float32).contiguous()
+
+    @property
+    def hidden_dim(self) -> int:
+        """Width of the hidden handed to the fast AR (fast_dim with a project_in)."""
+        return self.cfg.dim if self.project_in is None else self.project_in.shape[0]
+
+    def _fast_hidden(self, raw: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+        """raw [n, dim] post-norm hidden -> the fast AR's hidden [n, hidden_dim] (into out)."""
+        if self.project_in is None:
+            return raw if out is None else out
+        y = self.project_in.forward(raw.reshape(-1, self.cfg.dim), self.project_in_bias)
+        if out is None:
+            return y
+        out.view(-1, self.hidden_dim).copy_(y)
+        return out
+
     def slow_step(self, frame, pos: int = None, graph: bool = True):
         """frame: [1 + num_codebooks] ids of the previous frame; pos must equal the cache
         length (slow_ar.rs:259-271).  Returns (semantic_logits [vocab], hidden [1, 1, dim]),
@@ -320,16 +348,20 @@ class SlowAr(DecoderLM):
         ids = torch.as_tensor(frame, dtype=torch.int32).reshape(1, -1)
         logits, nxt, hidden = self.step(ids=ids, graph=graph, want_hidden=True)
         self._last_argmax = nxt
-        return logits[0], hidden.reshape(1, 1, -1)
+        return logits[0], self._fast_hidden(hidden).reshape(1, 1, -1)
 
     def slow_step_batch(self, frames, graph: bool = True, out=None):
         """frames: [n, 1 + num_codebooks]; ragged cache lengths need no left padding
-        (slow_ar.rs:456-499).  Returns (semantic_logits [n, vocab], hidden [n, 1, dim]);
-        out = (logits, next_ids, hidden) as for step()."""
+        (slow_ar.rs:456-499).  Returns (semantic_logits [n, vocab], hidden [n, 1, hidden_dim]);
+        out = (logits, next_ids, hidden) as for step() (hidden [n, hidden_dim])."""
+        hid_out = None
+        if out is not None and self.project_in is not None:  # the step writes the raw hidden first
+            raw = torch.empty((out[0].shape[0], self.cfg.dim), dtype=torch.float32, device=self.device)
+            out, hid_out = (out[0], out[1], raw), out[2]
         logits, nxt, hidden = self.step(ids=torch.as_tensor(frames, dtype=torch.int32), graph=graph, want_hidden=True,
                                         out=out)
         self._last_argmax = nxt
-        return logits, hidden.reshape(-1, 1, self.cfg.dim)
+        return logits, self._fast_hidden(hidden, hid_out).reshape(-1, 1, self.hidden_dim)
 
     def prefill(self, prompt, graph: bool = False):
         """SlowAr::prefill (slow_ar.rs:250-256): prompt [1 + num_codebooks, T] (rows =
@@ -338,7 +370,7 @@ class SlowAr(DecoderLM):
         p = torch.as_tensor(prompt, dtype=torch.int32).reshape(self.ids_per, -1).t().contiguous()
         logits, nxt, hidden = super().prefill(prompts=[p])
         self._last_argmax = nxt
-        return logits[0], hidden.reshape(1, 1, -1)
+        return logits[0], self._fast_hidden(hidden).reshape(1, 1, -1)
 
     def prefill_batch(self, prompts):
         """SlowAr::prefill_batch (slow_ar.rs:404-454): ragged prompts [1 + num_codebooks,
@@ -347,7 +379,7 @@ class SlowAr(DecoderLM):
         ps = [torch.as_tensor(p, dtype=torch.int32).reshape(self.ids_per, -1).t().contiguous() for p in prompts]
         logits, nxt, hidden = super().prefill(prompts=ps)
         self._last_argmax = nxt
-        return logits, hidden.reshape(len(ps), 1, -1)
+        return logits, self._fast_hidden(hidden).reshape(len(ps), 1, -1)
 
     def last_argmax(self) -> torch.Tensor:
         """Greedy argmax ids [n] of the last step's logits (device int32)."""

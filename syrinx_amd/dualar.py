@@ -50,6 +50,9 @@ def drive_batch(slow: SlowAr, fast: FastAr, prompts, stop_id: int, params: Drive
         raise ValueError(f"drive_batch: {n} prompts exceed the engines' max_batch")
     if fast.cfg.max_seq < n_cb:
         raise ValueError("drive_batch: the fast engine's cache is shorter than a frame")
+    if slow.hidden_dim != fast.cfg.dim:
+        raise ValueError(f"drive_batch: the slow AR hands over {slow.hidden_dim}-wide hiddens, the fast AR is "
+                         f"{fast.cfg.dim} wide (a narrower fast AR needs fast_project_in)")
     dev = slow.device
     stop = int(stop_id)
     sampler = FishSampler([params.seed + i for i in range(n)], params.sampling, semantic=(c.semantic_begin,
@@ -83,7 +86,7 @@ def generate_frames(slow: SlowAr, fast: FastAr, sampler: FishSampler, logits0, h
     dev = slow.device
     # fixed buffers: the expansion graph is captured on their addresses
     logits = logits0.contiguous()
-    hidden = hidden0.reshape(n, c.dim).contiguous()
+    hidden = hidden0.reshape(n, slow.hidden_dim).contiguous()
     nxt = torch.empty(n, dtype=torch.int32, device=dev)
     if frame is None:
         frame = torch.zeros((n, 1 + n_cb), dtype=torch.int32, device=dev)

@@ -28,7 +28,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-from .decoder import (ATTN_NORM, BK, BQ, BV, CODEBOOK_EMBED, EMBED, FFN_NORM, FINAL_NORM, HEAD, HEAD_BIAS, K_NORM,
+from .decoder import (ATTN_NORM, BK, BO, BQ, BV, CODEBOOK_EMBED, EMBED, FFN_NORM, FINAL_NORM, HEAD, HEAD_BIAS, K_NORM,
                       Q_NORM, W1, W2, W3, WK, WO, WQ, WQKV, WV, DecoderConfig, FastAr, Qwen2Lm, SlowAr,
                       cosyvoice2_lm_config, fish_s2_fast_ar_config, fish_s2_slow_ar_config)
 from .embedding import DEFAULT_EMBED_SCHEME, QEmbed
@@ -314,19 +314,22 @@ def _q(w: dict, name: str, dtype: GgmlDType) -> QMatMul:
     return QMatMul.from_qtensor(QTensor.quantize(t.contiguous(), dtype))
 
 
-# The Fish weights fish_engines runs as QMatMul projections; every other tensor is a
-# vector or a dense table.
+# The Fish weights fish_engines runs only as QMatMul projections; every other tensor is a
+# vector or a dense table.  embeddings.weight is a dense table (the token embedding
+# gathers it) even where the tied head quantizes it.
 _FISH_LINEAR = re.compile(r"^(layers|fast_layers)\.\d+\.(attention\.(wqkv|wo)|feed_forward\.(w1|w2|w3))\.weight$")
 
 
 def is_fish_projection(name: str) -> bool:
-    return bool(_FISH_LINEAR.match(name)) or name in ("embeddings.weight", "fast_output.weight")
+    return bool(_FISH_LINEAR.match(name)) or name in ("output.weight", "fast_output.weight", "fast_project_in.weight")
 
 
 def save_fish_gguf(w: dict, path: str, dtype: GgmlDType = GgmlDType.Q4K) -> None:
-    """Quantize a load_fish_lm bag once and store it as GGUF: the projections (and the tied
-    slow head / fast output tables) as `dtype` blocks made by Candle's from_float, the
-    norms and embedding tables f32.  load_fish_gguf reads it back for fish_engines."""
+    """Quantize a load_fish_lm bag once and store it as GGUF: the projections (and an untied
+    slow head, the fast output and fast_project_in) as `dtype` blocks made by Candle's
+    from_float; the norms, biases and embedding tables f32 -- embeddings.weight too, which
+    the token embedding gathers and a tied head quantizes when the engines are built.
+    load_fish_gguf reads it back for fish_engines."""
     from . import gguf
     tensors = []
     for name in sorted(w):
@@ -348,15 +351,28 @@ def load_fish_gguf(path: str, device="cuda:0") -> dict:
     return out
 
 
+def _attn_flags(w: dict, base: str) -> dict:
+    """The attention variant of a block stack, from its tensors as the reference derives it
+    (slow_ar.rs:86-98, fast_ar.rs:53-65): qkv / o bias and QK-RMSNorm present in layer 0."""
+    return dict(qkv_bias=int(f"{base}.0.attention.wqkv.bias" in w), o_bias=int(f"{base}.0.attention.wo.bias" in w),
+                qk_norm=int(f"{base}.0.attention.q_norm.weight" in w))
+
+
 def _wire_fish(lm, w: dict, base: str, L: int, dtype: GgmlDType, qk_norm: bool) -> None:
+    c = lm.cfg
+    q, kv = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
     for l in range(L):
         p = f"{base}.{l}"
-        for bias in ("attention.wqkv.bias", "attention.wo.bias"):
-            if f"{p}.{bias}" in w:
-                raise NotImplementedError(f"{p}.{bias}: the engine's Fish blocks carry no qkv/o bias")
         for slot, nm in ((WQKV, "attention.wqkv"), (WO, "attention.wo"), (W1, "feed_forward.w1"),
                          (W3, "feed_forward.w3"), (W2, "feed_forward.w2")):
             lm.set_linear(l, slot, _q(w, f"{p}.{nm}.weight", dtype))
+        if c.qkv_bias:  # the fused [q; k; v] bias, split into the engine's three slots
+            b = w[f"{p}.attention.wqkv.bias"].reshape(-1)
+            lm.set_vector(l, BQ, b[:q])
+            lm.set_vector(l, BK, b[q:q + kv])
+            lm.set_vector(l, BV, b[q + kv:q + 2 * kv])
+        if c.o_bias:
+            lm.set_vector(l, BO, w[f"{p}.attention.wo.bias"])
         lm.set_vector(l, ATTN_NORM, w[f"{p}.attention_norm.weight"])
         lm.set_vector(l, FFN_NORM, w[f"{p}.ffn_norm.weight"])
         if qk_norm:
@@ -368,10 +384,12 @@ def fish_engines(w: dict, n_codebooks: int = 10, semantic_begin: int = 151678, s
                  max_seq: int = 1280, max_batch: int = 1, dtype: GgmlDType = GgmlDType.Q4K, device="cuda:0",
                  head_dim: int = 128):
     """SlowAr + FastAr over a load_fish_lm bag, projections quantized to `dtype`.  The slow
-    head is tied to `embeddings` unless `output.weight` ships (slow_ar.rs:216-221); the
-    fast AR has no QK-norm (its tensors decide, fast_ar.rs:53-65)."""
-    if "fast_project_in.weight" in w:
-        raise NotImplementedError("fast_project_in: this checkpoint's fast AR is narrower than the slow AR")
+    head is tied to `embeddings` unless `output.weight` ships (slow_ar.rs:213-221), and the
+    token embedding gathers the dense `embeddings.weight` either way (slow_ar.rs:117; a
+    GGUF bag holds that table only quantized, and then the embedding dequantizes its
+    rows).  qkv / o bias and QK-norm of each stack come from its tensors (slow_ar.rs:86-98,
+    fast_ar.rs:53-65); a `fast_project_in` maps the slow hidden onto a narrower fast AR
+    (slow_ar.rs:230-243)."""
     Ls, Lf = _fish_layers(w, "layers"), _fish_layers(w, "fast_layers")
     emb = w["embeddings.weight"]
     vocab, dim = emb.shape
@@ -385,15 +403,19 @@ def fish_engines(w: dict, n_codebooks: int = 10, semantic_begin: int = 151678, s
     cfg = fish_s2_slow_ar_config(n_layers=Ls, max_seq=max_seq, max_batch=max_batch, dtype=dtype, n_codebooks=n_codebooks,
                                  dim=dim, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, intermediate=inter,
                                  vocab=vocab, codebook_size=cb.shape[0] // n_codebooks, semantic_begin=semantic_begin,
-                                 semantic_end=semantic_end,
-                                 qk_norm=int("layers.0.attention.q_norm.weight" in w))
-    if "output.weight" in w:
-        raise NotImplementedError("an untied slow head (output.weight): the engine's Fish embedding is the head table")
+                                 semantic_end=semantic_end, tied_embedding=int("output.weight" not in w),
+                                 **_attn_flags(w, "layers"))
     slow = SlowAr(cfg, device=device)
     _wire_fish(slow, w, "layers", Ls, dtype, bool(cfg.qk_norm))
-    slow.set_linear(-1, HEAD, _q(w, "embeddings.weight", dtype))
+    slow.set_linear(-1, HEAD, _q(w, "output.weight" if "output.weight" in w else "embeddings.weight", dtype))
+    if not isinstance(emb, QTensor):
+        slow.set_vector(-1, EMBED, emb)
+    elif not cfg.tied_embedding:
+        raise ValueError("embeddings.weight is quantized but the head is output.weight: no table to embed from")
     slow.set_vector(-1, FINAL_NORM, w["norm.weight"])
     slow.set_vector(-1, CODEBOOK_EMBED, cb)
+    if "fast_project_in.weight" in w:
+        slow.set_project_in(_q(w, "fast_project_in.weight", dtype), w.get("fast_project_in.bias"))
     fe = w["fast_embeddings.weight"]
     fo = w["fast_output.weight"]
     fw = w["fast_layers.0.attention.wqkv.weight"]
@@ -402,8 +424,7 @@ def fish_engines(w: dict, n_codebooks: int = 10, semantic_begin: int = 151678, s
                                   max_batch=max_batch, dtype=dtype, dim=fe.shape[1], n_heads=f_heads,
                                   n_kv_heads=(fw.shape[0] - f_heads * hd) // (2 * hd), head_dim=hd,
                                   intermediate=w["fast_layers.0.feed_forward.w1.weight"].shape[0],
-                                  embed_rows=fe.shape[0],
-                                  qk_norm=int("fast_layers.0.attention.q_norm.weight" in w))
+                                  embed_rows=fe.shape[0], **_attn_flags(w, "fast_layers"))
     fast = FastAr(fcfg, device=device)
     _wire_fish(fast, w, "fast_layers", Lf, dtype, bool(fcfg.qk_norm))
     fast.set_linear(-1, HEAD, _q(w, "fast_output.weight", dtype))

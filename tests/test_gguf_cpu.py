@@ -188,7 +188,10 @@ def test_errors():
 
 def test_fish_projection_names():
     assert is_fish_projection("layers.3.attention.wqkv.weight") and is_fish_projection("fast_layers.0.feed_forward.w2.weight")
-    assert is_fish_projection("embeddings.weight") and is_fish_projection("fast_output.weight")
+    assert is_fish_projection("output.weight") and is_fish_projection("fast_output.weight")
+    assert is_fish_projection("fast_project_in.weight")
+    # embeddings.weight stays a dense table: the token embedding gathers it (slow_ar.rs:117)
     for n in ("layers.3.attention_norm.weight", "codebook_embeddings.weight", "fast_embeddings.weight",
-              "layers.0.attention.q_norm.weight", "norm.weight"):
+              "layers.0.attention.q_norm.weight", "norm.weight", "embeddings.weight", "layers.0.attention.wo.bias",
+              "fast_project_in.bias"):
         assert not is_fish_projection(n)

@@ -47,8 +47,8 @@ def _fast_cfg(max_batch):
                                     n_heads=4, n_kv_heads=2, head_dim=64, intermediate=512)
 
 
-def _slow_cfg(max_batch):
-    return D.fish_s2_slow_ar_config(n_layers=2, max_seq=40, max_batch=max_batch, vocab=400, dim=256, n_heads=4,
+def _slow_cfg(max_batch, dim=256):
+    return D.fish_s2_slow_ar_config(n_layers=2, max_seq=40, max_batch=max_batch, vocab=400, dim=dim, n_heads=4,
                                     n_kv_heads=2, head_dim=64, intermediate=512, n_codebooks=NCB, codebook_size=R,
                                     semantic_begin=BEGIN, semantic_end=BEGIN + R - 1)
 
@@ -188,12 +188,26 @@ def _replay_drive(slow, fast, prompts, outs, n_frames):
     return slow_logits, fast_logits, hid
 
 
-@pytest.mark.parametrize("stop_from_run", [False, True])
-def test_drive_batch_matches_oracle_draws(cuda, model_oracle, stop_from_run):
+# "project_in": a slow AR of width 512 over the 256-wide fast AR, joined by a Q4_K
+# fast_project_in with bias (slow_ar.rs:230-243), as in the s2_pro() default geometry
+# (a 1024-wide fast AR under the 2560-wide slow one, common/config.rs:213-226).
+@pytest.mark.parametrize("variant", ["plain", "stop_from_run", "project_in"])
+def test_drive_batch_matches_oracle_draws(cuda, model_oracle, variant):
+    stop_from_run = variant == "stop_from_run"
     n, max_new = 2, 10
-    scfg, fcfg = _slow_cfg(n), _fast_cfg(n)
+    scfg, fcfg = _slow_cfg(n, dim=512 if variant == "project_in" else 256), _fast_cfg(n)
     slow, WS = _build(scfg, cuda, 41, n, cls=D.SlowAr)
     fast, WF = _build(fcfg, cuda, 42, n, cls=D.FastAr)
+    if variant == "project_in":
+        from syrinx_amd import GgmlDType, QMatMul, QTensor
+        rng_p = np.random.default_rng(44)
+        wp = (rng_p.standard_normal((fcfg.dim, scfg.dim)) * 0.05).astype(np.float32)
+        bp = (rng_p.standard_normal(fcfg.dim) * 0.02).astype(np.float32)
+        qt = QTensor.quantize(torch.from_numpy(wp).to(cuda), GgmlDType.Q4K)
+        slow.set_project_in(QMatMul.from_qtensor(qt), torch.from_numpy(bp))
+        WS["project_in"] = qt.data().cpu().numpy().reshape(fcfg.dim, -1)
+        WS["project_in_bias"] = bp
+        assert slow.hidden_dim == fcfg.dim
     rng = np.random.default_rng(43)
     prompts = []
     for T in (5, 9):

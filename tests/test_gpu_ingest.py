@@ -163,27 +163,43 @@ def test_cv2_engine_from_checkpoint_matches_oracle(cuda, tmp_path, ora, model_or
 FD, FNH, FNKV, FI, FV, R, NCB, BEGIN = 256, 4, 2, 512, 400, 128, 6, 200
 
 
-def _fish_checkpoint(d):
+SD_FULL = 512  # the "full" variant's slow width (its fast AR stays FD wide, joined by fast_project_in)
+
+
+def _fish_checkpoint(d, variant="plain"):
+    """A sharded s2 checkpoint.  "full": the slow stack also carries wqkv.bias and
+    wo.bias, an untied text_model.lm_head, and a fast AR narrower than the slow AR
+    behind fast_project_in (weight and bias) -- every variant the reference's loader
+    detects from the tensors (slow_ar.rs:86-98, :213-243)."""
     g = torch.Generator().manual_seed(11)
     bf = torch.bfloat16
+    full = variant == "full"
+    SD = SD_FULL if full else FD
     t = {}
-    for base, n, qk in (("text_model.model.layers", 2, True), ("audio_decoder.layers", 2, False)):
+    for base, n, qk, D_ in (("text_model.model.layers", 2, True, SD), ("audio_decoder.layers", 2, False, FD)):
         for l in range(n):
             p = f"{base}.{l}"
-            t[f"{p}.attention.wqkv.weight"] = _rand(g, (FNH + 2 * FNKV) * HD, FD, dtype=bf)
-            t[f"{p}.attention.wo.weight"] = _rand(g, FD, FNH * HD, dtype=bf)
-            t[f"{p}.feed_forward.w1.weight"] = _rand(g, FI, FD, dtype=bf)
-            t[f"{p}.feed_forward.w3.weight"] = _rand(g, FI, FD, dtype=bf)
-            t[f"{p}.feed_forward.w2.weight"] = _rand(g, FD, FI, dtype=bf)
-            t[f"{p}.attention_norm.weight"] = _rand(g, FD, std=0.1, mean=1.0, dtype=bf)
-            t[f"{p}.ffn_norm.weight"] = _rand(g, FD, std=0.1, mean=1.0, dtype=bf)
+            t[f"{p}.attention.wqkv.weight"] = _rand(g, (FNH + 2 * FNKV) * HD, D_, dtype=bf)
+            t[f"{p}.attention.wo.weight"] = _rand(g, D_, FNH * HD, dtype=bf)
+            t[f"{p}.feed_forward.w1.weight"] = _rand(g, FI, D_, dtype=bf)
+            t[f"{p}.feed_forward.w3.weight"] = _rand(g, FI, D_, dtype=bf)
+            t[f"{p}.feed_forward.w2.weight"] = _rand(g, D_, FI, dtype=bf)
+            t[f"{p}.attention_norm.weight"] = _rand(g, D_, std=0.1, mean=1.0, dtype=bf)
+            t[f"{p}.ffn_norm.weight"] = _rand(g, D_, std=0.1, mean=1.0, dtype=bf)
             if qk:
                 t[f"{p}.attention.q_norm.weight"] = _rand(g, HD, std=0.1, mean=1.0, dtype=bf)
                 t[f"{p}.attention.k_norm.weight"] = _rand(g, HD, std=0.1, mean=1.0, dtype=bf)
-    t["text_model.model.embeddings.weight"] = _rand(g, FV, FD, dtype=bf)
-    t["text_model.model.norm.weight"] = _rand(g, FD, std=0.1, mean=1.0, dtype=bf)
+            if full and qk:
+                t[f"{p}.attention.wqkv.bias"] = _rand(g, (FNH + 2 * FNKV) * HD, std=0.05, dtype=bf)
+                t[f"{p}.attention.wo.bias"] = _rand(g, D_, std=0.05, dtype=bf)
+    t["text_model.model.embeddings.weight"] = _rand(g, FV, SD, dtype=bf)
+    t["text_model.model.norm.weight"] = _rand(g, SD, std=0.1, mean=1.0, dtype=bf)
+    if full:
+        t["text_model.lm_head.weight"] = _rand(g, FV, SD, dtype=bf)
+        t["fast_project_in.weight"] = _rand(g, FD, SD, std=0.05, dtype=bf)
+        t["fast_project_in.bias"] = _rand(g, FD, std=0.05, dtype=bf)
     t["audio_decoder.embeddings.weight"] = _rand(g, R, FD, std=0.5, dtype=bf)
-    t["audio_decoder.codebook_embeddings.weight"] = _rand(g, NCB * R, FD, std=0.5, dtype=bf)
+    t["audio_decoder.codebook_embeddings.weight"] = _rand(g, NCB * R, SD, std=0.5, dtype=bf)
     t["audio_decoder.norm.weight"] = _rand(g, FD, std=0.1, mean=1.0, dtype=bf)
     t["audio_decoder.output.weight"] = _rand(g, R, FD, dtype=bf)
     t["audio_tower.conv.weight"] = _rand(g, 4, 4)  # multimodal encoders are dropped
@@ -196,15 +212,20 @@ def _fish_checkpoint(d):
     return t
 
 
-def test_fish_engines_from_sharded_checkpoint_match_oracle(cuda, tmp_path, ora, model_oracle):
-    src = _fish_checkpoint(tmp_path)
+@pytest.mark.parametrize("variant", ["plain", "full"])
+def test_fish_engines_from_sharded_checkpoint_match_oracle(cuda, tmp_path, ora, model_oracle, variant):
+    src = _fish_checkpoint(tmp_path, variant)
+    full = variant == "full"
+    SD = SD_FULL if full else FD
     w = I.load_fish_lm(str(tmp_path), device=cuda)
     assert "audio_tower.conv.weight" not in w and all(v.dtype == torch.float32 for v in w.values())
     slow, fast = I.fish_engines(w, n_codebooks=NCB, semantic_begin=BEGIN, semantic_end=BEGIN + R - 1, max_seq=16,
                                 max_batch=1, dtype=GgmlDType.Q4K, device=cuda)
     assert (slow.cfg.n_layers, slow.cfg.dim, slow.cfg.n_heads, slow.cfg.n_kv_heads, slow.cfg.head_dim,
-            slow.cfg.vocab, slow.cfg.codebook_size, slow.cfg.qk_norm) == (2, FD, FNH, FNKV, HD, FV, R, 1)
-    assert (fast.cfg.n_layers, fast.cfg.vocab, fast.cfg.max_seq, fast.cfg.qk_norm) == (2, R, NCB, 0)
+            slow.cfg.vocab, slow.cfg.codebook_size, slow.cfg.qk_norm) == (2, SD, FNH, FNKV, HD, FV, R, 1)
+    assert (slow.cfg.qkv_bias, slow.cfg.o_bias, slow.cfg.tied_embedding) == ((1, 1, 0) if full else (0, 0, 1))
+    assert (fast.cfg.n_layers, fast.cfg.vocab, fast.cfg.max_seq, fast.cfg.qk_norm, fast.cfg.o_bias) == (2, R, NCB, 0, 0)
+    assert slow.hidden_dim == FD
 
     qz = lambda k: ora.quantize(ora.Q4K, _f32(src[k]))  # noqa: E731
     tally = _Tally()
@@ -220,10 +241,17 @@ def test_fish_engines_from_sharded_checkpoint_match_oracle(cuda, tmp_path, ora, 
             if n_cb:
                 W[("q_norm", l)] = _f32(src[f"{p}.attention.q_norm.weight"])
                 W[("k_norm", l)] = _f32(src[f"{p}.attention.k_norm.weight"])
-        if n_cb:  # the slow head is tied to the embeddings; MCF codebook table
-            W["head"] = qz("text_model.model.embeddings.weight")
+            if n_cb and full:
+                W[("bqkv", l)] = _f32(src[f"{p}.attention.wqkv.bias"])
+                W[("bo", l)] = _f32(src[f"{p}.attention.wo.bias"])
+        if n_cb:  # the slow head (tied to the embeddings unless lm_head ships); MCF over the dense table
+            W["head"] = qz("text_model.lm_head.weight" if full else "text_model.model.embeddings.weight")
+            W["embed"] = _f32(src["text_model.model.embeddings.weight"])
             W["final_norm"] = _f32(src["text_model.model.norm.weight"])
             W["codebook"] = _f32(src["audio_decoder.codebook_embeddings.weight"])
+            if full:
+                W["project_in"] = qz("fast_project_in.weight")
+                W["project_in_bias"] = _f32(src["fast_project_in.bias"])
         else:
             W["head"] = qz("audio_decoder.output.weight")
             W["final_norm"] = _f32(src["audio_decoder.norm.weight"])
@@ -232,10 +260,11 @@ def test_fish_engines_from_sharded_checkpoint_match_oracle(cuda, tmp_path, ora, 
         eng.reset(1)
         if n_cb:
             for frame in ([BEGIN + 3, 1, 2, 3, 4, 5, 6], [17, 0, 0, 0, 0, 0, 0], [BEGIN + 100, 9, 8, 7, 6, 5, 4]):
-                lg, _, hid = eng.step(ids=torch.tensor([frame], dtype=torch.int32), want_hidden=True)
+                lg, hid = eng.slow_step_batch(torch.tensor([frame], dtype=torch.int32), graph=False)
                 want = orc.step_one(0, frame=np.array(frame))
                 _check(lg[0].cpu().numpy(), orc, want, f"slow frame {frame[0]}", tally)
-                _check(hid[0].cpu().numpy(), orc, orc.hidden, "slow hidden")
+                _check(hid.reshape(-1).cpu().numpy(), orc, orc.hidden, "slow hidden (through fast_project_in)"
+                       if full else "slow hidden")
         else:
             h0 = np.random.default_rng(5).standard_normal(FD).astype(np.float32)
             lg, _ = eng.step(embeds=torch.from_numpy(h0)[None])
@@ -262,6 +291,7 @@ def test_fish_engines_from_gguf_equal_engines_from_checkpoint(cuda, tmp_path, or
     assert c.tensor_infos[name].ggml_dtype == int(GgmlDType.Q4K) and c.tensor_infos[name].shape == (FD, FI)
     assert bytes(c.tensor_bytes(name)) == ora.quantize(ora.Q4K, _f32(src[f"text_model.model.{name}"])).tobytes()
     assert c.tensor_infos["norm.weight"].ggml_dtype == 0
+    assert c.tensor_infos["embeddings.weight"].ggml_dtype == 0  # the dense table the embedding gathers
     g = I.load_fish_gguf(path, device=cuda)
     kw = dict(n_codebooks=NCB, semantic_begin=BEGIN, semantic_end=BEGIN + R - 1, max_seq=16, max_batch=1,
               dtype=GgmlDType.Q4K, device=cuda)

@@ -133,6 +133,11 @@ CASES = [
     (G.Q4K, 19456, 2560, 16),  # Qwen3-4B fused w1|w3 at the 16-stream batch
     (G.Q4K, 16400, 512, 7),    # last workgroup: one live tile, the other clamped
     (G.Q4K, 16389, 1024, 5),   # last workgroup: five live rows
+    # Q8_0 at the Qwen3-4B widths: tall matrices with a partial last workgroup
+    (G.Q8_0, 16389, 2560, 1),
+    (G.Q8_0, 19456, 2560, 1),  # Qwen3-4B fused w1|w3
+    (G.Q8_0, 2560, 9728, 1),   # w2 (K = 9728: 304 blocks per row)
+    (G.Q8_0, 16389, 2560, 3),
 ]
 
 
@@ -238,18 +243,20 @@ def test_concurrent_forward_on_one_handle(cuda, ora):
         _eq_bits(o, wnt)
 
 
-def test_full_size_tied_head_q4k(cuda, ora):
-    # The Qwen3-4B tied LM head [155776 x 2560] at full size, bit-exact on every row.
+@pytest.mark.parametrize("dt", [G.Q4K, G.Q8_0])
+def test_full_size_tied_head(cuda, ora, dt):
+    # The Qwen3-4B tied LM head [155776 x 2560] at full size, bit-exact on every row (Q8_0:
+    # the 424 MB head of the Q8_0 decode configuration).
     n, k = 155776, 2560
     g = torch.Generator(device=cuda).manual_seed(11)
     w = torch.randn(n, k, device=cuda, generator=g) * 0.02
-    qt = QTensor.quantize(w, G.Q4K)
+    qt = QTensor.quantize(w, dt)
     del w
     qmm = QMatMul.from_qtensor(qt)
     x = _acts(1, k, 12)
     y = qmm.forward(torch.from_numpy(x).to(cuda)).cpu().numpy()
     blocks = qt.data().cpu().numpy().reshape(n, -1)
-    _eq_bits(y, ora.matmul(ora.Q4K, x, blocks))
+    _eq_bits(y, ora.matmul(int(dt), x, blocks))
 
 
 # ------------------------------------------------------------------ prefill GEMM (MFMA)
@@ -257,6 +264,12 @@ PREFILL = [
     (300, 512, 200),     # rows and outputs not multiples of the 128 x 128 tile, with bias
     (6144, 2560, 512),   # Qwen3-4B fused wqkv at a 512-token prompt
     (2560, 9728, 128),   # down projection, K = 9728 (38 blocks)
+    # the other three projections of a Qwen3-4B layer at 512 tokens, each with the split
+    # plan the default forward picks: wo and w2 split K six ways (40 tiles for 256 CUs),
+    # the fused w1|w3 runs 256 whole tiles and splits the remaining 48 five ways
+    (2560, 4096, 512),   # wo
+    (19456, 2560, 512),  # w1|w3
+    (2560, 9728, 512),   # w2
 ]
 
 
@@ -359,7 +372,11 @@ def test_prefill_gemm_within_f16_rounding_bound(cuda, ora, n, k, m):
     assert (err <= tol).all(), f"{int((err > tol).sum())} outputs beyond the bound; worst ratio {float((err / tol).max()):.3g}"
     # typical error, relative to the output scale
     rel = float(np.sqrt(np.mean(err ** 2)) / np.sqrt(np.mean(y64 ** 2)))
+    print(f"prefill GEMM [{n}x{k}] at {m} rows: rms rel err {rel:.2e}, worst/bound {float((err / tol).max()):.3f}")
     assert rel < 2e-3, rel
+    # the split partials are added in a fixed order: a second call gives the same bits
+    y2 = qmm.forward(xt, bias=None if b is None else torch.from_numpy(b).to(cuda)).cpu().numpy()
+    _eq_bits(y2, y.astype(np.float32))
     # the exact path stays available and bit-identical for the same call
     if m <= 200:
         y_exact = qmm.forward(xt, bias=None if b is None else torch.from_numpy(b).to(cuda), exact=True).cpu().numpy()
