@@ -28,7 +28,10 @@ CPU baseline:
                 sums), graph-replayed, against the 2.5 PFLOP/s dense f16 peak;
   skinny_batch  16 concurrent streams, ragged KV lengths uniform over 256..2048;
   fish_frame    Fish s2-pro dual-AR frames at batch 1: the slow step + the semantic draw +
-                the 4-layer fast AR's 10 codebook positions with nine device draws.
+                the 4-layer fast AR's 10 codebook positions with nine device draws;
+  cv_generate   CosyVoice2 speech-token generation (Qwen2Lm::generate) on the device: the
+                assembled prompt prefilled, then per token the RAS draw and the decode step
+                on the drawn id, 24 layers, Q8_0.
 
 CPU baselines (`cpu_baseline`: all threads this GPU's share of the host allows, at most
 16; `cpu_baseline_1thread`): the oracle -- the CPU restatement of Candle 0.8's generic
@@ -58,7 +61,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16/bf16 MFMA, MI355X
 Q4K, Q8_0 = 12, 8
-LINES = ("gemv_q8_0", "cv2_decode", "q8_0_decode", "prefill", "skinny_batch", "fish_frame")
+LINES = ("gemv_q8_0", "cv2_decode", "q8_0_decode", "prefill", "skinny_batch", "fish_frame", "cv_generate")
 
 
 def parse():
@@ -72,12 +75,14 @@ def parse():
     ap.add_argument("--gemv-iters", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--only", default=",".join(LINES), help="comma-separated extra lines to run")
-    ap.add_argument("--mode", default="decode", choices=["decode", "decode1", "gemv", "copy", "prefill", "frame"])
+    ap.add_argument("--mode", default="decode",
+                    choices=["decode", "decode1", "gemv", "copy", "prefill", "frame", "generate", "hash"])
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--prefill-iters", type=int, default=20)
     ap.add_argument("--skinny-batch", type=int, default=16)
     ap.add_argument("--skinny-steps", type=int, default=64)
     ap.add_argument("--frames", type=int, default=64, help="fish_frame line: timed frames")
+    ap.add_argument("--gen-tokens", type=int, default=256, help="cv_generate line: generated tokens")
     return ap.parse_args()
 
 
@@ -222,7 +227,7 @@ def gemv_roofline(lm, torch, iters, rows=1):
     # counters were collected for the 16-row Qwen3-4B-shape pass (the skinny-batch line)
     traffic = None
     if kernel == "k_gemv_mma_q4k_rec" and rows == 16 and c.dim == 2560 and c.n_layers == 36:
-        t = measured_traffic(SKINNY_TRAFFIC_FILE)
+        t = measured_traffic(SKINNY_TRAFFIC_FILE, kernel)
         traffic = None if t is None else round(t)
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -235,17 +240,42 @@ def gemv_roofline(lm, torch, iters, rows=1):
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv2_q4k_qwen3_4b_decode_traffic.txt")
 SKINNY_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv_mma_q4k_rec_qwen3_4b_16stream_traffic.txt")
 
+# The sources each measured kernel is built from: a counter summary records their hash,
+# and a summary whose hash differs from the sources in this tree is stale (not reported).
+_CSRC = os.path.join(ROOT, "syrinx_amd", "csrc")
+_COMMON = ("sxq_common.h", "sxq_kernels.h", "sxq_quant_dev.h", "sxq_sync_dev.h")
+KERNEL_SOURCES = {
+    "k_gemv2_q4k": ("sxq_gemv.hip", "sxq_gemv_dev.h") + _COMMON,
+    "k_gemv_mma_q4k_rec": ("sxq_gemv.hip", "sxq_gemv_dev.h") + _COMMON,
+    "k_gemm_q4k": ("sxq_gemm.hip",) + _COMMON,
+}
 
-def measured_traffic(path=TRAFFIC_FILE):
-    """HBM bytes per GEMV launch from a committed counter summary."""
+
+def kernel_sources_sha256(kernel):
+    import hashlib
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES[kernel]:
+        with open(os.path.join(_CSRC, name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
+def measured_traffic(path=TRAFFIC_FILE, kernel="k_gemv2_q4k"):
+    """HBM bytes per GEMV launch from a committed counter summary, or None when the
+    summary is missing or was measured on other kernel sources than this tree's."""
+    vals = {}
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
+                k, sep, v = line.partition(":")
+                if sep and k in ("traffic_bytes_per_launch", "kernel_sources_sha256"):
+                    vals[k] = v.strip()
     except OSError:
-        pass
-    return None
+        return None
+    if vals.get("kernel_sources_sha256") != kernel_sources_sha256(kernel):
+        log(f"{os.path.basename(path)}: measured on other {kernel} sources than these; traffic not reported")
+        return None
+    return float(vals["traffic_bytes_per_launch"]) if "traffic_bytes_per_launch" in vals else None
 
 
 def timed_decode(lm, torch, frame, kv, steps, warmup, batch=1):
@@ -531,6 +561,46 @@ def fish_frames(D, torch, kv, frames, warmup, cpu, n=1):
     return res
 
 
+def cv_generate(D, torch, tokens, cpu):
+    """CosyVoice2 Qwen2Lm::generate on the device (syrinx_amd.generate): the step-0 input
+    [sos, 64 text rows, task_id, 160 prompt-speech rows] prefilled, then `tokens` tokens,
+    each a RAS draw on the device followed by a graph-replayed decode step on the drawn
+    id (the stop ids masked throughout -- min_len = max_len -- so the length is fixed).
+    Timed by the host clock around the whole call (prefill included; the loop reads one
+    id per token)."""
+    from syrinx_amd.generate import COSYVOICE2, CosyVoiceLm
+    dev = torch.device("cuda:0")
+    n_text, n_prompt = 64, 160
+    lm = build_model(D, torch, "cv2", Q8_0, 2 + n_text + n_prompt + tokens + 8, 1)
+    g = torch.Generator(device=dev).manual_seed(9)
+    c = lm.cfg
+    speech = torch.randn(c.embed_rows, c.dim, device=dev, generator=g) * 0.02
+    lm.set_vector(-1, D.EMBED, speech)
+    cv = CosyVoiceLm(lm, torch.randn(4096, c.dim, device=dev, generator=g) * 0.02, speech,
+                     torch.randn(2, c.dim, device=dev, generator=g) * 0.02, COSYVOICE2)
+    text = [(i * 37) % 4096 for i in range(n_text)]
+    prompt = [(i * 53) % 6561 for i in range(n_prompt)]
+    cv.generate(text, prompt, 16, 16, 1)  # warm-up: captures the step graph
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks = cv.generate(text, prompt, tokens, tokens, 1)
+    sec = time.perf_counter() - t0
+    assert len(toks) == tokens
+    lb, hb = lm.weight_bytes()
+    achieved = (lb + hb) * tokens / sec / 1e9
+    out = {"workload": f"CosyVoice2 LM (Qwen2-0.5B shape, 24 layers, Q8_0) speech-token generation: step-0 input of "
+                       f"{2 + n_text + n_prompt} rows prefilled, {tokens} tokens, each a device RAS draw (top_p 0.8, "
+                       f"top_k 25, window 10) + a graph-replayed decode step on the drawn id",
+           "value": round(tokens / sec, 2), "unit": "tok/s (prefill included)", "ms_per_token": round(sec * 1e3 / tokens, 4),
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_token": lb + hb,
+                        "kernel": "whole token (weights streamed once per step)"}}
+    if cpu:
+        out.update(cpu_layer_token(torch, dev, c, Q8_0, 1, "CosyVoice2 Q8_0"))
+    del cv, lm
+    return out
+
+
 def copy_calibration(torch, iters=8):
     """A plain device-to-device copy of 1 GiB: its counters give the FETCH/WRITE scale."""
     n = 1 << 30
@@ -580,6 +650,9 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the GEMVs would shard "
               "by output rows, one shard per GPU)", file=sys.stderr)
         sys.exit(2)
+    if args.mode == "hash":
+        print(json.dumps({k: kernel_sources_sha256(k) for k in KERNEL_SOURCES}))
+        return
     import torch
     if args.mode == "copy":
         copy_calibration(torch)
@@ -591,6 +664,9 @@ def main():
     cpu = not args.no_cpu
     if args.mode == "frame":
         print(json.dumps({"mode": "frame", "fish_frame": fish_frames(D, torch, args.kv, args.frames, 8, cpu)}))
+        return
+    if args.mode == "generate":
+        print(json.dumps({"mode": "generate", "cv_generate": cv_generate(D, torch, args.gen_tokens, cpu)}))
         return
     if args.mode == "gemv":
         dt = Q4K if args.dtype == "q4k" else Q8_0
@@ -638,6 +714,9 @@ def main():
     if "fish_frame" in only:
         lines["fish_frame"] = fish_frames(D, torch, args.kv, args.frames, 8, cpu)
         log(f"fish frames: {lines['fish_frame']['value']} frames/s")
+    if "cv_generate" in only:
+        lines["cv_generate"] = cv_generate(D, torch, args.gen_tokens, cpu)
+        log(f"cv generate: {lines['cv_generate']['value']} tok/s")
     if "prefill" in only:
         lines["prefill"] = prefill_gemms(torch, args.prefill_tokens, args.prefill_iters, cpu)
         log(f"prefill: {lines['prefill']['us_per_layer']} us/layer, {lines['prefill']['value']} TFLOP/s")

@@ -100,6 +100,15 @@ def cosyvoice2_lm_config(n_layers=24, max_seq=1024, max_batch=1, dtype=GgmlDType
     return DecoderConfig(**base)
 
 
+def cosyvoice3_lm_config(n_layers=24, max_seq=1024, max_batch=1, dtype=GgmlDType.Q8_0, **kw) -> DecoderConfig:
+    """CosyVoice3 LM (crates/syrinx-lm/src/cv3/mod.rs:44-68, lm.rs:143-147): the CosyVoice2
+    Qwen2-0.5B body with a bias-free llm_decoder [6761 x 896] (6561 speech ids + 200
+    control ids) and a 6761-row speech_embedding, which also holds the sos / task_id rows."""
+    base = dict(head_bias=0, vocab=6761, embed_rows=6761)
+    base.update(kw)
+    return cosyvoice2_lm_config(n_layers=n_layers, max_seq=max_seq, max_batch=max_batch, dtype=dtype, **base)
+
+
 def fish_s2_fast_ar_config(n_layers=4, num_codebooks=10, residual_size=4096, max_batch=1, dtype=GgmlDType.Q4K,
                            **kw) -> DecoderConfig:
     """The s2-pro fast AR (the audio decoder, crates/syrinx-fish/src/s2/fast_ar.rs:1-66):

@@ -153,7 +153,8 @@ def cv2_engine(bag: Cv2Weights, max_seq: int = 1024, max_batch: int = 1, device=
     dt = bag.qmm[f"{pre}.0.self_attn.q_proj.weight"].dtype()
     cfg = cosyvoice2_lm_config(n_layers=L, max_seq=max_seq, max_batch=max_batch, dtype=dt, dim=q0[1],
                                n_heads=q0[0] // hd, n_kv_heads=k0[0] // hd, head_dim=hd, intermediate=gate[0],
-                               vocab=head[0], embed_rows=speech.rows_count if speech is not None else head[0] + 3)
+                               vocab=head[0], embed_rows=speech.rows_count if speech is not None else head[0] + 3,
+                               head_bias=int("llm_decoder.bias" in bag.w))
     lm = Qwen2Lm(cfg, device=device)
     for l in range(L):
         p = f"{pre}.{l}"
@@ -164,11 +165,25 @@ def cv2_engine(bag: Cv2Weights, max_seq: int = 1024, max_batch: int = 1, device=
                          (ATTN_NORM, "input_layernorm.weight"), (FFN_NORM, "post_attention_layernorm.weight")):
             lm.set_vector(l, slot, bag.w[f"{p}.{nm}"])
     lm.set_linear(-1, HEAD, bag.qmm["llm_decoder.weight"])
-    lm.set_vector(-1, HEAD_BIAS, bag.w["llm_decoder.bias"])
+    if cfg.head_bias:  # CosyVoice3's llm_decoder is bias-free (cv3/lm.rs:143-147)
+        lm.set_vector(-1, HEAD_BIAS, bag.w["llm_decoder.bias"])
     lm.set_vector(-1, FINAL_NORM, bag.w["llm.model.model.norm.weight"])
     if speech is not None:
         lm.set_embed_quantized(speech)
     return lm
+
+
+def cosyvoice_lm(bag: Cv2Weights, max_seq: int = 1024, device="cuda:0"):
+    """Qwen2Lm (CosyVoice2) or Cv3Lm (CosyVoice3, told apart by the 6761-row bias-free head)
+    ready to generate: cv2_engine over the bag plus its embedding tables (QEmbeds or dense)."""
+    from .generate import COSYVOICE2, COSYVOICE3, CosyVoiceLm
+    lm = cv2_engine(bag, max_seq=max_seq, max_batch=1, device=device)
+    variant = COSYVOICE2 if lm.cfg.head_bias else COSYVOICE3
+
+    def table(name):
+        return bag.qembed.get(name, bag.w.get(name))
+    return CosyVoiceLm(lm, table("llm.model.model.embed_tokens.weight"), table("speech_embedding.weight"),
+                       table("llm_embedding.weight"), variant)
 
 
 # --------------------------------------------------------------------------- Fish s2
@@ -433,6 +448,6 @@ def fish_engines(w: dict, n_codebooks: int = 10, semantic_begin: int = 151678, s
     return slow, fast
 
 
-__all__ = ["DecoderConfig", "load_cv2_quantized", "cv2_engine", "load_fish_lm", "fish_engines", "save_fish_gguf",
+__all__ = ["DecoderConfig", "load_cv2_quantized", "cv2_engine", "cosyvoice_lm", "load_fish_lm", "fish_engines", "save_fish_gguf",
            "load_fish_gguf", "is_fish_projection", "remap_qwen3_key",
            "resolve_shards", "fuse_qkv", "cv2_policy", "Footprint", "Cv2Weights"]
