@@ -334,13 +334,17 @@ sxq_status sxq_lm_prefill_trace_floats(const sxq_lm *lm, int64_t tokens, size_t 
  * A decode loop samples each step's logits on the GPU and writes the token straight into
  * the next step's ids, so only token ids (not logit rows) ever cross to the host.  Each
  * stream has its own SplitMix64 state (rng[s], device uint64, seeded by the caller with the
- * reference's seed and advanced per draw exactly as the reference advances it).  On the
- * device top_k must be 1..64 and RAS windows at most 64 ids.  out[s * out_stride] receives
- * stream s's token (an ids frame's semantic slot, say). */
+ * reference's seed and advanced per draw exactly as the reference advances it).  The Fish
+ * draws take any top_k >= 0 (0 = unbounded, common/sampling.rs:50-52); beyond 64 kept
+ * candidates the top-p cut is decided on fixed-point (2^-60) masses rather than the
+ * reference's f64 running sum, which can differ only when that sum lands within ~n * 2^-60
+ * of top_p.  The CosyVoice draw takes top_k 1..64 (its reference pins 25); RAS windows hold
+ * at most 64 ids.  out[s * out_stride] receives stream s's token (an ids frame's semantic
+ * slot, say). */
 typedef struct {
     float temperature;        /* softmax temperature of the normal draw */
     float top_p;              /* nucleus cutoff */
-    int32_t top_k;            /* candidate cap, 1..64 */
+    int32_t top_k;            /* candidate cap; 0 = unbounded */
     float repetition_penalty; /* codebook draws: divides positive / multiplies negative logits of `recent` ids; 1 = off */
     int32_t ras_win_size;     /* semantic draws: RAS window (recent semantic ids), <= 64 */
     float ras_high_temp;      /* RAS fallback draw */

@@ -976,7 +976,7 @@ sxq_status sxq_fish_fast_expand(sxq_lm* lm, int n, const float* hidden, const in
     if (n_codes < 1 || n_codes > c.max_seq)
         return fail(SXQ_ERR_INVALID, "fast_expand: %d codes per frame (the local cache holds %d)", n_codes, c.max_seq);
     if (semantic_stride < 1 || codes_stride < 1) return fail(SXQ_ERR_INVALID, "fast_expand: strides must be >= 1");
-    if (!fish_sampling_fits(*params)) return fail(SXQ_ERR_INVALID, "fast_expand: top_k %d outside 1..64", params->top_k);
+    if (!fish_sampling_fits(*params)) return fail(SXQ_ERR_INVALID, "fast_expand: top_k %d is negative", params->top_k);
     std::lock_guard<std::mutex> lock(lm->mu);
     if (lm->trace) return fail(SXQ_ERR_INVALID, "fast_expand: clear the step trace first");
     DeviceGuard g(lm->device);

@@ -16,7 +16,18 @@
 // device to its top_k (key, id) pairs in the reference's order -- key descending, ties by
 // ascending id -- by a radix select over the ordered key bits (4 passes of 8-bit digit
 // histograms, then a compaction that takes ties at the cut in id order), and the
-// reference's per-candidate float steps then run on one lane in its order.  Sums over the
+// reference's per-candidate float steps then run on one lane in its order.
+//
+// A Fish draw whose top_k is 0 (unbounded, common/sampling.rs:50-52) or above the 64
+// candidates one wave sorts keeps however many leading ids its top-p rule keeps: the cut is
+// found by a second radix descent that carries, per digit bin, the softmax mass of its
+// ids (as 2^-60 fixed-point integers, so the sums are exact and independent of the order
+// of the atomics; each mass is truncated by < 2^-60, so a top-p decision can differ from
+// the reference's f64 running sum only when that sum lands within ~n * 2^-60 of top_p).
+// When that keeps fewer than 64 ids the wave path above runs on them (the reference's
+// exact order); otherwise the whole workgroup draws over the kept ids in place: f64
+// normaliser, f32 probabilities, the inverse-CDF walk in id order (sums per contiguous
+// chunk of ids, then over the chunks in order).  Sums over the
 // whole row (softmax normalisers, the full-distribution draw) are f64 as in the reference,
 // added in a fixed tree order here rather than left to right (a difference below 1e-15
 // relative, which moves a draw only when the uniform lands that close to a boundary).
@@ -67,6 +78,7 @@ struct View {
 
 struct Shared {
     unsigned hist[256];
+    unsigned long long hmass[256];  // fixed-point softmax mass per digit bin (the top-p cut)
     float fred[kST / 64];
     double dred[kST / 64];
     unsigned wsum[kST / 64];
@@ -82,6 +94,7 @@ struct Shared {
     int need, result;
     double dval;
     float fval;
+    unsigned long long msel;  // mass before the selected bin (the top-p cut)
 };
 
 // Inclusive prefix sum over the 64 lanes of a wave.
@@ -132,12 +145,17 @@ SXQ_DEV double block_sum(double v, Shared& sh) {
     return sh.dval;
 }
 
-// The K largest keys of the view (key(e) a functor over element index), in the
-// reference's sort order, into sh.top_key / sh.top_id; returns K' = min(K, count).
+// The kept set of a draw in the reference's sort order (key descending, ties by id): every
+// element whose order key exceeds `key`, then the first `ties` (in id order) equal to it.
+struct Cut {
+    uint32_t key;
+    int ties;
+};
+
+// The cut of the K largest keys of the view (K <= count) by a radix descent on counts.
 template <class KeyF>
-SXQ_DEV int top_k_select(const View& v, KeyF key, int K, Shared& sh) {
+SXQ_DEV Cut count_cut(const View& v, KeyF key, int K, Shared& sh) {
     const int n = v.count(), tid = threadIdx.x;
-    K = min(K, n);
     uint32_t prefix = 0, mask = 0;
     int rem = K;
     for (int d = 24; d >= 0; d -= 8) {
@@ -173,6 +191,18 @@ SXQ_DEV int top_k_select(const View& v, KeyF key, int K, Shared& sh) {
         rem = sh.need;
         __syncthreads();
     }
+    return Cut{prefix, rem};
+}
+
+// The K largest keys of the view (key(e) a functor over element index), in the
+// reference's sort order, into sh.top_key / sh.top_id; returns K' = min(K, count).
+template <class KeyF>
+SXQ_DEV int top_k_select(const View& v, KeyF key, int K, Shared& sh) {
+    const int n = v.count(), tid = threadIdx.x;
+    K = min(K, n);
+    const Cut cut = count_cut(v, key, K, sh);
+    const uint32_t prefix = cut.key;
+    const int rem = cut.ties;
     // prefix = the K-th largest key; `rem` of the elements equal to it are taken, the
     // ones with the smallest ids: thread t scans the contiguous elements [t*c, t*c + c).
     const int chunk = (n + kST - 1) / kST, e0 = tid * chunk, e1 = min(n, e0 + chunk);
@@ -275,6 +305,229 @@ SXQ_DEV int fish_draw(Shared& sh, int K, double total, float mx, float temperatu
     return tok;
 }
 
+constexpr double kFix = 1152921504606846976.0;  // 2^60: the fixed-point unit of a softmax mass
+
+// The float whose order key is u.
+SXQ_DEV float key_float(uint32_t u) { return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u); }
+
+SXQ_DEV unsigned long long mass_q(float k, float mx, double tot) {
+    return (unsigned long long)(exp((double)(k - mx)) / tot * kFix);
+}
+
+// The ids logits_to_probs keeps by its top-p rule alone -- rank 0, then every rank whose
+// softmax mass before it (cum of exp(l - mx) / tot in sorted order) is <= top_p -- as a
+// cut, found by a radix descent on the digit bins' fixed-point masses; `kept` = their count.
+template <class KeyF>
+SXQ_DEV Cut mass_cut(const View& v, KeyF key, float mx, double tot, float top_p, Shared& sh, int& kept) {
+    const int n = v.count(), tid = threadIdx.x;
+    if (!(top_p >= 0.0f)) {  // cum 0 > top_p: rank 0 alone
+        kept = 1;
+        return count_cut(v, key, 1, sh);
+    }
+    const unsigned long long T = top_p >= 2.0f ? (1ull << 61) : (unsigned long long)((double)top_p * kFix);
+    uint32_t prefix = 0, mask = 0;
+    unsigned long long above = 0;  // mass of the elements ordered before the current prefix's
+    int cnt_above = 0;
+    for (int d = 24; d >= 0; d -= 8) {
+        for (int b = tid; b < 256; b += kST) {
+            sh.hist[b] = 0;
+            sh.hmass[b] = 0;
+        }
+        __syncthreads();
+        for (int e = tid; e < n; e += kST) {
+            const float k = key(e);
+            const uint32_t u = order_key(k);
+            if ((u & mask) == prefix) {
+                const int b = (u >> d) & 0xFF;
+                atomicAdd(&sh.hist[b], 1u);
+                const unsigned long long q = mass_q(k, mx, tot);
+                if (q) atomicAdd(&sh.hmass[b], q);
+            }
+        }
+        __syncthreads();
+        // the lowest non-empty bin whose mass before it is <= T (the non-empty bins that
+        // qualify are a prefix from the top: masses only grow down the order); lane l of
+        // wave 0 holds bins 255 - 4l .. 252 - 4l
+        if (tid < 64) {
+            const int top = 255 - 4 * tid;
+            unsigned long long m[4], msum = 0;
+            unsigned c[4], csum = 0;
+            for (int t = 0; t < 4; ++t) {
+                m[t] = sh.hmass[top - t];
+                c[t] = sh.hist[top - t];
+                msum += m[t];
+                csum += c[t];
+            }
+            unsigned long long mincl = msum;
+            unsigned cincl = csum;
+            for (int o = 1; o < 64; o <<= 1) {
+                const unsigned long long ym = __shfl_up(mincl, o, 64);
+                const unsigned yc = __shfl_up(cincl, o, 64);
+                if (tid >= o) {
+                    mincl += ym;
+                    cincl += yc;
+                }
+            }
+            unsigned long long mb = above + (mincl - msum);
+            unsigned cb = cincl - csum;
+            int best = -1;
+            unsigned long long best_m = 0;
+            unsigned best_c = 0;
+            for (int t = 0; t < 4; ++t) {
+                if (c[t] && mb <= T) {
+                    best = t;
+                    best_m = mb;
+                    best_c = cb;
+                }
+                mb += m[t];
+                cb += c[t];
+            }
+            const unsigned long long has = __ballot(best >= 0);
+            if (has && tid == 63 - __builtin_clzll(has)) {
+                sh.kth = (uint32_t)(top - best);
+                sh.need = cnt_above + (int)best_c;
+                sh.msel = best_m;
+            }
+        }
+        __syncthreads();
+        prefix |= sh.kth << d;
+        mask |= 0xFFu << d;
+        cnt_above = sh.need;
+        above = sh.msel;
+        __syncthreads();
+    }
+    // the ties at the cut, in id order: tie j has mass above + j * q before it
+    const int nties = (int)sh.hist[prefix & 0xFF];
+    const unsigned long long q = mass_q(key_float(prefix), mx, tot);
+    int ties = nties;
+    if (q) {
+        const unsigned long long j = (T - above) / q + 1;
+        if (j < (unsigned long long)nties) ties = (int)j;
+    }
+    kept = cnt_above + ties;
+    __syncthreads();
+    return Cut{prefix, ties};
+}
+
+// logits_to_probs + multinomial1 over a kept set (a cut) of any size, by the whole
+// workgroup: thread t takes the contiguous ids [t*c, t*c + c); the exponentials
+// exp(l / t - kmax) (kmax = the view's largest key / t, rank 0's), their f64 sum, the f32
+// probabilities renormalised by it and their f64 total are summed per chunk in id order,
+// then over the chunks in order; the uniform's chunk is found on thread 0 and walked by
+// its owner.  Only thread 0 advances rng.  Returns the id, or -1 (the reference's
+// fall-through, mapped by the caller).
+template <class KeyF>
+SXQ_DEV int wide_draw(const View& v, KeyF key, Cut cut, float mx, float temperature, uint64_t& rng, Shared& sh,
+                      double* chunk_sum) {
+    const int n = v.count(), tid = threadIdx.x;
+    const int chunk = (n + kST - 1) / kST, e0 = tid * chunk, e1 = min(n, e0 + chunk);
+    unsigned ties = 0;
+    for (int e = e0; e < e1; ++e) ties += order_key(key(e)) == cut.key;
+    const unsigned tie0 = block_excl_scan(ties, sh);
+    const float t = fmaxf(temperature, 1e-5f);
+    const float kmax = mx / t;
+    auto kept = [&](float k, unsigned& rank) {
+        const uint32_t u = order_key(k);
+        if (u > cut.key) return true;
+        return u == cut.key && rank++ < (unsigned)cut.ties;
+    };
+    double ps = 0.0;
+    unsigned r = tie0;
+    for (int e = e0; e < e1; ++e) {
+        const float k = key(e);
+        if (kept(k, r)) ps += exp((double)(k / t - kmax));
+    }
+    chunk_sum[tid] = ps;
+    __syncthreads();
+    if (tid == 0) {
+        double a = 0.0;
+        for (int i = 0; i < kST; ++i) a += chunk_sum[i];
+        sh.dval = a;
+    }
+    __syncthreads();
+    const double psum = sh.dval;
+    auto prob = [&](float k) {
+        float p = (float)exp((double)(k / t - kmax));
+        if (psum > 0.0) p = (float)((double)p / psum);
+        return p;
+    };
+    double ts = 0.0;
+    r = tie0;
+    for (int e = e0; e < e1; ++e) {
+        const float k = key(e);
+        if (kept(k, r)) ts += (double)prob(k);
+    }
+    __syncthreads();  // psum read by every thread before chunk_sum is reused
+    chunk_sum[tid] = ts;
+    __syncthreads();
+    if (tid == 0) {
+        double total = 0.0;
+        for (int i = 0; i < kST; ++i) total += chunk_sum[i];
+        sh.result = -1;
+        if (total <= 0.0) {
+            sh.need = -1;
+            sh.result = 0;  // multinomial1's empty distribution
+        } else {
+            const double u = splitmix_f64(rng) * total;
+            double acc = 0.0;
+            int c = 0;
+            for (; c < kST - 1 && acc + chunk_sum[c] <= u; ++c) acc += chunk_sum[c];
+            sh.need = c;
+            sh.dred[0] = acc;
+            sh.dval = u;
+        }
+    }
+    __syncthreads();
+    if (tid == sh.need) {
+        double acc = sh.dred[0];
+        r = tie0;
+        for (int e = e0; e < e1; ++e) {
+            const float k = key(e);
+            if (!kept(k, r)) continue;
+            acc += (double)prob(k);
+            if (sh.dval < acc) {
+                sh.result = v.id(e);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    const int tok = sh.result;
+    __syncthreads();
+    return tok;
+}
+
+// One Fish draw (logits_to_probs + multinomial1) by the whole workgroup.  kcap = the
+// candidate cap (top_k, or the view's size when top_k is 0).  Up to 64 candidates: the
+// top kcap are sorted and drawn on wave 0 in the reference's exact order.  A larger cap:
+// the top-p cut decides how many are kept; fewer than 64 go the wave-0 way (staged one
+// beyond the cut, so the exact running sum decides the last one), more are drawn in place.
+// The token is returned to every thread; thread 0's rng is the advanced state.
+template <class KeyF>
+SXQ_DEV int block_draw(const View& v, KeyF key, float mx, double tot, float temperature, float top_p, int kcap,
+                       uint64_t& rng, Shared& sh, double* chunk_sum) {
+    const int tid = threadIdx.x, n = v.count();
+    int K = kcap;
+    if (kcap > kMaxTopK) {
+        int kept = 0;
+        Cut cut = mass_cut(v, key, mx, tot, top_p, sh, kept);
+        if (kept >= kMaxTopK) {
+            if (kept > kcap) cut = count_cut(v, key, kcap, sh);
+            return wide_draw(v, key, cut, mx, temperature, rng, sh, chunk_sum);
+        }
+        K = min(kept + 1, n);
+    }
+    K = top_k_select(v, key, K, sh);
+    if (tid < 64) {
+        const int tok = fish_draw(sh, K, tot, mx, temperature, top_p, kcap, rng);
+        if (tid == 0) sh.result = tok;
+    }
+    __syncthreads();
+    const int tok = sh.result;
+    __syncthreads();
+    return tok;
+}
+
 struct FishArgs {
     const float* logits;
     int64_t stride;
@@ -296,6 +549,7 @@ struct FishArgs {
 template <int MODE>
 __global__ __launch_bounds__(kST) void k_sample_fish(FishArgs A) {
     __shared__ Shared sh;
+    __shared__ double chunk_sum[kST];
     const int s = blockIdx.x, tid = threadIdx.x;
     const float* row = A.logits + (int64_t)s * A.stride;
     const sxq_fish_sampling& P = A.p;
@@ -347,14 +601,13 @@ __global__ __launch_bounds__(kST) void k_sample_fish(FishArgs A) {
     double tot = 0.0;
     for (int e = tid; e < n; e += kST) tot += exp((double)(key(e) - mx));
     tot = block_sum(tot, sh);
-    const int K = top_k_select(v, key, P.top_k, sh);
-    if (tid >= 64) return;
+    const int kcap = P.top_k <= 0 ? n : min(P.top_k, n);  // k_cap: 0 = unbounded
     uint64_t rng = A.rng[s];
-    int tok = fish_draw(sh, K, tot, mx, P.temperature, P.top_p, P.top_k, rng);
+    int tok = block_draw(v, key, mx, tot, P.temperature, P.top_p, kcap, rng, sh, chunk_sum);
     if (tok < 0) tok = A.vocab - 1;
     int high = -1;
     if (MODE == 0) {
-        high = fish_draw(sh, K, tot, mx, P.ras_high_temp, P.ras_high_top_p, P.top_k, rng);
+        high = block_draw(v, key, mx, tot, P.ras_high_temp, P.ras_high_top_p, kcap, rng, sh, chunk_sum);
         if (high < 0) high = A.vocab - 1;
     }
     if (tid != 0) return;
@@ -507,10 +760,13 @@ __global__ void k_first_codes(const int32_t* __restrict__ semantic, int sem_stri
     if (codes) codes[(int64_t)s * codes_stride] = (int32_t)c;
 }
 
-sxq_status check_common(int n, int vocab, int top_k, const void* logits, const void* rng, const void* out) {
+// wide: the Fish draws, which take any top_k >= 0 (0 = unbounded); the CosyVoice draw
+// (its reference pins top_k = 25) takes 1..64.
+sxq_status check_common(int n, int vocab, int top_k, const void* logits, const void* rng, const void* out, bool wide) {
     if (n < 1 || n > 65535 || vocab < 1) return fail(SXQ_ERR_INVALID, "sample: bad shape (%d streams, %d ids)", n, vocab);
-    if (top_k < 1 || top_k > kMaxTopK)
-        return fail(SXQ_ERR_INVALID, "sample: top_k %d outside 1..%d on the device", top_k, kMaxTopK);
+    if (wide ? top_k < 0 : (top_k < 1 || top_k > kMaxTopK))
+        return fail(SXQ_ERR_INVALID, wide ? "sample: top_k %d is negative" : "sample: top_k %d outside 1..%d on the device",
+                    top_k, kMaxTopK);
     if (!logits || !rng || !out) return fail(SXQ_ERR_INVALID, "sample: null pointer");
     return SXQ_OK;
 }
@@ -520,7 +776,7 @@ sxq_status check_common(int n, int vocab, int top_k, const void* logits, const v
 namespace sxq {
 namespace abi {
 
-bool fish_sampling_fits(const sxq_fish_sampling& p) { return p.top_k >= 1 && p.top_k <= kMaxTopK; }
+bool fish_sampling_fits(const sxq_fish_sampling& p) { return p.top_k >= 0; }
 
 hipError_t launch_sample_codebook(const float* logits, int64_t stride, int n, int vocab, const sxq_fish_sampling& p,
                                   uint64_t* rng, const int32_t* active, int32_t* out, int out_stride, int32_t* out2,
@@ -547,7 +803,7 @@ sxq_status sxq_sample_semantic(int device, const float* logits, int64_t logits_s
                                const sxq_fish_sampling* p, uint64_t* rng, int32_t* window, int32_t* window_len,
                                int32_t* active, int32_t* out, int out_stride, void* stream) {
     if (!p) return fail(SXQ_ERR_INVALID, "sample_semantic: null parameters");
-    sxq_status st = check_common(n, vocab, p->top_k, logits, rng, out);
+    sxq_status st = check_common(n, vocab, p->top_k, logits, rng, out, true);
     if (st != SXQ_OK) return st;
     if (p->ras_win_size < 0 || p->ras_win_size > kMaxWindow)
         return fail(SXQ_ERR_INVALID, "sample_semantic: ras_win_size %d outside 0..%d", p->ras_win_size, kMaxWindow);
@@ -564,7 +820,7 @@ sxq_status sxq_sample_codebook(int device, const float* logits, int64_t logits_s
                                const sxq_fish_sampling* p, uint64_t* rng, const int32_t* recent, int n_recent,
                                const int32_t* active, int32_t* out, int out_stride, void* stream) {
     if (!p) return fail(SXQ_ERR_INVALID, "sample_codebook: null parameters");
-    sxq_status st = check_common(n, vocab, p->top_k, logits, rng, out);
+    sxq_status st = check_common(n, vocab, p->top_k, logits, rng, out, true);
     if (st != SXQ_OK) return st;
     if (n_recent < 0 || n_recent > kMaxWindow || (n_recent > 0 && !recent))
         return fail(SXQ_ERR_INVALID, "sample_codebook: %d recent ids (at most %d)", n_recent, kMaxWindow);
@@ -580,7 +836,7 @@ sxq_status sxq_sample_codebook(int device, const float* logits, int64_t logits_s
 sxq_status sxq_sample_ras(int device, float* logits, int64_t logits_stride, int n, int vocab, int ignore_eos,
                           int eos_begin, int eos_end, float top_p, int top_k, int win, float tau_r, uint64_t* rng,
                           int32_t* decoded, int32_t* decoded_len, int32_t* out, int out_stride, void* stream) {
-    sxq_status st = check_common(n, vocab, top_k, logits, rng, out);
+    sxq_status st = check_common(n, vocab, top_k, logits, rng, out, false);
     if (st != SXQ_OK) return st;
     if (win < 0 || win > kMaxWindow) return fail(SXQ_ERR_INVALID, "sample_ras: window %d outside 0..%d", win, kMaxWindow);
     if (!decoded != !decoded_len) return fail(SXQ_ERR_INVALID, "sample_ras: decoded and decoded_len go together");

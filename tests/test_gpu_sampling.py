@@ -72,6 +72,65 @@ def test_codebook_draws_with_repetition_penalty_equal_oracle(cuda):
             assert got[i] == refs[i].sample_codebook(x[i], list(recent[i])), (step, i)
 
 
+# top_k 0 is unbounded (common/sampling.rs:50-52); caps above 64 keep more candidates than
+# one wave sorts.  Flat logits keep thousands of ids under top_p, peaked ones a few (the
+# staged wave path), ties put the cut inside a run of equal logits, top_p >= 1 keeps all.
+WIDE = [
+    # (top_k, top_p, logit scale, ties)
+    (0, 0.9, 0.3, False),
+    (0, 0.9, 0.3, True),
+    (0, 0.7, 3.0, False),    # peaked: fewer than 64 kept
+    (200, 0.9, 0.3, False),  # the cap binds before top_p
+    (1000, 1.0, 0.5, True),  # top_p keeps everything, the cap cuts inside ties
+    (0, 1.5, 0.5, False),    # every id kept
+]
+
+
+@pytest.mark.parametrize("top_k,top_p,scale,ties", WIDE)
+def test_codebook_draws_unbounded_top_k_equal_oracle(cuda, top_k, top_p, scale, ties):
+    n, vocab = 8, 4096
+    params = SamplingParams(temperature=0.9, top_p=top_p, top_k=top_k, repetition_penalty=1.2)
+    dev = FishSampler([31 * i + 5 for i in range(n)], params, device=cuda)
+    refs = [S.FishSampler(31 * i + 5, temperature=0.9, top_p=top_p, top_k=top_k, repetition_penalty=1.2)
+            for i in range(n)]
+    rng = np.random.default_rng(11)
+    for step in range(6):
+        x = _logits(rng, n, vocab, scale, ties)
+        recent = rng.integers(0, vocab, (n, 4)).astype(np.int32)
+        got = dev.sample_codebook(torch.from_numpy(x).to(cuda), torch.from_numpy(recent).to(cuda)).cpu().numpy()
+        for i in range(n):
+            assert got[i] == refs[i].sample_codebook(x[i], list(recent[i])), (step, i)
+    np.testing.assert_array_equal(dev.rng.cpu().numpy().astype(np.uint64),
+                                  np.array([r.rng.state for r in refs], np.uint64))
+
+
+@pytest.mark.parametrize("top_k,scale", [(0, 0.2), (0, 2.0), (500, 0.2)])
+def test_semantic_draws_unbounded_top_k_equal_oracle(cuda, top_k, scale):
+    """The slow-AR draw over the 155776-id vocabulary with the 4096-id semantic range: an
+    unbounded (or 500) cap keeps ~3500 semantic ids of flat logits under top_p 0.9."""
+    n, vocab = 4, 155776
+    begin, end, stop = 151678, 155773, 151645
+    params = SamplingParams(top_k=top_k)
+    dev = FishSampler([9 + i for i in range(n)], params, (begin, end, stop), device=cuda)
+    refs = [S.FishSampler(9 + i, top_k=top_k) for i in range(n)]
+    windows = [[] for _ in range(n)]
+    rng = np.random.default_rng(12)
+    for step in range(6):
+        x = _logits(rng, n, vocab, scale)
+        if step % 2 == 1:
+            for i in range(n):
+                if windows[i]:
+                    x[i, windows[i][-1]] += 3.0
+        got = dev.sample_semantic(torch.from_numpy(x).to(cuda)).cpu().numpy()
+        for i in range(n):
+            want = refs[i].sample_semantic(x[i], windows[i], begin, end, stop)
+            assert got[i] == want, (step, i, got[i], want)
+            if want != stop:
+                windows[i] = (windows[i] + [want])[-params.ras_win_size:]
+    np.testing.assert_array_equal(dev.rng.cpu().numpy().astype(np.uint64),
+                                  np.array([r.rng.state for r in refs], np.uint64))
+
+
 @pytest.mark.parametrize("ignore_eos", [False, True])
 def test_cosyvoice_ras_draws_equal_oracle(cuda, ignore_eos):
     """CosyVoice2 speech vocabulary (6564, stop ids 6561..6563): log_softmax, nucleus
