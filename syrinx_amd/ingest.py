@@ -7,7 +7,7 @@ Host mirror of the reference's two LM loaders, with every quantization on the GP
   the unused ``lm_head`` dropped, the three embedding tables per-row int4 (int8 for odd
   widths), every other 2-D weight whose inner dim is a multiple of 32 a Q4_0 QMatMul, the
   other 2-D weights dense f16, 1-D weights f32; with its footprint report
-  (cv2/load.rs:125-160, cv2/quant.rs:92-123).
+  (cv2/load.rs:124-155, cv2/quant.rs:91-118).
 * ``load_fish_lm`` -- s2's load_lm (crates/syrinx-fish/src/s2/load.rs:32-51): shard
   resolution (:96-136), the key remap onto the fish-native names (:148-263), the q/k/v fusion
   (:271-312); tensors are cast to f32 as they are read.
@@ -49,7 +49,7 @@ def read_safetensors(path: str, device) -> dict:
 
 # --------------------------------------------------------------------------- CosyVoice2
 def is_unused_text_head(name: str) -> bool:
-    """cv2/load.rs:194-196: the Qwen2 text head the speech path never calls."""
+    """cv2/load.rs:158-170: the Qwen2 text head the speech path never calls."""
     return "lm_head" in name
 
 
@@ -57,13 +57,13 @@ CV2_EMBED_TABLES = ("llm.model.model.embed_tokens.weight", "llm_embedding.weight
 
 
 def is_embedding_table(name: str) -> bool:
-    """cv2/load.rs:199-203."""
+    """cv2/load.rs:172-177."""
     return name in CV2_EMBED_TABLES
 
 
 @dataclass
 class Footprint:
-    """cv2/quant.rs:99-123."""
+    """cv2/quant.rs:91-118."""
     quant_bytes: int
     embed_bytes: int
     dense_bytes: int
@@ -89,7 +89,7 @@ class Cv2Weights:
         return Footprint(self.quant_bytes, sum(e.bytes for e in self.qembed.values()), dense, len(self.qmm))
 
     def dense_breakdown(self):
-        """(name, bytes) of every dense weight, largest first (cv2/load.rs:172-187)."""
+        """(name, bytes) of every dense weight, largest first (cv2/load.rs:140-155)."""
         v = [(k, t.numel() * t.element_size()) for k, t in self.w.items()]
         return sorted(v, key=lambda kv: -kv[1])
 

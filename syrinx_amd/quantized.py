@@ -161,7 +161,6 @@ class QMatMul:
         self._shape = None
         self._dtype = None
         self._device = None
-        self._graph_ws = []  # workspaces of captured forwards, alive as long as this QMatMul
 
     @staticmethod
     def from_qtensor(qt: QTensor) -> "QMatMul":
@@ -246,14 +245,16 @@ class QMatMul:
         bptr = _ptr(bias) if bias is not None else None
         if torch.cuda.is_current_stream_capturing():
             # Under graph capture the forward takes a workspace of its own from torch's
-            # graph memory pool, which the graph keeps: replays never share the library's
-            # eager workspace with other calls.
+            # graph memory pool: replays never share the library's eager workspace with
+            # other calls.  The workspace lives as long as the captured output y (as a
+            # graph's own intermediates do), so a caller that re-captures and drops the old
+            # outputs releases the old workspaces with them.
             need = ctypes.c_size_t()
             check(lib().sxq_qmm_workspace_size(self._h, xs.numel() // k, flags, ctypes.byref(need)))
             ws = torch.empty(max(int(need.value), 1), dtype=torch.uint8, device=xs.device)
             check(lib().sxq_qmm_forward_ws(self._h, _ptr(xs), shape, xs.dim(), strides, _ptr(y), bptr, flags,
                                            _ptr(ws), ws.numel(), _stream_ptr(xs.device)))
-            self._graph_ws.append(ws)
+            y._sxq_graph_workspace = ws
         else:
             check(lib().sxq_qmm_forward(self._h, _ptr(xs), shape, xs.dim(), strides, _ptr(y), bptr, flags,
                                         _stream_ptr(xs.device)))

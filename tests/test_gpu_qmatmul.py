@@ -411,6 +411,32 @@ def test_forward_captured_in_a_graph(cuda, ora):
             np.testing.assert_array_equal(y.cpu().numpy(), want, err_msg=f"{dt} m={m} replay {rep}")
 
 
+def test_captured_workspaces_are_released_with_their_outputs(cuda, ora):
+    """Each captured forward's workspace lives as long as its output: capturing the same
+    QMatMul again and again (dropping the old graph and output) holds no more device
+    memory than one capture does."""
+    n, k, m = 2560, 4096, 128  # the prefill GEMM: a multi-MB workspace per capture
+    blocks = ora.quantize(ora.Q4K, _weights(n, k, 66))
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    x = torch.from_numpy(_acts(m, k, 67)).to(cuda)
+    want = qmm.forward(x).cpu().numpy()
+    torch.cuda.synchronize()
+    held = []
+    for rep in range(6):
+        s = torch.cuda.Stream(device=cuda)
+        s.wait_stream(torch.cuda.current_stream(cuda))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            y = qmm.forward(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), want)
+        del graph, y
+        torch.cuda.synchronize()
+        held.append(torch.cuda.memory_allocated(cuda))
+    assert max(held[1:]) <= held[0], held
+
+
 def test_captured_forward_survives_a_larger_eager_call(cuda, ora):
     """Capture a one-row forward, then run an eager 128-row prefill forward (which grows
     the library's shared workspace), then replay: the graph's workspace is its own, so
