@@ -30,13 +30,16 @@ hipError_t launch_attention(int vdt, const float* q, const float* kc, const floa
 // hipErrorInvalidValue when the head group is not a whole number of activation blocks
 // (attn_decode_fits); the caller then uses the three-kernel path.
 bool attn_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits);
+// grid_splits (both fused launches): the splits per (stream, KV head) the grid holds, at
+// least every stream's (len + 64) / 64 at this launch; 0 = every split of max_seq.  A
+// smaller grid leaves out workgroups that would only find their split empty.
 // Allow the fused kernel its dynamic LDS (above 64 KB); call once before launching.
 hipError_t attn_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits);
 hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, int nh, int nkv, int hd, const float* qn,
                                    const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
                                    const int* len, float* kc, float* vc, int64_t kv_stream_stride, int max_seq,
                                    int max_splits, float* part, unsigned* counter, uint8_t* act, float* ctx_out,
-                                   float* q_out, hipStream_t s, MmaRec* rec = nullptr);
+                                   float* q_out, hipStream_t s, MmaRec* rec = nullptr, int grid_splits = 0);
 hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s,
                                  MmaRec* rec = nullptr);
 // table: the dense input table [table_rows][dim], or null to dequantize the rows of the tied head w
@@ -115,6 +118,6 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
                                       const float* sin_t, const int* len, float* kc, float* vc, int max_seq,
                                       int max_splits, float* part, unsigned* counter, uint8_t* act, const QWeight& wo,
                                       float* y, unsigned* ready, unsigned* ready_next, float* ctx_out, float* q_out,
-                                      hipStream_t s);
+                                      hipStream_t s, int grid_splits = 0);
 
 }  // namespace sxq

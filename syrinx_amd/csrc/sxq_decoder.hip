@@ -582,7 +582,7 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
                                    const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
                                    const int* len, float* kc, float* vc, int64_t kv_stream_stride, int max_seq,
                                    int max_splits, float* part, unsigned* counter, uint8_t* act, float* ctx_out,
-                                   float* q_out, hipStream_t s, MmaRec* rec) {
+                                   float* q_out, hipStream_t s, MmaRec* rec, int grid_splits) {
     if (!attn_decode_fits(vdt, nh, nkv, hd, max_splits) || max_seq > kMaxSplitsFused * kAttnSplitFused)
         return hipErrorInvalidValue;
     if (rec && (vdt != kQ8K || B > 16)) return hipErrorInvalidValue;
@@ -613,7 +613,8 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
     A.ready = nullptr;
     A.pub_off = 0;
     A.rec = rec;
-    const dim3 grid(B, nkv, (max_seq + kAttnSplitFused - 1) / kAttnSplitFused);  // partial records: max_splits per head
+    const int all = (max_seq + kAttnSplitFused - 1) / kAttnSplitFused;  // partial records: max_splits per head
+    const dim3 grid(B, nkv, grid_splits > 0 && grid_splits < all ? grid_splits : all);
     const size_t lds = attn_decode_lds(nh, nkv, hd, max_splits);
     void* args[] = {&A};
     return hipLaunchKernel(attn_decode_kernel(vdt, hd, nh / nkv), grid, dim3(kAttnThreads), args, lds, s);
@@ -734,7 +735,7 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
                                       const float* sin_t, const int* len, float* kc, float* vc, int max_seq,
                                       int max_splits, float* part, unsigned* counter, uint8_t* act, const QWeight& wo,
                                       float* y, unsigned* ready, unsigned* ready_next, float* ctx_out, float* q_out,
-                                      hipStream_t s) {
+                                      hipStream_t s, int grid_splits) {
     if (!attn_wo_decode_fits(vdt, nh, nkv, hd, max_splits, wo, (int)wo.n) ||
         max_seq > kMaxSplitsFused * kAttnSplitFused || ready == ready_next)
         return hipErrorInvalidValue;
@@ -771,7 +772,8 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
     W.n = (int)wo.n;
     W.nb = (int)wo.nb;
     W.R = wo_rows(W.nb);
-    W.n_attn = nkv * ((max_seq + kAttnSplitFused - 1) / kAttnSplitFused);
+    const int all = (max_seq + kAttnSplitFused - 1) / kAttnSplitFused;
+    W.n_attn = nkv * (grid_splits > 0 && grid_splits < all ? grid_splits : all);
     W.y = y;
     W.ready_next = ready_next;
     W.need = (unsigned)nkv;

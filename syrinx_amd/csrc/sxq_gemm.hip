@@ -112,6 +112,58 @@ __global__ __launch_bounds__(256) void k_x_to_f16_perm(const float* __restrict__
     }
 }
 
+// The same conversion in one pass over x, for rows of k <= 1024 * V4 elements: the row is
+// loaded once (every thread's V4 float4 loads issued together), its max |x| reduced while
+// it goes to LDS, and the f16 positions gathered from LDS -- thread t writes the 16-byte
+// chunks t, t + 256, ... of the row (chunk c: block c / 32, positions 8 (c mod 32) .. + 7),
+// so the row's writes are contiguous.  The bits are k_x_to_f16_perm's.
+template <int V4>
+__global__ __launch_bounds__(256) void k_x_to_f16_perm1(const float* __restrict__ x, int64_t ldx, int m, int k,
+                                                        _Float16* __restrict__ xh, float* __restrict__ rs) {
+    extern __shared__ float4 rowbuf[];  // the row, k floats
+    __shared__ float wmax[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n4 = k >> 2;
+    const int64_t r = blockIdx.x;
+    const bool live = r < m;
+    const float4* xr = (const float4*)(x + r * ldx);
+    float4 v[V4];
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int i = tid + 256 * j;
+        v[j] = live && i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V4; ++j) {
+        const int i = tid + 256 * j;
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+        if (i < n4) rowbuf[i] = v[j];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if (lane == 0) wmax[wave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int e = 0;
+    if (amax >= kF16Safe && amax <= 3.0e38f) {  // as k_x_to_f16_perm
+        int ex = 0;
+        (void)frexpf(amax, &ex);
+        e = ex - 15;
+    }
+    const float sc = ldexpf(1.0f, -e);
+    if (tid == 0) rs[r] = ldexpf(1.0f, e);
+    const int nchunks = k >> 3;  // 32 chunks of 8 positions per block
+    for (int c = tid; c < nchunks; c += 256) {
+        const int b = c >> 5, l = c & 31;
+        const float* el = (const float*)rowbuf + 256 * b + q4k_perm_elem(8 * l);
+        half8 h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = (_Float16)(el[32 * (j & 1) + 8 * (j >> 1)] * sc);
+        *(half8*)(xh + r * k + 8 * c) = h;
+    }
+}
+
 // The 8 (scale, min) pairs of a Q4_K block header (get_scale_min_k4), times d and dmin:
 // sv[j] = d * sc_j, nm[j] = -(dmin * m_j), both exact in f32 (11-bit times 6-bit
 // significands).  The 12 scale bytes are header bytes 4..15 (dwords y, z, w = q[0..3],
@@ -548,8 +600,16 @@ size_t gemm_q4k_workspace(int64_t n, int m, int64_t k) {
 hipError_t launch_gemm_q4k_prep(const float* x, int64_t ldx, int m, int64_t n, int k, void* ws, hipStream_t s) {
     const GemmPlan p = gemm_plan(n, m, k);
     const int rows = gemm_xh_rows(m);
-    hipLaunchKernelGGL(k_x_to_f16_perm, dim3((unsigned)rows), dim3(256), 0, s, x, ldx, m, k, (_Float16*)ws,
-                       (float*)((uint8_t*)ws + p.xh_bytes));
+    _Float16* xh = (_Float16*)ws;
+    float* rs = (float*)((uint8_t*)ws + p.xh_bytes);
+    const bool two_pass = getenv("SXQ_X2F16_TWO_PASS") != nullptr;  // A/B: the two-pass conversion
+    const size_t row_lds = (size_t)k * sizeof(float);
+    if (!two_pass && k <= 4096)
+        hipLaunchKernelGGL(k_x_to_f16_perm1<4>, dim3((unsigned)rows), dim3(256), row_lds, s, x, ldx, m, k, xh, rs);
+    else if (!two_pass && k <= 12288)
+        hipLaunchKernelGGL(k_x_to_f16_perm1<12>, dim3((unsigned)rows), dim3(256), row_lds, s, x, ldx, m, k, xh, rs);
+    else
+        hipLaunchKernelGGL(k_x_to_f16_perm, dim3((unsigned)rows), dim3(256), 0, s, x, ldx, m, k, xh, rs);
     return hipGetLastError();
 }
 

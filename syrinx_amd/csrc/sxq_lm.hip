@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
@@ -43,9 +44,11 @@ struct GraphKey {
     int n;
     bool embeds;
     const float* trace;
+    int splits;  // attention splits per (stream, KV head) in the grid
     bool operator<(const GraphKey& o) const {
         if (n != o.n) return n < o.n;
         if (embeds != o.embeds) return embeds < o.embeds;
+        if (splits != o.splits) return splits < o.splits;
         return trace < o.trace;
     }
 };
@@ -90,6 +93,7 @@ struct sxq_lm {
     bool swiglu = false;        // one decode row: gate|up GEMV with SwiGLU epilogue + quantizing down GEMV
     float* act_f32 = nullptr;   // SwiGLU output row of that pair [max_batch][intermediate]
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
+    int grid_splits = 0;     // attention splits the step being enqueued launches (0: all of max_seq)
     hipStream_t cap = nullptr;
     std::map<GraphKey, hipGraphExec_t> graphs;
     std::map<std::string, hipGraphExec_t> expand_graphs;  // keyed by the raw bytes of the arguments
@@ -164,6 +168,19 @@ void drop_graphs(sxq_lm* lm) {
     lm->graphs.clear();
     for (auto& kv : lm->expand_graphs) (void)hipGraphExecDestroy(kv.second);
     lm->expand_graphs.clear();
+}
+
+// Attention splits (of kAttnSplitFused positions) per (stream, KV head) the next step's
+// grid holds: enough for the longest of its n streams, rounded up to a bucket of
+// kSplitBucket so that a captured step serves several lengths.
+constexpr int kSplitBucket = 4;
+int step_grid_splits(const sxq_lm* lm, int n) {
+    const int all = (lm->c.max_seq + kAttnSplitFused - 1) / kAttnSplitFused;
+    static const bool full = getenv("SXQ_ATTN_FULL_GRID") != nullptr;  // A/B: the grid of every split
+    if (full) return all;
+    int need = 1;
+    for (int s = 0; s < n; ++s) need = std::max(need, (lm->h_len[s] + kAttnSplitFused) / kAttnSplitFused);
+    return std::min(all, (need + kSplitBucket - 1) / kSplitBucket * kSplitBucket);
 }
 
 // Per-layer trace segments (each [n, size] f32): hn_attn, qkv, q, ctx, h_mid, hn_ffn,
@@ -247,12 +264,12 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                                                 c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len,
                                                 kc, vc, c.max_seq, lm->max_splits, lm->part, lm->attn_count, lm->act_o,
                                                 L.wo.w, lm->h, lm->wo_ready + l, lm->wo_ready + (l + 1) % c.n_layers,
-                                                ctx_slot, q_slot, s));
+                                                ctx_slot, q_slot, s, lm->grid_splits));
             else
                 STEP(launch_attention_decode(lm->vdt, lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn,
                                              kn, c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len,
                                              kc, vc, lm->kv_stream_stride, c.max_seq, lm->max_splits, lm->part,
-                                             lm->attn_count, lm->act_o, ctx_slot, q_slot, s, rec_o));
+                                             lm->attn_count, lm->act_o, ctx_slot, q_slot, s, rec_o, lm->grid_splits));
         } else {
             STEP(launch_qk_rope_append(lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn, kn, c.norm_eps,
                                        c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len, lm->qbuf, kc, vc,
@@ -311,6 +328,7 @@ struct ExpandArgs {
 
 hipError_t enqueue_expand(sxq_lm* lm, const ExpandArgs& a, hipStream_t s) {
     const sxq_lm_config& c = lm->c;
+    lm->grid_splits = 0;  // the expansion's positions run from 0 to n_codes - 1: every split
     hipError_t e = launch_fill_int(lm->d_len, a.n, 0, s);
     if (e == hipSuccess)
         e = hipMemcpyAsync(lm->h, a.hidden, sizeof(float) * (size_t)a.n * c.dim, hipMemcpyDeviceToDevice, s);
@@ -931,8 +949,9 @@ sxq_status sxq_lm_step(sxq_lm* lm, int n, const int32_t* ids, const float* embed
     const bool emb = embeds != nullptr;
     if (ids) HIP_TRY(hipMemcpyAsync(lm->d_ids, ids, sizeof(int) * n * lm->ids_per, hipMemcpyDeviceToDevice, st), "lm_step: ids");
     if (emb) HIP_TRY(hipMemcpyAsync(lm->h, embeds, sizeof(float) * n * lm->c.dim, hipMemcpyDeviceToDevice, st), "lm_step: embeds");
+    lm->grid_splits = step_grid_splits(lm, n);
     if (flags & SXQ_LM_GRAPH) {
-        const GraphKey key{n, emb, lm->trace};
+        const GraphKey key{n, emb, lm->trace, lm->grid_splits};
         auto it = lm->graphs.find(key);
         if (it == lm->graphs.end()) {
             // Capture on the library's own stream (the legacy default stream cannot capture).

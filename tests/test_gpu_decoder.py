@@ -435,24 +435,28 @@ def test_ragged_batch_matches_per_stream_oracle(cuda, model_oracle, lengths):
     tally.mostly_tight()
 
 
-def test_graph_replay_equals_eager_and_feeds_back_argmax(cuda):
+# (250, 3): the longer stream crosses 256 positions, where the step's attention grid grows
+# by a bucket of four 64-position splits (a graph per bucket).
+@pytest.mark.parametrize("lens,steps", [((12, 30), 4), ((250, 3), 10)])
+def test_graph_replay_equals_eager_and_feeds_back_argmax(cuda, lens, steps):
     cfg = _fish_small(n_layers=2, max_batch=2)
+    cfg.max_seq = 320
     res = {}
     for mode in ("eager", "graph"):
         lm, _ = _build(cfg, cuda, 10, 2)
-        lm.kv_fill_random([12, 30], seed=11)
+        lm.kv_fill_random(list(lens), seed=11)
         fr = _frames(np.random.default_rng(12), 2, cfg)
         outs = []
         logits, nxt = lm.step(ids=torch.from_numpy(fr), graph=(mode == "graph"))
         outs.append(logits.cpu().numpy())
-        for _ in range(4):  # greedy: reuse the device-side argmax
+        for _ in range(steps):  # greedy: reuse the device-side argmax
             _ = torch.zeros(1000, device=cuda).sum().item()  # eager work between replays
             logits2, nxt2 = lm.step(n=2, graph=(mode == "graph"))
             torch.cuda.synchronize()
             outs.append(logits2.cpu().numpy())
             assert (nxt2.cpu().numpy() == np.argmax(outs[-1], axis=1)).all()
         res[mode] = outs
-        assert lm.lengths(2) == [17, 35]
+        assert lm.lengths(2) == [L + steps + 1 for L in lens]
     for a, b in zip(res["eager"], res["graph"]):
         np.testing.assert_array_equal(a, b)
 

@@ -335,6 +335,24 @@ def _prefill_check(ora, x, blocks, k, y, b=None):
     assert (err <= tol).all(), f"{int((err > tol).sum())} outputs beyond the bound; worst ratio {float((err / tol).max()):.3g}"
 
 
+@pytest.mark.parametrize("k", [512, 2560, 4096, 9728])
+def test_one_pass_f16_conversion_equals_two_pass(cuda, ora, monkeypatch, k):
+    """The prefill GEMM's x -> f16 (GEMM K order) conversion in one pass over the row gives
+    the two-pass kernel's bits: the products of both are identical, for rows with and
+    without the power-of-two scaling (values beyond f16's range)."""
+    n, m = 384, 96
+    blocks = ora.quantize(ora.Q4K, _weights(n, k, 70))
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), G.Q4K, device=cuda))
+    x = _acts(m, k, 71)
+    x[5] *= 1e5   # a row scaled by 2^-e before the rounding
+    x[7, 3] = 7e4
+    xt = torch.from_numpy(x).to(cuda)
+    y1 = qmm.forward(xt).cpu().numpy()
+    monkeypatch.setenv("SXQ_X2F16_TWO_PASS", "1")
+    y2 = qmm.forward(xt).cpu().numpy()
+    _eq_bits(y1, y2)
+
+
 @pytest.mark.parametrize("splits", ["1", "3"])
 def test_prefill_gemm_split_counts_agree(cuda, ora, monkeypatch, splits):
     """The same product with K unsplit and split unevenly across workgroups (4 blocks
