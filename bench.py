@@ -224,10 +224,17 @@ def gemv_roofline(lm, torch, iters, rows=1):
     ms = e0.elapsed_time(e1) / iters
     achieved = algo / (ms * 1e-3) / 1e9
     kernel = ("k_gemv_mma_q4k_rec" if rows > 4 else "k_gemv2_q4k") if c.weight_dtype == Q4K else "k_gemv2_q80"
-    # counters were collected for the 16-row Qwen3-4B-shape pass (the skinny-batch line)
-    traffic = None
+    # counters were collected for the 16-row Qwen3-4B-shape pass (the skinny-batch line) and
+    # for the one-row Q8_0 passes of the CosyVoice2 and Qwen3-4B shapes
+    traffic, path = None, None
     if kernel == "k_gemv_mma_q4k_rec" and rows == 16 and c.dim == 2560 and c.n_layers == 36:
-        t = measured_traffic(SKINNY_TRAFFIC_FILE, kernel)
+        path = SKINNY_TRAFFIC_FILE
+    elif kernel == "k_gemv2_q80" and rows == 1 and c.dim == 896 and c.n_layers == 24:
+        path = CV2_TRAFFIC_FILE
+    elif kernel == "k_gemv2_q80" and rows == 1 and c.dim == 2560 and c.n_layers == 36:
+        path = Q80_TRAFFIC_FILE
+    if path:
+        t = measured_traffic(path, kernel)
         traffic = None if t is None else round(t)
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -239,6 +246,8 @@ def gemv_roofline(lm, torch, iters, rows=1):
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv2_q4k_qwen3_4b_decode_traffic.txt")
 SKINNY_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv_mma_q4k_rec_qwen3_4b_16stream_traffic.txt")
+CV2_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv2_q80_qwen2_0_5b_decode_traffic.txt")
+Q80_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemv2_q80_qwen3_4b_decode_traffic.txt")
 
 # The sources each measured kernel is built from: a counter summary records their hash,
 # and a summary whose hash differs from the sources in this tree is stale (not reported).
@@ -247,6 +256,7 @@ _COMMON = ("sxq_common.h", "sxq_kernels.h", "sxq_quant_dev.h", "sxq_sync_dev.h")
 KERNEL_SOURCES = {
     "k_gemv2_q4k": ("sxq_gemv.hip", "sxq_gemv_dev.h") + _COMMON,
     "k_gemv_mma_q4k_rec": ("sxq_gemv.hip", "sxq_gemv_dev.h") + _COMMON,
+    "k_gemv2_q80": ("sxq_gemv.hip", "sxq_gemv_dev.h") + _COMMON,
     "k_gemm_q4k": ("sxq_gemm.hip",) + _COMMON,
 }
 

@@ -418,7 +418,9 @@ sxq_status sxq_lm_read_kv(const sxq_lm *lm, int layer, int stream_idx, int kv_he
 /* Copy a step buffer of the first n streams (device) for tests: 0 = residual stream
  * after the last layer [n, dim], 1 = logits [n, vocab], 2 = last layer's q|k|v
  * projection [n, qkv], 3 = last layer's gate|up [n, 2*intermediate], 4 = last layer's
- * post-RoPE queries [n, n_heads*head_dim].  No reference counterpart. */
+ * post-RoPE queries [n, n_heads*head_dim], 5 = the silu(g)*u row the fused one-row
+ * gate|up GEMV last wrote [n, intermediate] (zero until it runs).  No reference
+ * counterpart. */
 sxq_status sxq_lm_read_state(const sxq_lm *lm, int which, int n_streams, float *out, void *stream);
 /* Test instrumentation (no reference counterpart): with a trace buffer set, every
  * step also records its f32 intermediates, for n_streams streams, in this order:
@@ -432,6 +434,14 @@ sxq_status sxq_lm_trace_floats(const sxq_lm *lm, int n_streams, size_t *floats);
 sxq_status sxq_lm_set_trace(sxq_lm *lm, float *trace, size_t capacity_floats);
 /* Bytes of quantized projection weights read by one step (layers + head). */
 sxq_status sxq_lm_weight_bytes(const sxq_lm *lm, size_t *layer_bytes, size_t *head_bytes);
+/* Which fused launches a one-stream step of this engine runs (test instrumentation, no
+ * reference counterpart): bit 0 the decode attention in one kernel, bit 1 attention and
+ * the O projection in one launch, bit 2 the SwiGLU pair (gate|up with the SiLU*mul
+ * epilogue, down with the quantizing prologue). */
+#define SXQ_LM_PATH_ATTN 1u
+#define SXQ_LM_PATH_ATTN_WO 2u
+#define SXQ_LM_PATH_SWIGLU 4u
+sxq_status sxq_lm_paths(const sxq_lm *lm, unsigned *paths);
 sxq_status sxq_lm_destroy(sxq_lm *lm);
 
 #ifdef __cplusplus

@@ -84,6 +84,7 @@ _SIGS = {
     "sxq_lm_trace_floats": (_I, [_P, _I, _P]),
     "sxq_lm_set_trace": (_I, [_P, _P, _SZ]),
     "sxq_lm_weight_bytes": (_I, [_P, _P, _P]),
+    "sxq_lm_paths": (_I, [_P, _P]),
     "sxq_lm_destroy": (_I, [_P]),
 }
 

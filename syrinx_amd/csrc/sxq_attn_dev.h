@@ -99,13 +99,12 @@ SXQ_DEV void rope_store(float2 y, int interleaved, float* dst, float* gdst, int 
 // The group's context slice (thread t < T holds elements 4t .. 4t + 3, zeros past T): the
 // optional f32 record, then the activation blocks of the O projection -- the quantizers'
 // lane layout, wave w quantizing chunk w of 256 elements.
-// PUB (Q8_K): the slice is read by other workgroups of the same launch (the O projection
-// of k_attn_wo_decode), so it is quantized into LDS at smem + A.pub_off bytes, copied out
+// PUB: the slice is read by other workgroups of the same launch (the O projection of
+// k_attn_wo_decode), so it is quantized into LDS at smem + A.pub_off bytes, copied out
 // by wave 0 with agent-coherent 16-byte stores and, once those have completed, counted
 // in A.ready.
 template <int VDT, int HD, bool PUB = false>
 SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, float4 v, float* smem) {
-    static_assert(!PUB || VDT == kQ8K, "published slices are Q8_K blocks");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int dim = A.nh * HD;
     if (tid < T && A.ctx_out) *(float4*)(A.ctx_out + (int64_t)s * dim + (int64_t)g * gd + 4 * tid) = v;
@@ -115,10 +114,15 @@ SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, f
     uint8_t* qdst = arow + (size_t)blk_first * act_block_bytes(VDT);
     if constexpr (PUB) {
         uint8_t* ql = (uint8_t*)smem + A.pub_off;
-        if (tid < ((T + 63) & ~63)) wave_quantize_q8k<false>(v, lane, ql + (size_t)wave * sizeof(ActQ8K));
+        if (tid < ((T + 63) & ~63)) {
+            if constexpr (VDT == kQ8K)
+                wave_quantize_q8k<false>(v, lane, ql + (size_t)wave * sizeof(ActQ8K));
+            else
+                wave_quantize_q8_0<false>(v, lane, wave * 8 + (lane >> 3) < gd / 32, ql + (size_t)wave * 8 * sizeof(ActQ8_0));
+        }
         lds_barrier();
         if (wave == 0) {
-            const int nu4 = (gd / 256) * (int)(sizeof(ActQ8K) / 16);
+            const int nu4 = VDT == kQ8K ? (gd / 256) * (int)(sizeof(ActQ8K) / 16) : (gd / 32) * (int)(sizeof(ActQ8_0) / 16);
             const __amdgpu_buffer_rsrc_t r = coherent_rsrc(qdst, (uint32_t)nu4 * 16);
             for (int i = lane; i < nu4; i += 64) store16_coherent(r, (uint32_t)i * 16, ((const float4*)ql)[i]);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice has reached the coherent level

@@ -623,111 +623,226 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
 // ---- batch-1 decode attention + O projection as one launch ---------------------------
 // Workgroups [0, n_attn) are k_attn_decode's (split sp = id / n_kv of head group
 // g = id % n_kv), publishing their quantized context slices (attn_emit_context, PUB); the
-// rest each own R rows of the Q4_K O projection (k_gemv2_q4k's tile, 512 threads): they
-// issue their weight loads and the residual load at once, then one thread waits for the
-// n_kv slices (a bounded poll of the ready counter), the context row is staged into LDS
-// with agent-coherent loads, and the tile's products and in-order fold follow -- the same
-// arithmetic as the separate launches, bit for bit.  The wait cannot block the attention:
-// the workgroups of a launch are dispatched in id order, so every attention workgroup
-// holds its CU before the first projection workgroup does, and it never waits for one.
-// Should the poll run out anyway (about a second), the tile's outputs are NaN rather
-// than stale.
+// rest each own R rows of the O projection (512 threads; k_gemv2_q4k's tile for Q4_K,
+// k_gemv2_q80's tasks for Q8_0 / Q4_0): they issue their weight loads and the residual
+// load at once, then one thread waits for the n_kv slices (a bounded poll of the ready
+// counter), the context row is staged into LDS with agent-coherent loads, and the tile's
+// products and in-order fold follow -- the same arithmetic as the separate launches, bit
+// for bit.  The wait cannot block the attention: the workgroups of a launch are
+// dispatched in id order, so every attention workgroup holds its CU before the first
+// projection workgroup does, and it never waits for one.  Should the poll run out anyway
+// (about a second), the tile's outputs are NaN rather than stale.
 struct WoArgs {
-    const uint4* hdr;  // Q4_K block headers, 16 B per block, [n][nb]
-    const uint4* qs;   // Q4_K quants, 128 B per block, [n][nb]
+    const void* hdr;   // Q4_K block headers (16 B per block) or Q8_0 / Q4_0 f16 scales, [n][nb]
+    const uint4* qs;   // quants: 128 / 32 / 16 B per block, [n][nb]
     int n, nb, R;      // output rows, blocks per row, rows per workgroup
     int n_attn;        // attention workgroups ahead of the projection's
     float* y;          // the residual stream row [n], updated in place: y = y + ctx . W^T
     unsigned* ready_next;
     unsigned need;  // slices in the context row (n_kv)
 };
-constexpr int kWoTm = 1;  // task rounds of a projection tile: R * nb <= kWoTm * 128
+constexpr int kWoTm = 1;  // task rounds of a Q4_K projection tile: R * nb <= kWoTm * 128
 constexpr int kWoPollCap = 1 << 22;
+constexpr int kWoQ4K = 0, kWoQ8_0 = 1, kWoQ4_0 = 2;  // the O projection's weight type
 
-template <int HD, int GC>
+// One thread polls the ready counter (bounded), then the context row (act_u4 16-byte
+// pieces) is staged into LDS at the coherent level (this XCD's L2 may hold an earlier
+// layer's row).  Returns false when the poll ran out.
+SXQ_DEV bool wo_wait_stage(const AttnArgs& A, const WoArgs& W, uint4* lds, int act_u4, bool* flag) {
+    if (threadIdx.x == 0) {
+        int it = 0;
+        while (__hip_atomic_load(A.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < W.need && it < kWoPollCap) {
+            __builtin_amdgcn_s_sleep(1);
+            ++it;
+        }
+        *flag = it < kWoPollCap;
+    }
+    lds_barrier();  // (also: every thread's first-pass fold has read the products)
+    const bool ok = *flag;
+    const __amdgpu_buffer_rsrc_t ar = coherent_rsrc(A.act, (uint32_t)act_u4 * 16);
+    for (int i = threadIdx.x; i < act_u4; i += kAttnThreads) {
+        const float4 x = load16_coherent(ar, (uint32_t)i * 16);
+        lds[i] = make_uint4(__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w));
+    }
+    lds_barrier();
+    return ok;
+}
+
+template <int WT, int HD, int GC, int TM>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_attn_wo_decode(AttnArgs A,
                                                                                                           WoArgs W) {
-    constexpr int NT = kAttnThreads, TM = kWoTm;
+    constexpr int NT = kAttnThreads;
+    constexpr int VDT = WT == kWoQ4K ? kQ8K : kQ8_0;
     extern __shared__ float4 smem4[];
     __shared__ bool flag;
     const int id = blockIdx.x;
     if (id < W.n_attn) {
-        attn_decode_body<kQ8K, HD, NT, GC, true>(A, 0, id % A.nkv, id / A.nkv, (float*)smem4, &flag);
+        attn_decode_body<VDT, HD, NT, GC, true>(A, 0, id % A.nkv, id / A.nkv, (float*)smem4, &flag);
         return;
     }
     uint4* lds = (uint4*)smem4;
     const int tid = threadIdx.x, t = id - W.n_attn;
     const int nb = W.nb, row0 = t * W.R, rows = min(W.R, W.n - row0), tasks = rows * nb;
-    uint4 q[TM][kQ4kCpl], h[TM];
-    q4k_tile_load<NT, TM>(W.hdr, W.qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
-    const int r = tid >> 3, l = tid & 7;
-    const float res = W.y[row0 + min(r, rows - 1)];  // clamped, unconditional; used by lane class 0 of rows < rows
-    issue_point();
-    if (tid == 0 && t == 0) __hip_atomic_store(W.ready_next, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int act_u4 = nb * (int)(sizeof(ActQ8K) / 16);
-    const __amdgpu_buffer_rsrc_t ar = coherent_rsrc(A.act, (uint32_t)act_u4 * 16);
-    float* pr = (float*)(lds + act_u4);  // product chains [R + 1][9][CS]
-    bool ok = true;
-    float v = 0.0f;
-    // Two passes over the same code: the first, on whatever the LDS holds, runs while the
-    // attention does and leaves the products' and the fold's instructions in the
-    // instruction cache (their first fetch would otherwise sit on the critical path);
-    // the second waits for the context and computes the result.
+    if constexpr (WT == kWoQ4K) {
+        uint4 q[TM][kQ4kCpl], h[TM];
+        q4k_tile_load<NT, TM>((const uint4*)W.hdr, W.qs, (uint32_t)row0 * (uint32_t)nb, tasks, q, h);
+        const int r = tid >> 3, l = tid & 7;
+        const float res = W.y[row0 + min(r, rows - 1)];  // clamped, unconditional; used by lane class 0 of rows < rows
+        issue_point();
+        if (tid == 0 && t == 0) __hip_atomic_store(W.ready_next, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int act_u4 = nb * (int)(sizeof(ActQ8K) / 16);
+        float* pr = (float*)(lds + act_u4);  // product chains [R + 1][9][CS]
+        bool ok = true;
+        float v = 0.0f;
+        // Two passes over the same code: the first, on whatever the LDS holds, runs while
+        // the attention does and leaves the products' and the fold's instructions in the
+        // instruction cache (their first fetch would otherwise sit on the critical path);
+        // the second waits for the context and computes the result.
 #pragma nounroll
-    for (int pass = 0; pass < 2; ++pass) {
-        if (pass == 1) {
-            if (tid == 0) {
-                int it = 0;
-                while (__hip_atomic_load(A.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < W.need &&
-                       it < kWoPollCap) {
-                    __builtin_amdgcn_s_sleep(1);
-                    ++it;
-                }
-                flag = it < kWoPollCap;
-            }
-            lds_barrier();  // (also: every thread's first-pass fold has read the chains)
-            ok = flag;
-            // the context row into LDS, read at the coherent level (this XCD's L2 may
-            // hold an earlier layer's row)
-            for (int i = tid; i < act_u4; i += NT) {
-                const float4 x = load16_coherent(ar, (uint32_t)i * 16);
-                lds[i] = make_uint4(__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w));
-            }
-            lds_barrier();
+        for (int pass = 0; pass < 2; ++pass) {
+            if (pass == 1) ok = wo_wait_stage(A, W, lds, act_u4, &flag);
+            q4k_tile_products<1, NT, TM>(q, h, (const ActQ8K*)lds, nb, 1, rows, W.R, pr);
+            __syncthreads();
+            v = q4k_tile_fold(pr, nb, W.R, 0, rows);
         }
-        q4k_tile_products<1, NT, TM>(q, h, (const ActQ8K*)lds, nb, 1, rows, W.R, pr);
-        __syncthreads();
-        v = q4k_tile_fold(pr, nb, W.R, 0, rows);
+        if (r < rows && l == 0) W.y[row0 + r] = ok ? res + v : __builtin_nanf("");
+    } else {
+        // k_gemv2_q80's tasks for one activation row: a lane pair per Q8_0 task, one lane
+        // per Q4_0 task; products ((float)isum * d_w) * d_a in task slots, each row's
+        // blocks then added in order by one thread
+        constexpr bool Q4 = WT == kWoQ4_0;
+        constexpr int LPT = Q4 ? 1 : 2, TPI = NT / LPT, QU4 = Q4 ? 1 : 2;
+        const uint16_t* dw16 = (const uint16_t*)W.hdr;
+        const int half = Q4 ? 0 : (tid & 1), slot = tid / LPT;
+        const int64_t base = (int64_t)row0 * nb;
+        uint4 w[TM];
+        float dw[TM];
+#pragma unroll
+        for (int u = 0; u < TM; ++u) {
+            const int tt = min(u * TPI + slot, tasks - 1);
+            w[u] = W.qs[(base + tt) * QU4 + half];
+            dw[u] = h2f(dw16[base + tt]);
+        }
+        const float res = W.y[row0 + min(tid, rows - 1)];  // clamped, unconditional; used by threads < rows
+        issue_point();
+        if (tid == 0 && t == 0) __hip_atomic_store(W.ready_next, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int act_u4 = nb * (int)(sizeof(ActQ8_0) / 16);
+        const ActQ8_0* la = (const ActQ8_0*)lds;
+        float* pr = (float*)(lds + act_u4);  // product slots [TM * TPI]
+        bool ok = true;
+        float v = 0.0f;
+#pragma nounroll
+        for (int pass = 0; pass < 2; ++pass) {  // as for Q4_K: a warm-up pass, then the real one
+            if (pass == 1) ok = wo_wait_stage(A, W, lds, act_u4, &flag);
+#pragma unroll
+            for (int u = 0; u < TM; ++u) {
+                if (u * TPI >= tasks) break;
+                const ActQ8_0& a = la[(u * TPI + slot) % nb];
+                int isum;
+                if (Q4) {
+                    const uint4 A0 = ((const uint4*)a.qs)[0], A1 = ((const uint4*)a.qs)[1];
+                    const uint32_t wd[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+                    const int Alo[4] = {(int)A0.x, (int)A0.y, (int)A0.z, (int)A0.w};
+                    const int Ahi[4] = {(int)A1.x, (int)A1.y, (int)A1.z, (int)A1.w};
+                    isum = -8 * a.asum;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        isum = __builtin_amdgcn_sdot4((int)(wd[k] & 0x0F0F0F0Fu), Alo[k], isum, false);
+                        isum = __builtin_amdgcn_sdot4((int)((wd[k] >> 4) & 0x0F0F0F0Fu), Ahi[k], isum, false);
+                    }
+                } else {
+                    const uint4 Av = ((const uint4*)a.qs)[half];
+                    int sd = __builtin_amdgcn_sdot4((int)w[u].x, (int)Av.x, 0, false);
+                    sd = __builtin_amdgcn_sdot4((int)w[u].y, (int)Av.y, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)w[u].z, (int)Av.z, sd, false);
+                    sd = __builtin_amdgcn_sdot4((int)w[u].w, (int)Av.w, sd, false);
+                    isum = sd + dpp_xor1(sd);
+                }
+                pr[u * TPI + slot] = ((float)isum * dw[u]) * a.d;
+            }
+            __syncthreads();
+            if (tid < rows) {
+                const float* p = pr + tid * nb;
+                float sumf = 0.0f;
+                for (int b = 0; b < nb; ++b) sumf += p[b];
+                v = sumf;
+            }
+            __syncthreads();  // the next pass rewrites the slots
+        }
+        if (tid < rows) W.y[row0 + tid] = ok ? res + v : __builtin_nanf("");
     }
-    if (r < rows && l == 0) W.y[row0 + r] = ok ? res + v : __builtin_nanf("");
 }
 
 static int wo_rows(int nb) { return max(1, min(kAttnThreads / 8, kWoTm * (kAttnThreads / kQ4kLanes) / nb)); }
+// Q8_0 / Q4_0 tiles: the fewest task rounds (1, 2 or 4) that keep the projection within
+// 320 workgroups; R rows of nb tasks each fill them.
+static int wo_tasks_per_round(int dtype) { return dtype == kQ4_0 ? kAttnThreads : kAttnThreads / 2; }
+static int wo_tm_q80(int n, int nb, int dtype) {
+    for (int tm : {1, 2, 4}) {
+        const int R = min(64, tm * wo_tasks_per_round(dtype) / nb);
+        if (R >= 1 && (n + R - 1) / R <= 320) return tm;
+    }
+    return 4;
+}
+static int wo_rows_q80(int n, int nb, int dtype) {
+    return max(1, min(64, wo_tm_q80(n, nb, dtype) * wo_tasks_per_round(dtype) / nb));
+}
 static size_t wo_pub_off(int nh, int nkv, int hd, int max_splits) {
     return (attn_decode_lds(nh, nkv, hd, max_splits) + 15) & ~(size_t)15;
 }
-static size_t attn_wo_lds(int nh, int nkv, int hd, int max_splits, int nb) {
-    const size_t G = nh / nkv;
-    const size_t attn = wo_pub_off(nh, nkv, hd, max_splits) + (G * hd / 256) * sizeof(ActQ8K);
-    const size_t R = wo_rows(nb);
-    const size_t wo = (size_t)nb * sizeof(ActQ8K) + (R + 1) * 9 * q4k_chain_stride(nb) * sizeof(float);
-    return attn > wo ? attn : wo;
+static size_t attn_wo_lds(int nh, int nkv, int hd, int max_splits, const QWeight& wo) {
+    const size_t G = nh / nkv, nb = (size_t)wo.nb;
+    size_t attn = wo_pub_off(nh, nkv, hd, max_splits), proj;
+    if (wo.dtype == kQ4K) {
+        attn += (G * hd / 256) * sizeof(ActQ8K);
+        proj = nb * sizeof(ActQ8K) + (size_t)(wo_rows((int)nb) + 1) * 9 * q4k_chain_stride((int)nb) * sizeof(float);
+    } else {
+        attn += (G * hd / 32) * sizeof(ActQ8_0);
+        proj = nb * sizeof(ActQ8_0) +
+               (size_t)wo_tm_q80((int)wo.n, (int)nb, wo.dtype) * wo_tasks_per_round(wo.dtype) * sizeof(float);
+    }
+    return attn > proj ? attn : proj;
 }
-static const void* attn_wo_kernel(int hd, int G) {
-    if (hd == 128) return G == 4 ? (const void*)k_attn_wo_decode<128, 4> : (const void*)k_attn_wo_decode<128, 0>;
-    return (const void*)k_attn_wo_decode<64, 0>;
+template <int WT>
+static const void* attn_wo_kernel_tm(int hd, int G, int tm) {
+    if (tm == 4) {
+        if (hd == 128) return G == 4 ? (const void*)k_attn_wo_decode<WT, 128, 4, 4> : (const void*)k_attn_wo_decode<WT, 128, 0, 4>;
+        return G == 7 ? (const void*)k_attn_wo_decode<WT, 64, 7, 4> : (const void*)k_attn_wo_decode<WT, 64, 0, 4>;
+    }
+    if (tm == 2) {
+        if (hd == 128) return G == 4 ? (const void*)k_attn_wo_decode<WT, 128, 4, 2> : (const void*)k_attn_wo_decode<WT, 128, 0, 2>;
+        return G == 7 ? (const void*)k_attn_wo_decode<WT, 64, 7, 2> : (const void*)k_attn_wo_decode<WT, 64, 0, 2>;
+    }
+    if (hd == 128) return G == 4 ? (const void*)k_attn_wo_decode<WT, 128, 4, 1> : (const void*)k_attn_wo_decode<WT, 128, 0, 1>;
+    return G == 7 ? (const void*)k_attn_wo_decode<WT, 64, 7, 1> : (const void*)k_attn_wo_decode<WT, 64, 0, 1>;
+}
+static const void* attn_wo_kernel(int hd, int G, const QWeight& wo) {
+    if (wo.dtype == kQ4K) {
+        if (hd == 128)
+            return G == 4 ? (const void*)k_attn_wo_decode<kWoQ4K, 128, 4, kWoTm> : (const void*)k_attn_wo_decode<kWoQ4K, 128, 0, kWoTm>;
+        return (const void*)k_attn_wo_decode<kWoQ4K, 64, 0, kWoTm>;
+    }
+    const int tm = wo_tm_q80((int)wo.n, (int)wo.nb, wo.dtype);
+    return wo.dtype == kQ8_0 ? attn_wo_kernel_tm<kWoQ8_0>(hd, G, tm) : attn_wo_kernel_tm<kWoQ4_0>(hd, G, tm);
 }
 
 bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo, int dim) {
-    return vdt == kQ8K && wo.dtype == kQ4K && attn_decode_fits(vdt, nh, nkv, hd, max_splits) && wo.k == (int64_t)nh * hd &&
-           wo.n == dim && wo.nb >= 1 && wo.nb <= kWoTm * (kAttnThreads / kQ4kLanes) &&
-           attn_wo_lds(nh, nkv, hd, max_splits, (int)wo.nb) <= 160 * 1024;
+    if (!attn_decode_fits(vdt, nh, nkv, hd, max_splits) || wo.k != (int64_t)nh * hd || wo.n != dim || wo.nb < 1)
+        return false;
+    if (vdt == kQ8K && wo.dtype == kQ4K) {
+        if (wo.nb > kWoTm * (kAttnThreads / kQ4kLanes)) return false;
+    } else if (vdt == kQ8_0 && (wo.dtype == kQ8_0 || wo.dtype == kQ4_0)) {
+        if (wo.nb > 4 * wo_tasks_per_round(wo.dtype)) return false;
+    } else {
+        return false;
+    }
+    return attn_wo_lds(nh, nkv, hd, max_splits, wo) <= 160 * 1024;
 }
 
 hipError_t attn_wo_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo) {
     (void)vdt;
-    const int lds = (int)attn_wo_lds(nh, nkv, hd, max_splits, (int)wo.nb);
-    return hipFuncSetAttribute(attn_wo_kernel(hd, nh / nkv), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    const int lds = (int)attn_wo_lds(nh, nkv, hd, max_splits, wo);
+    return hipFuncSetAttribute(attn_wo_kernel(hd, nh / nkv, wo), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 }
 
 hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int nh, int nkv, int hd, const float* qn,
@@ -767,20 +882,20 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
     A.pub_off = (uint32_t)wo_pub_off(nh, nkv, hd, max_splits);
     A.rec = nullptr;
     WoArgs W;
-    W.hdr = (const uint4*)wo.hdr;
+    W.hdr = wo.hdr;
     W.qs = (const uint4*)wo.qs;
     W.n = (int)wo.n;
     W.nb = (int)wo.nb;
-    W.R = wo_rows(W.nb);
+    W.R = wo.dtype == kQ4K ? wo_rows(W.nb) : wo_rows_q80(W.n, W.nb, wo.dtype);
     const int all = (max_seq + kAttnSplitFused - 1) / kAttnSplitFused;
     W.n_attn = nkv * (grid_splits > 0 && grid_splits < all ? grid_splits : all);
     W.y = y;
     W.ready_next = ready_next;
     W.need = (unsigned)nkv;
     const int n_wo = (W.n + W.R - 1) / W.R;
-    const size_t lds = attn_wo_lds(nh, nkv, hd, max_splits, W.nb);
+    const size_t lds = attn_wo_lds(nh, nkv, hd, max_splits, wo);
     void* args[] = {&A, &W};
-    return hipLaunchKernel(attn_wo_kernel(hd, nh / nkv), dim3(W.n_attn + n_wo), dim3(kAttnThreads), args, lds, s);
+    return hipLaunchKernel(attn_wo_kernel(hd, nh / nkv, wo), dim3(W.n_attn + n_wo), dim3(kAttnThreads), args, lds, s);
 }
 
 hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s,

@@ -375,18 +375,33 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restric
 }
 
 // Q8_0 / Q4_0 task-split GEMV: a lane pair per Q8_0 task (16 bytes each), one lane per
-// Q4_0 task; NT threads per workgroup.
-template <int MMAX, bool Q4, bool NORM, int NT, int TM>
+// Q4_0 task; NT threads per workgroup.  PRO selects the activation prologue:
+//   kProStage  the Q8_0 activation blocks `act` [m][nb], staged into LDS;
+//   kProNorm   one row: RMSNorm + the Q8_0 quantizer of ni.x in the prologue;
+//   kProPair   kProNorm on the gate|up weight [2n][nb] as a SwiGLU pair: tile t holds gate
+//              rows [tR, tR + Rt) and the same up rows [n + tR, n + tR + Rt); the epilogue
+//              stores both halves into y (= gu [2n]) and a = silu(g) * u -- k_silu_mul_quant's
+//              arithmetic -- into act_out [n];
+//   kProQuant  one row: the f32 row ni.x [nb * 32] quantized to Q8_0 in LDS (chunk c of 256
+//              by wave c mod 16, k_silu_mul_quant's quantizer), the down projection of the pair.
+// The pair leaves the bits of the GEMV + SiLU*mul kernel + GEMV sequence.
+constexpr int kProStage = 0, kProNorm = 1, kProPair = 2, kProQuant = 3;
+template <int MMAX, bool Q4, int PRO, int NT, int TM>
 __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ dw16, const uint4* __restrict__ qs,
                                                   int n, int nb, const uint8_t* __restrict__ act, int m, int R,
                                                   float* y, int64_t ldy, const float* __restrict__ bias,
-                                                  const float* res, int64_t ldr, NormIn ni) {
-    static_assert(!NORM || (NT == 1024 && MMAX == 1), "the fused RMSNorm prologue is for one row, 1024 threads");
+                                                  const float* res, int64_t ldr, NormIn ni, float* act_out) {
+    static_assert(PRO == kProStage || (NT == 1024 && MMAX == 1), "the fused prologues are for one row, 1024 threads");
+    constexpr bool NORM = PRO == kProNorm || PRO == kProPair;
     extern __shared__ uint4 lds[];
     const ActQ8_0* la = (const ActQ8_0*)lds;
     const int row0 = blockIdx.x * R;
-    const int rows = min(R, n - row0);
+    // a pair tile: Rt gate rows, then the same up rows, n rows apart (tasks seg.. skip ahead)
+    const int Rt = min(R, n - row0);
+    const int rows = PRO == kProPair ? 2 * Rt : Rt;
     const int tasks = rows * nb;
+    const int seg = PRO == kProPair ? Rt * nb : tasks;
+    const int64_t skip = PRO == kProPair ? (int64_t)(n - Rt) * nb : 0;
     constexpr int LPT = Q4 ? 1 : 2, TPI = NT / LPT, QU4 = Q4 ? 1 : 2;
     const int TS = (tasks + TPI - 1) / TPI * TPI;  // product slots: whole rounds
     float* pr = (float*)(lds + (size_t)m * nb * (sizeof(ActQ8_0) / 16));  // [m][TS]
@@ -394,21 +409,45 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
     const int slot = threadIdx.x / LPT;
     const int64_t base = (int64_t)row0 * nb;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8_0) / 16);
-    uint4 av[Stage<NT, MMAX>::kPer];
-    float4 xv, wv;
-    if constexpr (NORM) norm_fetch(xv, wv, ni, nb * 32);
-    else act_fetch<NT, MMAX>(av, act, act_u4);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int J = 3;  // kProQuant: chunks per wave (nb <= 48 * 8)
+    uint4 av[PRO == kProStage ? Stage<NT, MMAX>::kPer : 1];
+    float4 xv, wv, qv[J];
+    if constexpr (NORM) {
+        norm_fetch(xv, wv, ni, nb * 32);
+    } else if constexpr (PRO == kProQuant) {
+        // the row's loads go ahead of the weight loads, which return after them
+        const int nch = (nb + 7) >> 3;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int cc = min(wave + 16 * j, nch - 1);
+            qv[j] = ld_global((const float4*)(opaque_ptr(ni.x) + cc * 256 + 4 * lane));
+        }
+        issue_point();
+    } else {
+        act_fetch<NT, MMAX>(av, act, act_u4);
+    }
     uint4 w[TM];
     float dw[TM];
 #pragma unroll
     for (int u = 0; u < TM; ++u) {
         const int t = min(u * TPI + slot, tasks - 1);
-        w[u] = qs[(base + t) * QU4 + half];
-        dw[u] = h2f(dw16[base + t]);
+        const int64_t wt = base + t + (t >= seg ? skip : 0);
+        w[u] = qs[wt * QU4 + half];
+        dw[u] = h2f(dw16[wt]);
     }
     if constexpr (NORM) {
         __shared__ float red[16];
         norm_quant_store<kQ8_0>(xv, wv, ni, nb * 32, (uint8_t*)lds, red);
+    } else if constexpr (PRO == kProQuant) {
+        // every wave calls the quantizer (a chunk past the row writes nothing)
+        const int nch = (nb + 7) >> 3;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int c = wave + 16 * j;
+            wave_quantize_q8_0<false>(qv[j], lane, c < nch && c * 8 + (lane >> 3) < nb,
+                                      (uint8_t*)lds + (size_t)min(c, nch - 1) * 8 * sizeof(ActQ8_0));
+        }
     } else {
         act_store<NT, MMAX>(av, lds, act, act_u4);
     }
@@ -452,6 +491,22 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
         b = min(b, b - (uint32_t)nb);  // unsigned: subtracts nb only when b >= nb
     }
     __syncthreads();
+    if constexpr (PRO == kProPair) {
+        __shared__ float sw[NT / 2];  // the tile's row results: gate [0, Rt), up [Rt, 2Rt)
+        for (int i = threadIdx.x; i < rows; i += NT) {
+            const float* p = pr + i * nb;
+            float sumf = 0.0f;
+            for (int b = 0; b < nb; ++b) sumf += p[b];
+            sw[i] = sumf;
+            y[i < Rt ? row0 + i : n + row0 + (i - Rt)] = sumf;
+        }
+        __syncthreads();
+        if (threadIdx.x < Rt) {
+            const float gv = sw[threadIdx.x], uv = sw[Rt + threadIdx.x];
+            act_out[row0 + threadIdx.x] = (gv / (1.0f + expf(-gv))) * uv;
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < rows * m; i += NT) {
         const int r = i / m, rr = i - r * m;
         const float* p = pr + rr * TS + r * nb;
@@ -577,10 +632,10 @@ static hipError_t gemv2_launch(const QWeight& w, const void* act, int m, float* 
             }
         } else if (w.dtype == kQ8_0) {
             if (const hipError_t e_ = allow_lds<k_gemv2_q80<MMAX, false, NORM, NT, TM>>(lds); e_ != hipSuccess) return e_;
-            hipLaunchKernelGGL((k_gemv2_q80<MMAX, false, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+            hipLaunchKernelGGL((k_gemv2_q80<MMAX, false, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni, (float*)nullptr);
         } else if (w.dtype == kQ4_0) {
             if (const hipError_t e_ = allow_lds<k_gemv2_q80<MMAX, true, NORM, NT, TM>>(lds); e_ != hipSuccess) return e_;
-            hipLaunchKernelGGL((k_gemv2_q80<MMAX, true, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni);
+            hipLaunchKernelGGL((k_gemv2_q80<MMAX, true, NORM, NT, TM>), grid, block, lds, s, (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, a, m, R, y, ldy, bias, res, ldr, ni, (float*)nullptr);
         } else {
             return hipErrorInvalidValue;
         }
@@ -1113,17 +1168,73 @@ static int swiglu_rows(int I, int nb) {
     return max(B, 1);
 }
 
+// Q8_0 / Q4_0 pairs: gate|up tiles over one workgroup per CU, or over two when one per CU
+// would take more than kTmax task rounds (w1|w3 19456 x 2560 in Q8_0: 12 rounds on 256
+// workgroups, 6 on 512 -- two 1024-thread workgroups of <= 64 VGPRs share a CU; measured
+// 539 against 522 tok/s for the Qwen3-4B-shape Q8_0 decode).
+static int swiglu_rows_q80(int I, int nb, int dtype) {
+    const int tpr = tasks_per_round(dtype, 1024);
+    int B = (I + 255) / 256;
+    if (2 * B * nb > tpr * kTmax) B = (I + 511) / 512;
+    return max(min(B, 1024 / 16), 1);
+}
+
 bool swiglu_pair_fits(const QWeight& gate_up, const QWeight& down) {
     const int I = (int)(gate_up.n / 2), nb = (int)gate_up.nb;
-    return gate_up.dtype == kQ4K && down.dtype == kQ4K && gate_up.n == 2 * (int64_t)I && down.k == I &&
-           gate_up.k <= kNormMaxDim && I % 256 == 0 && I / 256 <= 48 &&
-           gemv2_fits((int)down.n, (int)down.nb, 1, kQ4K, 1024) &&
-           2 * swiglu_rows(I, nb) * nb <= (1024 / kQ4kLanes) * kTmaxQ4k1024;
+    const int dt = gate_up.dtype;
+    if (down.dtype != dt || gate_up.n != 2 * (int64_t)I || down.k != I || gate_up.k > kNormMaxDim || I % 256 != 0 ||
+        I / 256 > 48 || !gemv2_fits((int)down.n, (int)down.nb, 1, dt, 1024))
+        return false;
+    if (dt == kQ4K) return 2 * swiglu_rows(I, nb) * nb <= (1024 / kQ4kLanes) * kTmaxQ4k1024;
+    if (dt == kQ8_0 || dt == kQ4_0) {
+        const int B = swiglu_rows_q80(I, nb, dt);
+        return 2 * B * nb <= tasks_per_round(dt, 1024) * kTmax && gemv2_lds(nb, 1, 2 * B, dt, 1024) <= 64 * 1024;
+    }
+    return false;
+}
+
+// The Q8_0 / Q4_0 pair: k_gemv2_q80 with the kProPair prologue and epilogue over the
+// gate|up weight, then with the kProQuant prologue over the down weight.
+template <bool Q4>
+static hipError_t swiglu_pair_q80(const QWeight& gate_up, const QWeight& down, const NormIn& ni, float* gu,
+                                  float* act_f32, float* y, const float* res, hipStream_t s) {
+    const int dt = gate_up.dtype;
+    const int I = (int)(gate_up.n / 2), nb = (int)gate_up.nb;
+    const int B = swiglu_rows_q80(I, nb, dt);
+    const int tpr = tasks_per_round(dt, 1024);
+    const size_t lds1 = gemv2_lds(nb, 1, 2 * B, dt, 1024);
+    hipError_t e = with_rounds((2 * B * nb + tpr - 1) / tpr, [&](auto tmc) -> hipError_t {
+        constexpr int TM = decltype(tmc)::value;
+        if (const hipError_t e_ = allow_lds<k_gemv2_q80<1, Q4, kProPair, 1024, TM>>(lds1); e_ != hipSuccess) return e_;
+        hipLaunchKernelGGL((k_gemv2_q80<1, Q4, kProPair, 1024, TM>), dim3((I + B - 1) / B), dim3(1024), lds1, s,
+                           (const uint16_t*)gate_up.hdr, (const uint4*)gate_up.qs, I, nb, (const uint8_t*)nullptr, 1,
+                           B, gu, (int64_t)0, (const float*)nullptr, (const float*)nullptr, (int64_t)0, ni, act_f32);
+        return hipSuccess;
+    });
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int n = (int)down.n, nb2 = (int)down.nb;
+    const int R = gemv2_rows(n, nb2, 1, dt, 1024);
+    const size_t lds2 = gemv2_lds(nb2, 1, R, dt, 1024);
+    NormIn q;
+    q.x = act_f32;
+    e = with_rounds((R * nb2 + tpr - 1) / tpr, [&](auto tmc) -> hipError_t {
+        constexpr int TM = decltype(tmc)::value;
+        if (const hipError_t e_ = allow_lds<k_gemv2_q80<1, Q4, kProQuant, 1024, TM>>(lds2); e_ != hipSuccess) return e_;
+        hipLaunchKernelGGL((k_gemv2_q80<1, Q4, kProQuant, 1024, TM>), dim3((n + R - 1) / R), dim3(1024), lds2, s,
+                           (const uint16_t*)down.hdr, (const uint4*)down.qs, n, nb2, (const uint8_t*)nullptr, 1, R, y,
+                           (int64_t)0, (const float*)nullptr, res, (int64_t)0, q, (float*)nullptr);
+        return hipSuccess;
+    });
+    if (e != hipSuccess) return e;
+    return hipGetLastError();
 }
 
 hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const NormIn& ni, float* gu, float* act_f32,
                               float* y, const float* res, hipStream_t s) {
     if (!swiglu_pair_fits(gate_up, down)) return hipErrorInvalidValue;
+    if (gate_up.dtype == kQ8_0) return swiglu_pair_q80<false>(gate_up, down, ni, gu, act_f32, y, res, s);
+    if (gate_up.dtype == kQ4_0) return swiglu_pair_q80<true>(gate_up, down, ni, gu, act_f32, y, res, s);
     const int I = (int)(gate_up.n / 2), nb = (int)gate_up.nb;
     const int B = swiglu_rows(I, nb);
     const size_t lds1 = gemv2_lds(nb, 1, 2 * B, kQ4K, 1024);

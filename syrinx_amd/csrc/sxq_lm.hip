@@ -678,6 +678,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     if (e == hipSuccess) e = hipMemset(lm->am_count, 0, sizeof(unsigned) * MB);
     if (e == hipSuccess) e = hipMemset(lm->attn_count, 0, sizeof(unsigned) * MB * c.n_kv_heads);
     if (e == hipSuccess) e = hipMemset(lm->wo_ready, 0, sizeof(unsigned) * c.n_layers);
+    if (e == hipSuccess) e = hipMemset(lm->act_f32, 0, sizeof(float) * (size_t)MB * I);
     if (e == hipSuccess && lm->rec_a) e = hipMemset(lm->rec_a, 0, sizeof(MmaRec) * (size_t)(c.dim / 256));
     if (e == hipSuccess && lm->rec_o) e = hipMemset(lm->rec_o, 0, sizeof(MmaRec) * (size_t)(lm->ctx / 256));
     if (e == hipSuccess && lm->rec_d) e = hipMemset(lm->rec_d, 0, sizeof(MmaRec) * (size_t)(I / 256));
@@ -1172,12 +1173,20 @@ sxq_status sxq_lm_read_state(const sxq_lm* lm, int which, int n, float* out, voi
     case 2: src = lm->qkv; per = lm->qkv_n; break;
     case 3: src = lm->gu; per = 2 * (size_t)lm->c.intermediate; break;
     case 4: src = lm->qbuf; per = lm->ctx; break;
+    case 5: src = lm->act_f32; per = lm->c.intermediate; break;
     default: return fail(SXQ_ERR_INVALID, "lm_read_state: unknown buffer %d", which);
     }
     DeviceGuard g(lm->device);
     HIP_TRY(g.err, "hipSetDevice");
     HIP_TRY(hipMemcpyAsync(out, src, sizeof(float) * per * n, hipMemcpyDeviceToDevice, (hipStream_t)stream),
             "lm_read_state");
+    return SXQ_OK;
+}
+
+sxq_status sxq_lm_paths(const sxq_lm* lm, unsigned* paths) {
+    if (!lm || !paths) return fail(SXQ_ERR_INVALID, "lm_paths: null pointer");
+    *paths = (lm->attn_fused ? SXQ_LM_PATH_ATTN : 0u) | (lm->wo_fused ? SXQ_LM_PATH_ATTN_WO : 0u) |
+             (lm->swiglu ? SXQ_LM_PATH_SWIGLU : 0u);
     return SXQ_OK;
 }
 

@@ -189,6 +189,14 @@ class DecoderLM:
         check(lib().sxq_lm_weight_bytes(self._h, ctypes.byref(lb), ctypes.byref(hb)))
         return int(lb.value), int(hb.value)
 
+    PATH_ATTN, PATH_ATTN_WO, PATH_SWIGLU = 1, 2, 4
+
+    def paths(self) -> int:
+        """The fused launches a one-stream step runs (tests): PATH_* bits."""
+        p = ctypes.c_uint()
+        check(lib().sxq_lm_paths(self._h, ctypes.byref(p)))
+        return int(p.value)
+
     # -- step ---------------------------------------------------------------------------
     def step(self, ids: torch.Tensor = None, embeds: torch.Tensor = None, n: int = None, graph: bool = False,
              want_logits: bool = True, want_hidden: bool = False, out=None):
@@ -299,10 +307,11 @@ class DecoderLM:
 
     def read_state(self, which: int, n: int = 1) -> torch.Tensor:
         """A step buffer (tests): 0 residual after the last layer, 1 logits, 2 last qkv,
-        3 last gate|up, 4 last post-RoPE queries."""
+        3 last gate|up, 4 last post-RoPE queries, 5 the silu(g)*u row of the fused one-row
+        gate|up GEMV (zero until it runs)."""
         c = self.cfg
         per = {0: c.dim, 1: c.vocab, 2: (c.n_heads + 2 * c.n_kv_heads) * c.head_dim, 3: 2 * c.intermediate,
-               4: c.n_heads * c.head_dim}[which]
+               4: c.n_heads * c.head_dim, 5: c.intermediate}[which]
         out = torch.empty((n, per), dtype=torch.float32, device=self.device)
         check(lib().sxq_lm_read_state(self._h, which, n, ctypes.c_void_p(out.data_ptr()),
                                       torch.cuda.current_stream(self.device).cuda_stream))

@@ -461,47 +461,83 @@ def test_graph_replay_equals_eager_and_feeds_back_argmax(cuda, lens, steps):
         np.testing.assert_array_equal(a, b)
 
 
+PAIR_KINDS = {  # the SwiGLU pair at each weight type: Qwen3-4B width (w1|w3 19456 x 2560, w2 2560 x 9728)
+    "fish_q4k": ("fish", GgmlDType.Q4K),       # and the CosyVoice2 width (9728 x 896, 896 x 4864)
+    "fish_q8_0": ("fish", GgmlDType.Q8_0),     # 12 task rounds per gate|up tile
+    "fish_q4_0": ("fish", GgmlDType.Q4_0),
+    "cv2_q8_0": ("cv2", GgmlDType.Q8_0),
+}
+
+
 @pytest.mark.parametrize("graph", [False, True])
-def test_swiglu_pair_equals_three_launches(cuda, monkeypatch, graph):
+@pytest.mark.parametrize("kind", sorted(PAIR_KINDS))
+def test_swiglu_pair_equals_three_launches(cuda, monkeypatch, graph, kind):
     """One decode row: the gate|up GEMV with the SwiGLU epilogue and the down GEMV that
-    quantizes in its prologue give the bits of GEMV + SiLU*mul kernel + GEMV."""
-    cfg = _fish_small(n_layers=2)
+    quantizes in its prologue give the bits of GEMV + SiLU*mul kernel + GEMV, for Q4_K,
+    Q8_0 and Q4_0 weights.  The pair's own output row (read_state 5) shows which path ran:
+    silu(g) * u of the step's gate|up row with the pair, untouched zeros without."""
+    cfg = _small_cfg(kind, 2)
     res = {}
     for mode in ("pair", "three"):
         if mode == "three":
             monkeypatch.setenv("SXQ_SWIGLU_UNFUSED", "1")  # read when the engine is created
         lm = D.DecoderLM(cfg, device=cuda)
+        assert bool(lm.paths() & lm.PATH_SWIGLU) == (mode == "pair"), lm.paths()
         lm.init_random(seed=41, std=0.02)
         lm.kv_fill_random([33], seed=42)
-        fr = _frames(np.random.default_rng(43), 1, cfg)
+        fr = _first_ids(kind, cfg, np.random.default_rng(43))
         logits, _ = lm.step(ids=torch.from_numpy(fr), graph=graph)
         outs = [logits.cpu().numpy()]
         for _ in range(3):
             logits, _ = lm.step(n=1, graph=graph)
             outs.append(logits.cpu().numpy())
         res[mode] = outs
+        act = lm.read_state(5).cpu().numpy()[0]
+        if mode == "pair":
+            gu = lm.read_state(3).cpu().numpy()[0].astype(np.float64)
+            g, u = gu[: cfg.intermediate], gu[cfg.intermediate:]
+            np.testing.assert_allclose(act, g / (1.0 + np.exp(-g)) * u, rtol=1e-5, atol=1e-7)
+            assert np.abs(act).max() > 0
+        else:
+            assert not act.any(), "the unfused engine ran the pair"
     for a, b in zip(res["pair"], res["three"]):
         np.testing.assert_array_equal(a, b)
 
 
+def _small_cfg(kind, n_layers):
+    model, dt = PAIR_KINDS[kind]
+    if model == "fish":
+        return _fish_small(n_layers=n_layers, dtype=dt)
+    return D.cosyvoice2_lm_config(n_layers=n_layers, max_seq=96, dtype=dt)
+
+
+def _first_ids(kind, cfg, rng):
+    if PAIR_KINDS[kind][0] == "fish":
+        return _frames(rng, 1, cfg)
+    return rng.integers(0, cfg.vocab, (1, 1)).astype(np.int32)
+
+
 @pytest.mark.parametrize("graph", [False, True])
 @pytest.mark.parametrize("kv", [33, 200])
-def test_attention_and_o_projection_in_one_launch_equals_two(cuda, monkeypatch, graph, kv):
+@pytest.mark.parametrize("kind", sorted(PAIR_KINDS))
+def test_attention_and_o_projection_in_one_launch_equals_two(cuda, monkeypatch, graph, kv, kind):
     """One decode row: attention with the O projection's workgroups in the same launch
     (waiting on per-layer ready counters, which consecutive layers zero for each other)
     gives the bits of the attention launch followed by the O-projection GEMV -- with one
     attention split (kv 33) and with a merge of four (kv 200), over three layers and five
-    steps, so every counter is used, zeroed and reused."""
-    cfg = _fish_small(n_layers=3)
+    steps, so every counter is used, zeroed and reused; Q4_K (Q8_K context slices) and
+    Q8_0 / Q4_0 (Q8_0 slices) projections, at the Qwen3-4B and the CosyVoice2 shapes."""
+    cfg = _small_cfg(kind, 3)
     cfg.max_seq = 256
     res = {}
     for mode in ("one", "two"):
         if mode == "two":
             monkeypatch.setenv("SXQ_ATTN_WO_UNFUSED", "1")  # read when the engine is created
         lm = D.DecoderLM(cfg, device=cuda)
+        assert bool(lm.paths() & lm.PATH_ATTN_WO) == (mode == "one"), lm.paths()
         lm.init_random(seed=51, std=0.02)
         lm.kv_fill_random([kv], seed=52)
-        fr = _frames(np.random.default_rng(53), 1, cfg)
+        fr = _first_ids(kind, cfg, np.random.default_rng(53))
         logits, _ = lm.step(ids=torch.from_numpy(fr), graph=graph)
         outs = [logits.cpu().numpy()]
         for _ in range(4):
