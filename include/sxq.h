@@ -60,6 +60,10 @@ typedef enum {
 #define SXQ_BIT_EXACT 2u   /* every row count through Candle's integer vec-dot (bit-identical); without it
                               a Q4_K weight with >= 64 rows of x runs the f16 MFMA prefill GEMM, whose
                               outputs differ from Candle's by less than 2^-10 * sum_k |w_k x_k| */
+#define SXQ_BF16_INPUT 4u  /* x holds bf16 values (the Fish GPU path's activations,
+                              crates/syrinx-fish/src/s2/mod.rs:113), passed through the same `x`
+                              pointer; they widen to f32 exactly on the device, so y is that of an f32
+                              x holding the same values, bit for bit.  y and bias stay f32. */
 
 /* Thread-local text of the last failure on this thread ("" if none). */
 const char *sxq_last_error(void);
@@ -126,7 +130,7 @@ sxq_status sxq_qmm_workspace_size(const sxq_qmm *qmm, int64_t m, unsigned flags,
  * sxq_qmm_workspace_size, 256-byte aligned) instead of the library's shared one: for
  * code under graph capture (the graph owns the workspace, so replays never alias other
  * calls) and callers that manage their own memory.  Calls that share one workspace
- * must not overlap.  flags: SXQ_BIT_EXACT only. */
+ * must not overlap.  flags: SXQ_BIT_EXACT, SXQ_BF16_INPUT. */
 sxq_status sxq_qmm_forward_ws(const sxq_qmm *qmm, const float *x, const int64_t *x_shape, int x_ndim,
                               const int64_t *x_strides, float *y, const float *bias, unsigned flags,
                               void *workspace, size_t workspace_bytes, void *stream);
@@ -140,7 +144,7 @@ sxq_status sxq_qmm_forward_ws(const sxq_qmm *qmm, const float *x, const int64_t 
  * GEMV fits at any usual row count, the prefill GEMM up to ~1024 rows at the Qwen3-4B
  * shapes).  Every call on one GPU shares that scratch: calls that overlap on a GPU (on
  * different streams, or replays of graphs holding such calls) race and must be ordered
- * by the caller.  flags: SXQ_BIT_EXACT only. */
+ * by the caller.  flags: SXQ_BIT_EXACT, SXQ_BF16_INPUT. */
 sxq_status sxq_qmm_forward_noalloc(const sxq_qmm *qmm, const float *x, const int64_t *x_shape, int x_ndim,
                                    const int64_t *x_strides, float *y, const float *bias, unsigned flags,
                                    void *stream);

@@ -24,6 +24,7 @@ STATUS_NAMES = {
 }
 HOST_PTRS = 1
 BIT_EXACT = 2  # SXQ_BIT_EXACT
+BF16_INPUT = 4  # SXQ_BF16_INPUT
 DEVICE_PTRS = 0
 
 

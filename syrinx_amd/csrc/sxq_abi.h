@@ -37,6 +37,7 @@ struct FwdPlan {
     int vdt = 0;
     int64_t nbv = 0;    // activation blocks per row
     size_t ws = 0;      // device workspace: activation blocks, or the GEMM's staging
+    size_t xconv = 0;   // SXQ_BF16_INPUT: the f32 copy of x at the workspace's end (inside ws)
 };
 // Candle's argument checks of QMatMul::forward (its error texts), then the plan; flags
 // outside `allowed` are rejected.

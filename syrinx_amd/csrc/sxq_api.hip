@@ -328,12 +328,21 @@ sxq_status plan_forward(const sxq_qmm* q, const int64_t* shape, int ndim, const 
     p->ws = m == 0 ? 0
                    : up256(p->gemm && !q80 ? gemm_q4k_workspace(q->w.n, (int)m, q->w.k)
                                            : (size_t)m * (size_t)p->nbv * act_block_bytes(p->vdt));
+    // bf16 input: widened to f32 at the workspace's end, then the f32 forward
+    p->xconv = (flags & SXQ_BF16_INPUT) && m > 0 ? up256((size_t)m * (size_t)q->w.k * 4) : 0;
+    p->ws += p->xconv;
     return SXQ_OK;
 }
 
 hipError_t run_forward(const sxq_qmm* q, const FwdPlan& p, const float* x, float* y, const float* bias, uint8_t* ws,
                        hipStream_t s) {
     const int64_t k = q->w.k, n = q->w.n, m = p.m;
+    if (p.xconv) {  // x is bf16: its exact f32 values at the end of the workspace
+        float* xf = (float*)(ws + p.ws - p.xconv);
+        const hipError_t e = launch_bf16_to_f32((const uint16_t*)(const void*)x, m * k, xf, s);
+        if (e != hipSuccess) return e;
+        x = xf;
+    }
     if (p.gemm && q->w.dtype == kQ4K) {
         hipError_t e = launch_gemm_q4k_prep(x, k, (int)m, n, (int)k, ws, s);
         if (e == hipSuccess) e = launch_gemm_q4k(q->w, ws, (int)m, y, n, bias, nullptr, 0, s);
@@ -356,7 +365,7 @@ extern "C" {
 sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shape, int ndim, const int64_t* strides,
                            float* y, const float* bias, unsigned flags, void* stream) {
     FwdPlan p;
-    sxq_status st = plan_forward(q, shape, ndim, strides, flags, SXQ_HOST_PTRS | SXQ_BIT_EXACT, &p);
+    sxq_status st = plan_forward(q, shape, ndim, strides, flags, SXQ_HOST_PTRS | SXQ_BIT_EXACT | SXQ_BF16_INPUT, &p);
     if (st != SXQ_OK) return st;
     if (p.m == 0) return SXQ_OK;
     if (!x || !y) return fail(SXQ_ERR_INVALID, "qmm_forward: null x or y");
@@ -374,7 +383,7 @@ sxq_status sxq_qmm_forward(const sxq_qmm* q, const float* x, const int64_t* shap
     const int64_t k = q->w.k, n = q->w.n, m = p.m;
 
     // One stream-ordered workspace: [plan | x | y | bias] (the last three only for host pointers).
-    const size_t xb = host ? (size_t)(m * k) * 4 : 0, yb = host ? (size_t)(m * n) * 4 : 0;
+    const size_t xb = host ? (size_t)(m * k) * ((flags & SXQ_BF16_INPUT) ? 2 : 4) : 0, yb = host ? (size_t)(m * n) * 4 : 0;
     const size_t bb = (host && bias) ? (size_t)n * 4 : 0;
     WorkspaceLease lease(q->device, p.ws + up256(xb) + up256(yb) + up256(bb), s);
     HIP_TRY(lease.err, "qmm_forward: workspace");
@@ -407,7 +416,7 @@ sxq_status sxq_qmm_workspace_size(const sxq_qmm* q, int64_t m, unsigned flags, s
     if (m < 0) return fail(SXQ_ERR_INVALID, "qmm_workspace_size: negative row count");
     const int64_t shape[2] = {m, q->w.k};
     FwdPlan p;
-    sxq_status st = plan_forward(q, shape, 2, nullptr, flags, SXQ_BIT_EXACT, &p);
+    sxq_status st = plan_forward(q, shape, 2, nullptr, flags, SXQ_BIT_EXACT | SXQ_BF16_INPUT, &p);
     if (st != SXQ_OK) return st;
     *bytes = p.ws;
     return SXQ_OK;
@@ -417,7 +426,7 @@ sxq_status sxq_qmm_forward_ws(const sxq_qmm* q, const float* x, const int64_t* s
                               const int64_t* strides, float* y, const float* bias, unsigned flags, void* workspace,
                               size_t workspace_bytes, void* stream) {
     FwdPlan p;
-    sxq_status st = plan_forward(q, shape, ndim, strides, flags, SXQ_BIT_EXACT, &p);
+    sxq_status st = plan_forward(q, shape, ndim, strides, flags, SXQ_BIT_EXACT | SXQ_BF16_INPUT, &p);
     if (st != SXQ_OK) return st;
     if (p.m == 0) return SXQ_OK;
     if (!x || !y) return fail(SXQ_ERR_INVALID, "qmm_forward_ws: null x or y");

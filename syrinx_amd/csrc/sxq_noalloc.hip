@@ -48,7 +48,7 @@ extern "C" {
 sxq_status sxq_qmm_forward_noalloc(const sxq_qmm* q, const float* x, const int64_t* shape, int ndim,
                                    const int64_t* strides, float* y, const float* bias, unsigned flags, void* stream) {
     FwdPlan p;
-    sxq_status st = plan_forward(q, shape, ndim, strides, flags, SXQ_BIT_EXACT, &p);
+    sxq_status st = plan_forward(q, shape, ndim, strides, flags, SXQ_BIT_EXACT | SXQ_BF16_INPUT, &p);
     if (st != SXQ_OK) return st;
     if (p.m == 0) return SXQ_OK;
     if (!x || !y) return fail(SXQ_ERR_INVALID, "qmm_forward_noalloc: null x or y");

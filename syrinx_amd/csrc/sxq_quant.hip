@@ -351,6 +351,17 @@ __global__ void k_fill_normal(float* __restrict__ y, int64_t n, uint64_t seed, f
     y[i] = (float)((double)mean + (double)stdv * z);
 }
 
+__global__ void k_bf16_to_f32(const uint16_t* __restrict__ x, int64_t n, float* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = __uint_as_float((uint32_t)x[i] << 16);
+}
+
+hipError_t launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_bf16_to_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, y);
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_normal(float* y, int64_t n, uint64_t seed, float mean, float stdv, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_fill_normal, dim3((n + 255) / 256), dim3(256), 0, s, y, n, seed, mean, stdv);

@@ -23,7 +23,7 @@ from typing import Sequence
 
 import torch
 
-from ._lib import BIT_EXACT, HOST_PTRS, SxqError, check, lib
+from ._lib import BF16_INPUT, BIT_EXACT, HOST_PTRS, SxqError, check, lib
 
 
 class GgmlDType(enum.IntEnum):
@@ -216,7 +216,9 @@ class QMatMul:
         return self._h.value if self._h is not None else 0
 
     def forward(self, xs: torch.Tensor, bias: torch.Tensor = None, exact: bool = False) -> torch.Tensor:
-        """Module::forward.  f32, contiguous, last dim == k, rank >= 2 (Candle's checks).
+        """Module::forward.  f32, contiguous, last dim == k, rank >= 2 (Candle's checks);
+        bf16 input (the Fish GPU path's activations) is also taken and widened to f32
+        exactly on the device (SXQ_BF16_INPUT).  The output is f32.
 
         Outputs equal Candle's CPU vec-dot bit for bit, except that a Q4_K weight applied
         to 64 or more rows runs the f16 MFMA prefill GEMM (error below
@@ -227,10 +229,10 @@ class QMatMul:
             if self._dense_f16:
                 y = (xs.to(torch.float16) @ w.t()).to(xs.dtype)
             else:
-                y = xs @ w.t()
+                y = xs.to(w.dtype) @ w.t()
             return y if bias is None else y + bias
-        if xs.dtype != torch.float32:
-            raise SxqError(2, f"unsupported dtype {xs.dtype} for op qmatmul (f32 only)")
+        if xs.dtype not in (torch.float32, torch.bfloat16):
+            raise SxqError(2, f"unsupported dtype {xs.dtype} for op qmatmul (f32 or bf16)")
         if not xs.is_cuda:
             raise SxqError(6, "QMatMul input must be on the GPU holding the weight")
         shape = (ctypes.c_int64 * xs.dim())(*xs.shape)
@@ -241,7 +243,7 @@ class QMatMul:
             bias = bias.to(device=xs.device, dtype=torch.float32).contiguous()
             if bias.numel() != n:
                 raise SxqError(4, f"bias of {bias.numel()} elements for {n} outputs")
-        flags = BIT_EXACT if exact else 0
+        flags = (BIT_EXACT if exact else 0) | (BF16_INPUT if xs.dtype == torch.bfloat16 else 0)
         bptr = _ptr(bias) if bias is not None else None
         if torch.cuda.is_current_stream_capturing():
             # Under graph capture the forward takes a workspace of its own from torch's

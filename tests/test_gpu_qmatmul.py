@@ -404,6 +404,67 @@ def test_prefill_gemm_within_f16_rounding_bound(cuda, ora, n, k, m):
         _eq_bits(y_exact, want)
 
 
+BF16_CASES = [  # (dtype, n, k, m): the GEMV, the 5..16-row matrix-core GEMV, both prefill GEMMs
+    (G.Q4K, 2560, 2560, 1), (G.Q4K, 1003, 2560, 9), (G.Q4K, 2560, 4096, 128), (G.Q8_0, 896, 896, 3),
+    (G.Q8_0, 4864, 896, 200), (G.Q4_0, 896, 896, 130),
+]
+
+
+@pytest.mark.parametrize("dt,n,k,m", BF16_CASES)
+def test_bf16_input_equals_f32_input_of_the_same_values(cuda, ora, dt, n, k, m):
+    """SXQ_BF16_INPUT: bf16 activations (the Fish GPU path's dtype) widen to f32 exactly, so
+    the outputs are those of the f32 input holding the same values, bit for bit -- on
+    device pointers, on host pointers and through the no-allocation entry point."""
+    import ctypes
+    from syrinx_amd._lib import BF16_INPUT, HOST_PTRS, check, lib
+    w = _weights(n, k, 70 + m)
+    blocks = ora.quantize(int(dt), w)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(blocks, (n, k), dt, device=cuda))
+    xb = torch.from_numpy(_acts(m, k, 71 + m)).to(torch.bfloat16).to(cuda)
+    want = qmm.forward(xb.float()).cpu().numpy()
+    _eq_bits(qmm.forward(xb).cpu().numpy(), want)
+    # host pointers: the bf16 bits from host memory
+    xh = xb.cpu().view(torch.int16).numpy().copy()
+    yh = np.empty((m, n), np.float32)
+    shape = (ctypes.c_int64 * 2)(m, k)
+    check(lib().sxq_qmm_forward(qmm._h, xh.ctypes.data_as(ctypes.c_void_p), shape, 2, None,
+                                yh.ctypes.data_as(ctypes.c_void_p), None, HOST_PTRS | BF16_INPUT, None))
+    _eq_bits(yh, want)
+    # the fixed-scratch entry point
+    y = torch.empty((m, n), dtype=torch.float32, device=cuda)
+    check(lib().sxq_qmm_forward_noalloc(qmm._h, ctypes.c_void_p(xb.data_ptr()), shape, 2, None,
+                                        ctypes.c_void_p(y.data_ptr()), None, BF16_INPUT,
+                                        ctypes.c_void_p(torch.cuda.current_stream(cuda).cuda_stream)))
+    _eq_bits(y.cpu().numpy(), want)
+
+
+def test_bf16_input_captured_in_a_graph(cuda, ora):
+    """A bf16 forward under graph capture takes its workspace (with the f32 copy of x)
+    from the graph's pool; replays give the eager bits."""
+    n, k, m = 2560, 2560, 3
+    w = _weights(n, k, 80)
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(ora.quantize(int(G.Q4K), w), (n, k), G.Q4K, device=cuda))
+    x = torch.from_numpy(_acts(m, k, 81)).to(torch.bfloat16).to(cuda)
+    want = qmm.forward(x).cpu().numpy()
+    s = torch.cuda.Stream(device=cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        y = qmm.forward(x)
+    for _ in range(3):
+        _ = torch.zeros(1000, device=cuda).sum().item()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        _eq_bits(y.cpu().numpy(), want)
+
+
+def test_unsupported_input_dtype_is_refused(cuda, ora):
+    qmm = QMatMul.from_qtensor(QTensor.from_blocks(ora.quantize(int(G.Q8_0), _weights(64, 64, 1)), (64, 64), G.Q8_0,
+                                                   device=cuda))
+    with pytest.raises(SxqError, match="unsupported dtype"):
+        qmm.forward(torch.zeros((1, 64), dtype=torch.float16, device=cuda))
+
+
 def test_forward_captured_in_a_graph(cuda, ora):
     # QMatMul.forward captured into a HIP graph (it takes a workspace of its own from the
     # graph's memory pool): GEMV, matrix-core GEMV and the split-K prefill GEMM, each
