@@ -6,6 +6,8 @@
 #include "sxq_kernels.h"
 
 namespace sxq {
+// bf16 -> f32 (exact: the bf16 bits are the f32's upper half), n elements (sxq_quant.hip).
+hipError_t launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t s);
 namespace abi {
 
 // Fish samplers shared with the fast-AR driver (sxq_sample.hip): the codebook draw into

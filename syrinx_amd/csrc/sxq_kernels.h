@@ -12,8 +12,6 @@ hipError_t launch_quantize_act(int vdt, bool canon, const float* x, int64_t ldx,
 hipError_t launch_from_float(int dt, const float* x, int64_t nblocks, void* out, hipStream_t s);
 // Dequantization (QTensor::dequantize) of canonical blocks.
 hipError_t launch_to_float(int dt, const void* blocks, int64_t nelem, float* y, hipStream_t s);
-// bf16 -> f32 (exact: the bf16 bits are the f32's upper half), n elements.
-hipError_t launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t s);
 // Canonical <-> device weight layout.
 hipError_t launch_repack(int dt, const void* canon, int64_t nblocks, void* hdr, void* qs, bool to_device,
                          hipStream_t s);
