@@ -8,6 +8,11 @@
 namespace sxq {
 // bf16 -> f32 (exact: the bf16 bits are the f32's upper half), n elements (sxq_quant.hip).
 hipError_t launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t s);
+// One-row Q8_0 / Q4_0 GEMV that quantizes its f32 row in the prologue (sxq_gemv.hip):
+// y = quant(x) . W^T (+ bias, + res), the bits of launch_quantize_act + launch_gemv.
+bool gemv_quant_fits(const QWeight& w);
+hipError_t launch_gemv_quant(const QWeight& w, const float* x, float* y, const float* bias, const float* res,
+                             hipStream_t s);
 namespace abi {
 
 // Fish samplers shared with the fast-AR driver (sxq_sample.hip): the codebook draw into

@@ -348,6 +348,9 @@ hipError_t run_forward(const sxq_qmm* q, const FwdPlan& p, const float* x, float
         if (e == hipSuccess) e = launch_gemm_q4k(q->w, ws, (int)m, y, n, bias, nullptr, 0, s);
         return e;
     }
+    // one row of Q8_0 / Q4_0: the GEMV quantizes x in its own prologue (one launch, same bits)
+    static const bool separate = getenv("SXQ_GEMV_QUANT_SEPARATE") != nullptr;  // A/B: two launches
+    if (m == 1 && !p.gemm && !separate && gemv_quant_fits(q->w)) return launch_gemv_quant(q->w, x, y, bias, nullptr, s);
     hipError_t e = launch_quantize_act(p.vdt, false, x, k, (int)m, (int)k, ws, s);
     if (p.gemm) return e == hipSuccess ? launch_gemm_q80(q->w, ws, (int)m, y, n, bias, nullptr, 0, s) : e;
     for (int64_t r0 = 0; r0 < m && e == hipSuccess; r0 += 16) {

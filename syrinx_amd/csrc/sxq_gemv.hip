@@ -383,7 +383,9 @@ __global__ __launch_bounds__(1024) void k_gemv2_q4k_quant(const uint4* __restric
 //              stores both halves into y (= gu [2n]) and a = silu(g) * u -- k_silu_mul_quant's
 //              arithmetic -- into act_out [n];
 //   kProQuant  one row: the f32 row ni.x [nb * 32] quantized to Q8_0 in LDS (chunk c of 256
-//              by wave c mod 16, k_silu_mul_quant's quantizer), the down projection of the pair.
+//              by wave c mod 16, the quantizer of k_silu_mul_quant and k_quantize_act; past
+//              the row's end a chunk reads zeros), the down projection of the pair and the
+//              one-row QMatMul forward.
 // The pair leaves the bits of the GEMV + SiLU*mul kernel + GEMV sequence.
 constexpr int kProStage = 0, kProNorm = 1, kProPair = 2, kProQuant = 3;
 template <int MMAX, bool Q4, int PRO, int NT, int TM>
@@ -391,7 +393,8 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
                                                   int n, int nb, const uint8_t* __restrict__ act, int m, int R,
                                                   float* y, int64_t ldy, const float* __restrict__ bias,
                                                   const float* res, int64_t ldr, NormIn ni, float* act_out) {
-    static_assert(PRO == kProStage || (NT == 1024 && MMAX == 1), "the fused prologues are for one row, 1024 threads");
+    static_assert(PRO == kProStage || (MMAX == 1 && (NT == 1024 || PRO == kProQuant)),
+                  "the fused prologues are for one row, the RMSNorm ones with 1024 threads");
     constexpr bool NORM = PRO == kProNorm || PRO == kProPair;
     extern __shared__ uint4 lds[];
     const ActQ8_0* la = (const ActQ8_0*)lds;
@@ -410,7 +413,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
     const int64_t base = (int64_t)row0 * nb;
     const int act_u4 = m * nb * (int)(sizeof(ActQ8_0) / 16);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    constexpr int J = 3;  // kProQuant: chunks per wave (nb <= 48 * 8)
+    constexpr int J = 3, NWV = NT / 64;  // kProQuant: chunks per wave (nb <= J * NWV * 8), waves
     uint4 av[PRO == kProStage ? Stage<NT, MMAX>::kPer : 1];
     float4 xv, wv, qv[J];
     if constexpr (NORM) {
@@ -420,8 +423,8 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
         const int nch = (nb + 7) >> 3;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int cc = min(wave + 16 * j, nch - 1);
-            qv[j] = ld_global((const float4*)(opaque_ptr(ni.x) + cc * 256 + 4 * lane));
+            const int cc = min(wave + NWV * j, nch - 1), e = cc * 256 + 4 * lane;
+            qv[j] = e < nb * 32 ? ld_global((const float4*)(opaque_ptr(ni.x) + e)) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         issue_point();
     } else {
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(NT) void k_gemv2_q80(const uint16_t* __restrict__ d
         const int nch = (nb + 7) >> 3;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int c = wave + 16 * j;
+            const int c = wave + NWV * j;
             wave_quantize_q8_0<false>(qv[j], lane, c < nch && c * 8 + (lane >> 3) < nb,
                                       (uint8_t*)lds + (size_t)min(c, nch - 1) * 8 * sizeof(ActQ8_0));
         }
@@ -1266,6 +1269,54 @@ hipError_t launch_swiglu_pair(const QWeight& gate_up, const QWeight& down, const
     });
     if (e != hipSuccess) return e;
     return hipGetLastError();
+}
+
+// Threads per workgroup of the one-row quantizing GEMV: 1024 where it fits (one workgroup
+// per CU quantizes the row once; [4864 x 896] Q8_0 per call 5.78 us against 5.97 for the
+// quantizer + GEMV launches, 6.04 against 6.13 with 256 threads), else 256 when its four
+// waves' three chunks each cover the row.
+static int gemv_quant_nt(const QWeight& w) {
+    const int n = (int)w.n, nb = (int)w.nb;
+    if (nb <= 3 * 16 * 8 && gemv2_fits(n, nb, 1, w.dtype, 1024)) return 1024;
+    if (nb <= 3 * 4 * 8 && gemv2_fits(n, nb, 1, w.dtype, 256)) return 256;
+    return 0;
+}
+
+bool gemv_quant_fits(const QWeight& w) { return (w.dtype == kQ8_0 || w.dtype == kQ4_0) && gemv_quant_nt(w) > 0; }
+
+template <int NT>
+static hipError_t gemv_quant_launch(const QWeight& w, const float* x, float* y, const float* bias, const float* res,
+                                    hipStream_t s) {
+    const int n = (int)w.n, nb = (int)w.nb, dt = w.dtype;
+    const int R = gemv2_rows(n, nb, 1, dt, NT);
+    const size_t lds = gemv2_lds(nb, 1, R, dt, NT);
+    const int tpr = tasks_per_round(dt, NT);
+    NormIn q;
+    q.x = x;
+    const hipError_t e = with_rounds((R * nb + tpr - 1) / tpr, [&](auto tmc) -> hipError_t {
+        constexpr int TM = decltype(tmc)::value;
+        if (dt == kQ8_0) {
+            if (const hipError_t e_ = allow_lds<k_gemv2_q80<1, false, kProQuant, NT, TM>>(lds); e_ != hipSuccess) return e_;
+            hipLaunchKernelGGL((k_gemv2_q80<1, false, kProQuant, NT, TM>), dim3((n + R - 1) / R), dim3(NT), lds, s,
+                               (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, (const uint8_t*)nullptr, 1, R, y,
+                               (int64_t)0, bias, res, (int64_t)0, q, (float*)nullptr);
+        } else {
+            if (const hipError_t e_ = allow_lds<k_gemv2_q80<1, true, kProQuant, NT, TM>>(lds); e_ != hipSuccess) return e_;
+            hipLaunchKernelGGL((k_gemv2_q80<1, true, kProQuant, NT, TM>), dim3((n + R - 1) / R), dim3(NT), lds, s,
+                               (const uint16_t*)w.hdr, (const uint4*)w.qs, n, nb, (const uint8_t*)nullptr, 1, R, y,
+                               (int64_t)0, bias, res, (int64_t)0, q, (float*)nullptr);
+        }
+        return hipSuccess;
+    });
+    if (e != hipSuccess) return e;
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_quant(const QWeight& w, const float* x, float* y, const float* bias, const float* res,
+                             hipStream_t s) {
+    if (!gemv_quant_fits(w)) return hipErrorInvalidValue;
+    return gemv_quant_nt(w) == 256 ? gemv_quant_launch<256>(w, x, y, bias, res, s)
+                                   : gemv_quant_launch<1024>(w, x, y, bias, res, s);
 }
 
 hipError_t launch_gemv_rmsnorm(const QWeight& w, const NormIn& ni, int m, uint8_t* act_scratch, float* y,
