@@ -466,6 +466,7 @@ PAIR_KINDS = {  # the SwiGLU pair at each weight type: Qwen3-4B width (w1|w3 194
     "fish_q8_0": ("fish", GgmlDType.Q8_0),     # 12 task rounds per gate|up tile
     "fish_q4_0": ("fish", GgmlDType.Q4_0),
     "cv2_q8_0": ("cv2", GgmlDType.Q8_0),
+    "cv2_q4_0": ("cv2", GgmlDType.Q4_0),       # the dtype the reference's load_quantized ships
 }
 
 
