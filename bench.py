@@ -316,8 +316,9 @@ def fish_frame(lm, torch, n=1):
 
 
 def q8_0_gemv(torch, cpu, copies=64, reps=20):
-    """Config 1: one Q8_0 GEMV [4864 x 896] per QMatMul.forward (activation quantization
-    + GEMV), 64 weight copies rotated so the weights stream from HBM, not the MALL."""
+    """Config 1: one Q8_0 GEMV [4864 x 896] per QMatMul.forward (one launch: the GEMV
+    quantizes x in its prologue), 64 weight copies rotated so the weights stream from HBM,
+    not the MALL."""
     from syrinx_amd import GgmlDType, QMatMul, QTensor
     dev = torch.device("cuda:0")
     n, k = 4864, 896
@@ -353,7 +354,7 @@ def q8_0_gemv(torch, cpu, copies=64, reps=20):
            "value": round(gbs, 1), "unit": "GB/s", "us_per_call": round(us, 3), "bytes_per_call": algo,
            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                        "kernel": "k_gemv2_q80 (+ the activation quantizer, per call)"}}
+                        "kernel": "k_gemv2_q80 (quantizing x in its prologue, one launch per call)"}}
     if cpu:
         import numpy as np
         ora = oracle_mod()
