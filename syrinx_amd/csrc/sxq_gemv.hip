@@ -901,9 +901,16 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
 // stay in place in the W' FMA ((1024 + 16 q) * (sc / 16) - 64 sc = q * sc, exact), and
 // full chunks run as straight-line code with the min term in wave 0 only, so the
 // scheduler overlaps the blocks.  Same float steps, same bits.
+//
+// Each workgroup takes the 16-row tiles blockIdx.x, blockIdx.x + gridDim.x, ... and runs
+// their chunks as one sequence (step q: tile q / nc, chunk q % nc), so the loads of a
+// tile's first chunks are in flight while the previous tile computes: a tile costs its
+// chunks' compute, not a workgroup's start-up and load latency.  A tile's class sums go
+// to LDS buffer (tile & 1) after its last chunk and are added and stored after the next
+// barrier; the next write to that buffer comes two tiles later, behind another barrier.
 constexpr int kRecBuf = 16 * kMmaWRow + kMmaHdr + kMmaChunk * 128 + kMmaChunk * 16;  // dwords per chunk buffer
-constexpr size_t kRecLds = 2 * (size_t)kRecBuf * 4;
-static_assert(kRecBuf >= 9 * 256, "the final class sums reuse a chunk buffer");
+constexpr int kRecXb = 9 * 256;  // dwords of one tile's class sums: [chain][activation row][weight row]
+constexpr size_t kRecLds = (2 * (size_t)kRecBuf + 2 * (size_t)kRecXb) * 4;
 
 SXQ_DEV half8_t mma_weight8_hi(uint32_t v, half2_t sc0, half2_t ns0, half2_t sc1, half2_t ns1) {
     const uint32_t u = v >> 8;
@@ -920,18 +927,21 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
                                                           int64_t ldr) {
     extern __shared__ uint4 lds[];
     uint32_t* l32 = (uint32_t*)lds;  // [2][kRecBuf]: weights [16][kMmaWRow], headers [2][256] uint4, bs [4][128], d [4][16]
+    float* xbs = (float*)(l32 + 2 * kRecBuf);  // [2][kRecXb]: class sums of a finished tile
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, nl = lane & 15;
-    const int row0 = blockIdx.x * kMmaRows;
     const int nc = (nb + kMmaChunk - 1) / kMmaChunk;
+    const int ntiles = (n + kMmaRows - 1) / kMmaRows;
+    const int Q = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x * nc;  // this workgroup's steps
+    auto tile_row0 = [&](int q) { return ((int)blockIdx.x + (q / nc) * (int)gridDim.x) * kMmaRows; };
     const uint8_t* rb = (const uint8_t*)rec;
 
-    // chunk copy (clamped, so every load is in bounds): weight piece tid (row tid >> 5,
-    // 16-byte piece tid & 31); tid < 256: the header of (row tid & 15, block (tid >> 6) & 3);
-    // tid 256..383: the records' bs (32 pieces per block); tid 384..399: their d
+    // chunk copy of step q (clamped, so every load is in bounds): weight piece tid (row
+    // tid >> 5, 16-byte piece tid & 31); tid < 256: the header of (row tid & 15, block
+    // (tid >> 6) & 3); tid 256..383: the records' bs (32 pieces per block); tid 384..399: their d
     uint4 swq0, sx;
-    auto stage_load = [&](int c) {
-        const int cc = min(c, nc - 1);
+    auto stage_load = [&](int q) {
+        const int qq = min(q, Q - 1), cc = qq % nc, row0 = tile_row0(qq);
         {
             const int r = min(row0 + (tid >> 5), n - 1), p = tid & 31;
             const int b = min(cc * kMmaChunk + (p >> 3), nb - 1);
@@ -948,8 +958,8 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
             sx = ((const uint4*)(rb + (size_t)b * sizeof(MmaRec) + offsetof(MmaRec, d)))[u & 3];
         }
     };
-    auto stage_store = [&](int c) {
-        uint32_t* bw = l32 + (c & 1) * kRecBuf;
+    auto stage_store = [&](int q) {
+        uint32_t* bw = l32 + (q & 1) * kRecBuf;
         *(uint4*)(bw + (tid >> 5) * kMmaWRow + (tid & 31) * 4) = swq0;
         if (tid < 256) {  // one decode per (block, g, row): scales 2g and 2g + 1 (the latter / 16), d, dmin, mins
             const uint4 sh = sx;
@@ -975,9 +985,9 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
             ((uint4*)(bw + 16 * kMmaWRow + kMmaHdr))[tid - 256] = sx;  // bs [4][128] floats, then d [4][16]
         }
     };
-    // this wave's activation operands of chunk c: block j, class w, row nl, slots 8g .. 8g + 7
-    auto load_a = [&](int c, half8_t (&A)[kMmaChunk]) {
-        const int cc = min(c, nc - 1);
+    // this wave's activation operands of step q's chunk: block j, class w, row nl, slots 8g .. 8g + 7
+    auto load_a = [&](int q, half8_t (&A)[kMmaChunk]) {
+        const int cc = min(q, Q - 1) % nc;
 #pragma unroll
         for (int j = 0; j < kMmaChunk; ++j) {
             const int b = min(cc * kMmaChunk + j, nb - 1);
@@ -987,8 +997,8 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
     // chains of lane (nl, g), accumulator element e: activation row 4g + e, weight row nl
     float s0c[4] = {0.f, 0.f, 0.f, 0.f}, sf[4] = {0.f, 0.f, 0.f, 0.f};
     const bool wave0 = __builtin_amdgcn_readfirstlane(w) == 0;
-    auto body = [&](int c, const half8_t (&A)[kMmaChunk], int live, auto full, auto w0) {
-        const uint32_t* bw = l32 + (c & 1) * kRecBuf;
+    auto body = [&](int q, const half8_t (&A)[kMmaChunk], int live, auto full, auto w0) {
+        const uint32_t* bw = l32 + (q & 1) * kRecBuf;
         const uint4* bh = (const uint4*)(bw + 16 * kMmaWRow);
         const float* bsv = (const float*)(bw + 16 * kMmaWRow + kMmaHdr);
         const float* dv = bsv + kMmaChunk * 128;
@@ -1034,55 +1044,64 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
     };
     using Yes = std::integral_constant<bool, true>;
     using No = std::integral_constant<bool, false>;
-    auto compute = [&](int c, const half8_t (&A)[kMmaChunk]) {
-        const int live = min(kMmaChunk, nb - c * kMmaChunk);
+    auto compute = [&](int q, const half8_t (&A)[kMmaChunk]) {
+        const int live = min(kMmaChunk, nb - (q % nc) * kMmaChunk);
         if (live == kMmaChunk) {
-            if (wave0) body(c, A, live, Yes{}, Yes{});
-            else body(c, A, live, Yes{}, No{});
+            if (wave0) body(q, A, live, Yes{}, Yes{});
+            else body(q, A, live, Yes{}, No{});
         } else {
-            if (wave0) body(c, A, live, No{}, Yes{});
-            else body(c, A, live, No{}, No{});
+            if (wave0) body(q, A, live, No{}, Yes{});
+            else body(q, A, live, No{}, No{});
+        }
+        if (q % nc == nc - 1) {  // the tile's last chunk: its class sums to LDS, fresh chains
+            float* xb = xbs + ((q / nc) & 1) * kRecXb;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = (4 * g + e) * 16 + nl;
+                xb[w * 256 + i] = s0c[e];
+                if (w == 0) xb[8 * 256 + i] = sf[e];
+                s0c[e] = 0.f;
+                sf[e] = 0.f;
+            }
         }
     };
-    // A0 / A1 alternate (the loop runs two chunks per trip, so both stay in registers):
-    // chunk c + 1's operands load while chunk c computes; the weights load two chunks ahead
+    // after the barrier that follows a tile's last chunk: add its class sums in class order
+    auto finish = [&](int q) {
+        if (q % nc != nc - 1) return;
+        const float* xb = xbs + ((q / nc) & 1) * kRecXb;
+        const int mr = tid >> 4, row = tile_row0(q) + (tid & 15);
+        if (tid < 256 && mr < m && row < n) {
+            float tot = -0.0f;
+#pragma unroll
+            for (int cl = 0; cl < 8; ++cl) tot += xb[cl * 256 + tid];
+            float v = xb[8 * 256 + tid] + tot;
+            if (bias) v = v + bias[row];
+            if (res) v = res[(int64_t)mr * ldr + row] + v;
+            y[(int64_t)mr * ldy + row] = v;
+        }
+    };
+    // A0 / A1 alternate (the loop runs two steps per trip, so both stay in registers):
+    // step q + 1's operands load while step q computes; the weights load two steps ahead
     half8_t A0[kMmaChunk], A1[kMmaChunk];
     stage_load(0);
     load_a(0, A0);
     stage_store(0);
     stage_load(1);
     __syncthreads();
-    for (int c = 0; c < nc; c += 2) {
-        load_a(c + 1, A1);
-        compute(c, A0);
-        if (c + 1 < nc) stage_store(c + 1);
-        stage_load(c + 2);
+    for (int q = 0; q < Q; q += 2) {
+        load_a(q + 1, A1);
+        compute(q, A0);
+        if (q + 1 < Q) stage_store(q + 1);
+        stage_load(q + 2);
         __syncthreads();
-        if (c + 1 >= nc) break;
-        load_a(c + 2, A0);
-        compute(c + 1, A1);
-        if (c + 2 < nc) stage_store(c + 2);
-        stage_load(c + 3);
+        finish(q);
+        if (q + 1 >= Q) break;
+        load_a(q + 2, A0);
+        compute(q + 1, A1);
+        if (q + 2 < Q) stage_store(q + 2);
+        stage_load(q + 3);
         __syncthreads();
-    }
-    // the class sums meet in LDS (chunk buffer 0: every read of it is behind the last barrier)
-    float* xb = (float*)lds;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int i = (4 * g + e) * 16 + nl;
-        xb[w * 256 + i] = s0c[e];
-        if (w == 0) xb[8 * 256 + i] = sf[e];
-    }
-    __syncthreads();
-    const int mr = tid >> 4, row = row0 + (tid & 15);
-    if (tid < 256 && mr < m && row < n) {
-        float tot = -0.0f;
-#pragma unroll
-        for (int cl = 0; cl < 8; ++cl) tot += xb[cl * 256 + tid];
-        float v = xb[8 * 256 + tid] + tot;
-        if (bias) v = v + bias[row];
-        if (res) v = res[(int64_t)mr * ldr + row] + v;
-        y[(int64_t)mr * ldy + row] = v;
+        finish(q + 1);
     }
 }
 
@@ -1109,6 +1128,19 @@ static bool gemv_mma_on() {
     return mma;
 }
 
+// Compute units of the current device (cached per device).
+static int gemv_device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev] = v;
+    }
+    return cus[dev];
+}
+
 bool gemv_rec_fits(const QWeight& w, int m) {
     return !gemv_v1() && gemv_mma_on() && w.dtype == kQ4K && m > 4 && m <= 16 && w.n > 0;
 }
@@ -1120,8 +1152,19 @@ hipError_t launch_gemv_rec(const QWeight& w, const void* act, const MmaRec* rec,
         hipFuncSetAttribute((const void*)k_gemv_mma_q4k_rec, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRecLds);
     if (attr != hipSuccess) return attr;
     const int n = (int)w.n, nb = (int)w.nb;
-    hipLaunchKernelGGL(k_gemv_mma_q4k_rec, dim3((unsigned)((n + kMmaRows - 1) / kMmaRows)), dim3(512), kRecLds, s,
-                       (const uint4*)w.hdr, (const uint4*)w.qs, n, nb, rec, m, y, ldy, bias, res, ldr);
+    const int ntiles = (n + kMmaRows - 1) / kMmaRows;
+    // Workgroups: two per compute unit (the kernel's occupancy), the tiles dealt evenly
+    // (the fewest workgroups that keep the most tiles per workgroup).  SXQ_GEMV_REC_WG
+    // sets the target count for A/B measurement; 0 = one workgroup per tile.
+    int target = 2 * gemv_device_cus();
+    if (const char* e = getenv("SXQ_GEMV_REC_WG")) target = atoi(e);
+    int grid = ntiles;
+    if (target > 0 && target < ntiles) {
+        const int per = (ntiles + target - 1) / target;
+        grid = (ntiles + per - 1) / per;
+    }
+    hipLaunchKernelGGL(k_gemv_mma_q4k_rec, dim3((unsigned)grid), dim3(512), kRecLds, s, (const uint4*)w.hdr,
+                       (const uint4*)w.qs, n, nb, rec, m, y, ldy, bias, res, ldr);
     return hipGetLastError();
 }
 

@@ -629,6 +629,30 @@ def test_sixteen_streams_ragged_kv_256_to_2048(cuda, ora, model_oracle):
     assert lm.lengths(16) == [L + 2 for L in lengths]
 
 
+@pytest.mark.parametrize("width", [2560, 1024])
+def test_persistent_matrix_core_gemv_grids_agree(cuda, monkeypatch, width):
+    """The 5..16-row matrix-core GEMV with each workgroup walking many 16-row tiles (grid
+    targets of 3 and 7 workgroups: the chunk pipeline runs across tile boundaries, chunk
+    counts 1, 3, 4 and 10, partial last tiles) gives the bits of one workgroup per tile:
+    logits and hidden state of one step of 9 ragged streams through every projection
+    (wqkv, wo, w1|w3, w2, head) at the Qwen3-4B width and at a 1024-wide model."""
+    kw = {} if width == 2560 else dict(dim=1024, n_heads=8, n_kv_heads=2, intermediate=2816)
+    cfg = _fish_small(n_layers=1, max_batch=9, **kw)
+    lengths = [5, 70, 17, 0, 33, 1, 48, 60, 9]
+    fr = _frames(np.random.default_rng(43), 9, cfg)
+    outs = []
+    for target in ("0", "3", "7"):
+        monkeypatch.setenv("SXQ_GEMV_REC_WG", target)
+        lm, _ = _build_dev(cfg, cuda, 41)
+        lm.kv_fill_random(lengths, seed=42)
+        logits, _, hidden = lm.step(ids=torch.from_numpy(fr), want_hidden=True)
+        outs.append((logits.cpu().numpy(), hidden.cpu().numpy()))
+        del lm
+    for target, (lg, hd) in zip(("3", "7"), outs[1:]):
+        _bits_equal(lg, outs[0][0], f"width {width}, {target} workgroups: logits")
+        _bits_equal(hd, outs[0][1], f"width {width}, {target} workgroups: hidden")
+
+
 def test_cosyvoice2_q8_0_24_layers_at_kv_512(cuda, ora, model_oracle):
     """CosyVoice2 LM at its configuration: 24 layers, Q8_0, KV prefilled to 512
     positions (eight 64-position attention splits at head_dim 64).  Two steps (an
