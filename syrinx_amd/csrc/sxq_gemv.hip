@@ -18,8 +18,7 @@
 #include <stddef.h>
 #include <stdlib.h>
 
-#include <type_traits>
-
+#include <atomic>
 #include <type_traits>
 
 #include "sxq_decoder.h"
@@ -1130,15 +1129,15 @@ static bool gemv_mma_on() {
 
 // Compute units of the current device (cached per device).
 static int gemv_device_cus() {
-    static int cus[64] = {0};
+    static std::atomic<int> cus[64];  // 0 until first asked (threads may race to store the same value)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cus[dev] = v;
+    int c = cus[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev].store(c, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return c;
 }
 
 bool gemv_rec_fits(const QWeight& w, int m) {
