@@ -138,6 +138,13 @@ CASES = [
     (G.Q8_0, 19456, 2560, 1),  # Qwen3-4B fused w1|w3
     (G.Q8_0, 2560, 9728, 1),   # w2 (K = 9728: 304 blocks per row)
     (G.Q8_0, 16389, 2560, 3),
+    # one activation row of Q8_0 / Q4_0 (the GEMV quantizes x in its prologue): the
+    # smallest matrix, the widest row it takes (384 blocks), and a wider one (512 blocks:
+    # the quantizer and the GEMV as two launches)
+    (G.Q8_0, 1, 32, 1),
+    (G.Q4_0, 77, 12288, 1),
+    (G.Q8_0, 300, 16384, 1),
+    (G.Q4K, 1, 256, 1),        # the smallest Q4_K matrix
 ]
 
 
