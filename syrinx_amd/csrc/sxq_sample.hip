@@ -648,26 +648,72 @@ struct RasArgs {
 
 // ras_sampling over log_softmax(logits): the row is overwritten by its log-probabilities
 // (the stop ids -inf when ignore_eos), as log_softmax_vec + the mask produce them.
+// Keys of the draw (the probabilities exp(log-prob), rounded to f32) kept in LDS for rows of
+// up to this many ids (the CosyVoice heads: 6564 and 6761), so that the selection's six
+// passes read them rather than evaluate an f64 exponential per id each time; longer rows
+// recompute them.  The same values either way.
+constexpr int kRasLdsKeys = 8192;
+
 __global__ __launch_bounds__(kST) void k_sample_ras(RasArgs A) {
     __shared__ Shared sh;
     __shared__ double chunk_sum[kST];
+    __shared__ float keys[kRasLdsKeys];
+    __shared__ int hist_sh[kMaxWindow];
+    __shared__ int hist_len;
     const int s = blockIdx.x, tid = threadIdx.x, n = A.vocab;
     float* row = A.logits + (int64_t)s * A.stride;
+    // the repetition window, fetched first: its loads overlap the softmax
+    if (A.decoded && tid < A.win) hist_sh[tid] = A.decoded[(int64_t)s * A.win + tid];
+    if (tid == 0) hist_len = A.decoded_len ? A.decoded_len[s] : 0;
+    // rows of up to kRasLdsKeys ids: the row's values stay in registers for the three passes
+    constexpr int kRv = kRasLdsKeys / kST;
+    const bool lds_keys = n <= kRasLdsKeys;
+    float rv[kRv];
     float mx = -INFINITY;
-    for (int i = tid; i < n; i += kST) mx = fmaxf(mx, row[i]);
+    if (lds_keys) {
+#pragma unroll
+        for (int j = 0; j < kRv; ++j) {
+            const int i = tid + j * kST;
+            rv[j] = i < n ? row[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kRv; ++j)
+            if (tid + j * kST < n) mx = fmaxf(mx, rv[j]);
+    } else {
+        for (int i = tid; i < n; i += kST) mx = fmaxf(mx, row[i]);
+    }
     mx = block_max(mx, sh);
     double tot = 0.0;
-    for (int i = tid; i < n; i += kST) tot += exp((double)(row[i] - mx));
+    if (lds_keys) {
+#pragma unroll
+        for (int j = 0; j < kRv; ++j)
+            if (tid + j * kST < n) tot += exp((double)(rv[j] - mx));
+    } else {
+        for (int i = tid; i < n; i += kST) tot += exp((double)(row[i] - mx));
+    }
     tot = block_sum(tot, sh);
     const double lse = (double)mx + log(tot);
-    for (int i = tid; i < n; i += kST) {
-        float lp = (float)((double)row[i] - lse);
-        if (A.ignore_eos && i >= A.eos_begin && i < A.eos_end) lp = -INFINITY;
-        row[i] = lp;
+    if (lds_keys) {
+#pragma unroll
+        for (int j = 0; j < kRv; ++j) {
+            const int i = tid + j * kST;
+            if (i < n) {
+                float lp = (float)((double)rv[j] - lse);
+                if (A.ignore_eos && i >= A.eos_begin && i < A.eos_end) lp = -INFINITY;
+                row[i] = lp;
+                keys[i] = exp_f32(lp);
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += kST) {
+            float lp = (float)((double)row[i] - lse);
+            if (A.ignore_eos && i >= A.eos_begin && i < A.eos_end) lp = -INFINITY;
+            row[i] = lp;
+        }
     }
     __syncthreads();
     const View v{0, n, -1};
-    auto key = [&](int e) -> float { return exp_f32(row[e]); };
+    auto key = [&](int e) -> float { return lds_keys ? keys[e] : exp_f32(row[e]); };
     const int K = top_k_select(v, key, A.top_k, sh);
     uint64_t rng = A.rng[s];
     // nucleus: the leading candidates while cum (f32) < top_p and count < top_k, drawn
@@ -690,16 +736,14 @@ __global__ __launch_bounds__(kST) void k_sample_ras(RasArgs A) {
         }
         const int top = sh.top_id[pick < 0 ? 0 : pick];
         int rep = 0;
-        const int len = A.decoded_len ? A.decoded_len[s] : 0;
-        const int* hist = A.decoded ? A.decoded + (int64_t)s * A.win : nullptr;
-        for (int i = 0; hist && i < len; ++i) rep += hist[i] == top;
+        for (int i = 0; A.decoded && i < hist_len; ++i) rep += hist_sh[i] == top;
         sh.result = (float)rep >= (float)A.win * A.tau_r ? -1 : top;
     }
     __syncthreads();
     if (sh.result < 0) {  // random_sampling over the full distribution, ids in order
         const int chunk = (n + kST - 1) / kST, e0 = tid * chunk, e1 = min(n, e0 + chunk);
         double cs = 0.0;
-        for (int i = e0; i < e1; ++i) cs += (double)exp_f32(row[i]);
+        for (int i = e0; i < e1; ++i) cs += (double)key(i);
         chunk_sum[tid] = cs;
         __syncthreads();
         if (tid == 0) {
@@ -718,7 +762,7 @@ __global__ __launch_bounds__(kST) void k_sample_ras(RasArgs A) {
             double acc = sh.dred[0];
             int pick = e1 - 1;  // summed in another association than chunk_sum: stay in the chunk
             for (int i = e0; i < e1; ++i) {
-                acc += (double)exp_f32(row[i]);
+                acc += (double)key(i);
                 if (sh.dval < acc) {
                     pick = i;
                     break;
