@@ -552,13 +552,16 @@ def test_attention_and_o_projection_in_one_launch_equals_two(cuda, monkeypatch, 
         np.testing.assert_array_equal(a, b)
 
 
-def test_graph_replayed_at_shorter_lengths_than_captured(cuda):
+@pytest.mark.parametrize("kind,cut", [("fish_q4k", 40), ("cv2_q8_0", 40), ("cv2_q8_0", 100)])
+def test_graph_replayed_at_shorter_lengths_than_captured(cuda, kind, cut):
     """A step captured at a long length and replayed after the lengths were cut (the
     attention grid and every length-dependent choice were fixed at capture; the splits
-    past the new length now idle) gives the bits of an eager step at the new lengths."""
-    cfg = _fish_small(n_layers=2)
+    past the new length now idle) gives the bits of an eager step at the new lengths --
+    down to one split (cut 40, no merge) and to two (cut 100), at the Qwen3-4B and the
+    CosyVoice2 shapes."""
+    cfg = _small_cfg(kind, 2)
     cfg.max_seq = 256
-    fr = _frames(np.random.default_rng(73), 1, cfg)
+    fr = _first_ids(kind, cfg, np.random.default_rng(73))
     outs = []
     for graph in (True, False):
         lm = D.DecoderLM(cfg, device=cuda)
@@ -566,10 +569,10 @@ def test_graph_replayed_at_shorter_lengths_than_captured(cuda):
         lm.kv_fill_random([200], seed=72)
         if graph:
             lm.step(ids=torch.from_numpy(fr), graph=True)  # captured with four splits per head group
-        lm.set_lengths([40])
+        lm.set_lengths([cut])
         logits, _ = lm.step(ids=torch.from_numpy(fr), graph=graph)
         outs.append(logits.cpu().numpy())
-        assert lm.lengths(1) == [41]
+        assert lm.lengths(1) == [cut + 1]
     assert np.isfinite(outs[0]).all()
     np.testing.assert_array_equal(outs[0], outs[1])
 
