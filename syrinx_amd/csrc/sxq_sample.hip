@@ -613,7 +613,8 @@ __global__ __launch_bounds__(kST) void k_sample_fish(FishArgs A) {
     if (tid != 0) return;
     if (MODE == 0) {
         int* win = A.window ? A.window + (int64_t)s * P.ras_win_size : nullptr;
-        int len = A.window_len ? A.window_len[s] : 0;
+        // (clamped to 0..ras_win_size: a corrupt length can neither read nor write past the window)
+        int len = A.window_len ? min(max(A.window_len[s], 0), P.ras_win_size) : 0;
         bool in_window = false;
         for (int i = 0; win && i < len; ++i) in_window |= win[i] == tok;
         const bool semantic = tok >= P.semantic_begin && tok <= P.semantic_end;
@@ -664,7 +665,7 @@ __global__ __launch_bounds__(kST) void k_sample_ras(RasArgs A) {
     float* row = A.logits + (int64_t)s * A.stride;
     // the repetition window, fetched first: its loads overlap the softmax
     if (A.decoded && tid < A.win) hist_sh[tid] = A.decoded[(int64_t)s * A.win + tid];
-    if (tid == 0) hist_len = A.decoded_len ? A.decoded_len[s] : 0;
+    if (tid == 0) hist_len = A.decoded_len ? min(max(A.decoded_len[s], 0), A.win) : 0;  // (clamped to 0..win)
     // rows of up to kRasLdsKeys ids: the row's values stay in registers for the three passes
     constexpr int kRv = kRasLdsKeys / kST;
     const bool lds_keys = n <= kRasLdsKeys;
@@ -776,7 +777,7 @@ __global__ __launch_bounds__(kST) void k_sample_ras(RasArgs A) {
     const int tok = sh.result;
     if (A.decoded && (tok < A.eos_begin || tok >= A.eos_end) && A.win > 0) {  // the generate loop's history
         int* hist = A.decoded + (int64_t)s * A.win;
-        int len = A.decoded_len[s];
+        int len = min(max(A.decoded_len[s], 0), A.win);
         if (len == A.win) {
             for (int i = 1; i < len; ++i) hist[i - 1] = hist[i];
             --len;
