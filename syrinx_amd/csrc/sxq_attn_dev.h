@@ -394,7 +394,7 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
     const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(part_s, (uint32_t)nh * (uint32_t)max_splits * PR * 4);
     if (!attn_split<VDT, HD, NT, GC, PUB>(A, s, g, sp, pos, nsp, smem, part_s, prs)) return;
     // the last split of the group to arrive merges the group's heads
-    if (!publish_and_count(&A.counter[s * nkv + g], (unsigned)nsp, last)) return;
+    if (!publish_and_count(&A.counter[(s * nkv + g) * A.cstride], (unsigned)nsp, last)) return;
 
     // merge: ctx = sum_z exp(m_z - M) acc_z / sum_z exp(m_z - M) l_z, M = max_z m_z.
     // The tile LDS is free now: wts [G][nsp] | lsum [G] | red2 [nq][gd].
@@ -482,7 +482,7 @@ SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* sm
         v = make_float4(c.x / ls, c.y / ls, c.z / ls, c.w / ls);
     }
     attn_emit_context<VDT, HD, PUB>(A, s, g, gd, T, v, smem);
-    if (tid == 0) __hip_atomic_store(&A.counter[s * nkv + g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(&A.counter[(s * nkv + g) * A.cstride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace sxq

@@ -20,13 +20,21 @@ constexpr int kMaxSplits = 512;
 // The fused kernel: workgroup size and the most splits one of its merges takes.
 constexpr int kAttnThreads = 512;
 constexpr int kMaxSplitsFused = kMaxSplits * kAttnSplit / kAttnSplitFused;
+// Arrival counters that many workgroups of one launch update (the fused attention's per
+// head group, the O projection's per layer) sit kCounterStride words (256 B) apart: atomics
+// on one line are performed one after another (~14 ns each), so counters sharing a line
+// would queue every group's arrivals behind each other's.
+constexpr int kCounterStride = 64;
+// The stride the launches use: kCounterStride, or 1 with SXQ_COUNTERS_PACKED set (for
+// comparison; the buffers are sized for kCounterStride either way).
+int counter_stride();
 size_t attn_partial_lds(int nh, int nkv, int hd, int P);
 hipError_t launch_attention(int vdt, const float* q, const float* kc, const float* vc, const int* len, int B, int nh,
                             int nkv, int hd, int max_seq, int64_t kv_stream_stride, int P, int max_splits,
                             float* part, uint8_t* act, float* ctx_out, hipStream_t s);
 // Fused decode attention (QK-norm + RoPE + KV append + split partials + last-arriver
-// merge + quantization of the context); counter: [B * nkv] zero before the first call
-// (each call leaves it zero).  q_out / ctx_out optional (tests).  Returns
+// merge + quantization of the context); counter: [B * nkv * kCounterStride] zero before
+// the first call (each call leaves it zero).  q_out / ctx_out optional (tests).  Returns
 // hipErrorInvalidValue when the head group is not a whole number of activation blocks
 // (attn_decode_fits); the caller then uses the three-kernel path.
 bool attn_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits);
@@ -49,8 +57,8 @@ hipError_t launch_embed_mcf(const int* ids, int ids_per, int B, const float* tab
 hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
                               hipStream_t s);
 // Greedy argmax per stream; with `len` also advances each stream's cached length.
-// pval/pidx: [B * kArgmaxSlices] partials; counter: [B], zero before the first call
-// (each call leaves it zero again).
+// pval/pidx: [B * kArgmaxSlices] partials; counter: [B * kCounterStride], zero before the
+// first call (each call leaves it zero again).
 constexpr int kArgmaxSlices = 64;
 hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, int* len,
                          float* pval, int* pidx, unsigned* counter, hipStream_t s);
@@ -98,7 +106,8 @@ struct AttnArgs {
     int max_seq;
     float* part;  // partial records [B][nh][max_splits][hd + 4]
     int max_splits;
-    unsigned* counter;       // [B][nkv] arrival counters, zero between launches
+    unsigned* counter;       // [B][nkv] arrival counters, cstride words apart, zero between launches
+    int cstride;
     uint8_t* act;            // [B] quantized context rows (the O projection's input)
     float *ctx_out, *q_out;  // optional f32 copies of the context and the roped queries
     unsigned* ready;         // k_attn_wo_decode: context slices published so far
@@ -110,7 +119,8 @@ struct AttnArgs {
 // launch: the projection's workgroups follow the attention's and wait for the n_kv
 // context slices.  ready: this launch's counter, zero at the launch; ready_next: a counter
 // that no launch in flight uses, zeroed by this one (the counters of consecutive layers
-// chain this way: layer l's launch zeroes layer l + 1's).
+// chain this way: layer l's launch zeroes layer l + 1's; they sit counter_stride() words
+// apart).
 bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo, int dim);
 hipError_t attn_wo_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo);
 hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int nh, int nkv, int hd, const float* qn,

@@ -451,7 +451,7 @@ SXQ_DEV void argmax_merge(float& best, int& idx, float ov, int oi) {
 __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits, int vocab, int* __restrict__ ids,
                                                 int ids_per, int* __restrict__ out_ids, int* __restrict__ len,
                                                 float* __restrict__ pval, int* __restrict__ pidx,
-                                                unsigned* __restrict__ counter) {
+                                                unsigned* __restrict__ counter, int cstride) {
     __shared__ float bv[4];
     __shared__ int bi[4];
     __shared__ bool last;
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
         store_agent(&pval[s * kArgmaxSlices + b], best);
         store_agent(&pidx[s * kArgmaxSlices + b], idx);
     }
-    if (!publish_and_count(&counter[s], kArgmaxSlices, &last)) return;
+    if (!publish_and_count(&counter[s * cstride], kArgmaxSlices, &last)) return;
     if (wave == 0) {
         best = load_agent(&pval[s * kArgmaxSlices + lane]);
         idx = load_agent(&pidx[s * kArgmaxSlices + lane]);
@@ -483,7 +483,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
             ids[(int64_t)s * ids_per] = idx;
             if (out_ids) out_ids[s] = idx;
             if (len) len[s] += 1;
-            __hip_atomic_store(&counter[s], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&counter[s * cstride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -578,6 +578,11 @@ hipError_t attn_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits)
     return hipFuncSetAttribute(attn_decode_kernel(vdt, hd, nh / nkv), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 }
 
+int counter_stride() {
+    static const int stride = getenv("SXQ_COUNTERS_PACKED") ? 1 : kCounterStride;
+    return stride;
+}
+
 hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, int nh, int nkv, int hd, const float* qn,
                                    const float* kn, float eps, int interleaved, const float* cos_t, const float* sin_t,
                                    const int* len, float* kc, float* vc, int64_t kv_stream_stride, int max_seq,
@@ -607,6 +612,7 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
     A.part = part;
     A.max_splits = max_splits;
     A.counter = counter;
+    A.cstride = counter_stride();
     A.act = act;
     A.ctx_out = ctx_out;
     A.q_out = q_out;
@@ -875,6 +881,7 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
     A.part = part;
     A.max_splits = max_splits;
     A.counter = counter;
+    A.cstride = counter_stride();
     A.act = act;
     A.ctx_out = ctx_out;
     A.q_out = q_out;
@@ -926,7 +933,7 @@ hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* t
 hipError_t launch_argmax(const float* logits, int B, int vocab, int* ids, int ids_per, int* out_ids, int* len,
                          float* pval, int* pidx, unsigned* counter, hipStream_t s) {
     hipLaunchKernelGGL(k_argmax, dim3(B, kArgmaxSlices), dim3(256), 0, s, logits, vocab, ids, ids_per, out_ids, len,
-                       pval, pidx, counter);
+                       pval, pidx, counter, counter_stride());
     return hipGetLastError();
 }
 
