@@ -102,7 +102,7 @@ SXQ_DEV void rope_store(float2 y, int interleaved, float* dst, float* gdst, int 
 // PUB: the slice is read by other workgroups of the same launch (the O projection of
 // k_attn_wo_decode), so it is quantized into LDS at smem + A.pub_off bytes, copied out
 // by wave 0 with agent-coherent 16-byte stores and, once those have completed, counted
-// in A.ready.
+// in every copy of A.ready.
 template <int VDT, int HD, bool PUB = false>
 SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, float4 v, float* smem) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -126,7 +126,8 @@ SXQ_DEV void attn_emit_context(const AttnArgs& A, int s, int g, int gd, int T, f
             const __amdgpu_buffer_rsrc_t r = coherent_rsrc(qdst, (uint32_t)nu4 * 16);
             for (int i = lane; i < nu4; i += 64) store16_coherent(r, (uint32_t)i * 16, ((const float4*)ql)[i]);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice has reached the coherent level
-            if (lane == 0) __hip_atomic_fetch_add(A.ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane < A.ready_copies)  // every copy of the counter
+                __hip_atomic_fetch_add(A.ready + lane * A.cstride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }

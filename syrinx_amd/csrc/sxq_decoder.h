@@ -28,6 +28,12 @@ constexpr int kCounterStride = 64;
 // The stride the launches use: kCounterStride, or 1 with SXQ_COUNTERS_PACKED set (for
 // comparison; the buffers are sized for kCounterStride either way).
 int counter_stride();
+// The O projection's ready counter is kept in copies (counter_stride() words apart): every
+// context slice bumps each copy, and each projection workgroup polls one, so that the
+// hundreds of pollers and the slices' atomics do not all meet on one line.  ready_copies():
+// kReadyCopies, or SXQ_READY_COPIES (1..kReadyCopies).
+constexpr int kReadyCopies = 8;
+int ready_copies();
 size_t attn_partial_lds(int nh, int nkv, int hd, int P);
 hipError_t launch_attention(int vdt, const float* q, const float* kc, const float* vc, const int* len, int B, int nh,
                             int nkv, int hd, int max_seq, int64_t kv_stream_stride, int P, int max_splits,
@@ -110,7 +116,8 @@ struct AttnArgs {
     int cstride;
     uint8_t* act;            // [B] quantized context rows (the O projection's input)
     float *ctx_out, *q_out;  // optional f32 copies of the context and the roped queries
-    unsigned* ready;         // k_attn_wo_decode: context slices published so far
+    unsigned* ready;         // k_attn_wo_decode: context slices published so far (ready_copies copies)
+    int ready_copies;
     uint32_t pub_off;        // k_attn_wo_decode: LDS byte offset of the slice staging
     MmaRec* rec;             // optional (Q8_K, B <= 16): the context rows' MmaRec records too
 };
@@ -119,8 +126,8 @@ struct AttnArgs {
 // launch: the projection's workgroups follow the attention's and wait for the n_kv
 // context slices.  ready: this launch's counter, zero at the launch; ready_next: a counter
 // that no launch in flight uses, zeroed by this one (the counters of consecutive layers
-// chain this way: layer l's launch zeroes layer l + 1's; they sit counter_stride() words
-// apart).
+// chain this way: layer l's launch zeroes layer l + 1's); each is kReadyCopies counters
+// counter_stride() words apart.
 bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo, int dim);
 hipError_t attn_wo_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo);
 hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int nh, int nkv, int hd, const float* qn,

@@ -578,6 +578,15 @@ hipError_t attn_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits)
     return hipFuncSetAttribute(attn_decode_kernel(vdt, hd, nh / nkv), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 }
 
+int ready_copies() {
+    static const int copies = [] {
+        const char* e = getenv("SXQ_READY_COPIES");
+        const int v = e ? atoi(e) : kReadyCopies;
+        return v < 1 ? 1 : (v > kReadyCopies ? kReadyCopies : v);
+    }();
+    return copies;
+}
+
 int counter_stride() {
     static const int stride = getenv("SXQ_COUNTERS_PACKED") ? 1 : kCounterStride;
     return stride;
@@ -617,6 +626,7 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
     A.ctx_out = ctx_out;
     A.q_out = q_out;
     A.ready = nullptr;
+    A.ready_copies = 0;
     A.pub_off = 0;
     A.rec = rec;
     const int all = (max_seq + kAttnSplitFused - 1) / kAttnSplitFused;  // partial records: max_splits per head
@@ -654,10 +664,11 @@ constexpr int kWoQ4K = 0, kWoQ8_0 = 1, kWoQ4_0 = 2;  // the O projection's weigh
 // One thread polls the ready counter (bounded), then the context row (act_u4 16-byte
 // pieces) is staged into LDS at the coherent level (this XCD's L2 may hold an earlier
 // layer's row).  Returns false when the poll ran out.
-SXQ_DEV bool wo_wait_stage(const AttnArgs& A, const WoArgs& W, uint4* lds, int act_u4, bool* flag) {
+SXQ_DEV bool wo_wait_stage(const AttnArgs& A, const WoArgs& W, int t, uint4* lds, int act_u4, bool* flag) {
     if (threadIdx.x == 0) {
+        const unsigned* ready = A.ready + (t % A.ready_copies) * A.cstride;  // this tile's copy
         int it = 0;
-        while (__hip_atomic_load(A.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < W.need && it < kWoPollCap) {
+        while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < W.need && it < kWoPollCap) {
             __builtin_amdgcn_s_sleep(1);
             ++it;
         }
@@ -695,7 +706,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6,
         const int r = tid >> 3, l = tid & 7;
         const float res = W.y[row0 + min(r, rows - 1)];  // clamped, unconditional; used by lane class 0 of rows < rows
         issue_point();
-        if (tid == 0 && t == 0) __hip_atomic_store(W.ready_next, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid < A.ready_copies && t == 0)
+            __hip_atomic_store(W.ready_next + tid * A.cstride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int act_u4 = nb * (int)(sizeof(ActQ8K) / 16);
         float* pr = (float*)(lds + act_u4);  // product chains [R + 1][9][CS]
         bool ok = true;
@@ -706,7 +718,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6,
         // the second waits for the context and computes the result.
 #pragma nounroll
         for (int pass = 0; pass < 2; ++pass) {
-            if (pass == 1) ok = wo_wait_stage(A, W, lds, act_u4, &flag);
+            if (pass == 1) ok = wo_wait_stage(A, W, t, lds, act_u4, &flag);
             q4k_tile_products<1, NT, TM>(q, h, (const ActQ8K*)lds, nb, 1, rows, W.R, pr);
             __syncthreads();
             v = q4k_tile_fold(pr, nb, W.R, 0, rows);
@@ -731,7 +743,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6,
         }
         const float res = W.y[row0 + min(tid, rows - 1)];  // clamped, unconditional; used by threads < rows
         issue_point();
-        if (tid == 0 && t == 0) __hip_atomic_store(W.ready_next, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid < A.ready_copies && t == 0)
+            __hip_atomic_store(W.ready_next + tid * A.cstride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int act_u4 = nb * (int)(sizeof(ActQ8_0) / 16);
         const ActQ8_0* la = (const ActQ8_0*)lds;
         float* pr = (float*)(lds + act_u4);  // product slots [TM * TPI]
@@ -739,7 +752,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6,
         float v = 0.0f;
 #pragma nounroll
         for (int pass = 0; pass < 2; ++pass) {  // as for Q4_K: a warm-up pass, then the real one
-            if (pass == 1) ok = wo_wait_stage(A, W, lds, act_u4, &flag);
+            if (pass == 1) ok = wo_wait_stage(A, W, t, lds, act_u4, &flag);
 #pragma unroll
             for (int u = 0; u < TM; ++u) {
                 if (u * TPI >= tasks) break;
@@ -886,6 +899,7 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
     A.ctx_out = ctx_out;
     A.q_out = q_out;
     A.ready = ready;
+    A.ready_copies = ready_copies();
     A.pub_off = (uint32_t)wo_pub_off(nh, nkv, hd, max_splits);
     A.rec = nullptr;
     WoArgs W;

@@ -89,7 +89,7 @@ struct sxq_lm {
     // per-layer counters (layer l's launch zeroes layer l + 1's); wo_dirty: a step was
     // enqueued only in part, so the counters are zeroed before the next one
     bool wo_fused = false, wo_dirty = false;
-    unsigned* wo_ready = nullptr;  // [n_layers], likewise
+    unsigned* wo_ready = nullptr;  // [n_layers][kReadyCopies], likewise
     bool swiglu = false;        // one decode row: gate|up GEMV with SwiGLU epilogue + quantizing down GEMV
     float* act_f32 = nullptr;   // SwiGLU output row of that pair [max_batch][intermediate]
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
@@ -226,7 +226,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
     if (tr) STEP(record(lm->h, (size_t)n * c.dim));
     const bool wo_fused = lm->wo_fused && n == 1;
     if (lm->wo_dirty) {
-        STEP(launch_fill_int((int*)lm->wo_ready, c.n_layers * kCounterStride, 0, s));
+        STEP(launch_fill_int((int*)lm->wo_ready, c.n_layers * kReadyCopies * kCounterStride, 0, s));
         lm->wo_dirty = false;
     }
     lm->wo_dirty = wo_fused;  // until the whole step is enqueued
@@ -263,8 +263,8 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                 STEP(launch_attention_wo_decode(lm->vdt, lm->qkv, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn, kn,
                                                 c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len,
                                                 kc, vc, c.max_seq, lm->max_splits, lm->part, lm->attn_count, lm->act_o,
-                                                L.wo.w, lm->h, lm->wo_ready + (size_t)l * counter_stride(),
-                                                lm->wo_ready + (size_t)((l + 1) % c.n_layers) * counter_stride(),
+                                                L.wo.w, lm->h, lm->wo_ready + (size_t)l * kReadyCopies * counter_stride(),
+                                                lm->wo_ready + (size_t)((l + 1) % c.n_layers) * kReadyCopies * counter_stride(),
                                                 ctx_slot, q_slot, s, lm->grid_splits));
             else
                 STEP(launch_attention_decode(lm->vdt, lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn,
@@ -642,7 +642,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->am_idx, sizeof(int) * MB * kArgmaxSlices);
     A((void**)&lm->am_count, sizeof(unsigned) * MB * kCounterStride);
     A((void**)&lm->attn_count, sizeof(unsigned) * MB * c.n_kv_heads * kCounterStride);
-    A((void**)&lm->wo_ready, sizeof(unsigned) * c.n_layers * kCounterStride);
+    A((void**)&lm->wo_ready, sizeof(unsigned) * c.n_layers * kReadyCopies * kCounterStride);
     if (e != hipSuccess) {
         destroy_lm(lm);
         return hip_fail(e, "lm_create: allocation");
@@ -678,7 +678,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     if (e == hipSuccess) e = hipMemset(lm->d_ids, 0, sizeof(int) * MB * lm->ids_per);
     if (e == hipSuccess) e = hipMemset(lm->am_count, 0, sizeof(unsigned) * MB * kCounterStride);
     if (e == hipSuccess) e = hipMemset(lm->attn_count, 0, sizeof(unsigned) * MB * c.n_kv_heads * kCounterStride);
-    if (e == hipSuccess) e = hipMemset(lm->wo_ready, 0, sizeof(unsigned) * c.n_layers * kCounterStride);
+    if (e == hipSuccess) e = hipMemset(lm->wo_ready, 0, sizeof(unsigned) * c.n_layers * kReadyCopies * kCounterStride);
     if (e == hipSuccess) e = hipMemset(lm->act_f32, 0, sizeof(float) * (size_t)MB * I);
     if (e == hipSuccess && lm->rec_a) e = hipMemset(lm->rec_a, 0, sizeof(MmaRec) * (size_t)(c.dim / 256));
     if (e == hipSuccess && lm->rec_o) e = hipMemset(lm->rec_o, 0, sizeof(MmaRec) * (size_t)(lm->ctx / 256));
