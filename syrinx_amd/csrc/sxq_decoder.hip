@@ -461,9 +461,19 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
     const float* x = logits + (int64_t)s * vocab;
     float best = -INFINITY;
     int idx = 0x7FFFFFFF;
-    for (int i = lo + tid; i < hi; i += 256) {
-        const float v = x[i];
-        if (v > best) { best = v; idx = i; }  // per-thread indices rise: first max kept
+    // a thread's loads issued together (kArgmaxBatch at a time), then compared in index
+    // order: per-thread indices rise, so the first max is kept
+    constexpr int kArgmaxBatch = 16;
+    for (int i0 = lo + tid; i0 < hi; i0 += kArgmaxBatch * 256) {
+        float v[kArgmaxBatch];
+#pragma unroll
+        for (int j = 0; j < kArgmaxBatch; ++j) {
+            const int i = i0 + j * 256;
+            v[j] = i < hi ? x[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int j = 0; j < kArgmaxBatch; ++j)
+            if (v[j] > best) { best = v[j]; idx = i0 + j * 256; }
     }
     for (int o = 32; o >= 1; o >>= 1) argmax_merge(best, idx, __shfl_xor(best, o, 64), __shfl_xor(idx, o, 64));
     if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
