@@ -20,11 +20,6 @@ constexpr int kMaxSplits = 512;
 // The fused kernel: workgroup size and the most splits one of its merges takes.
 constexpr int kAttnThreads = 512;
 constexpr int kMaxSplitsFused = kMaxSplits * kAttnSplit / kAttnSplitFused;
-// Arrival counters that many workgroups of one launch update (the fused attention's per
-// head group, the O projection's per layer) sit kCounterStride words (256 B) apart: atomics
-// on one line are performed one after another (~14 ns each), so counters sharing a line
-// would queue every group's arrivals behind each other's.
-constexpr int kCounterStride = 64;
 // The stride the launches use: kCounterStride, or 1 with SXQ_COUNTERS_PACKED set (for
 // comparison; the buffers are sized for kCounterStride either way).
 int counter_stride();

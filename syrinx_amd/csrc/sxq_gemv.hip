@@ -901,12 +901,19 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
 // full chunks run as straight-line code with the min term in wave 0 only, so the
 // scheduler overlaps the blocks.  Same float steps, same bits.
 //
-// Each workgroup takes the 16-row tiles blockIdx.x, blockIdx.x + gridDim.x, ... and runs
-// their chunks as one sequence (step q: tile q / nc, chunk q % nc), so the loads of a
-// tile's first chunks are in flight while the previous tile computes: a tile costs its
-// chunks' compute, not a workgroup's start-up and load latency.  A tile's class sums go
-// to LDS buffer (tile & 1) after its last chunk and are added and stored after the next
-// barrier; the next write to that buffer comes two tiles later, behind another barrier.
+// The work is dealt in units: a 16-row tile, or with ks > 1 one of a tile's ks K-slices
+// (cpu = ceil(nc / ks) chunks each, chunks past the row's blocks computing nothing).  Each
+// workgroup takes the units blockIdx.x, blockIdx.x + gridDim.x, ... and runs their chunks
+// as one sequence (step q: unit q / cpu, chunk q % cpu of it), so the loads of a unit's
+// first chunks are in flight while the previous unit computes: a unit costs its chunks'
+// compute, not a workgroup's start-up and load latency.  A unit's class sums go to LDS
+// buffer (unit & 1) after its last chunk and are used after the next barrier; the next
+// write to that buffer comes two units later, behind another barrier.  With ks = 1 they
+// are added in class order and stored: Candle's chains, the same bits.  With ks > 1 (the
+// tiles alone would leave compute units idle) each slice's chains go to `part` and the
+// tile's last slice to arrive (a counter per tile, kCounterStride words apart, reset
+// after use) adds the slices' chains in slice order before the class order: the same
+// terms in another association (float rounding only), in a fixed order (deterministic).
 constexpr int kRecBuf = 16 * kMmaWRow + kMmaHdr + kMmaChunk * 128 + kMmaChunk * 16;  // dwords per chunk buffer
 constexpr int kRecXb = 9 * 256;  // dwords of one tile's class sums: [chain][activation row][weight row]
 constexpr size_t kRecLds = (2 * (size_t)kRecBuf + 2 * (size_t)kRecXb) * 4;
@@ -920,27 +927,52 @@ SXQ_DEV half8_t mma_weight8_hi(uint32_t v, half2_t sc0, half2_t ns0, half2_t sc1
     return half8_t{x0.x, x0.y, x1.x, x1.y, x2.x, x2.y, x3.x, x3.y};
 }
 
+constexpr int kRecMaxKs = kGemvRecMaxKs;
+
 __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restrict__ hdr, const uint4* __restrict__ qs,
                                                           int n, int nb, const MmaRec* __restrict__ rec, int m, float* y,
                                                           int64_t ldy, const float* __restrict__ bias, const float* res,
-                                                          int64_t ldr) {
+                                                          int64_t ldr, int ks, float* part, unsigned* count) {
     extern __shared__ uint4 lds[];
+    __shared__ bool last;
     uint32_t* l32 = (uint32_t*)lds;  // [2][kRecBuf]: weights [16][kMmaWRow], headers [2][256] uint4, bs [4][128], d [4][16]
-    float* xbs = (float*)(l32 + 2 * kRecBuf);  // [2][kRecXb]: class sums of a finished tile
+    float* xbs = (float*)(l32 + 2 * kRecBuf);  // [2][kRecXb]: class sums of a finished unit
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, nl = lane & 15;
     const int nc = (nb + kMmaChunk - 1) / kMmaChunk;
-    const int ntiles = (n + kMmaRows - 1) / kMmaRows;
-    const int Q = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x * nc;  // this workgroup's steps
-    auto tile_row0 = [&](int q) { return ((int)blockIdx.x + (q / nc) * (int)gridDim.x) * kMmaRows; };
+    const int cpu = (nc + ks - 1) / ks;  // chunks per unit
+    const int units = (n + kMmaRows - 1) / kMmaRows * ks;
+    const int Q = (units - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x * cpu;  // this workgroup's steps
+    // A step: the workgroup's unit count u (its parity picks the class-sum buffer), the
+    // chunk c within the unit, the unit's tile and K-slice.  Steps advance by adds and
+    // compares; the only divisions by cpu and ks are the ones above and here.  Steps
+    // past the last one (loads issued ahead) point past the tiles, whose loads clamp.
+    struct Step {
+        int u, c, tile, sl;
+    };
+    const int gq = (int)gridDim.x / ks, gr = (int)gridDim.x % ks;
+    auto adv = [&](Step s) {
+        if (++s.c == cpu) {
+            s.c = 0;
+            ++s.u;
+            s.tile += gq;
+            s.sl += gr;
+            if (s.sl >= ks) {
+                s.sl -= ks;
+                ++s.tile;
+            }
+        }
+        return s;
+    };
+    auto chunk = [&](const Step& s) { return s.sl * cpu + s.c; };  // >= nc: past the row's blocks
     const uint8_t* rb = (const uint8_t*)rec;
 
-    // chunk copy of step q (clamped, so every load is in bounds): weight piece tid (row
+    // chunk copy of step s (clamped, so every load is in bounds): weight piece tid (row
     // tid >> 5, 16-byte piece tid & 31); tid < 256: the header of (row tid & 15, block
     // (tid >> 6) & 3); tid 256..383: the records' bs (32 pieces per block); tid 384..399: their d
     uint4 swq0, sx;
-    auto stage_load = [&](int q) {
-        const int qq = min(q, Q - 1), cc = qq % nc, row0 = tile_row0(qq);
+    auto stage_load = [&](const Step& s) {
+        const int cc = chunk(s), row0 = s.tile * kMmaRows;
         {
             const int r = min(row0 + (tid >> 5), n - 1), p = tid & 31;
             const int b = min(cc * kMmaChunk + (p >> 3), nb - 1);
@@ -985,8 +1017,8 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
         }
     };
     // this wave's activation operands of step q's chunk: block j, class w, row nl, slots 8g .. 8g + 7
-    auto load_a = [&](int q, half8_t (&A)[kMmaChunk]) {
-        const int cc = min(q, Q - 1) % nc;
+    auto load_a = [&](const Step& s, half8_t (&A)[kMmaChunk]) {
+        const int cc = chunk(s);
 #pragma unroll
         for (int j = 0; j < kMmaChunk; ++j) {
             const int b = min(cc * kMmaChunk + j, nb - 1);
@@ -1043,8 +1075,8 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
     };
     using Yes = std::integral_constant<bool, true>;
     using No = std::integral_constant<bool, false>;
-    auto compute = [&](int q, const half8_t (&A)[kMmaChunk]) {
-        const int live = min(kMmaChunk, nb - (q % nc) * kMmaChunk);
+    auto compute = [&](int q, const Step& s, const half8_t (&A)[kMmaChunk]) {
+        const int live = min(kMmaChunk, nb - chunk(s) * kMmaChunk);  // <= 0: nothing to add
         if (live == kMmaChunk) {
             if (wave0) body(q, A, live, Yes{}, Yes{});
             else body(q, A, live, Yes{}, No{});
@@ -1052,8 +1084,8 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
             if (wave0) body(q, A, live, No{}, Yes{});
             else body(q, A, live, No{}, No{});
         }
-        if (q % nc == nc - 1) {  // the tile's last chunk: its class sums to LDS, fresh chains
-            float* xb = xbs + ((q / nc) & 1) * kRecXb;
+        if (s.c == cpu - 1) {  // the unit's last chunk: its class sums to LDS, fresh chains
+            float* xb = xbs + (s.u & 1) * kRecXb;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int i = (4 * g + e) * 16 + nl;
@@ -1064,16 +1096,46 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
             }
         }
     };
-    // after the barrier that follows a tile's last chunk: add its class sums in class order
-    auto finish = [&](int q) {
-        if (q % nc != nc - 1) return;
-        const float* xb = xbs + ((q / nc) & 1) * kRecXb;
-        const int mr = tid >> 4, row = tile_row0(q) + (tid & 15);
-        if (tid < 256 && mr < m && row < n) {
+    // after the barrier that follows a unit's last chunk (every thread calls it)
+    auto finish = [&](const Step& s) {
+        if (s.c != cpu - 1) return;
+        const float* xb = xbs + (s.u & 1) * kRecXb;
+        const int t = s.tile;
+        const int mr = tid >> 4, row = t * kMmaRows + (tid & 15);
+        const bool out = tid < 256 && mr < m && row < n;
+        float c[9];
+        if (ks == 1) {
+            if (out)
+#pragma unroll
+                for (int cl = 0; cl < 9; ++cl) c[cl] = xb[cl * 256 + tid];
+        } else {
+            // this slice's chains to part [tile][slice][9][256]; the tile's last slice adds them
+            const __amdgpu_buffer_rsrc_t pr = coherent_rsrc(part + (size_t)t * ks * kRecXb, (uint32_t)(ks * kRecXb * 4));
+            for (int i = tid; i < kRecXb / 4; i += 512)
+                store16_coherent(pr, (uint32_t)(s.sl * kRecXb + 4 * i) * 4, ((const float4*)xb)[i]);
+            if (!publish_and_count(&count[t * kCounterStride], (unsigned)ks, &last)) return;
+            if (out) {
+                float v[kRecMaxKs][9];
+#pragma unroll
+                for (int k = 0; k < kRecMaxKs; ++k)
+#pragma unroll
+                    for (int cl = 0; cl < 9; ++cl)
+                        if (k < ks) v[k][cl] = load_agent(part + ((size_t)t * ks + k) * kRecXb + cl * 256 + tid);
+#pragma unroll
+                for (int cl = 0; cl < 9; ++cl) {
+                    c[cl] = v[0][cl];
+#pragma unroll
+                    for (int k = 1; k < kRecMaxKs; ++k)
+                        if (k < ks) c[cl] += v[k][cl];
+                }
+            }
+            if (tid == 0) __hip_atomic_store(&count[t * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (out) {  // the class sums in class order, then the min chain
             float tot = -0.0f;
 #pragma unroll
-            for (int cl = 0; cl < 8; ++cl) tot += xb[cl * 256 + tid];
-            float v = xb[8 * 256 + tid] + tot;
+            for (int cl = 0; cl < 8; ++cl) tot += c[cl];
+            float v = c[8] + tot;
             if (bias) v = v + bias[row];
             if (res) v = res[(int64_t)mr * ldr + row] + v;
             y[(int64_t)mr * ldy + row] = v;
@@ -1082,25 +1144,29 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
     // A0 / A1 alternate (the loop runs two steps per trip, so both stay in registers):
     // step q + 1's operands load while step q computes; the weights load two steps ahead
     half8_t A0[kMmaChunk], A1[kMmaChunk];
-    stage_load(0);
-    load_a(0, A0);
+    Step s0 = {0, 0, (int)blockIdx.x / ks, (int)blockIdx.x % ks}, s1 = adv(s0);  // steps q, q + 1
+    stage_load(s0);
+    load_a(s0, A0);
     stage_store(0);
-    stage_load(1);
+    stage_load(s1);
     __syncthreads();
     for (int q = 0; q < Q; q += 2) {
-        load_a(q + 1, A1);
-        compute(q, A0);
+        const Step s2 = adv(s1), s3 = adv(s2);
+        load_a(s1, A1);
+        compute(q, s0, A0);
         if (q + 1 < Q) stage_store(q + 1);
-        stage_load(q + 2);
+        stage_load(s2);
         __syncthreads();
-        finish(q);
+        finish(s0);
         if (q + 1 >= Q) break;
-        load_a(q + 2, A0);
-        compute(q + 1, A1);
+        load_a(s2, A0);
+        compute(q + 1, s1, A1);
         if (q + 2 < Q) stage_store(q + 2);
-        stage_load(q + 3);
+        stage_load(s3);
         __syncthreads();
-        finish(q + 1);
+        finish(s1);
+        s0 = s2;
+        s1 = s3;
     }
 }
 
@@ -1145,25 +1211,36 @@ bool gemv_rec_fits(const QWeight& w, int m) {
 }
 
 hipError_t launch_gemv_rec(const QWeight& w, const void* act, const MmaRec* rec, int m, float* y, int64_t ldy,
-                           const float* bias, const float* res, int64_t ldr, hipStream_t s) {
+                           const float* bias, const float* res, int64_t ldr, hipStream_t s, const GemvRecWs* ws) {
     if (!rec || !gemv_rec_fits(w, m)) return launch_gemv(w, act, m, y, ldy, bias, res, ldr, s);
     static const hipError_t attr =
         hipFuncSetAttribute((const void*)k_gemv_mma_q4k_rec, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRecLds);
     if (attr != hipSuccess) return attr;
     const int n = (int)w.n, nb = (int)w.nb;
-    const int ntiles = (n + kMmaRows - 1) / kMmaRows;
-    // Workgroups: two per compute unit (the kernel's occupancy), the tiles dealt evenly
-    // (the fewest workgroups that keep the most tiles per workgroup).  SXQ_GEMV_REC_WG
-    // sets the target count for A/B measurement; 0 = one workgroup per tile.
+    const int ntiles = (n + kMmaRows - 1) / kMmaRows, nc = (nb + kMmaChunk - 1) / kMmaChunk;
+    // Workgroups: two per compute unit (the kernel's occupancy), the units dealt evenly
+    // (the fewest workgroups that keep the most units per workgroup).  SXQ_GEMV_REC_WG
+    // sets the target count for A/B measurement; 0 = one workgroup per unit.
     int target = 2 * gemv_device_cus();
     if (const char* e = getenv("SXQ_GEMV_REC_WG")) target = atoi(e);
-    int grid = ntiles;
-    if (target > 0 && target < ntiles) {
-        const int per = (ntiles + target - 1) / target;
-        grid = (ntiles + per - 1) / per;
+    // K-slices: as many as the tiles leave workgroups for (read per call: SXQ_BIT_EXACT)
+    int ks = 1;
+    const char* exact = getenv("SXQ_BIT_EXACT");
+    if (ws && ws->part && !(exact && exact[0] != '0') && ntiles <= kGemvRecMaxSplitTiles && target > 0 &&
+        2 * ntiles <= target) {
+        const int want = min(min(kGemvRecMaxKs, nc), target / ntiles);
+        const int cpu = (nc + want - 1) / want;
+        ks = (nc + cpu - 1) / cpu;  // no slice without a chunk
+    }
+    const int units = ntiles * ks;
+    int grid = units;
+    if (target > 0 && target < units) {
+        const int per = (units + target - 1) / target;
+        grid = (units + per - 1) / per;
     }
     hipLaunchKernelGGL(k_gemv_mma_q4k_rec, dim3((unsigned)grid), dim3(512), kRecLds, s, (const uint4*)w.hdr,
-                       (const uint4*)w.qs, n, nb, rec, m, y, ldy, bias, res, ldr);
+                       (const uint4*)w.qs, n, nb, rec, m, y, ldy, bias, res, ldr, ks, ks > 1 ? ws->part : nullptr,
+                       ks > 1 ? ws->count : nullptr);
     return hipGetLastError();
 }
 

@@ -34,9 +34,31 @@ hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64
 // The same product, for the m (5..16) rows launch_gemv runs on the Q4_K matrix-core GEMV,
 // read from the MmaRec records [nb] the quantizers wrote beside `act` (the same values):
 // gemv_rec_fits tells when it applies; otherwise (or with rec null) this is launch_gemv.
+// ws (optional): where the tiles alone would leave compute units idle (the 2560-row wo
+// and w2 at 16 rows: 160 tiles), each tile's K is split over up to kGemvRecMaxKs
+// workgroups whose class-sum chains the tile's last slice adds in slice order: the
+// same terms in another association (float rounding only, deterministic), not Candle's
+// bits.  Without ws, or with SXQ_BIT_EXACT set, every tile runs in one workgroup and
+// the result is bit-identical to Candle's vec-dot.  The workspace belongs to one stream
+// of launches at a time.
+// Arrival counters that many workgroups of one launch update (the fused attention's per
+// head group, the O projection's per layer, a split GEMV's per tile) sit kCounterStride
+// words (256 B) apart: atomics on one line are performed one after another (~14 ns
+// each), so counters sharing a line would queue every group's arrivals behind each
+// other's.
+constexpr int kCounterStride = 64;
+constexpr int kGemvRecMaxKs = 4;
+constexpr int kGemvRecMaxSplitTiles = 256;  // the most tiles a split launch has
+struct GemvRecWs {
+    float* part = nullptr;       // [kGemvRecMaxSplitTiles * kGemvRecMaxKs][9][256] slice chains
+    unsigned* count = nullptr;   // [kGemvRecMaxSplitTiles * kCounterStride], zero between launches
+    static size_t part_bytes() { return sizeof(float) * (size_t)kGemvRecMaxSplitTiles * kGemvRecMaxKs * 9 * 256; }
+    static size_t count_bytes() { return sizeof(unsigned) * (size_t)kGemvRecMaxSplitTiles * kCounterStride; }
+};
 bool gemv_rec_fits(const QWeight& w, int m);
 hipError_t launch_gemv_rec(const QWeight& w, const void* act, const MmaRec* rec, int m, float* y, int64_t ldy,
-                           const float* bias, const float* res, int64_t ldr, hipStream_t s);
+                           const float* bias, const float* res, int64_t ldr, hipStream_t s,
+                           const GemvRecWs* ws = nullptr);
 
 // RMSNorm of f32 rows x [m, k] (crates/syrinx-fish/src/s2/nn.rs:100-106), the result
 // quantized and multiplied: y = quant(rmsnorm(x) * w_norm) . W^T (+ bias, + res).

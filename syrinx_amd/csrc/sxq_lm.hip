@@ -90,6 +90,7 @@ struct sxq_lm {
     // enqueued only in part, so the counters are zeroed before the next one
     bool wo_fused = false, wo_dirty = false;
     unsigned* wo_ready = nullptr;  // [n_layers][kReadyCopies], likewise
+    GemvRecWs rec_ws;              // 5..16 streams: the matrix-core GEMV's K-split workspace
     bool swiglu = false;        // one decode row: gate|up GEMV with SwiGLU epilogue + quantizing down GEMV
     float* act_f32 = nullptr;   // SwiGLU output row of that pair [max_batch][intermediate]
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
@@ -280,7 +281,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                                   c.max_seq, lm->kv_stream_stride, kAttnSplit, lm->max_splits, lm->part, lm->act_o,
                                   tr ? slot((size_t)n * lm->ctx) : nullptr, s));
         }
-        if (!wo_fused) STEP(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->h, c.dim, L.bo, lm->h, c.dim, s));
+        if (!wo_fused) STEP(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->h, c.dim, L.bo, lm->h, c.dim, s, &lm->rec_ws));
         if (tr) STEP(record(lm->h, nd));
         if (lm->swiglu && n == 1) {
             STEP(launch_swiglu_pair(L.w13.w, L.w2.w, norm_in(lm->h, L.ffn_norm, tr ? slot(nd) : nullptr), lm->gu,
@@ -292,7 +293,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                                      lm->gu, 2 * I, nullptr, nullptr, 0, s, rec_a));
             if (tr) STEP(record(lm->gu, (size_t)n * 2 * I));
             STEP(launch_silu_mul_quant(lm->vdt, lm->gu, n, I, lm->act_d, tr ? slot((size_t)n * I) : nullptr, s, rec_d));
-            STEP(launch_gemv_rec(L.w2.w, lm->act_d, rec_d, n, lm->h, c.dim, nullptr, lm->h, c.dim, s));
+            STEP(launch_gemv_rec(L.w2.w, lm->act_d, rec_d, n, lm->h, c.dim, nullptr, lm->h, c.dim, s, &lm->rec_ws));
         }
         if (tr) STEP(record(lm->h, nd));
     }
@@ -635,6 +636,10 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
         A((void**)&lm->rec_a, sizeof(MmaRec) * (size_t)(c.dim / 256));
         A((void**)&lm->rec_o, sizeof(MmaRec) * (size_t)(lm->ctx / 256));
         A((void**)&lm->rec_d, sizeof(MmaRec) * (size_t)(I / 256));
+        if (MB >= 5) {
+            A((void**)&lm->rec_ws.part, GemvRecWs::part_bytes());
+            A((void**)&lm->rec_ws.count, GemvRecWs::count_bytes());
+        }
     }
     A((void**)&lm->d_ids, sizeof(int) * MB * lm->ids_per);
     A((void**)&lm->d_next, sizeof(int) * MB);
@@ -683,6 +688,7 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     if (e == hipSuccess && lm->rec_a) e = hipMemset(lm->rec_a, 0, sizeof(MmaRec) * (size_t)(c.dim / 256));
     if (e == hipSuccess && lm->rec_o) e = hipMemset(lm->rec_o, 0, sizeof(MmaRec) * (size_t)(lm->ctx / 256));
     if (e == hipSuccess && lm->rec_d) e = hipMemset(lm->rec_d, 0, sizeof(MmaRec) * (size_t)(I / 256));
+    if (e == hipSuccess && lm->rec_ws.count) e = hipMemset(lm->rec_ws.count, 0, GemvRecWs::count_bytes());
     lm->attn_fused = getenv("SXQ_ATTN_UNFUSED") == nullptr && attn_decode_fits(lm->vdt, c.n_heads, c.n_kv_heads, hd, lm->max_splits);
     lm->swiglu = getenv("SXQ_SWIGLU_UNFUSED") == nullptr && swiglu_pair_fits(lm->layers[0].w13.w, lm->layers[0].w2.w);
     if (e == hipSuccess && lm->attn_fused &&
@@ -1117,10 +1123,11 @@ sxq_status sxq_lm_gemv_pass(sxq_lm* lm, int n, int with_head, void* stream) {
     const MmaRec* rec_d = rec_ok ? lm->rec_d : nullptr;
     for (int l = 0; l < c.n_layers; ++l) {
         LmLayer& L = lm->layers[l];
-        HIP_TRY(launch_gemv_rec(L.wqkv.w, lm->act_a, rec_a, n, lm->qkv, lm->qkv_n, L.bqkv, nullptr, 0, s), "lm_gemv_pass");
-        HIP_TRY(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->gu, c.dim, L.bo, nullptr, 0, s), "lm_gemv_pass");
-        HIP_TRY(launch_gemv_rec(L.w13.w, lm->act_a, rec_a, n, lm->gu, 2 * I, nullptr, nullptr, 0, s), "lm_gemv_pass");
-        HIP_TRY(launch_gemv_rec(L.w2.w, lm->act_d, rec_d, n, lm->gu, c.dim, nullptr, nullptr, 0, s), "lm_gemv_pass");
+        const GemvRecWs* ws = &lm->rec_ws;
+        HIP_TRY(launch_gemv_rec(L.wqkv.w, lm->act_a, rec_a, n, lm->qkv, lm->qkv_n, L.bqkv, nullptr, 0, s, ws), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(L.wo.w, lm->act_o, rec_o, n, lm->gu, c.dim, L.bo, nullptr, 0, s, ws), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(L.w13.w, lm->act_a, rec_a, n, lm->gu, 2 * I, nullptr, nullptr, 0, s, ws), "lm_gemv_pass");
+        HIP_TRY(launch_gemv_rec(L.w2.w, lm->act_d, rec_d, n, lm->gu, c.dim, nullptr, nullptr, 0, s, ws), "lm_gemv_pass");
     }
     if (with_head)
         HIP_TRY(launch_gemv_rec(lm->head.w, lm->act_a, rec_a, n, lm->logits, c.vocab, nullptr, nullptr, 0, s),
