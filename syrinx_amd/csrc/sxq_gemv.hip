@@ -910,10 +910,11 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k(const uint4* __restrict__ 
 // buffer (unit & 1) after its last chunk and are used after the next barrier; the next
 // write to that buffer comes two units later, behind another barrier.  With ks = 1 they
 // are added in class order and stored: Candle's chains, the same bits.  With ks > 1 (the
-// tiles alone would leave compute units idle) each slice's chains go to `part` and the
-// tile's last slice to arrive (a counter per tile, kCounterStride words apart, reset
-// after use) adds the slices' chains in slice order before the class order: the same
-// terms in another association (float rounding only), in a fixed order (deterministic).
+// tiles alone would leave compute units idle) each slice adds its own chains the same
+// way into one partial per output, `part` [tile][slice][256], and the tile's last slice
+// to arrive (a counter per tile, kCounterStride words apart, reset after use) adds the
+// partials in slice order: the same terms in another association (float rounding
+// only), in a fixed order (deterministic).
 constexpr int kRecBuf = 16 * kMmaWRow + kMmaHdr + kMmaChunk * 128 + kMmaChunk * 16;  // dwords per chunk buffer
 constexpr int kRecXb = 9 * 256;  // dwords of one tile's class sums: [chain][activation row][weight row]
 constexpr size_t kRecLds = (2 * (size_t)kRecBuf + 2 * (size_t)kRecXb) * 4;
@@ -1103,39 +1104,30 @@ __global__ __launch_bounds__(512) void k_gemv_mma_q4k_rec(const uint4* __restric
         const int t = s.tile;
         const int mr = tid >> 4, row = t * kMmaRows + (tid & 15);
         const bool out = tid < 256 && mr < m && row < n;
-        float c[9];
-        if (ks == 1) {
-            if (out)
+        // the unit's class sums in class order, then the min chain
+        float v = 0.0f;
+        if (tid < 256) {
+            float tot = -0.0f;
 #pragma unroll
-                for (int cl = 0; cl < 9; ++cl) c[cl] = xb[cl * 256 + tid];
-        } else {
-            // this slice's chains to part [tile][slice][9][256]; the tile's last slice adds them
-            const __amdgpu_buffer_rsrc_t pr = coherent_rsrc(part + (size_t)t * ks * kRecXb, (uint32_t)(ks * kRecXb * 4));
-            for (int i = tid; i < kRecXb / 4; i += 512)
-                store16_coherent(pr, (uint32_t)(s.sl * kRecXb + 4 * i) * 4, ((const float4*)xb)[i]);
+            for (int cl = 0; cl < 8; ++cl) tot += xb[cl * 256 + tid];
+            v = xb[8 * 256 + tid] + tot;
+        }
+        if (ks > 1) {  // this slice's partials to part; the tile's last slice adds them in slice order
+            if (tid < 256) store_agent(part + ((size_t)t * ks + s.sl) * 256 + tid, v);
             if (!publish_and_count(&count[t * kCounterStride], (unsigned)ks, &last)) return;
             if (out) {
-                float v[kRecMaxKs][9];
+                float pv[kRecMaxKs];
 #pragma unroll
                 for (int k = 0; k < kRecMaxKs; ++k)
+                    if (k < ks) pv[k] = load_agent(part + ((size_t)t * ks + k) * 256 + tid);
+                v = pv[0];
 #pragma unroll
-                    for (int cl = 0; cl < 9; ++cl)
-                        if (k < ks) v[k][cl] = load_agent(part + ((size_t)t * ks + k) * kRecXb + cl * 256 + tid);
-#pragma unroll
-                for (int cl = 0; cl < 9; ++cl) {
-                    c[cl] = v[0][cl];
-#pragma unroll
-                    for (int k = 1; k < kRecMaxKs; ++k)
-                        if (k < ks) c[cl] += v[k][cl];
-                }
+                for (int k = 1; k < kRecMaxKs; ++k)
+                    if (k < ks) v += pv[k];
             }
             if (tid == 0) __hip_atomic_store(&count[t * kCounterStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (out) {  // the class sums in class order, then the min chain
-            float tot = -0.0f;
-#pragma unroll
-            for (int cl = 0; cl < 8; ++cl) tot += c[cl];
-            float v = c[8] + tot;
+        if (out) {
             if (bias) v = v + bias[row];
             if (res) v = res[(int64_t)mr * ldr + row] + v;
             y[(int64_t)mr * ldy + row] = v;
@@ -1223,12 +1215,15 @@ hipError_t launch_gemv_rec(const QWeight& w, const void* act, const MmaRec* rec,
     // sets the target count for A/B measurement; 0 = one workgroup per unit.
     int target = 2 * gemv_device_cus();
     if (const char* e = getenv("SXQ_GEMV_REC_WG")) target = atoi(e);
-    // K-slices: as many as the tiles leave workgroups for (read per call: SXQ_BIT_EXACT)
+    // K-slices: as many as the tiles leave workgroups for (2 for the 160-tile wo, 3 for
+    // w2: 4077 tok/s on the 16-stream step against 4035 with 2 for both and 3804 with 4;
+    // SXQ_GEMV_REC_KS sets the count for A/B).  SXQ_BIT_EXACT (read per call): one.
     int ks = 1;
     const char* exact = getenv("SXQ_BIT_EXACT");
     if (ws && ws->part && !(exact && exact[0] != '0') && ntiles <= kGemvRecMaxSplitTiles && target > 0 &&
         2 * ntiles <= target) {
-        const int want = min(min(kGemvRecMaxKs, nc), target / ntiles);
+        int want = min(min(kGemvRecMaxKs, nc), target / ntiles);
+        if (const char* e = getenv("SXQ_GEMV_REC_KS")) want = min(min(kGemvRecMaxKs, nc), max(1, atoi(e)));
         const int cpu = (nc + want - 1) / want;
         ks = (nc + cpu - 1) / cpu;  // no slice without a chunk
     }

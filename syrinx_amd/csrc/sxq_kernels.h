@@ -36,9 +36,9 @@ hipError_t launch_gemv(const QWeight& w, const void* act, int m, float* y, int64
 // gemv_rec_fits tells when it applies; otherwise (or with rec null) this is launch_gemv.
 // ws (optional): where the tiles alone would leave compute units idle (the 2560-row wo
 // and w2 at 16 rows: 160 tiles), each tile's K is split over up to kGemvRecMaxKs
-// workgroups whose class-sum chains the tile's last slice adds in slice order: the
-// same terms in another association (float rounding only, deterministic), not Candle's
-// bits.  Without ws, or with SXQ_BIT_EXACT set, every tile runs in one workgroup and
+// workgroups, each adding its own class chains into one partial per output, and the
+// tile's last slice adds the partials in slice order: the same terms in another
+// association (float rounding only, deterministic), not Candle's bits.  Without ws, or with SXQ_BIT_EXACT set, every tile runs in one workgroup and
 // the result is bit-identical to Candle's vec-dot.  The workspace belongs to one stream
 // of launches at a time.
 // Arrival counters that many workgroups of one launch update (the fused attention's per
@@ -50,9 +50,9 @@ constexpr int kCounterStride = 64;
 constexpr int kGemvRecMaxKs = 4;
 constexpr int kGemvRecMaxSplitTiles = 256;  // the most tiles a split launch has
 struct GemvRecWs {
-    float* part = nullptr;       // [kGemvRecMaxSplitTiles * kGemvRecMaxKs][9][256] slice chains
+    float* part = nullptr;       // [kGemvRecMaxSplitTiles * kGemvRecMaxKs][256] slice partials
     unsigned* count = nullptr;   // [kGemvRecMaxSplitTiles * kCounterStride], zero between launches
-    static size_t part_bytes() { return sizeof(float) * (size_t)kGemvRecMaxSplitTiles * kGemvRecMaxKs * 9 * 256; }
+    static size_t part_bytes() { return sizeof(float) * (size_t)kGemvRecMaxSplitTiles * kGemvRecMaxKs * 256; }
     static size_t count_bytes() { return sizeof(unsigned) * (size_t)kGemvRecMaxSplitTiles * kCounterStride; }
 };
 bool gemv_rec_fits(const QWeight& w, int m);
