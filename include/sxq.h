@@ -303,7 +303,12 @@ sxq_status sxq_lm_reset(sxq_lm *lm, int n_streams, void *stream);
  *            crates/syrinx-fish/src/s2/slow_ar.rs:207-246, consumed at
  *            crates/syrinx-fish/src/common/dualar.rs:196);
  *   next_ids int32 [n_streams] greedy argmax of the logits, or NULL.
- * Each stream's token is placed at its current length, which then advances by one. */
+ * Each stream's token is placed at its current length, which then advances by one.
+ * Projections keep Candle's bits, except with 5..16 streams where a projection's 16-row
+ * tiles would leave compute units idle (the 2560-row wo and w2): their K is split over
+ * workgroups whose partials are added in a fixed order (deterministic; within 1e-6 of
+ * sum |w x| per output).  The environment variable SXQ_BIT_EXACT=1 (read at each
+ * launch, so at capture for a graph) keeps every projection bit-identical. */
 sxq_status sxq_lm_step(sxq_lm *lm, int n_streams, const int32_t *ids, const float *embeds, float *logits,
                        float *hidden, int32_t *next_ids, unsigned flags, void *stream);
 /* sxq_lm_prefill flags */
