@@ -416,11 +416,21 @@ __global__ __launch_bounds__(256) void k_embed_mcf(const int* __restrict__ ids, 
     if (e < dim) {
         float x = !tok_ok ? 0.0f : table ? table[(int64_t)tok * dim + e] : weight_elem(w, tok, e);
         if (n_cb > 0) {
+            // the codebooks' values are loaded kCbBatch at a time (all in flight together),
+            // then added in codebook order
+            constexpr int kCbBatch = 16;
             float vq = 0.0f;
-            for (int i = 0; i < n_cb; ++i) {
-                const int code = fr[1 + i];
-                const float v = (code >= 0 && code < cb_size) ? cb[((int64_t)code + (int64_t)i * cb_size) * dim + e] : 0.0f;
-                vq = i == 0 ? v : vq + v;
+            for (int i0 = 0; i0 < n_cb; i0 += kCbBatch) {
+                float v[kCbBatch];
+#pragma unroll
+                for (int j = 0; j < kCbBatch; ++j) {
+                    const int i = i0 + j;
+                    const int code = i < n_cb ? fr[1 + i] : -1;
+                    v[j] = (code >= 0 && code < cb_size) ? cb[((int64_t)code + (int64_t)i * cb_size) * dim + e] : 0.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < kCbBatch; ++j)
+                    if (i0 + j < n_cb) vq = i0 + j == 0 ? v[j] : vq + v[j];
             }
             x = (x + vq * (sem ? 1.0f : 0.0f)) * (sem ? inv_scale : 1.0f);
         }
