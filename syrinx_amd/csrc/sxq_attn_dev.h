@@ -176,6 +176,52 @@ SXQ_DEV void attn_load_v(attn_v4f (&vr4)[HD / 32], const AttnArgs& A, int64_t he
     }
 }
 
+// The loads of a split issued before the stream's length is known (SPEC, batch 1): the
+// length (a scalar load, so waiting for it does not wait for the vector loads), the
+// norm + RoPE inputs with the step's RoPE row (A.rope_row: cos then sin at the stream's
+// position, copied by the step's embedding kernel), then the key and value tiles of all
+// P positions (rows clamped to the cache; rows past the length are never read: the
+// softmax masks their scores and the weighted values stop at the length).  Wave w
+// loads item min(w, G): a query head, or the new key from wave G on (used only by the
+// split holding the position); with G == NW wave 0 also loads the new key as rin2.
+template <int HD>
+struct SplitLoads {
+    RopeIn rin, rin2;
+    int item;
+    float4 kr[HD / 32];
+    attn_v4f vr4[HD / 32];
+};
+template <int HD, int NT, int GC>
+SXQ_DEV int attn_spec_loads(SplitLoads<HD>& R, const AttnArgs& A, int s, int g, int sp) {
+    constexpr int P = NT / 8, NW = NT / 64, VR = HD / 32;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = A.len[s];
+    issue_point();  // the length's load first
+    const int nh = A.nh, G = GC > 0 ? GC : nh / A.nkv;
+    const float* row = A.qkv + (int64_t)s * A.qkv_n;
+    const float *cr = A.rope_row, *sr = A.rope_row + HD / 2;
+    R.item = min(wave, G);
+    const bool isq = R.item < G;
+    R.rin = rope_load<HD>(row + (int64_t)(isq ? g * G + R.item : nh + g) * HD, isq ? A.qn : A.kn, A.interleaved, cr, sr,
+                          lane);
+    if (G == NW && wave == 0) R.rin2 = rope_load<HD>(row + (int64_t)(nh + g) * HD, A.kn, A.interleaved, cr, sr, lane);
+    const int64_t head_off = (int64_t)s * A.kv_stream_stride + (int64_t)g * A.max_seq * HD;
+    const int p0 = sp * P, last = A.max_seq - 1;
+    {
+        const int kp = tid >> 3, kcol = 4 * (tid & 7);
+        const float* krow = A.kc + head_off + (int64_t)min(p0 + kp, last) * HD + kcol;
+#pragma unroll
+        for (int j = 0; j < HD / 32; ++j) R.kr[j] = ld_global((const float4*)(krow + 32 * j));
+    }
+#pragma unroll
+    for (int r = 0; r < VR; ++r) {
+        const int e = r * 4 * NT + 4 * tid, vr = e / HD, col = e - vr * HD;
+        R.vr4[r] = ld_global((const attn_v4f*)(A.vc + head_off + (int64_t)min(p0 + vr, last) * HD + col));
+    }
+    issue_point();
+    return pos;
+}
+
 // The partials of one split of the fused decode attention, NT threads: split sp of KV
 // head group g of stream s, P = NT/8 cached positions [sp*P, sp*P + P) (the stream holds
 // pos + 1 positions in nsp splits), leaving the split's partials {m, l, 0, 0, acc[hd]}
@@ -201,7 +247,7 @@ SXQ_DEV void attn_load_v(attn_v4f (&vr4)[HD / 32], const AttnArgs& A, int64_t he
 // back by another thread of the workgroup (the partials are published after it).
 template <int VDT, int HD, int NT, int GC, bool PUB = false>
 SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int nsp, float* smem, float* part_s,
-                        __amdgpu_buffer_rsrc_t prs) {
+                        __amdgpu_buffer_rsrc_t prs, SplitLoads<HD>* pre = nullptr) {
     constexpr int P = NT / 8, KJ = HD / 32, PR = HD + 4, NW = NT / 64, VR = HD / 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int L = pos + 1, p0 = sp * P;
@@ -224,24 +270,39 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
     const int kp = tid >> 3, kcol = 4 * (tid & 7);
 
     // 1. this wave's norm + RoPE item (every wave loads one; idle waves repeat the last),
-    //    then the key and value tiles
+    //    then the key and value tiles -- or, from the loads issued before the length
+    //    (pre), the same with the new value's row put in place
     const int nitem = G + (has_new ? 1 : 0);
-    const int item = min(wave, nitem - 1);
+    const int item = pre ? pre->item : min(wave, nitem - 1);
     const bool isq = item < G;
     const float* inw = isq ? A.qn : A.kn;
-    const RopeIn rin =
-        rope_load<HD>(row + (int64_t)(isq ? g * G + item : nh + g) * HD, inw, A.interleaved, cos_row, sin_row, lane);
+    RopeIn rin;
     float4 kr[KJ];
     attn_v4f vr4[VR];
-    attn_load_k<HD, NT>(kr, A, head_off, sp, L);
-    attn_load_v<HD, NT>(vr4, A, head_off, vrow_new, sp, L, nsp);
-    issue_point();
+    if (pre) {
+        rin = pre->rin;
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) kr[j] = pre->kr[j];
+#pragma unroll
+        for (int r = 0; r < VR; ++r) {
+            vr4[r] = pre->vr4[r];
+            const int e = r * 4 * NT + 4 * tid, vr = e / HD;
+            if (has_new && vr == slot) vr4[r] = ld_global((const attn_v4f*)(vrow_new + (e - vr * HD)));
+        }
+    } else {
+        rin = rope_load<HD>(row + (int64_t)(isq ? g * G + item : nh + g) * HD, inw, A.interleaved, cos_row, sin_row,
+                            lane);
+        attn_load_k<HD, NT>(kr, A, head_off, sp, L);
+        attn_load_v<HD, NT>(vr4, A, head_off, vrow_new, sp, L, nsp);
+        issue_point();
+    }
     // 2. norm + RoPE in registers while the tiles are in flight
     {
         float2 y = rope_pair<HD>(rin, inw != nullptr, A.eps, A.inv_hd, lane);
         float2 y2 = make_float2(0.0f, 0.0f);
         if (wave + NW < nitem) {  // G == NW: the new key is a second item of wave 0
-            const RopeIn r2 = rope_load<HD>(row + (int64_t)(nh + g) * HD, A.kn, A.interleaved, cos_row, sin_row, lane);
+            const RopeIn r2 = pre ? pre->rin2
+                                  : rope_load<HD>(row + (int64_t)(nh + g) * HD, A.kn, A.interleaved, cos_row, sin_row, lane);
             y2 = rope_pair<HD>(r2, A.kn != nullptr, A.eps, A.inv_hd, lane);
         }
         float* kapp = A.kc + head_off + (int64_t)pos * HD;  // the new key's cache row
@@ -383,17 +444,18 @@ SXQ_DEV bool attn_split(const AttnArgs& A, int s, int g, int sp, int pos, int ns
 // Requires HD in {64, 128}, G <= 8 and G*HD a whole number of activation blocks; GC is
 // G as a compile-time constant (the Qwen3-4B and Qwen2-0.5B groups), or 0 to read it
 // from A at run time.
-template <int VDT, int HD, int NT, int GC, bool PUB = false>
+template <int VDT, int HD, int NT, int GC, bool PUB = false, bool SPEC = false>
 SXQ_DEV void attn_decode_body(const AttnArgs& A, int s, int g, int sp, float* smem, bool* last) {
     constexpr int P = NT / 8, PR = HD + 4;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = A.len[s], nsp = (pos + P) / P;
+    SplitLoads<HD> R;
+    const int pos = SPEC ? attn_spec_loads<HD, NT, GC>(R, A, s, g, sp) : A.len[s], nsp = (pos + P) / P;
     if (sp >= nsp) return;
     const int nh = A.nh, nkv = A.nkv, max_splits = A.max_splits;
     const int G = GC > 0 ? GC : nh / nkv, gd = G * HD, T = gd / 4, nq = NT / T;
     float* part_s = A.part + (int64_t)s * nh * max_splits * PR;
     const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(part_s, (uint32_t)nh * (uint32_t)max_splits * PR * 4);
-    if (!attn_split<VDT, HD, NT, GC, PUB>(A, s, g, sp, pos, nsp, smem, part_s, prs)) return;
+    if (!attn_split<VDT, HD, NT, GC, PUB>(A, s, g, sp, pos, nsp, smem, part_s, prs, SPEC ? &R : nullptr)) return;
     // the last split of the group to arrive merges the group's heads
     if (!publish_and_count(&A.counter[(s * nkv + g) * A.cstride], (unsigned)nsp, last)) return;
 

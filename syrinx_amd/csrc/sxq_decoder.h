@@ -51,12 +51,22 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
                                    float* q_out, hipStream_t s, MmaRec* rec = nullptr, int grid_splits = 0);
 hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s,
                                  MmaRec* rec = nullptr);
+// The RoPE row at stream 0's length, copied by the step's embedding kernel (beside its own
+// work) for the fused attention of every layer: out[i] = cos_t[len[0] * half + i],
+// out[half + i] = sin_t[...], i < half (<= 128).
+struct RopeRow {
+    const int* len = nullptr;
+    const float* cos_t = nullptr;
+    const float* sin_t = nullptr;
+    int half = 0;
+    float* out = nullptr;
+};
 // table: the dense input table [table_rows][dim], or null to dequantize the rows of the tied head w
 hipError_t launch_embed_mcf(const int* ids, int ids_per, int B, const float* table, int64_t table_rows,
                             const QWeight& w, int dim, const float* cb, int n_cb, int cb_size, int sem_begin,
-                            int sem_end, float* h, hipStream_t s);
+                            int sem_end, float* h, hipStream_t s, const RopeRow& rr = RopeRow());
 hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
-                              hipStream_t s);
+                              hipStream_t s, const RopeRow& rr = RopeRow());
 // Greedy argmax per stream; with `len` also advances each stream's cached length.
 // pval/pidx: [B * kArgmaxSlices] partials; counter: [B * kCounterStride], zero before the
 // first call (each call leaves it zero again).
@@ -115,6 +125,7 @@ struct AttnArgs {
     int ready_copies;
     uint32_t pub_off;        // k_attn_wo_decode: LDS byte offset of the slice staging
     MmaRec* rec;             // optional (Q8_K, B <= 16): the context rows' MmaRec records too
+    const float* rope_row;   // k_attn_wo_decode: stream 0's RoPE row (cos [hd/2], sin [hd/2]), or null
 };
 
 // Batch-1 decode attention and the O projection (Q4_K, y += ctx . Wo^T in place) as one
@@ -125,11 +136,15 @@ struct AttnArgs {
 // counter_stride() words apart.
 bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo, int dim);
 hipError_t attn_wo_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo);
+// rope_row (optional): the step's RoPE row at stream 0's length (cos [hd/2] then sin,
+// copied there earlier in the step, e.g. by launch_embed_* with RopeRow): the splits then
+// issue their loads before the length returns (the queries' and new key's inputs with
+// that row, both tiles); without it they wait for the length first.
 hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int nh, int nkv, int hd, const float* qn,
                                       const float* kn, float eps, int interleaved, const float* cos_t,
                                       const float* sin_t, const int* len, float* kc, float* vc, int max_seq,
                                       int max_splits, float* part, unsigned* counter, uint8_t* act, const QWeight& wo,
                                       float* y, unsigned* ready, unsigned* ready_next, float* ctx_out, float* q_out,
-                                      hipStream_t s, int grid_splits = 0);
+                                      hipStream_t s, int grid_splits = 0, const float* rope_row = nullptr);
 
 }  // namespace sxq

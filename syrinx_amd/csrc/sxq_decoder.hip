@@ -402,11 +402,21 @@ SXQ_DEV float weight_elem(const QWeight& w, int64_t r, int e) {
 // of :117), else the dequantized rows of the tied head w (rows = w.n).  Without codebooks
 // (n_cb = 0) this is the plain gather E[tok].  Ids outside the table (token >= rows,
 // code >= cb_size, negatives) read nothing: their rows count as zero.
+// The step's RoPE row (RopeRow): workgroup (0, 0)'s first 2 * half threads, beside their
+// embedding element.
+SXQ_DEV void rope_row_copy(const RopeRow& rr) {
+    if (rr.out && blockIdx.x == 0 && blockIdx.y == 0 && (int)threadIdx.x < 2 * rr.half) {
+        const int t = threadIdx.x, i = t < rr.half ? t : t - rr.half;
+        rr.out[t] = (t < rr.half ? rr.cos_t : rr.sin_t)[(int64_t)rr.len[0] * rr.half + i];
+    }
+}
+
 __global__ __launch_bounds__(256) void k_embed_mcf(const int* __restrict__ ids, int ids_per,
                                                    const float* __restrict__ table, int64_t rows, QWeight w, int dim,
                                                    const float* __restrict__ cb, int n_cb, int cb_size,
                                                    int sem_begin, int sem_end, float inv_scale,
-                                                   float* __restrict__ h) {
+                                                   float* __restrict__ h, RopeRow rr) {
+    rope_row_copy(rr);
     const int s = blockIdx.x;
     const int* fr = ids + (int64_t)s * ids_per;
     const int tok = fr[0];
@@ -440,7 +450,8 @@ __global__ __launch_bounds__(256) void k_embed_mcf(const int* __restrict__ ids, 
 
 __global__ __launch_bounds__(256) void k_embed_dense(const int* __restrict__ ids, int ids_per,
                                                      const float* __restrict__ table, int rows, int dim,
-                                                     float* __restrict__ h) {
+                                                     float* __restrict__ h, RopeRow rr) {
+    rope_row_copy(rr);
     const int s = blockIdx.x;
     const int tok = ids[(int64_t)s * ids_per];
     const bool ok = tok >= 0 && tok < rows;
@@ -647,6 +658,7 @@ hipError_t launch_attention_decode(int vdt, const float* qkv, int B, int qkv_n, 
     A.q_out = q_out;
     A.ready = nullptr;
     A.ready_copies = 0;
+    A.rope_row = nullptr;
     A.pub_off = 0;
     A.rec = rec;
     const int all = (max_seq + kAttnSplitFused - 1) / kAttnSplitFused;  // partial records: max_splits per head
@@ -705,7 +717,8 @@ SXQ_DEV bool wo_wait_stage(const AttnArgs& A, const WoArgs& W, int t, uint4* lds
     return ok;
 }
 
-template <int WT, int HD, int GC, int TM>
+// SPEC: the attention splits issue their loads before the length returns (A.rope_row).
+template <int WT, int HD, int GC, int TM, bool SPEC>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_attn_wo_decode(AttnArgs A,
                                                                                                           WoArgs W) {
     constexpr int NT = kAttnThreads;
@@ -714,7 +727,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(6,
     __shared__ bool flag;
     const int id = blockIdx.x;
     if (id < W.n_attn) {
-        attn_decode_body<VDT, HD, NT, GC, true>(A, 0, id % A.nkv, id / A.nkv, (float*)smem4, &flag);
+        attn_decode_body<VDT, HD, NT, GC, true, SPEC>(A, 0, id % A.nkv, id / A.nkv, (float*)smem4, &flag);
         return;
     }
     uint4* lds = (uint4*)smem4;
@@ -842,27 +855,31 @@ static size_t attn_wo_lds(int nh, int nkv, int hd, int max_splits, const QWeight
     }
     return attn > proj ? attn : proj;
 }
-template <int WT>
-static const void* attn_wo_kernel_tm(int hd, int G, int tm) {
-    if (tm == 4) {
-        if (hd == 128) return G == 4 ? (const void*)k_attn_wo_decode<WT, 128, 4, 4> : (const void*)k_attn_wo_decode<WT, 128, 0, 4>;
-        return G == 7 ? (const void*)k_attn_wo_decode<WT, 64, 7, 4> : (const void*)k_attn_wo_decode<WT, 64, 0, 4>;
-    }
-    if (tm == 2) {
-        if (hd == 128) return G == 4 ? (const void*)k_attn_wo_decode<WT, 128, 4, 2> : (const void*)k_attn_wo_decode<WT, 128, 0, 2>;
-        return G == 7 ? (const void*)k_attn_wo_decode<WT, 64, 7, 2> : (const void*)k_attn_wo_decode<WT, 64, 0, 2>;
-    }
-    if (hd == 128) return G == 4 ? (const void*)k_attn_wo_decode<WT, 128, 4, 1> : (const void*)k_attn_wo_decode<WT, 128, 0, 1>;
-    return G == 7 ? (const void*)k_attn_wo_decode<WT, 64, 7, 1> : (const void*)k_attn_wo_decode<WT, 64, 0, 1>;
+template <int WT, int TM, bool SPEC>
+static const void* attn_wo_kernel_g(int hd, int G) {
+    if (hd == 128)
+        return G == 4 ? (const void*)k_attn_wo_decode<WT, 128, 4, TM, SPEC> : (const void*)k_attn_wo_decode<WT, 128, 0, TM, SPEC>;
+    return G == 7 ? (const void*)k_attn_wo_decode<WT, 64, 7, TM, SPEC> : (const void*)k_attn_wo_decode<WT, 64, 0, TM, SPEC>;
 }
-static const void* attn_wo_kernel(int hd, int G, const QWeight& wo) {
+template <int WT, bool SPEC>
+static const void* attn_wo_kernel_tm(int hd, int G, int tm) {
+    if (tm == 4) return attn_wo_kernel_g<WT, 4, SPEC>(hd, G);
+    if (tm == 2) return attn_wo_kernel_g<WT, 2, SPEC>(hd, G);
+    return attn_wo_kernel_g<WT, 1, SPEC>(hd, G);
+}
+template <bool SPEC>
+static const void* attn_wo_kernel_s(int hd, int G, const QWeight& wo) {
     if (wo.dtype == kQ4K) {
         if (hd == 128)
-            return G == 4 ? (const void*)k_attn_wo_decode<kWoQ4K, 128, 4, kWoTm> : (const void*)k_attn_wo_decode<kWoQ4K, 128, 0, kWoTm>;
-        return (const void*)k_attn_wo_decode<kWoQ4K, 64, 0, kWoTm>;
+            return G == 4 ? (const void*)k_attn_wo_decode<kWoQ4K, 128, 4, kWoTm, SPEC>
+                          : (const void*)k_attn_wo_decode<kWoQ4K, 128, 0, kWoTm, SPEC>;
+        return (const void*)k_attn_wo_decode<kWoQ4K, 64, 0, kWoTm, SPEC>;
     }
     const int tm = wo_tm_q80((int)wo.n, (int)wo.nb, wo.dtype);
-    return wo.dtype == kQ8_0 ? attn_wo_kernel_tm<kWoQ8_0>(hd, G, tm) : attn_wo_kernel_tm<kWoQ4_0>(hd, G, tm);
+    return wo.dtype == kQ8_0 ? attn_wo_kernel_tm<kWoQ8_0, SPEC>(hd, G, tm) : attn_wo_kernel_tm<kWoQ4_0, SPEC>(hd, G, tm);
+}
+static const void* attn_wo_kernel(int hd, int G, const QWeight& wo, bool spec) {
+    return spec ? attn_wo_kernel_s<true>(hd, G, wo) : attn_wo_kernel_s<false>(hd, G, wo);
 }
 
 bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo, int dim) {
@@ -881,7 +898,10 @@ bool attn_wo_decode_fits(int vdt, int nh, int nkv, int hd, int max_splits, const
 hipError_t attn_wo_decode_prepare(int vdt, int nh, int nkv, int hd, int max_splits, const QWeight& wo) {
     (void)vdt;
     const int lds = (int)attn_wo_lds(nh, nkv, hd, max_splits, wo);
-    return hipFuncSetAttribute(attn_wo_kernel(hd, nh / nkv, wo), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    hipError_t e = hipFuncSetAttribute(attn_wo_kernel(hd, nh / nkv, wo, false), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(attn_wo_kernel(hd, nh / nkv, wo, true), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    return e;
 }
 
 hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int nh, int nkv, int hd, const float* qn,
@@ -889,7 +909,7 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
                                       const float* sin_t, const int* len, float* kc, float* vc, int max_seq,
                                       int max_splits, float* part, unsigned* counter, uint8_t* act, const QWeight& wo,
                                       float* y, unsigned* ready, unsigned* ready_next, float* ctx_out, float* q_out,
-                                      hipStream_t s, int grid_splits) {
+                                      hipStream_t s, int grid_splits, const float* rope_row) {
     if (!attn_wo_decode_fits(vdt, nh, nkv, hd, max_splits, wo, (int)wo.n) ||
         max_seq > kMaxSplitsFused * kAttnSplitFused || ready == ready_next)
         return hipErrorInvalidValue;
@@ -920,6 +940,7 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
     A.q_out = q_out;
     A.ready = ready;
     A.ready_copies = ready_copies();
+    A.rope_row = rope_row;
     A.pub_off = (uint32_t)wo_pub_off(nh, nkv, hd, max_splits);
     A.rec = nullptr;
     WoArgs W;
@@ -936,7 +957,8 @@ hipError_t launch_attention_wo_decode(int vdt, const float* qkv, int qkv_n, int 
     const int n_wo = (W.n + W.R - 1) / W.R;
     const size_t lds = attn_wo_lds(nh, nkv, hd, max_splits, wo);
     void* args[] = {&A, &W};
-    return hipLaunchKernel(attn_wo_kernel(hd, nh / nkv, wo), dim3(W.n_attn + n_wo), dim3(kAttnThreads), args, lds, s);
+    return hipLaunchKernel(attn_wo_kernel(hd, nh / nkv, wo, rope_row != nullptr), dim3(W.n_attn + n_wo), dim3(kAttnThreads),
+                           args, lds, s);
 }
 
 hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t* act, float* act_f32, hipStream_t s,
@@ -950,17 +972,20 @@ hipError_t launch_silu_mul_quant(int vdt, const float* gu, int B, int I, uint8_t
 
 hipError_t launch_embed_mcf(const int* ids, int ids_per, int B, const float* table, int64_t table_rows,
                             const QWeight& w, int dim, const float* cb, int n_cb, int cb_size, int sem_begin,
-                            int sem_end, float* h, hipStream_t s) {
+                            int sem_end, float* h, hipStream_t s, const RopeRow& rr) {
+    if (rr.out && (rr.half < 1 || rr.half > 128 || !rr.len || !rr.cos_t || !rr.sin_t)) return hipErrorInvalidValue;
     const float inv_scale = 1.0f / sqrtf((float)n_cb + 1.0f);
     const int64_t rows = table ? table_rows : w.n;
     hipLaunchKernelGGL(k_embed_mcf, dim3(B, (dim + 255) / 256), dim3(256), 0, s, ids, ids_per, table, rows, w, dim, cb,
-                       n_cb, cb_size, sem_begin, sem_end, inv_scale, h);
+                       n_cb, cb_size, sem_begin, sem_end, inv_scale, h, rr);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_dense(const int* ids, int ids_per, int B, const float* table, int rows, int dim, float* h,
-                              hipStream_t s) {
-    hipLaunchKernelGGL(k_embed_dense, dim3(B, (dim + 255) / 256), dim3(256), 0, s, ids, ids_per, table, rows, dim, h);
+                              hipStream_t s, const RopeRow& rr) {
+    if (rr.out && (rr.half < 1 || rr.half > 128 || !rr.len || !rr.cos_t || !rr.sin_t)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed_dense, dim3(B, (dim + 255) / 256), dim3(256), 0, s, ids, ids_per, table, rows, dim, h,
+                       rr);
     return hipGetLastError();
 }
 

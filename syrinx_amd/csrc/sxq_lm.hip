@@ -91,6 +91,9 @@ struct sxq_lm {
     bool wo_fused = false, wo_dirty = false;
     unsigned* wo_ready = nullptr;  // [n_layers][kReadyCopies], likewise
     GemvRecWs rec_ws;              // 5..16 streams: the matrix-core GEMV's K-split workspace
+    // one stream through the fused attention: stream 0's RoPE row, copied by the step's
+    // embedding kernel (null: SXQ_ATTN_SPEC=0, the attention reads the tables after the length)
+    float* rope_row = nullptr;
     bool swiglu = false;        // one decode row: gate|up GEMV with SwiGLU epilogue + quantizing down GEMV
     float* act_f32 = nullptr;   // SwiGLU output row of that pair [max_batch][intermediate]
     float* trace = nullptr;  // optional f32 record of every intermediate of a step (tests)
@@ -213,16 +216,27 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
         tr += floats;
         return p;
     };
+    // one stream through the fused attention: the embedding kernel also copies the step's
+    // RoPE row, so that the attention splits issue their loads before the length returns
+    const bool spec = lm->rope_row && n == 1 && lm->wo_fused && !from_embeds && !lm->embed_scheme;
+    RopeRow rr;
+    if (spec) {
+        rr.len = lm->d_len;
+        rr.cos_t = lm->rope_cos;
+        rr.sin_t = lm->rope_sin;
+        rr.half = c.head_dim / 2;
+        rr.out = lm->rope_row;
+    }
     if (!from_embeds) {
         if (c.n_codebooks > 0 || (c.tied_embedding && !lm->embed))
             STEP(launch_embed_mcf(lm->d_ids, lm->ids_per, n, lm->embed, embed_rows(c), lm->head.w, c.dim, lm->cb_embed,
-                                  c.n_codebooks, c.codebook_size, c.semantic_begin, c.semantic_end, lm->h, s));
+                                  c.n_codebooks, c.codebook_size, c.semantic_begin, c.semantic_end, lm->h, s, rr));
         else if (lm->embed_scheme)
             STEP(launch_embed_gather(lm->embed_scheme, lm->embed_q, lm->embed_scale, embed_rows(c),
                                      c.dim, lm->d_ids, lm->ids_per, n, lm->h, s));
         else
             STEP(launch_embed_dense(lm->d_ids, lm->ids_per, n, lm->embed, embed_rows(c), c.dim,
-                                    lm->h, s));
+                                    lm->h, s, rr));
     }
     if (tr) STEP(record(lm->h, (size_t)n * c.dim));
     const bool wo_fused = lm->wo_fused && n == 1;
@@ -266,7 +280,7 @@ hipError_t enqueue_step(sxq_lm* lm, int n, bool from_embeds, hipStream_t s) {
                                                 kc, vc, c.max_seq, lm->max_splits, lm->part, lm->attn_count, lm->act_o,
                                                 L.wo.w, lm->h, lm->wo_ready + (size_t)l * kReadyCopies * counter_stride(),
                                                 lm->wo_ready + (size_t)((l + 1) % c.n_layers) * kReadyCopies * counter_stride(),
-                                                ctx_slot, q_slot, s, lm->grid_splits));
+                                                ctx_slot, q_slot, s, lm->grid_splits, spec ? lm->rope_row : nullptr));
             else
                 STEP(launch_attention_decode(lm->vdt, lm->qkv, n, lm->qkv_n, c.n_heads, c.n_kv_heads, c.head_dim, qn,
                                              kn, c.norm_eps, c.rope_interleaved, lm->rope_cos, lm->rope_sin, lm->d_len,
@@ -648,6 +662,8 @@ sxq_status sxq_lm_create(int device, const sxq_lm_config* cfg, sxq_lm** out) {
     A((void**)&lm->am_count, sizeof(unsigned) * MB * kCounterStride);
     A((void**)&lm->attn_count, sizeof(unsigned) * MB * c.n_kv_heads * kCounterStride);
     A((void**)&lm->wo_ready, sizeof(unsigned) * c.n_layers * kReadyCopies * kCounterStride);
+    if (const char* e_spec = getenv("SXQ_ATTN_SPEC"); !(e_spec && e_spec[0] == '0'))
+        A((void**)&lm->rope_row, sizeof(float) * 256);
     if (e != hipSuccess) {
         destroy_lm(lm);
         return hip_fail(e, "lm_create: allocation");
