@@ -20,6 +20,10 @@
  * buffer (a replay could overlap any later eager call): sxq_qmm_forward refuses it, and
  * the caller passes a workspace of its own to sxq_qmm_forward_ws, which the graph then
  * keeps alive.
+ * A decode engine (sxq_lm) owns its KV caches and work buffers, like the reference's
+ * `&mut self` steps: its calls are serialised on the host (a per-engine lock), and the
+ * GPU work of calls enqueued on one stream runs in call order.  Calls of one engine on
+ * different streams share those buffers, so the caller orders them (an event).
  */
 #ifndef SXQ_H
 #define SXQ_H
