@@ -509,6 +509,8 @@ def test_swiglu_pair_equals_three_launches(cuda, monkeypatch, graph, kind):
     for mode in ("pair", "three"):
         if mode == "three":
             monkeypatch.setenv("SXQ_SWIGLU_UNFUSED", "1")  # read when the engine is created
+        else:
+            monkeypatch.delenv("SXQ_SWIGLU_UNFUSED", raising=False)
         lm = D.DecoderLM(cfg, device=cuda)
         assert bool(lm.paths() & lm.PATH_SWIGLU) == (mode == "pair"), lm.paths()
         lm.init_random(seed=41, std=0.02)
@@ -561,6 +563,9 @@ def test_attention_and_o_projection_in_one_launch_equals_two(cuda, monkeypatch, 
     for mode in ("one", "two"):
         if mode == "two":
             monkeypatch.setenv("SXQ_ATTN_WO_UNFUSED", "1")  # read when the engine is created
+        else:  # the fused launch needs the fused attention as well
+            monkeypatch.delenv("SXQ_ATTN_WO_UNFUSED", raising=False)
+            monkeypatch.delenv("SXQ_ATTN_UNFUSED", raising=False)
         lm = D.DecoderLM(cfg, device=cuda)
         assert bool(lm.paths() & lm.PATH_ATTN_WO) == (mode == "one"), lm.paths()
         lm.init_random(seed=51, std=0.02)
