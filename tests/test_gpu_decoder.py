@@ -16,6 +16,8 @@ Two levels, both on identical quantized weights:
    the logits by up to ~2e-2 (measured on the oracle alone).  So every step must agree
    to LOGIT_RTOL_FLIP, and most steps -- all, barring a flip -- to LOGIT_RTOL.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -504,6 +506,9 @@ def test_swiglu_pair_equals_three_launches(cuda, monkeypatch, graph, kind):
     quantizes in its prologue give the bits of GEMV + SiLU*mul kernel + GEMV, for Q4_K,
     Q8_0 and Q4_0 weights.  The pair's own output row (read_state 5) shows which path ran:
     silu(g) * u of the step's gate|up row with the pair, untouched zeros without."""
+    if os.environ.get("SXQ_GEMV_WG"):
+        pytest.skip("SXQ_GEMV_WG regrids the GEMVs (read once per process): the pair's tiles are laid out "
+                    "for the default grid, so the engine runs three launches")
     cfg = _small_cfg(kind, 2)
     res = {}
     for mode in ("pair", "three"):
